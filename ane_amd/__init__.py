@@ -1,0 +1,346 @@
+"""ane_amd -- MI355X (gfx950) implementation of ane's quantized compute path.
+
+Python mirror of the reference's C++ entry points for this path:
+
+* ``Op`` -- the opcode numbering of the reference's ``enum class ane::Op``
+  (include/ane/ane.hpp:47-177) plus ``dense_fused_i8`` (README.md:84-97).
+* ``encode`` / ``dispatch`` -- ``ane::dispatch`` (include/ane/ane.hpp:206-220):
+  ``[op:u8]`` followed by each argument's little-endian bytes, handed to the
+  C entry point ``stream_exec`` of ``libane_amd.so``.
+* thin wrappers over the kernel-level C ABI (``include/ane_hip.h``) that take
+  torch tensors for device memory and the current torch stream.
+
+The native library is required: importing works without it (so the CPU test
+suite can inspect the package), but every call raises if it is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+import struct
+from pathlib import Path
+from typing import Any, Iterable
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libane_amd.so"
+
+
+class Op(enum.IntEnum):
+    """Opcode numbers served by this build (reference include/ane/ane.hpp:47-177)."""
+
+    dense_i8 = 0x18
+    quantize_fp32_i8 = 0x19
+    dequantize_i8_fp32 = 0x1A
+    pack_b_i8 = 0x1B
+    quantize_fp32_i8_channelwise = 0x1C
+    dense_u8s8 = 0x1E
+    q8_0_gemv = 0x57
+    dense_fused_i8 = 0x80
+
+
+class AneError(RuntimeError):
+    """A call into libane_amd.so returned a non-zero ane_status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"ane status {status}: {message}")
+        self.status = status
+
+
+STATUS = {
+    0: "ANE_OK",
+    1: "ANE_ERR_INVALID_ARG",
+    2: "ANE_ERR_BAD_POINTER",
+    3: "ANE_ERR_BUFFER_TOO_SMALL",
+    4: "ANE_ERR_UNKNOWN_OPCODE",
+    5: "ANE_ERR_TRUNCATED",
+    6: "ANE_ERR_HIP",
+    7: "ANE_ERR_NO_DEVICE",
+    8: "ANE_ERR_WORKSPACE",
+}
+
+# Symbols include/ane_hip.h declares; the library must export every one.
+EXPORTS = (
+    "stream_exec",
+    "ane_last_error",
+    "ane_last_error_message",
+    "ane_set_stream",
+    "ane_stream_exec_async",
+    "ane_hip_quantize_workspace_size",
+    "ane_hip_quantize_fp32_i8",
+    "ane_hip_dequantize_i8_fp32",
+    "ane_hip_quantize_channelwise",
+    "ane_hip_packed_b_size",
+    "ane_hip_pack_b_i8",
+    "ane_hip_dense_i8",
+    "ane_hip_dense_fused_i8_workspace_size",
+    "ane_hip_dense_fused_i8",
+    "ane_hip_gemm_s8_i32",
+    "ane_hip_q8_0_gemv",
+    "ane_hip_q8_0_mul_mat_workspace_size",
+    "ane_hip_q8_0_mul_mat",
+    "ane_hip_device_check",
+    "ane_hip_version",
+)
+
+_lib: ctypes.CDLL | None = None
+
+_c = ctypes
+_P = _c.c_void_p
+_SIGS: dict[str, tuple[Any, list[Any]]] = {
+    "stream_exec": (None, [_P, _c.c_size_t]),
+    "ane_last_error": (_c.c_int, []),
+    "ane_last_error_message": (_c.c_char_p, []),
+    "ane_set_stream": (None, [_P]),
+    "ane_stream_exec_async": (_c.c_int, [_P, _c.c_size_t, _P]),
+    "ane_hip_quantize_workspace_size": (_c.c_size_t, [_c.c_uint64]),
+    "ane_hip_quantize_fp32_i8": (_c.c_int, [_c.c_uint64, _c.c_int, _P, _P, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_dequantize_i8_fp32": (_c.c_int, [_c.c_uint64, _c.c_float, _P, _P, _P]),
+    "ane_hip_quantize_channelwise": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]),
+    "ane_hip_packed_b_size": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),
+    "ane_hip_pack_b_i8": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P]),
+    "ane_hip_dense_i8": (
+        _c.c_int,
+        [_c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_float, _c.c_float, _c.c_uint8, _P, _P, _P, _P,
+         _c.c_int, _P],
+    ),
+    "ane_hip_dense_fused_i8_workspace_size": (_c.c_size_t, [_c.c_int32, _c.c_int32, _c.c_int32]),
+    "ane_hip_dense_fused_i8": (
+        _c.c_int,
+        [_c.c_int32, _c.c_int32, _c.c_int32, _c.c_float, _c.c_int, _P, _P, _P, _P, _P, _c.c_size_t, _P],
+    ),
+    "ane_hip_gemm_s8_i32": (
+        _c.c_int,
+        [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _c.c_uint32, _P, _c.c_uint32, _P, _P],
+    ),
+    "ane_hip_q8_0_gemv": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]),
+    "ane_hip_q8_0_mul_mat_workspace_size": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),
+    "ane_hip_q8_0_mul_mat": (
+        _c.c_int,
+        [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _c.c_size_t, _P],
+    ),
+    "ane_hip_device_check": (_c.c_int, []),
+    "ane_hip_version": (_c.c_char_p, []),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load libane_amd.so (built by ``python -m ane_amd.build``); raise if absent."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m ane_amd.build` "
+                "(there is no CPU fallback for this library)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | ctypes.RTLD_GLOBAL)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+# ---------------------------------------------------------------- encoding
+class _Arg:
+    __slots__ = ("fmt", "value", "keep")
+
+    def __init__(self, fmt: str, value: Any, keep: Any = None):
+        self.fmt = fmt
+        self.value = value
+        self.keep = keep
+
+
+class Record(bytes):
+    """An encoded record that also holds the tensors its pointers refer to,
+    so a temporary operand cannot be freed (and its memory reused) between
+    encoding and execution."""
+
+    keep: tuple = ()
+
+
+def u8(v: int) -> _Arg:
+    return _Arg("<B", int(v))
+
+
+def boolean(v: bool) -> _Arg:
+    return _Arg("<B", 1 if v else 0)
+
+
+def u32(v: int) -> _Arg:
+    return _Arg("<I", int(v))
+
+
+def i32(v: int) -> _Arg:
+    return _Arg("<i", int(v))
+
+
+def f32(v: float) -> _Arg:
+    return _Arg("<f", float(v))
+
+
+def ptr(v: Any) -> _Arg:
+    """Any pointer operand: a torch tensor (its data_ptr) or an integer address."""
+    if hasattr(v, "data_ptr"):
+        return _Arg("<Q", int(v.data_ptr()), keep=v)
+    return _Arg("<Q", int(v or 0))
+
+
+def encode(op: int, *args: _Arg) -> Record:
+    """Byte record of ane::dispatch(op, args...) (include/ane/ane.hpp:206-220)."""
+    out = bytearray([int(op) & 0xFF])
+    keep = []
+    for a in args:
+        if not isinstance(a, _Arg):
+            raise TypeError("dispatch arguments must be typed: u32/i32/f32/u8/boolean/ptr")
+        out += struct.pack(a.fmt, a.value)
+        if a.keep is not None:
+            keep.append(a.keep)
+    rec = Record(bytes(out))
+    rec.keep = tuple(keep)
+    return rec
+
+
+# Typed records with the reference's argument order (Appendix of the opcode
+# table: bytecode_interpreter.s parse sites cited in ane_amd/csrc/stream_exec.cpp).
+def rec_dense_i8(M, N, K, sa, sb, relu, A, Bp, bias, C, unsigned_a=False) -> bytes:
+    op = Op.dense_u8s8 if unsigned_a else Op.dense_i8
+    return encode(op, u32(M), u32(N), u32(K), f32(sa), f32(sb), boolean(relu), ptr(A), ptr(Bp),
+                  ptr(bias), ptr(C))
+
+
+def rec_quantize(count, src, dst, scale_out) -> bytes:
+    return encode(Op.quantize_fp32_i8, u32(count), ptr(src), ptr(dst), ptr(scale_out))
+
+
+def rec_dequantize(count, scale, src, dst) -> bytes:
+    return encode(Op.dequantize_i8_fp32, u32(count), f32(scale), ptr(src), ptr(dst))
+
+
+def rec_pack_b(K, N, src, dst) -> bytes:
+    return encode(Op.pack_b_i8, u32(K), u32(N), ptr(src), ptr(dst))
+
+
+def rec_channelwise(rows, cols, src, dst, scales) -> bytes:
+    return encode(Op.quantize_fp32_i8_channelwise, u32(rows), u32(cols), ptr(src), ptr(dst), ptr(scales))
+
+
+def rec_q8_0_gemv(M, K, x, W, y) -> bytes:
+    return encode(Op.q8_0_gemv, u32(M), u32(K), ptr(x), ptr(W), ptr(y))
+
+
+def rec_dense_fused_i8(M, N, K, scale, relu, A, B, C) -> bytes:
+    return encode(Op.dense_fused_i8, i32(M), i32(N), i32(K), f32(scale), boolean(relu), ptr(A), ptr(B),
+                  ptr(C))
+
+
+# ---------------------------------------------------------------- execution
+def _stream_handle(stream: Any = None) -> int:
+    if stream is None:
+        import torch
+
+        stream = torch.cuda.current_stream()
+    if hasattr(stream, "cuda_stream"):
+        return int(stream.cuda_stream)
+    return int(stream or 0)
+
+
+def stream_exec(data: bytes | Iterable[bytes], stream: Any = None) -> None:
+    """Run encoded records through the C entry point ``stream_exec`` on
+    ``stream`` (default: torch's current stream) and raise AneError on failure."""
+    records = [data] if isinstance(data, (bytes, bytearray)) else list(data)
+    data = b"".join(records)  # `records` keeps every operand alive until the call returns
+    L = lib()
+    L.ane_set_stream(_stream_handle(stream))
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    L.stream_exec(buf, len(data))
+    st = L.ane_last_error()
+    del records
+    if st != 0:
+        raise AneError(st, L.ane_last_error_message().decode(errors="replace"))
+
+
+def dispatch(op: int, *args: _Arg, stream: Any = None) -> None:
+    """``ane::dispatch(op, args...)`` with explicitly typed arguments."""
+    stream_exec(encode(op, *args), stream=stream)
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        raise AneError(status, f"{what}: {STATUS.get(status, '?')}")
+
+
+def _p(t: Any) -> int:
+    if t is None:
+        return 0
+    return int(t.data_ptr()) if hasattr(t, "data_ptr") else int(t)
+
+
+# Kernel-level wrappers (device tensors, current torch stream unless given).
+def quantize_fp32_i8(src, dst, scale_out, count=None, pad16=True, workspace=None, stream=None):
+    import torch
+
+    n = src.numel() if count is None else count
+    L = lib()
+    wsb = L.ane_hip_quantize_workspace_size(n)
+    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=src.device)
+    check(L.ane_hip_quantize_fp32_i8(n, 1 if pad16 else 0, _p(src), _p(dst), _p(scale_out), _p(ws), wsb,
+                                     _stream_handle(stream)), "quantize_fp32_i8")
+
+
+def dense_fused_i8(M, N, K, scale, relu, A, B, C, scales_out=None, workspace=None, stream=None):
+    import torch
+
+    L = lib()
+    wsb = L.ane_hip_dense_fused_i8_workspace_size(M, N, K)
+    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=A.device)
+    check(L.ane_hip_dense_fused_i8(M, N, K, scale, 1 if relu else 0, _p(A), _p(B), _p(C), _p(scales_out),
+                                   _p(ws), wsb, _stream_handle(stream)), "dense_fused_i8")
+
+
+def dense_fused_i8_workspace_size(M, N, K) -> int:
+    return int(lib().ane_hip_dense_fused_i8_workspace_size(M, N, K))
+
+
+def gemm_s8_i32(A, Bt, acc, M, N, K, lda=None, ldb=None, stream=None):
+    check(lib().ane_hip_gemm_s8_i32(M, N, K, _p(A), lda or K, _p(Bt), ldb or K, _p(acc),
+                                    _stream_handle(stream)), "gemm_s8_i32")
+
+
+def q8_0_gemv(M, K, x, W, y, stream=None):
+    check(lib().ane_hip_q8_0_gemv(M, K, _p(x), _p(W), _p(y), _stream_handle(stream)), "q8_0_gemv")
+
+
+def q8_0_mul_mat_workspace_size(K, T) -> int:
+    return int(lib().ane_hip_q8_0_mul_mat_workspace_size(K, T))
+
+
+def q8_0_mul_mat(N, K, T, x, W, y, workspace=None, stream=None):
+    import torch
+
+    L = lib()
+    wsb = L.ane_hip_q8_0_mul_mat_workspace_size(K, T)
+    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=W.device)
+    check(L.ane_hip_q8_0_mul_mat(N, K, T, _p(x), _p(W), _p(y), _p(ws), wsb, _stream_handle(stream)),
+          "q8_0_mul_mat")
+
+
+def pack_b_i8(K, N, src, dst, stream=None):
+    check(lib().ane_hip_pack_b_i8(K, N, _p(src), _p(dst), _stream_handle(stream)), "pack_b_i8")
+
+
+def packed_b_size(K, N) -> int:
+    return int(lib().ane_hip_packed_b_size(K, N))
+
+
+def dense_i8(M, N, K, sa, sb, relu, A, Bp, bias, C, unsigned_a=False, stream=None):
+    check(lib().ane_hip_dense_i8(M, N, K, sa, sb, 1 if relu else 0, _p(A), _p(Bp), _p(bias), _p(C),
+                                 1 if unsigned_a else 0, _stream_handle(stream)), "dense_i8")
+
+
+def require_gpu() -> None:
+    """Raise unless libane_amd.so is loadable and a gfx950 device is present."""
+    st = lib().ane_hip_device_check()
+    if st != 0:
+        raise AneError(st, "no usable gfx950 device")

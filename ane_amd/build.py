@@ -1,0 +1,90 @@
+"""Build recipe for ane_amd/libane_amd.so (gfx950) and the CPU oracle.
+
+Run ``python -m ane_amd.build`` (or ``__graft_entry__.build()``).  The
+library is built in-tree so it travels with the repository snapshot; object
+files go to ``ane_amd/_build/``.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_build"
+LIB = PKG / "libane_amd.so"
+
+ARCH = "gfx950"
+
+# -ffp-contract=off: the epilogues and quantizers must round after every
+# fmul/fadd exactly like the reference's unfused SVE instructions.
+# packed-fp32-ops is disabled for every HIP translation unit.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build ane_amd)")
+
+
+def _run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+
+
+def build_library(verbose: bool = False) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    cc = hipcc()
+    jobs = []
+    for src in sorted(CSRC.glob("*.hip")):
+        obj = OBJ / (src.stem + ".o")
+        jobs.append([cc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+    for src in sorted(CSRC.glob("*.cpp")):
+        obj = OBJ / (src.stem + ".host.o")
+        jobs.append([cc, *HOST_FLAGS, "-I/opt/rocm/include", "-c", str(src), "-o", str(obj)])
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        list(ex.map(_run, jobs))
+    objs = [str(p) for p in sorted(OBJ.glob("*.o"))]
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+def build_oracle(verbose: bool = False) -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+    out = ROOT / "oracle" / "libane_oracle.so"
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
+def build_all(verbose: bool = False) -> None:
+    build_oracle(verbose)
+    build_library(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,450 @@
+// gemm_i8.hip -- int8 x int8 -> int32 contraction on gfx950 MFMA with the
+// fused dequant / scale / bias / ReLU epilogue of the ane dense opcodes:
+//   dense_i8 (0x18) and dense_u8s8 (0x1E): B in the SMOPA panel format
+//     (bytecode_interpreter.s:1978-2446, 2835-3300);
+//   dense_fused_i8 (README.md:84-97): fp32 A and B quantized per tensor by
+//     two streaming kernels, B written transposed (K contiguous per column)
+//     so both MFMA operands load as 16-byte rows;
+//   gemm_s8_i32: raw accumulators for tests.
+//
+// Tile: 128 x 128 output per 256-thread workgroup, K staged through LDS in
+// 128-byte slices, four waves each owning a 64 x 64 block of 2 x 2
+// v_mfma_i32_32x32x32_i8 tiles.  Both operand tiles sit in LDS as
+// [row][128 bytes] with the 16-byte chunk index XOR-swizzled by (row>>1)&7
+// so the ds_read_b128 of 16 consecutive rows hits 16 distinct bank groups.
+#include "common.hpp"
+
+namespace ane {
+
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kGThreads = 256;
+
+enum BLayout : int { kBTransposed = 0, kBPanel = 1 };
+
+struct GemmParams {
+    const int8_t* A;      // row-major, K contiguous
+    uint64_t lda;         // bytes between rows of A
+    const int8_t* B;      // Bt (N x K, K contiguous) or SMOPA panels
+    uint64_t ldb;         // Bt: bytes between rows; panel: groups per panel (G)
+    uint32_t rowsA;       // rows of A that may be read (others read as 0)
+    uint32_t colsB;       // columns of B that may be read (others read as 0)
+    uint32_t Kp;          // contraction length, multiple of 16
+    uint32_t Mout, Nout;  // output rows / columns written
+    float s;              // epilogue multiplier (when sdev == nullptr)
+    const float* sdev;    // device {sa, sb}: s = (sa*sb)*smul
+    float smul;
+    const float* bias;    // fp32[Nout] or nullptr (adds +0.0f)
+    float lo;             // ReLU floor: +0 or -FLT_MAX
+    float* C;             // fp32 output, row stride ldc
+    uint64_t ldc;
+    int32_t* Craw;        // raw int32 output instead (debug entry)
+};
+
+__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
+    return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+template <int BL, bool AU8>
+__global__ void __launch_bounds__(kGThreads)
+k_gemm_i8(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t sA[kBM * kBK];
+    __shared__ __attribute__((aligned(16))) int8_t sB[kBN * kBK];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = tid >> 6;
+    const uint32_t row0 = blockIdx.y * kBM;
+    const uint32_t col0 = blockIdx.x * kBN;
+    const uint32_t wr0 = (wave >> 1) * 64;
+    const uint32_t wc0 = (wave & 1) * 64;
+
+    v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+    int colsum[2] = {0, 0};  // AU8 only: sum_k B[k][j] for this lane's columns
+
+    for (uint32_t k0 = 0; k0 < p.Kp; k0 += kBK) {
+        // ---- A tile: 128 rows x 8 chunks of 16 bytes, 4 per thread
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const uint32_t idx = it * kGThreads + tid;
+            const uint32_t r = idx >> 3, c = idx & 7;
+            const uint32_t gr = row0 + r, gk = k0 + c * 16;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (gr < p.rowsA && gk < p.Kp) {
+                v = *reinterpret_cast<const uint4*>(p.A + (uint64_t)gr * p.lda + gk);
+                if (AU8) {  // uint8 a -> int8 (a - 128); the bias is added back in the epilogue
+                    v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+                }
+            }
+            *reinterpret_cast<uint4*>(sA + swz(r, c)) = v;
+        }
+        // ---- B tile
+        if (BL == kBTransposed) {
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const uint32_t idx = it * kGThreads + tid;
+                const uint32_t r = idx >> 3, c = idx & 7;
+                const uint32_t gc = col0 + r, gk = k0 + c * 16;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (gc < p.colsB && gk < p.Kp)
+                    v = *reinterpret_cast<const uint4*>(p.B + (uint64_t)gc * p.ldb + gk);
+                *reinterpret_cast<uint4*>(sB + swz(r, c)) = v;
+            }
+        } else {
+            // 8 panels of 16 columns; the k-slice of one panel is 32 groups
+            // x 64 bytes, contiguous.  A 16-byte piece = 4 columns x 4 k.
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const uint32_t idx = it * kGThreads + tid;
+                const uint32_t pl = idx >> 7, ch = idx & 127;
+                const uint32_t gl = ch >> 2, q = ch & 3;
+                const uint32_t gp = (col0 >> 4) + pl, gg = (k0 >> 2) + gl;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (gp * 16 < p.colsB && gg * 4 < p.Kp)
+                    v = *reinterpret_cast<const uint4*>(p.B + ((uint64_t)gp * p.ldb + gg) * 64 + q * 16);
+                const uint32_t cbase = pl * 16 + q * 4;
+                const uint32_t chunk = gl >> 2, sub = (gl & 3) * 4;
+                *reinterpret_cast<uint32_t*>(sB + swz(cbase + 0, chunk) + sub) = v.x;
+                *reinterpret_cast<uint32_t*>(sB + swz(cbase + 1, chunk) + sub) = v.y;
+                *reinterpret_cast<uint32_t*>(sB + swz(cbase + 2, chunk) + sub) = v.z;
+                *reinterpret_cast<uint32_t*>(sB + swz(cbase + 3, chunk) + sub) = v.w;
+            }
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int ks = 0; ks < kBK / 32; ks++) {
+            const uint32_t chunk = ks * 2 + (lane >> 5);
+            v4i a[2], b[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+                a[mi] = *reinterpret_cast<const v4i*>(sA + swz(wr0 + mi * 32 + (lane & 31), chunk));
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                b[ni] = *reinterpret_cast<const v4i*>(sB + swz(wc0 + ni * 32 + (lane & 31), chunk));
+                if (AU8) {
+                    colsum[ni] = __builtin_amdgcn_sdot4(b[ni].x, 0x01010101, colsum[ni], false);
+                    colsum[ni] = __builtin_amdgcn_sdot4(b[ni].y, 0x01010101, colsum[ni], false);
+                    colsum[ni] = __builtin_amdgcn_sdot4(b[ni].z, 0x01010101, colsum[ni], false);
+                    colsum[ni] = __builtin_amdgcn_sdot4(b[ni].w, 0x01010101, colsum[ni], false);
+                }
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    if (AU8) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) colsum[ni] += __shfl_xor(colsum[ni], 32, kWave);
+    }
+
+    // ---- epilogue: C = fmaxA(fadd(fmul((float)acc, s), bias[j]), lo)
+    float s = p.s;
+    if (p.sdev) s = __fmul_rn(__fmul_rn(p.sdev[0], p.sdev[1]), p.smul);
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+        const uint32_t j = col0 + wc0 + ni * 32 + (lane & 31);
+        if (j >= p.Nout) continue;
+        const float bj = p.bias ? p.bias[j] : 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t i = row0 + wr0 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (i >= p.Mout) continue;
+                int32_t v = acc[mi][ni][r];
+                if (AU8) v = (int32_t)((uint32_t)v + 128u * (uint32_t)colsum[ni]);
+                if (p.Craw) {
+                    p.Craw[(uint64_t)i * p.ldc + j] = v;
+                } else {
+                    float f = __fadd_rn(__fmul_rn((float)v, s), bj);
+                    p.C[(uint64_t)i * p.ldc + j] = fmax_a(f, p.lo);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dense_fused_i8 operand preparation.
+
+constexpr uint32_t kFusedPartials = 1024;
+
+// Pass 1 over both tensors: blocks [0, nbA) reduce A, [nbA, nbA+nbB) reduce B.
+__global__ void __launch_bounds__(256)
+k_absmax_two(const float* __restrict__ A, uint64_t nA, uint32_t nbA,
+             const float* __restrict__ B, uint64_t nB, uint32_t nbB,
+             uint32_t* __restrict__ partials) {
+    __shared__ uint32_t red[4];
+    const bool isA = blockIdx.x < nbA;
+    const float* src = isA ? A : B;
+    const uint64_t n = isA ? nA : nB;
+    const uint32_t b = isA ? blockIdx.x : blockIdx.x - nbA;
+    const uint32_t nbk = isA ? nbA : nbB;
+    const uint64_t tid = (uint64_t)b * 256 + threadIdx.x;
+    const uint64_t stride = (uint64_t)nbk * 256;
+    uint32_t m = 0;
+    uint64_t head = 0;
+    if ((((uintptr_t)src) & 15) == 0) {
+        const uint64_t n4 = n >> 2;
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        for (uint64_t i = tid; i < n4; i += stride) {
+            float4 v = s4[i];
+            uint32_t a = abs_key(v.x), c = abs_key(v.y), d = abs_key(v.z), e = abs_key(v.w);
+            a = a > c ? a : c;
+            d = d > e ? d : e;
+            a = a > d ? a : d;
+            m = m > a ? m : a;
+        }
+        head = n4 << 2;
+    }
+    for (uint64_t i = head + tid; i < n; i += stride) {
+        uint32_t a = abs_key(src[i]);
+        m = m > a ? m : a;
+    }
+    m = block_max_u32_256(m, red);
+    if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__device__ __forceinline__ float fold_partials(const uint32_t* partials, uint32_t n,
+                                               uint32_t* red) {
+    uint32_t m = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        uint32_t a = partials[i];
+        m = m > a ? m : a;
+    }
+    return __uint_as_float(block_max_u32_256(m, red));
+}
+
+// Pass 2: blocks [0, nqA) quantize A row-major into qA (M x Kp, zero k-pad);
+// blocks [nqA, ...) quantize 64 x 64 tiles of B transposed into qBt (N x Kp).
+__global__ void __launch_bounds__(256)
+k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_t M,
+               uint32_t N, uint32_t K, uint32_t Kp, const uint32_t* __restrict__ partials,
+               uint32_t nbA, uint32_t nbB, uint32_t nqA, int8_t* __restrict__ qA,
+               int8_t* __restrict__ qBt, float* __restrict__ scales) {
+    __shared__ uint32_t red[4];
+    __shared__ int8_t tileT[64][64 + 4];
+    const bool isA = blockIdx.x < nqA;
+    const float amax = isA ? fold_partials(partials, nbA, red)
+                           : fold_partials(partials + nbA, nbB, red);
+    float scale, inv;
+    quant_params(amax, scale, inv);
+    if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == nqA)) scales[isA ? 0 : 1] = scale;
+
+    if (isA) {
+        // 16 output bytes per thread; chunk index over M x (Kp/16).
+        const uint64_t chunks_per_row = Kp / 16;
+        const uint64_t total = (uint64_t)M * chunks_per_row;
+        const bool vec = ((K & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
+        for (uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x; c < total;
+             c += (uint64_t)nqA * 256) {
+            const uint64_t i = c / chunks_per_row;
+            const uint32_t k = (uint32_t)(c % chunks_per_row) * 16;
+            const float* src = A + i * K + k;
+            uint32_t w[4] = {0, 0, 0, 0};
+            if (vec && k + 16 <= K) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4 v = reinterpret_cast<const float4*>(src)[q];
+                    w[q] = (uint32_t)(quant1(v.x, inv) & 0xff) |
+                           ((uint32_t)(quant1(v.y, inv) & 0xff) << 8) |
+                           ((uint32_t)(quant1(v.z, inv) & 0xff) << 16) |
+                           ((uint32_t)(quant1(v.w, inv) & 0xff) << 24);
+                }
+            } else {
+                for (int e = 0; e < 16; e++)
+                    if (k + e < K) w[e >> 2] |= (uint32_t)(quant1(src[e], inv) & 0xff) << (8 * (e & 3));
+            }
+            *reinterpret_cast<uint4*>(qA + i * Kp + k) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        return;
+    }
+    // B tile (k0, n0) of 64 x 64: read rows of B, write rows of qBt.
+    const uint32_t tb = blockIdx.x - nqA;
+    const uint32_t ntn = (N + 63) / 64;
+    const uint32_t k0 = (tb / ntn) * 64, n0 = (tb % ntn) * 64;
+    {
+        const uint32_t kk = threadIdx.x >> 2, nn = (threadIdx.x & 3) * 16;
+        const uint32_t gk = k0 + kk;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t gn = n0 + nn + e;
+            int q = 0;
+            if (gk < K && gn < N) q = quant1(B[(uint64_t)gk * N + gn], inv);
+            tileT[nn + e][kk] = (int8_t)q;
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t nn = threadIdx.x >> 2, kc = (threadIdx.x & 3) * 16;
+        const uint32_t gn = n0 + nn, gk = k0 + kc;
+        if (gn < N && gk < Kp) {
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                w[q] = *reinterpret_cast<const uint32_t*>(&tileT[nn][kc + 4 * q]);
+            *reinterpret_cast<uint4*>(qBt + (uint64_t)gn * Kp + gk) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+template <int BL, bool AU8>
+static int launch_gemm(const GemmParams& p, hipStream_t s) {
+    if (p.Mout == 0 || p.Nout == 0) return ANE_OK;
+    dim3 grid((p.Nout + kBN - 1) / kBN, (p.Mout + kBM - 1) / kBM);
+    if (grid.y > 65535) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL((k_gemm_i8<BL, AU8>), grid, dim3(kGThreads), 0, s, p);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+static bool aligned16(const void* ptr) { return (((uintptr_t)ptr) & 15) == 0; }
+
+}  // namespace ane
+
+using namespace ane;
+
+extern "C" int ane_hip_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
+                                uint8_t flags, const void* A, const int8_t* Bp,
+                                const float* bias, float* C, int a_unsigned, void* stream) {
+    const uint64_t Kp = ceil_to(K, 64);
+    uint64_t Mp = ceil_to(M, 16);
+    if (Mp == 0) Mp = 16;  // the reference's tile-row loop runs at least once
+    if (N == 0) return ANE_OK;
+    if (!A || !Bp || !bias || !C) return ANE_ERR_BAD_POINTER;
+    if (!aligned16(A) || !aligned16(Bp)) return ANE_ERR_INVALID_ARG;
+    if (Kp > 0x7fffffffull || Mp > 0xffffffffull) return ANE_ERR_INVALID_ARG;
+    GemmParams p{};
+    p.A = (const int8_t*)A;
+    p.lda = Kp;
+    p.B = Bp;
+    p.ldb = Kp / 4;
+    p.rowsA = (uint32_t)Mp;
+    p.colsB = (uint32_t)ceil_to(N, 16);
+    p.Kp = (uint32_t)Kp;
+    p.Mout = (uint32_t)Mp;
+    p.Nout = N;
+    p.s = sa * sb;  // host fmul, IEEE single (bytecode_interpreter.s:2017)
+    p.sdev = nullptr;
+    p.bias = bias;
+    p.lo = (flags & 1) ? 0.0f : -3.40282347e+38f;
+    p.C = C;
+    p.ldc = N;
+    hipStream_t s = (hipStream_t)stream;
+    return a_unsigned ? launch_gemm<kBPanel, true>(p, s) : launch_gemm<kBPanel, false>(p, s);
+}
+
+extern "C" int ane_hip_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int8_t* A,
+                                   uint32_t lda, const int8_t* Bt, uint32_t ldb, int32_t* acc,
+                                   void* stream) {
+    if (M == 0 || N == 0) return ANE_OK;
+    if (!A || !Bt || !acc) return ANE_ERR_BAD_POINTER;
+    if ((K & 15) || (lda & 15) || (ldb & 15) || !aligned16(A) || !aligned16(Bt) || lda < K ||
+        ldb < K)
+        return ANE_ERR_INVALID_ARG;
+    GemmParams p{};
+    p.A = A;
+    p.lda = lda;
+    p.B = Bt;
+    p.ldb = ldb;
+    p.rowsA = M;
+    p.colsB = N;
+    p.Kp = K;
+    p.Mout = M;
+    p.Nout = N;
+    p.s = 1.0f;
+    p.lo = 0.0f;
+    p.Craw = acc;
+    p.ldc = N;
+    return launch_gemm<kBTransposed, false>(p, (hipStream_t)stream);
+}
+
+static uint64_t fused_kp(int32_t K) { return ceil_to((uint64_t)(K > 0 ? K : 0), 16); }
+
+extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K) {
+    if (M < 0 || N < 0 || K < 0) return 0;
+    const uint64_t Kp = fused_kp(K);
+    uint64_t bytes = 256;                                  // scales + alignment slack
+    bytes += ceil_to((uint64_t)kFusedPartials * 2 * 4, 256);  // absmax partials
+    bytes += ceil_to((uint64_t)M * Kp, 256);               // qA
+    bytes += ceil_to((uint64_t)N * Kp, 256);               // qBt
+    return (size_t)bytes;
+}
+
+static uint32_t fused_blocks(uint64_t n) {
+    uint64_t b = (n / 4 + 1024 - 1) / 1024;
+    if (b < 1) b = 1;
+    if (b > kFusedPartials) b = kFusedPartials;
+    return (uint32_t)b;
+}
+
+extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale, int relu,
+                                      const float* A, const float* B, float* C,
+                                      float* scales_out, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    if (M < 0 || N < 0 || K < 0) return ANE_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return ANE_OK;
+    if (!C || (K > 0 && (!A || !B))) return ANE_ERR_BAD_POINTER;
+    if (!workspace || !aligned16(workspace) ||
+        workspace_bytes < ane_hip_dense_fused_i8_workspace_size(M, N, K))
+        return ANE_ERR_WORKSPACE;
+    hipStream_t s = (hipStream_t)stream;
+    const uint64_t Kp = fused_kp(K);
+    uint8_t* ws = (uint8_t*)workspace;
+    float* scales = (float*)ws;
+    uint32_t* partials = (uint32_t*)(ws + 256);
+    int8_t* qA = (int8_t*)(ws + 256 + ceil_to((uint64_t)kFusedPartials * 2 * 4, 256));
+    int8_t* qBt = qA + ceil_to((uint64_t)M * Kp, 256);
+
+    const uint64_t nA = (uint64_t)M * (uint64_t)K, nB = (uint64_t)K * (uint64_t)N;
+    const uint32_t nbA = fused_blocks(nA), nbB = fused_blocks(nB);
+    hipLaunchKernelGGL(k_absmax_two, dim3(nbA + nbB), dim3(256), 0, s, A, nA, nbA, B, nB, nbB,
+                       partials);
+    uint64_t nqA = ((uint64_t)M * (Kp / 16) + 255) / 256;
+    if (nqA > 2048) nqA = 2048;
+    if (nqA < 1) nqA = 1;
+    const uint64_t nqB = ((Kp + 63) / 64) * (((uint64_t)N + 63) / 64);
+    if (Kp > 0) {
+        if (nqA + nqB > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
+        hipLaunchKernelGGL(k_quantize_two, dim3((uint32_t)(nqA + nqB)), dim3(256), 0, s, A, B,
+                           (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, partials, nbA, nbB,
+                           (uint32_t)nqA, qA, qBt, scales);
+    } else {
+        // K == 0: no operands to quantize; both scales are 1 (zero guard).
+        hipLaunchKernelGGL(k_quantize_two, dim3(2), dim3(256), 0, s, A, B, (uint32_t)M,
+                           (uint32_t)N, 0u, 0u, partials, nbA, nbB, 1u, qA, qBt, scales);
+    }
+    ANE_HIP_CHECK_LAUNCH();
+    if (scales_out) {
+        hipError_t e = hipMemcpyAsync(scales_out, scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return ANE_ERR_HIP;
+    }
+    GemmParams p{};
+    p.A = qA;
+    p.lda = Kp;
+    p.B = qBt;
+    p.ldb = Kp;
+    p.rowsA = (uint32_t)M;
+    p.colsB = (uint32_t)N;
+    p.Kp = (uint32_t)Kp;
+    p.Mout = (uint32_t)M;
+    p.Nout = (uint32_t)N;
+    p.sdev = scales;
+    p.smul = scale;
+    p.bias = nullptr;
+    p.lo = relu ? 0.0f : -3.40282347e+38f;
+    p.C = C;
+    p.ldc = (uint64_t)N;
+    return launch_gemm<kBTransposed, false>(p, s);
+}

@@ -1,0 +1,388 @@
+// stream_exec.cpp -- the reference's C-ABI boundary, re-implemented as a host
+// decoder that launches the gfx950 kernels.
+//
+// Reference: extern "C" void stream_exec(const uint8_t*, size_t)
+// (include/ane/ane.hpp:37-39), implemented there by the SME2 interpreter
+// loop of src/bytecode_interpreter.s:11-36 (fetch opcode byte, jump through a
+// 128-entry table, stop at data+size; slot 0x00 exits).  Records are the
+// packed little-endian serialisation made by ane::dispatch
+// (include/ane/ane.hpp:206-220): [op:u8] then each argument's object bytes.
+//
+// Differences from the reference, all additive:
+//  * operands are device pointers; every operand extent is checked against
+//    its HIP allocation before anything is launched, so a short or host
+//    buffer becomes an error instead of a GPU memory fault;
+//  * scalar outputs (quantize scale_out, channelwise scales) may also be
+//    host memory: they are computed on the device and copied back;
+//  * errors are recorded per thread (ane_last_error) since the signature
+//    returns void; execution stops at the first failing record.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/ane_hip.h"
+
+namespace {
+
+thread_local int t_status = ANE_OK;
+thread_local std::string t_message;
+thread_local hipStream_t t_stream = nullptr;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_message = buf;
+    return status;
+}
+
+// ---------------------------------------------------------------- workspace
+// One grow-only device buffer per (device, stream).  Work on one stream is
+// ordered, so reusing its buffer between records is safe; growing it waits
+// for the stream first.  Freed at process exit.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace>* g_ws = nullptr;
+
+int get_workspace(hipStream_t s, size_t bytes, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(ANE_ERR_HIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (!g_ws) g_ws = new std::map<std::pair<int, hipStream_t>, Workspace>();
+    Workspace& w = (*g_ws)[{dev, s}];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            if (hipStreamSynchronize(s) != hipSuccess) return fail(ANE_ERR_HIP, "stream sync failed");
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        if (hipMalloc(&w.ptr, want) != hipSuccess) {
+            (void)hipGetLastError();
+            w.ptr = nullptr;
+            return fail(ANE_ERR_HIP, "workspace hipMalloc(%zu) failed", want);
+        }
+        w.bytes = want;
+    }
+    *out = w.ptr;
+    return ANE_OK;
+}
+
+// ------------------------------------------------------------ pointer checks
+enum class Where { kDevice, kHost };
+
+// Returns ANE_OK if [p, p+bytes) lies inside one device-accessible
+// allocation.  *where reports unregistered host memory when host_ok.
+int check_range(const void* p, uint64_t bytes, const char* name, bool host_ok, Where* where) {
+    if (where) *where = Where::kDevice;
+    if (bytes == 0) return ANE_OK;
+    if (!p) return fail(ANE_ERR_BAD_POINTER, "%s is null", name);
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof attr);
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess || attr.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        if (host_ok) {
+            if (where) *where = Where::kHost;
+            return ANE_OK;
+        }
+        return fail(ANE_ERR_BAD_POINTER,
+                    "%s (%p) is not device-accessible memory (use hipMalloc/hipMallocManaged/"
+                    "hipHostMalloc)",
+                    name, p);
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    e = hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p);
+    if (e != hipSuccess || !base) {
+        (void)hipGetLastError();
+        return fail(ANE_ERR_BAD_POINTER, "%s (%p): allocation extent unknown", name, p);
+    }
+    const uint64_t off = (uint64_t)((const char*)p - (const char*)base);
+    if (off > size || bytes > size - off)
+        return fail(ANE_ERR_BUFFER_TOO_SMALL, "%s needs %llu bytes at %p, allocation holds %llu", name,
+                    (unsigned long long)bytes, p, (unsigned long long)(size - (off > size ? size : off)));
+    return ANE_OK;
+}
+
+#define CHECK(expr)                 \
+    do {                            \
+        int st__ = (expr);          \
+        if (st__ != ANE_OK) return st__; \
+    } while (0)
+
+uint64_t ceil_u(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
+
+// ------------------------------------------------------------ record reader
+struct Reader {
+    const uint8_t* p;
+    size_t left;
+    bool ok = true;
+    template <typename T>
+    T get() {
+        T v{};
+        if (left < sizeof(T)) {
+            ok = false;
+            left = 0;
+            return v;
+        }
+        std::memcpy(&v, p, sizeof(T));
+        p += sizeof(T);
+        left -= sizeof(T);
+        return v;
+    }
+    template <typename T>
+    T* ptr() {
+        uint64_t v = get<uint64_t>();
+        return reinterpret_cast<T*>((uintptr_t)v);
+    }
+};
+
+int hip_status(int st, const char* what) {
+    if (st == ANE_OK) return ANE_OK;
+    if (t_message.empty()) return fail(st, "%s failed with status %d", what, st);
+    return st;
+}
+
+// Runs a quantize-type record whose scalar outputs may live in host memory.
+int copy_back(hipStream_t s, void* host_dst, const void* dev_src, size_t bytes) {
+    if (hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ANE_ERR_HIP, "copy of scalar outputs to host failed");
+    }
+    return ANE_OK;
+}
+
+// 0x19 [count:u32][src][dst][scale_out]  (bytecode_interpreter.s:1885-1890)
+int op_quantize(Reader& r, hipStream_t s) {
+    const uint32_t count = r.get<uint32_t>();
+    const float* src = r.ptr<const float>();
+    int8_t* dst = r.ptr<int8_t>();
+    float* scale_out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "quantize_fp32_i8 record truncated");
+    uint64_t n = ceil_u(count, 16);
+    if (n == 0) n = 16;
+    Where w;
+    CHECK(check_range(src, n * 4, "quantize_fp32_i8 src", false, nullptr));
+    CHECK(check_range(dst, n, "quantize_fp32_i8 dst", false, nullptr));
+    CHECK(check_range(scale_out, 4, "quantize_fp32_i8 scale_out", true, &w));
+    const size_t wsb = ane_hip_quantize_workspace_size(n) + 256;
+    void* ws = nullptr;
+    CHECK(get_workspace(s, wsb, &ws));
+    float* dev_scale = w == Where::kHost ? (float*)ws : scale_out;
+    void* part = (uint8_t*)ws + 256;
+    CHECK(hip_status(ane_hip_quantize_fp32_i8(count, 1, src, dst, dev_scale, part, wsb - 256, s),
+                     "quantize_fp32_i8"));
+    if (w == Where::kHost) CHECK(copy_back(s, scale_out, dev_scale, 4));
+    return ANE_OK;
+}
+
+// 0x1A [count:u32][scale:f32][src][dst]  (bytecode_interpreter.s:1959-1963)
+int op_dequantize(Reader& r, hipStream_t s) {
+    const uint32_t count = r.get<uint32_t>();
+    const float scale = r.get<float>();
+    const int8_t* src = r.ptr<const int8_t>();
+    float* dst = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "dequantize_i8_fp32 record truncated");
+    const uint64_t n = ceil_u(count, 16);
+    CHECK(check_range(src, n, "dequantize_i8_fp32 src", false, nullptr));
+    CHECK(check_range(dst, n * 4, "dequantize_i8_fp32 dst", false, nullptr));
+    return hip_status(ane_hip_dequantize_i8_fp32(count, scale, src, dst, s), "dequantize_i8_fp32");
+}
+
+// 0x1B [K:u32][N:u32][src][dst]  (bytecode_interpreter.s:2460-2464)
+int op_pack_b(Reader& r, hipStream_t s) {
+    const uint32_t K = r.get<uint32_t>();
+    const uint32_t N = r.get<uint32_t>();
+    const int8_t* src = r.ptr<const int8_t>();
+    int8_t* dst = r.ptr<int8_t>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "pack_b_i8 record truncated");
+    CHECK(check_range(src, (uint64_t)K * N, "pack_b_i8 src", false, nullptr));
+    CHECK(check_range(dst, ane_hip_packed_b_size(K, N), "pack_b_i8 dst", false, nullptr));
+    return hip_status(ane_hip_pack_b_i8(K, N, src, dst, s), "pack_b_i8");
+}
+
+// 0x1C [rows:u32][cols:u32][src][dst][scales]  (bytecode_interpreter.s:2592-2597)
+int op_channelwise(Reader& r, hipStream_t s) {
+    const uint32_t rows = r.get<uint32_t>();
+    const uint32_t cols = r.get<uint32_t>();
+    const float* src = r.ptr<const float>();
+    int8_t* dst = r.ptr<int8_t>();
+    float* scales = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "quantize_fp32_i8_channelwise record truncated");
+    if (rows == 0) return ANE_OK;
+    uint64_t cpad = ceil_u(cols, 16);
+    if (cpad == 0) cpad = 16;
+    Where w;
+    CHECK(check_range(src, (uint64_t)rows * cpad * 4, "channelwise src", false, nullptr));
+    CHECK(check_range(dst, (uint64_t)rows * cpad, "channelwise dst", false, nullptr));
+    CHECK(check_range(scales, (uint64_t)rows * 4, "channelwise scales", true, &w));
+    float* dev_scales = scales;
+    if (w == Where::kHost) {
+        void* ws = nullptr;
+        CHECK(get_workspace(s, (size_t)rows * 4, &ws));
+        dev_scales = (float*)ws;
+    }
+    CHECK(hip_status(ane_hip_quantize_channelwise(rows, cols, src, dst, dev_scales, s),
+                     "quantize_fp32_i8_channelwise"));
+    if (w == Where::kHost) CHECK(copy_back(s, scales, dev_scales, (size_t)rows * 4));
+    return ANE_OK;
+}
+
+// 0x18 / 0x1E [M][N][K][sa][sb][flags:u8][A][Bp][bias][C]
+// (bytecode_interpreter.s:1997-2007, 2851-2861)
+int op_dense(Reader& r, hipStream_t s, bool a_unsigned) {
+    const uint32_t M = r.get<uint32_t>();
+    const uint32_t N = r.get<uint32_t>();
+    const uint32_t K = r.get<uint32_t>();
+    const float sa = r.get<float>();
+    const float sb = r.get<float>();
+    const uint8_t flags = r.get<uint8_t>();
+    const void* A = r.ptr<const void>();
+    const int8_t* Bp = r.ptr<const int8_t>();
+    const float* bias = r.ptr<const float>();
+    float* C = r.ptr<float>();
+    const char* nm = a_unsigned ? "dense_u8s8" : "dense_i8";
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "%s record truncated", nm);
+    if (N == 0) return ANE_OK;  // every column store is predicated off
+    const uint64_t Kp = ceil_u(K, 64);
+    uint64_t Mp = ceil_u(M, 16);
+    if (Mp == 0) Mp = 16;
+    const uint64_t P = ceil_u(N, 16) / 16, G = Kp / 4;
+    if (((uintptr_t)A & 15) || ((uintptr_t)Bp & 15))
+        return fail(ANE_ERR_INVALID_ARG, "%s: A and B_packed must be 16-byte aligned", nm);
+    CHECK(check_range(A, Mp * Kp, "dense A", false, nullptr));
+    CHECK(check_range(Bp, P * G * 64, "dense B_packed", false, nullptr));
+    CHECK(check_range(bias, (uint64_t)N * 4, "dense bias", false, nullptr));
+    CHECK(check_range(C, Mp * N * 4, "dense C", false, nullptr));
+    return hip_status(ane_hip_dense_i8(M, N, K, sa, sb, flags, A, Bp, bias, C, a_unsigned ? 1 : 0, s),
+                      nm);
+}
+
+// 0x57 [M:u32][K:u32][x][W][y]  (bytecode_interpreter.s:7017-7023)
+int op_q8_0_gemv(Reader& r, hipStream_t s) {
+    const uint32_t M = r.get<uint32_t>();
+    const uint32_t K = r.get<uint32_t>();
+    const float* x = r.ptr<const float>();
+    const void* W = r.ptr<const void>();
+    float* y = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "q8_0_gemv record truncated");
+    if (M == 0) return ANE_OK;
+    const uint64_t nb = K >> 5;
+    CHECK(check_range(x, nb * 32 * 4, "q8_0_gemv x", false, nullptr));
+    CHECK(check_range(W, (uint64_t)M * nb * 34, "q8_0_gemv W", false, nullptr));
+    CHECK(check_range(y, (uint64_t)M * 4, "q8_0_gemv y", false, nullptr));
+    if ((uintptr_t)W & 1) return fail(ANE_ERR_INVALID_ARG, "q8_0_gemv: W must be 2-byte aligned");
+    return hip_status(ane_hip_q8_0_gemv(M, K, x, W, y, s), "q8_0_gemv");
+}
+
+// 0x80 [M:i32][N:i32][K:i32][scale:f32][relu:bool][A][B][C]  (README.md:87-97)
+int op_dense_fused(Reader& r, hipStream_t s) {
+    const int32_t M = r.get<int32_t>();
+    const int32_t N = r.get<int32_t>();
+    const int32_t K = r.get<int32_t>();
+    const float scale = r.get<float>();
+    const uint8_t relu = r.get<uint8_t>();
+    const float* A = r.ptr<const float>();
+    const float* B = r.ptr<const float>();
+    float* C = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "dense_fused_i8 record truncated");
+    if (M < 0 || N < 0 || K < 0) return fail(ANE_ERR_INVALID_ARG, "dense_fused_i8: negative shape");
+    if (M == 0 || N == 0) return ANE_OK;
+    CHECK(check_range(A, (uint64_t)M * K * 4, "dense_fused_i8 A", false, nullptr));
+    CHECK(check_range(B, (uint64_t)K * N * 4, "dense_fused_i8 B", false, nullptr));
+    CHECK(check_range(C, (uint64_t)M * N * 4, "dense_fused_i8 C", false, nullptr));
+    const size_t wsb = ane_hip_dense_fused_i8_workspace_size(M, N, K);
+    void* ws = nullptr;
+    CHECK(get_workspace(s, wsb, &ws));
+    return hip_status(ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, ws, wsb, s),
+                      "dense_fused_i8");
+}
+
+int run(const uint8_t* data, size_t size, hipStream_t s) {
+    t_message.clear();
+    if (size && !data) return fail(ANE_ERR_BAD_POINTER, "stream is null");
+    Reader r{data, size};
+    while (r.left > 0) {
+        const size_t at = size - r.left;
+        const uint8_t op = r.get<uint8_t>();
+        int st = ANE_OK;
+        switch (op) {
+            case 0x00:
+                return ANE_OK;  // jump-table slot 0 is .L_exit
+            case ANE_OP_DENSE_I8: st = op_dense(r, s, false); break;
+            case ANE_OP_QUANTIZE_FP32_I8: st = op_quantize(r, s); break;
+            case ANE_OP_DEQUANTIZE_I8_FP32: st = op_dequantize(r, s); break;
+            case ANE_OP_PACK_B_I8: st = op_pack_b(r, s); break;
+            case ANE_OP_QUANTIZE_FP32_I8_CHANNELWISE: st = op_channelwise(r, s); break;
+            case ANE_OP_DENSE_U8S8: st = op_dense(r, s, true); break;
+            case ANE_OP_Q8_0_GEMV: st = op_q8_0_gemv(r, s); break;
+            case ANE_OP_DENSE_FUSED_I8: st = op_dense_fused(r, s); break;
+            default:
+                return fail(ANE_ERR_UNKNOWN_OPCODE,
+                            "opcode 0x%02x at byte %zu is not part of the quantized path served by "
+                            "this build",
+                            op, at);
+        }
+        if (st != ANE_OK) {
+            if (t_message.empty()) fail(st, "record at byte %zu failed", at);
+            return st;
+        }
+    }
+    return ANE_OK;
+}
+
+}  // namespace
+
+extern "C" void stream_exec(const uint8_t* data, size_t size) {
+    hipStream_t s = t_stream;
+    int st = run(data, size, s);
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipGetLastError();
+        if (st == ANE_OK) st = fail(ANE_ERR_HIP, "hipStreamSynchronize failed");
+    }
+    t_status = st;
+}
+
+extern "C" int ane_stream_exec_async(const uint8_t* data, size_t size, void* stream) {
+    int st = run(data, size, (hipStream_t)stream);
+    t_status = st;
+    return st;
+}
+
+extern "C" int ane_last_error(void) { return t_status; }
+
+extern "C" const char* ane_last_error_message(void) {
+    return t_status == ANE_OK ? "" : t_message.c_str();
+}
+
+extern "C" void ane_set_stream(void* stream) { t_stream = (hipStream_t)stream; }
+
+extern "C" int ane_hip_device_check(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return ANE_ERR_NO_DEVICE;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return ANE_ERR_HIP;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ANE_ERR_NO_DEVICE;
+    return ANE_OK;
+}
+
+extern "C" const char* ane_hip_version(void) { return "ane_amd 0.1 (gfx950)"; }

@@ -1,0 +1,157 @@
+/*
+ * ane_hip.h -- C ABI of the MI355X (gfx950) implementation of ane's
+ * quantized compute path.
+ *
+ * Two layers, both exported by ane_amd/libane_amd.so:
+ *
+ *  1. The reference's own boundary: stream_exec(), the single entry point
+ *     that ane::dispatch() serialises into (reference include/ane/ane.hpp:37-39,
+ *     exported by src/bytecode_interpreter.s:11-12 as _stream_exec).  Same
+ *     record layouts, same opcode numbers.  Operands are device pointers
+ *     (hipMalloc / hipMallocManaged / hipHostMalloc); the call is synchronous
+ *     like the reference's, and failures are reported through
+ *     ane_last_error() because the reference signature returns void.
+ *
+ *  2. The kernel-level ABI (ane_hip_*): device pointers, an explicit HIP
+ *     stream (hipStream_t passed as void*, 0 = the null stream), an int
+ *     status return (ANE_OK == 0), asynchronous with respect to the host.
+ *     Entry points that need scratch memory take a caller-owned workspace
+ *     (size from the matching *_workspace_size function) and never allocate.
+ *
+ * All functions are thread-safe.  Nothing here allocates device memory
+ * except stream_exec (a grow-only per-device workspace for the opcodes that
+ * need one, freed at process exit).
+ */
+#ifndef ANE_HIP_H
+#define ANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+enum ane_status {
+    ANE_OK = 0,
+    ANE_ERR_INVALID_ARG = 1,      /* shape/size outside the documented range  */
+    ANE_ERR_BAD_POINTER = 2,      /* null or not device-accessible            */
+    ANE_ERR_BUFFER_TOO_SMALL = 3, /* operand extent exceeds its allocation    */
+    ANE_ERR_UNKNOWN_OPCODE = 4,   /* opcode this build does not implement     */
+    ANE_ERR_TRUNCATED = 5,        /* record runs past the end of the stream   */
+    ANE_ERR_HIP = 6,              /* a HIP runtime call failed                */
+    ANE_ERR_NO_DEVICE = 7,        /* no gfx950 device                         */
+    ANE_ERR_WORKSPACE = 8         /* workspace pointer null or too small      */
+};
+
+/* Opcodes served by this build (values identical to the reference's
+ * enum class ane::Op, include/ane/ane.hpp:47-177, plus dense_fused_i8). */
+#define ANE_OP_DENSE_I8 0x18
+#define ANE_OP_QUANTIZE_FP32_I8 0x19
+#define ANE_OP_DEQUANTIZE_I8_FP32 0x1A
+#define ANE_OP_PACK_B_I8 0x1B
+#define ANE_OP_QUANTIZE_FP32_I8_CHANNELWISE 0x1C
+#define ANE_OP_DENSE_U8S8 0x1E
+#define ANE_OP_Q8_0_GEMV 0x57
+#define ANE_OP_DENSE_FUSED_I8 0x80 /* README.md:84-97; absent from the reference enum */
+
+/* ------------------------------------------------- reference boundary */
+
+/* Replaces extern "C" void stream_exec(const uint8_t*, size_t)
+ * (reference include/ane/ane.hpp:37-39; bytecode_interpreter.s:11-36).
+ * Decodes and runs every record of the stream on the calling thread's
+ * stream (ane_set_stream), then synchronises it.  Stops at the first failing
+ * record; ane_last_error() reports why (ANE_OK after a full run). */
+void stream_exec(const uint8_t* data, size_t size);
+
+/* Status of the last stream_exec on this thread, and a human-readable
+ * message for it.  No reference counterpart (the reference validates
+ * nothing: bytecode_interpreter.s:31-36). */
+int ane_last_error(void);
+const char* ane_last_error_message(void);
+
+/* Stream used by stream_exec on this thread (void* = hipStream_t). */
+void ane_set_stream(void* stream);
+
+/* stream_exec without the final synchronisation and with an explicit
+ * stream; returns the status instead of storing it.  Host-memory scalar
+ * outputs (quantize scale_out, channelwise scales) still synchronise. */
+int ane_stream_exec_async(const uint8_t* data, size_t size, void* stream);
+
+/* ------------------------------------------------- kernel-level ABI */
+
+/* 0x19 quantize_fp32_i8 (bytecode_interpreter.s:1876-1950).
+ * Processes n = pad16 ? max(16, ceil16(count)) : count elements.
+ * scale_out is a device pointer. */
+size_t ane_hip_quantize_workspace_size(uint64_t n);
+int ane_hip_quantize_fp32_i8(uint64_t count, int pad16, const float* src,
+                             int8_t* dst, float* scale_out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* 0x1A dequantize_i8_fp32 (bytecode_interpreter.s:1951-1977):
+ * dst[i] = (float)src[i] * scale, i < ceil16(count). */
+int ane_hip_dequantize_i8_fp32(uint64_t count, float scale, const int8_t* src,
+                               float* dst, void* stream);
+
+/* 0x1C quantize_fp32_i8_channelwise (bytecode_interpreter.s:2583-2662):
+ * rows of width/stride cpad = max(16, ceil16(cols)). */
+int ane_hip_quantize_channelwise(uint32_t rows, uint32_t cols, const float* src,
+                                 int8_t* dst, float* scales, void* stream);
+
+/* 0x1B pack_b_i8 (bytecode_interpreter.s:2447-2582): K x N row-major int8 ->
+ * SMOPA panel format of ane_hip_packed_b_size(K, N) bytes. */
+size_t ane_hip_packed_b_size(uint32_t K, uint32_t N);
+int ane_hip_pack_b_i8(uint32_t K, uint32_t N, const int8_t* src, int8_t* dst,
+                      void* stream);
+
+/* 0x18 dense_i8 / 0x1E dense_u8s8 (bytecode_interpreter.s:1978-2446,
+ * 2835-3300).  A: int8 (a_unsigned = 0) or uint8 (1), max(16,ceil16(M)) rows
+ * of Kp = ceil64(K) bytes; Bp from pack_b_i8(Kp, N); bias fp32[N];
+ * C fp32 rows 0 .. max(16, ceil16(M))-1, columns < N, row stride N. */
+int ane_hip_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
+                     uint8_t flags, const void* A, const int8_t* Bp,
+                     const float* bias, float* C, int a_unsigned, void* stream);
+
+/* Op::dense_fused_i8 (README.md:84-97; the reference defines no handler):
+ * fp32 A (M x K, stride K) and B (K x N, stride N) each quantized per tensor
+ * with the 0x19 arithmetic, int8 x int8 -> int32 on MFMA, then
+ * C = fmaxA((float)acc * ((sa*sb)*scale) + 0.0f, relu ? +0 : -FLT_MAX).
+ * Writes exactly M x N.  Optional outputs (may be null): the quantized
+ * operands' scales (device float[2] = {sa, sb}). */
+size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K);
+int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
+                           int relu, const float* A, const float* B, float* C,
+                           float* scales_out, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Raw int32 accumulators of the int8 MFMA contraction (test/debug entry):
+ * acc[i*N+j] = sum_{k<K} A[i*lda+k] * Bt[j*ldb+k], wrapping int32.
+ * A and Bt are int8 row-major with K contiguous. */
+int ane_hip_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int8_t* A,
+                        uint32_t lda, const int8_t* Bt, uint32_t ldb,
+                        int32_t* acc, void* stream);
+
+/* 0x57 q8_0_gemv "R mode" (bytecode_interpreter.s:7010-7063): fp32 x,
+ * y[m] = FADDV16 of 16 fma lanes, bit-identical to the reference's
+ * arithmetic.  W: M rows of (K/32) 34-byte blocks. */
+int ane_hip_q8_0_gemv(uint32_t M, uint32_t K, const float* x, const void* W,
+                      float* y, void* stream);
+
+/* q8_0 "G mode" (x quantized to Q8_0 per 32-block on the fly, int8 dots):
+ * y[t*N+m] for T tokens of x (T x K fp32).  Workspace holds the quantized
+ * activations.  Serves the ggml GGML_OP_MUL_MAT hook
+ * (reference src/ggml-backend/ggml-ane.cpp:119-154) for all ne11 tokens. */
+size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T);
+int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,
+                         const void* W, float* y, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Library/device information: returns ANE_OK if a gfx950 device is usable. */
+int ane_hip_device_check(void);
+const char* ane_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANE_HIP_H */

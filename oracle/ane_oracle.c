@@ -1,0 +1,339 @@
+/*
+ * ane_oracle.c -- scalar CPU restatement of ane's quantized compute path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the CPU baseline, never the
+ * product).  Build: oracle/Makefile, flags -O2 -ffp-contract=off, no
+ * -ffast-math, so every float operation below is one IEEE binary32 rounding
+ * exactly as written.  See ane_oracle.h for what pins each function.
+ */
+#include "ane_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+int oracle_set_threads(int n) {
+#ifdef _OPENMP
+    if (n <= 0) n = omp_get_num_procs();
+    g_threads = n;
+#else
+    (void)n;
+    g_threads = 1;
+#endif
+    return g_threads;
+}
+
+/* AArch64 FMAX/FMIN (not FMAXNM): NaN in -> NaN out; max(+0,-0) = +0,
+ * min(+0,-0) = -0.  Used by the handlers at bytecode_interpreter.s:1900,
+ * 1937-1938, 2293-2294. */
+static inline float fmaxA(float a, float b) {
+    if (isnan(a)) return a;
+    if (isnan(b)) return b;
+    if (a == b) return signbit(a) ? b : a;
+    return a > b ? a : b;
+}
+static inline float fminA(float a, float b) {
+    if (isnan(a)) return a;
+    if (isnan(b)) return b;
+    if (a == b) return signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+
+/* FCVTZS to int32: NaN -> 0, truncation, saturation. */
+static inline int32_t cvtzs(float x) {
+    if (isnan(x)) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal half: renormalise */
+            int e = -1;
+            do { man <<= 1; e++; } while (!(man & 0x400));
+            man &= 0x3ff;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp - 15 + 127) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Pass 1 of bytecode_interpreter.s:1893-1905: amax = max |x| (fabs + FMAX,
+ * NaN-propagating, order irrelevant). */
+static float absmax_n(const float* src, size_t n) {
+    float amax = 0.0f;
+    for (size_t i = 0; i < n; i++) amax = fmaxA(amax, fabsf(src[i]));
+    return amax;
+}
+
+/* bytecode_interpreter.s:1906-1920: zero guard then two IEEE divisions.
+ * (fcmp s16,#0.0 / b.eq: a NaN amax is "not equal" and divides.) */
+static void quant_params(float amax, float* scale, float* inv) {
+    if (amax == 0.0f) {
+        *scale = 1.0f;
+        *inv = 127.0f;
+    } else {
+        *scale = amax / 127.0f;
+        *inv = 127.0f / amax;
+    }
+}
+
+/* bytecode_interpreter.s:1932-1944: fmul, fmax -127, fmin 127, frintn,
+ * fcvtzs, st1b (low byte). */
+static inline int8_t quant1(float x, float inv) {
+    float t = x * inv;
+    t = fmaxA(t, -127.0f);
+    t = fminA(t, 127.0f);
+    t = rintf(t); /* round-to-nearest-even in the default mode */
+    return (int8_t)(uint8_t)(uint32_t)cvtzs(t);
+}
+
+void oracle_quantize_exact(size_t n, const float* src, int8_t* dst,
+                           float* scale_out) {
+    float scale, inv;
+    quant_params(absmax_n(src, n), &scale, &inv);
+    *scale_out = scale;
+    for (size_t i = 0; i < n; i++) dst[i] = quant1(src[i], inv);
+}
+
+void oracle_quantize_fp32_i8(uint32_t count, const float* src, int8_t* dst,
+                             float* scale_out) {
+    /* do { 16 lanes } while (i < count): at least one vector. */
+    size_t n = ((size_t)count + 15) & ~(size_t)15;
+    if (n == 0) n = 16;
+    oracle_quantize_exact(n, src, dst, scale_out);
+}
+
+void oracle_dequantize_i8_fp32(uint32_t count, float scale, const int8_t* src,
+                               float* dst) {
+    /* cbz count -> nothing; else 16-lane steps (count%16 != 0 never
+     * terminates in the reference; this restatement stops at ceil16). */
+    size_t n = ((size_t)count + 15) & ~(size_t)15;
+    for (size_t i = 0; i < n; i++) dst[i] = (float)src[i] * scale;
+}
+
+void oracle_quantize_fp32_i8_channelwise(uint32_t rows, uint32_t cols,
+                                         const float* src, int8_t* dst,
+                                         float* scales) {
+    size_t cpad = ((size_t)cols + 15) & ~(size_t)15;
+    if (cpad == 0) cpad = 16;
+    for (uint32_t r = 0; r < rows; r++) {
+        const float* s = src + (size_t)r * cpad;
+        int8_t* d = dst + (size_t)r * cpad;
+        float scale, inv;
+        quant_params(absmax_n(s, cpad), &scale, &inv);
+        scales[r] = scale;
+        for (size_t i = 0; i < cpad; i++) d[i] = quant1(s[i], inv);
+    }
+}
+
+size_t oracle_packed_b_size(uint32_t K, uint32_t N) {
+    size_t G = (((size_t)K + 3) & ~(size_t)3) / 4;
+    size_t P = (((size_t)N + 15) & ~(size_t)15) / 16;
+    return P * G * 64;
+}
+
+/* bytecode_interpreter.s:2459-2582: dst[(p*G+g)*64 + 4c + d] =
+ * B[4g+d][16p+c], zero where 4g+d >= K or 16p+c >= N. */
+void oracle_pack_b_i8(uint32_t K, uint32_t N, const int8_t* src, int8_t* dst) {
+    size_t G = (((size_t)K + 3) & ~(size_t)3) / 4;
+    size_t P = (((size_t)N + 15) & ~(size_t)15) / 16;
+    for (size_t p = 0; p < P; p++)
+        for (size_t g = 0; g < G; g++)
+            for (size_t c = 0; c < 16; c++)
+                for (size_t d = 0; d < 4; d++) {
+                    size_t k = 4 * g + d, col = 16 * p + c;
+                    dst[(p * G + g) * 64 + 4 * c + d] =
+                        (k < K && col < N) ? src[k * N + col] : 0;
+                }
+}
+
+/* bytecode_interpreter.s:1995-2446 (dense_i8) and 2849-3300 (dense_u8s8). */
+void oracle_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
+                     uint8_t flags, const void* A, const int8_t* Bp,
+                     const float* bias, float* C, int a_unsigned) {
+    size_t Kp = ((size_t)K + 63) & ~(size_t)63;      /* :2038-2039 */
+    size_t Mp = ((size_t)M + 15) & ~(size_t)15;      /* :2033-2034 */
+    if (Mp == 0) Mp = 16;                            /* do-while tile rows */
+    size_t G = Kp / 4;
+    float s = sa * sb;                               /* :2017 one fmul */
+    float lo = (flags & 1) ? 0.0f : -3.40282347e+38f; /* :2021-2028 */
+    const int8_t* As = (const int8_t*)A;
+    const uint8_t* Au = (const uint8_t*)A;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long ii = 0; ii < (long)Mp; ii++) {
+        size_t i = (size_t)ii;
+        for (size_t j = 0; j < N; j++) {
+            uint32_t acc = 0; /* za tiles: wrapping int32 */
+            const int8_t* panel = Bp + (j / 16) * G * 64 + (j % 16) * 4;
+            for (size_t k = 0; k < Kp; k++) {
+                int32_t a = a_unsigned ? (int32_t)Au[i * Kp + k]
+                                       : (int32_t)As[i * Kp + k];
+                int32_t b = (int32_t)panel[(k / 4) * 64 + (k % 4)];
+                acc += (uint32_t)(a * b);
+            }
+            /* scvtf, fmul, fadd bias, fmax lo: :2269-2294, no fusion */
+            float v = (float)(int32_t)acc;
+            v = v * s;
+            v = v + bias[j];
+            C[i * N + j] = fmaxA(v, lo);
+        }
+    }
+}
+
+void oracle_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int8_t* A,
+                        uint32_t lda, const int8_t* B, uint32_t ldb,
+                        int32_t* acc) {
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long ii = 0; ii < (long)M; ii++) {
+        size_t i = (size_t)ii;
+        uint32_t* row = (uint32_t*)malloc(sizeof(uint32_t) * (N ? N : 1));
+        memset(row, 0, sizeof(uint32_t) * N);
+        for (size_t k = 0; k < K; k++) {
+            int32_t a = A[i * lda + k];
+            const int8_t* b = B + k * ldb;
+            for (size_t j = 0; j < N; j++) row[j] += (uint32_t)(a * (int32_t)b[j]);
+        }
+        for (size_t j = 0; j < N; j++) acc[i * N + j] = (int32_t)row[j];
+        free(row);
+    }
+}
+
+void oracle_dense_fused_rows(int32_t row0, int32_t row1, int32_t N, int32_t K,
+                             float s, int relu, const int8_t* qA,
+                             const int8_t* qB, float* C) {
+    float lo = relu ? 0.0f : -3.40282347e+38f;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long ii = row0; ii < (long)row1; ii++) {
+        size_t i = (size_t)ii;
+        uint32_t* row = (uint32_t*)malloc(sizeof(uint32_t) * (N ? N : 1));
+        memset(row, 0, sizeof(uint32_t) * (size_t)N);
+        for (size_t k = 0; k < (size_t)K; k++) {
+            int32_t a = qA[i * (size_t)K + k];
+            const int8_t* b = qB + k * (size_t)N;
+            for (size_t j = 0; j < (size_t)N; j++)
+                row[j] += (uint32_t)(a * (int32_t)b[j]);
+        }
+        for (size_t j = 0; j < (size_t)N; j++) {
+            float v = (float)(int32_t)row[j];
+            v = v * s;
+            v = v + 0.0f; /* mirrors the zero-bias fadd: -0 -> +0 */
+            C[i * (size_t)N + j] = fmaxA(v, lo);
+        }
+        free(row);
+    }
+}
+
+void oracle_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
+                           int relu, const float* A, const float* B, float* C) {
+    if (M <= 0 || N <= 0) return;
+    size_t na = (size_t)M * (size_t)(K > 0 ? K : 0);
+    size_t nb = (size_t)(K > 0 ? K : 0) * (size_t)N;
+    int8_t* qA = (int8_t*)malloc(na ? na : 1);
+    int8_t* qB = (int8_t*)malloc(nb ? nb : 1);
+    float sa, sb;
+    oracle_quantize_exact(na, A, qA, &sa);
+    oracle_quantize_exact(nb, B, qB, &sb);
+    float s = sa * sb;
+    s = s * scale;
+    oracle_dense_fused_rows(0, M, N, K > 0 ? K : 0, s, relu, qA, qB, C);
+    free(qA);
+    free(qB);
+}
+
+/* FADDV over 16 fp32 lanes: recursive halving, lo + hi at every level
+ * (bytecode_interpreter.s:7060; Arm ARM Reduce()).  Equals an xor-butterfly
+ * with offsets 1, 2, 4, 8. */
+static float faddv16(const float* a) {
+    float t8[8], t4[4], t2[2];
+    for (int l = 0; l < 8; l++) t8[l] = a[2 * l] + a[2 * l + 1];
+    for (int l = 0; l < 4; l++) t4[l] = t8[2 * l] + t8[2 * l + 1];
+    for (int l = 0; l < 2; l++) t2[l] = t4[2 * l] + t4[2 * l + 1];
+    return t2[0] + t2[1];
+}
+
+/* bytecode_interpreter.s:7016-7063. */
+void oracle_q8_0_gemv(uint32_t M, uint32_t K, const float* x,
+                      const uint8_t* W, float* y) {
+    size_t nb = K >> 5; /* :7026 lsr #5: K%32 ignored */
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        size_t m = (size_t)mm;
+        const uint8_t* row = W + m * nb * 34;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t* blk = row + b * 34;
+            uint16_t dh = (uint16_t)(blk[0] | (blk[1] << 8));
+            float d = oracle_f16_to_f32(dh); /* fcvt s,h exact :7036-7038 */
+            for (int h = 0; h < 2; h++)
+                for (int l = 0; l < 16; l++) {
+                    float w = (float)(int8_t)blk[2 + 16 * h + l] * d; /* scvtf, fmul */
+                    acc[l] = fmaf(w, x[32 * b + 16 * h + l], acc[l]); /* fmla */
+                }
+        }
+        y[m] = faddv16(acc); /* faddv s4, p0, z4.s (:7060) */
+    }
+}
+
+void oracle_q8_0_quantize_x(uint32_t K, const float* x, int8_t* qx, float* dx) {
+    size_t nb = K >> 5;
+    for (size_t b = 0; b < nb; b++)
+        oracle_quantize_exact(32, x + 32 * b, qx + 32 * b, dx + b);
+}
+
+void oracle_q8_0_mul_mat_g(uint32_t N, uint32_t K, uint32_t T, const float* x,
+                           const uint8_t* W, float* y) {
+    size_t nb = K >> 5;
+    int8_t* qx = (int8_t*)malloc((size_t)T * nb * 32 + 1);
+    float* dx = (float*)malloc(sizeof(float) * ((size_t)T * nb + 1));
+    for (uint32_t t = 0; t < T; t++)
+        oracle_q8_0_quantize_x(K, x + (size_t)t * K, qx + (size_t)t * nb * 32,
+                               dx + (size_t)t * nb);
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)N; mm++) {
+        size_t m = (size_t)mm;
+        const uint8_t* row = W + m * nb * 34;
+        for (uint32_t t = 0; t < T; t++) {
+            const int8_t* q = qx + (size_t)t * nb * 32;
+            const float* d = dx + (size_t)t * nb;
+            float p[16];
+            for (int l = 0; l < 16; l++) p[l] = 0.0f;
+            for (size_t b = 0; b < nb; b++) {
+                const uint8_t* blk = row + b * 34;
+                float dw = oracle_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                int32_t isum = 0;
+                for (int i = 0; i < 32; i++)
+                    isum += (int32_t)(int8_t)blk[2 + i] * (int32_t)q[32 * b + i];
+                float dd = dw * d[b];
+                p[b % 16] = fmaf((float)isum, dd, p[b % 16]);
+            }
+            y[(size_t)t * N + m] = faddv16(p);
+        }
+    }
+    free(qx);
+    free(dx);
+}

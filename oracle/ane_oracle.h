@@ -1,0 +1,125 @@
+/*
+ * ane_oracle.h -- CPU restatement of ane's quantized compute path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the GPU path is compared
+ * against (and the timed CPU baseline in bench.py).  The product library
+ * (ane_amd/libane_amd.so) never links, loads or calls anything here; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may.
+ *
+ * Every function restates one opcode handler of the reference's
+ * src/bytecode_interpreter.s (AArch64 SME2 assembly, which cannot be built
+ * or run on this x86/amdgcn toolchain) in scalar C, with the same IEEE
+ * binary32 operation sequence.  Citations are file:line in the reference.
+ *
+ * Pinning (what fixes each function independently of this restatement):
+ *   quantize_fp32_i8 / channelwise / dequantize : tests/test_oracle.py
+ *       numpy float32 restatement, the reference KAT
+ *       tests/test_dsl_coverage.cpp:334-368 (x=(i-128)*0.1, err<1.5*scale),
+ *       closed forms (sign symmetry, |q|<=127, amax element -> +-127).
+ *   pack_b_i8      : brute-force index permutation on tiny shapes + the
+ *       inverse map (unpack(pack(B)) == B, zero padding).
+ *   dense_i8 / u8s8 / gemm_s8_i32 : exact int64 numpy matmul, the reference
+ *       KATs test_remaining_ops.cpp:131-184 (A=(i%11)-5, B=(i%13)-6) and
+ *       test_dsl_coverage.cpp:240-260 / test_program_demo.cpp:148-178
+ *       (all-ones -> 4 and 16); epilogue = three float32 numpy ops.
+ *   dense_fused_i8 : composition of the above; equals the reference's own
+ *       composition quantize->pack_b_i8->dense_i8 (test_mnist_i8.cpp:198-207,
+ *       303-314) at scale 1.0 (checked in tests).
+ *   q8_0_gemv (R)  : block layout pinned by test_remaining_ops.cpp:230-325
+ *       (get_rows_q8_0); FADDV tree and fma pinned by closed-form cases
+ *       (one-hot x, power-of-two data that makes every sum exact, and a
+ *       tree-order case whose sequential sum differs).
+ *   q8_0 G mode    : the build's own definition (the reference has no
+ *       quantized-activation matvec); isum_b pinned exactly by integer
+ *       numpy, combination order pinned by an independent numpy loop with
+ *       exact fma (float64 product/sum then a single rounding).
+ */
+#ifndef ANE_ORACLE_H
+#define ANE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Threads used by the row-parallel loops (OpenMP).  Returns the count in use. */
+int oracle_set_threads(int n);
+
+/* 0x19  bytecode_interpreter.s:1885-1950.  Reads and writes
+ * n = max(16, ceil16(count)) elements (the handler is a do-while over
+ * 16-lane vectors).  Writes *scale_out. */
+void oracle_quantize_fp32_i8(uint32_t count, const float* src, int8_t* dst,
+                             float* scale_out);
+
+/* Same arithmetic over exactly n elements (used by dense_fused_i8 and the
+ * Q8_0 activation quantizer). */
+void oracle_quantize_exact(size_t n, const float* src, int8_t* dst,
+                           float* scale_out);
+
+/* 0x1A  bytecode_interpreter.s:1951-1977.  dst[i] = (float)src[i] * scale for
+ * ceil16(count) elements (count == 0 -> nothing). */
+void oracle_dequantize_i8_fp32(uint32_t count, float scale, const int8_t* src,
+                               float* dst);
+
+/* 0x1C  bytecode_interpreter.s:2583-2662.  Per row absmax quantize; row
+ * stride and processed width are cpad = max(16, ceil16(cols)). */
+void oracle_quantize_fp32_i8_channelwise(uint32_t rows, uint32_t cols,
+                                         const float* src, int8_t* dst,
+                                         float* scales);
+
+/* 0x1B  bytecode_interpreter.s:2447-2582.  SMOPA panel format. */
+size_t oracle_packed_b_size(uint32_t K, uint32_t N);
+void oracle_pack_b_i8(uint32_t K, uint32_t N, const int8_t* src, int8_t* dst);
+
+/* 0x18 / 0x1E  bytecode_interpreter.s:1978-2446 / 2835-3300.
+ * a_unsigned = 0 -> dense_i8 (smopa), 1 -> dense_u8s8 (usmopa).
+ * Writes rows 0 .. max(16, ceil16(M))-1, columns 0..N-1 of C (stride N). */
+void oracle_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
+                     uint8_t flags, const void* A, const int8_t* Bp,
+                     const float* bias, float* C, int a_unsigned);
+
+/* Raw int32 accumulators of the dense_i8 contraction (no epilogue) over the
+ * logical region: acc[i*N+j] = sum_{k<K} A[i*lda+k] * B[k*ldb+j]
+ * (A int8 row-major, B int8 K x N row-major), wrapping int32. */
+void oracle_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int8_t* A,
+                        uint32_t lda, const int8_t* B, uint32_t ldb,
+                        int32_t* acc);
+
+/* README.md:84-97 Op::dense_fused_i8 (not implemented by the reference; the
+ * build's definition): per-tensor absmax quantize of A (M*K) and B (K*N),
+ * int32 contraction, C = fmaxA((float)acc * ((sa*sb)*scale) + 0.0f, lo). */
+void oracle_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
+                           int relu, const float* A, const float* B, float* C);
+
+/* Rows [row0, row1) of dense_fused_i8 given already-quantized operands
+ * (used by the bounded CPU-baseline sample). */
+void oracle_dense_fused_rows(int32_t row0, int32_t row1, int32_t N, int32_t K,
+                             float s, int relu, const int8_t* qA,
+                             const int8_t* qB, float* C);
+
+/* 0x57  bytecode_interpreter.s:7010-7063, "R mode": fp32 x, 16 fma lanes per
+ * row, FADDV pairwise tree.  W rows are concatenated 34-byte Q8_0 blocks. */
+void oracle_q8_0_gemv(uint32_t M, uint32_t K, const float* x,
+                      const uint8_t* W, float* y);
+
+/* "G mode" activation quantizer: each 32-element block of x quantized with
+ * the 0x19 arithmetic (absmax, zero guard), scale kept in fp32. */
+void oracle_q8_0_quantize_x(uint32_t K, const float* x, int8_t* qx, float* dx);
+
+/* "G mode" multi-token matvec: for t < T, m < N:
+ *   isum_b = sum_i qw[m,b,i] * qx[t,b,i]           (exact int32)
+ *   p[b % 16] = fmaf((float)isum_b, d_w[m,b] * dx[t,b], p[b % 16])  b ascending
+ *   y[t*N + m] = FADDV tree of p[0..15] (the 0x57 horizontal sum order)
+ * x is T x K fp32 (row stride K), y is T x N fp32 (row stride N). */
+void oracle_q8_0_mul_mat_g(uint32_t N, uint32_t K, uint32_t T, const float* x,
+                           const uint8_t* W, float* y);
+
+/* IEEE half -> float (exact), as fcvt s, h. */
+float oracle_f16_to_f32(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANE_ORACLE_H */

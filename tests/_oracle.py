@@ -1,0 +1,165 @@
+"""ctypes binding of the CPU oracle (oracle/libane_oracle.so).
+
+Test infrastructure only: the checker the GPU results are compared with.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "libane_oracle.so"
+
+_lib = None
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+class Oracle:
+    def __init__(self, lib):
+        self.lib = lib
+        c = ctypes
+        P = c.c_void_p
+        sig = {
+            "oracle_set_threads": (c.c_int, [c.c_int]),
+            "oracle_quantize_fp32_i8": (None, [c.c_uint32, P, P, P]),
+            "oracle_quantize_exact": (None, [c.c_size_t, P, P, P]),
+            "oracle_dequantize_i8_fp32": (None, [c.c_uint32, c.c_float, P, P]),
+            "oracle_quantize_fp32_i8_channelwise": (None, [c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_packed_b_size": (c.c_size_t, [c.c_uint32, c.c_uint32]),
+            "oracle_pack_b_i8": (None, [c.c_uint32, c.c_uint32, P, P]),
+            "oracle_dense_i8": (None, [c.c_uint32, c.c_uint32, c.c_uint32, c.c_float, c.c_float,
+                                       c.c_uint8, P, P, P, P, c.c_int]),
+            "oracle_gemm_s8_i32": (None, [c.c_uint32, c.c_uint32, c.c_uint32, P, c.c_uint32, P,
+                                          c.c_uint32, P]),
+            "oracle_dense_fused_i8": (None, [c.c_int32, c.c_int32, c.c_int32, c.c_float, c.c_int,
+                                             P, P, P]),
+            "oracle_dense_fused_rows": (None, [c.c_int32, c.c_int32, c.c_int32, c.c_int32,
+                                               c.c_float, c.c_int, P, P, P]),
+            "oracle_q8_0_gemv": (None, [c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_q8_0_quantize_x": (None, [c.c_uint32, P, P, P]),
+            "oracle_q8_0_mul_mat_g": (None, [c.c_uint32, c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_f16_to_f32": (c.c_float, [c.c_uint16]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    def set_threads(self, n: int) -> int:
+        return self.lib.oracle_set_threads(n)
+
+    # 0x19 with the reference's padding: returns (q over n padded elems, scale)
+    def quantize(self, x: np.ndarray, count: int | None = None):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        count = x.size if count is None else count
+        n = max(16, -(-count // 16) * 16)
+        assert x.size >= n
+        q = np.zeros(n, np.int8)
+        s = np.zeros(1, np.float32)
+        self.lib.oracle_quantize_fp32_i8(count, _p(x), _p(q), _p(s))
+        return q, s[0]
+
+    def quantize_exact(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        q = np.zeros(max(x.size, 1), np.int8)
+        s = np.zeros(1, np.float32)
+        self.lib.oracle_quantize_exact(x.size, _p(x), _p(q), _p(s))
+        return q[: x.size], s[0]
+
+    def dequantize(self, q: np.ndarray, scale: float, count: int | None = None):
+        q = np.ascontiguousarray(q, dtype=np.int8)
+        count = q.size if count is None else count
+        n = -(-count // 16) * 16
+        out = np.zeros(max(n, 1), np.float32)
+        self.lib.oracle_dequantize_i8_fp32(count, scale, _p(q), _p(out))
+        return out[:n]
+
+    def channelwise(self, x: np.ndarray, rows: int, cols: int):
+        cpad = max(16, -(-cols // 16) * 16)
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        assert x.size >= rows * cpad
+        q = np.zeros(rows * cpad, np.int8)
+        s = np.zeros(max(rows, 1), np.float32)
+        self.lib.oracle_quantize_fp32_i8_channelwise(rows, cols, _p(x), _p(q), _p(s))
+        return q, s[:rows]
+
+    def packed_b_size(self, K: int, N: int) -> int:
+        return int(self.lib.oracle_packed_b_size(K, N))
+
+    def pack_b(self, B: np.ndarray, K: int, N: int):
+        B = np.ascontiguousarray(B, dtype=np.int8).ravel()
+        out = np.zeros(max(self.packed_b_size(K, N), 1), np.int8)
+        self.lib.oracle_pack_b_i8(K, N, _p(B), _p(out))
+        return out[: self.packed_b_size(K, N)]
+
+    def dense_i8(self, M, N, K, sa, sb, flags, A, Bp, bias, unsigned_a=False):
+        Mp = max(16, -(-M // 16) * 16)
+        A = np.ascontiguousarray(A)
+        Bp = np.ascontiguousarray(Bp, dtype=np.int8)
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        C = np.zeros((Mp, max(N, 1)), np.float32)
+        self.lib.oracle_dense_i8(M, N, K, sa, sb, flags, _p(A), _p(Bp), _p(bias), _p(C),
+                                 1 if unsigned_a else 0)
+        return C[:, :N]
+
+    def gemm_s8_i32(self, A, B, M, N, K):
+        A = np.ascontiguousarray(A, dtype=np.int8)
+        B = np.ascontiguousarray(B, dtype=np.int8)
+        acc = np.zeros((M, N), np.int32)
+        self.lib.oracle_gemm_s8_i32(M, N, K, _p(A), K, _p(B), N, _p(acc))
+        return acc
+
+    def dense_fused_i8(self, M, N, K, scale, relu, A, B):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        B = np.ascontiguousarray(B, dtype=np.float32)
+        C = np.zeros((M, N), np.float32)
+        self.lib.oracle_dense_fused_i8(M, N, K, scale, 1 if relu else 0, _p(A), _p(B), _p(C))
+        return C
+
+    def dense_fused_rows(self, row0, row1, N, K, s, relu, qA, qB):
+        qA = np.ascontiguousarray(qA, dtype=np.int8)
+        qB = np.ascontiguousarray(qB, dtype=np.int8)
+        C = np.zeros((row1, N), np.float32)  # rows below row0 untouched
+        self.lib.oracle_dense_fused_rows(row0, row1, N, K, s, 1 if relu else 0, _p(qA), _p(qB),
+                                         _p(C))
+        return C[row0:row1]
+
+    def q8_0_gemv(self, M, K, x, W):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        y = np.zeros(max(M, 1), np.float32)
+        self.lib.oracle_q8_0_gemv(M, K, _p(x), _p(W), _p(y))
+        return y[:M]
+
+    def q8_0_quantize_x(self, K, x):
+        nb = K >> 5
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        qx = np.zeros(max(nb * 32, 1), np.int8)
+        dx = np.zeros(max(nb, 1), np.float32)
+        self.lib.oracle_q8_0_quantize_x(K, _p(x), _p(qx), _p(dx))
+        return qx[: nb * 32], dx[:nb]
+
+    def q8_0_mul_mat_g(self, N, K, T, x, W):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        y = np.zeros((max(T, 1), max(N, 1)), np.float32)
+        self.lib.oracle_q8_0_mul_mat_g(N, K, T, _p(x), _p(W), _p(y))
+        return y[:T, :N]
+
+    def f16_to_f32(self, h: int) -> float:
+        return self.lib.oracle_f16_to_f32(h)
+
+
+def load() -> Oracle:
+    global _lib
+    if _lib is None:
+        if not ORACLE_SO.exists():
+            subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+        _lib = Oracle(ctypes.CDLL(str(ORACLE_SO)))
+    return _lib

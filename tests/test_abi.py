@@ -1,0 +1,130 @@
+"""The C-ABI boundary without a GPU: exports, byte encoding, decoder errors.
+
+Covers include/ane_hip.h (every declared function is exported by
+libane_amd.so), the Python mirror of ane::dispatch against the C++ header
+(include/ane/ane.hpp compiled with g++), and the decoder's error paths that
+return before any HIP call.
+"""
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import ane_amd
+from ane_amd import Op, boolean, encode, f32, i32, ptr, u32
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ane_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(\w+)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "defined")))
+
+
+def test_header_matches_python_export_list():
+    assert declared_functions() == sorted(ane_amd.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    assert ane_amd.LIB_PATH.exists(), "build libane_amd.so first (python -m ane_amd.build)"
+    L = ane_amd.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(ane_amd.LIB_PATH)],
+                             capture_output=True, text=True, check=True).stdout
+        exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+        assert set(declared_functions()) <= exported
+
+
+def test_pure_host_queries():
+    L = ane_amd.lib()
+    assert L.ane_hip_version().startswith(b"ane_amd")
+    assert L.ane_hip_packed_b_size(832, 128) == 8 * 208 * 64
+    assert L.ane_hip_packed_b_size(128, 10) == 1 * 32 * 64
+    assert L.ane_hip_dense_fused_i8_workspace_size(4096, 4096, 4096) >= 2 * 4096 * 4096
+    assert L.ane_hip_q8_0_mul_mat_workspace_size(4096, 1) >= 4096 + 128 * 4
+
+
+def test_record_sizes():
+    """Appendix of the opcode table: dense 54 B, quantize 29, dequantize 25,
+    pack 25, channelwise 33, q8_0_gemv 33, dense_fused_i8 42."""
+    assert len(ane_amd.rec_dense_i8(1, 2, 3, 1.0, 1.0, True, 0, 0, 0, 0)) == 54
+    assert len(ane_amd.rec_quantize(16, 0, 0, 0)) == 29
+    assert len(ane_amd.rec_dequantize(16, 1.0, 0, 0)) == 25
+    assert len(ane_amd.rec_pack_b(4, 16, 0, 0)) == 25
+    assert len(ane_amd.rec_channelwise(1, 16, 0, 0, 0)) == 33
+    assert len(ane_amd.rec_q8_0_gemv(1, 32, 0, 0, 0)) == 33
+    assert len(ane_amd.rec_dense_fused_i8(1, 1, 1, 1.0, True, 0, 0, 0)) == 42
+
+
+def test_python_encoding_matches_cpp_header(tmp_path):
+    gxx = shutil.which("g++")
+    if not gxx:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "encode_dump"
+    subprocess.run([gxx, "-std=c++20", f"-I{ROOT / 'include'}", str(ROOT / "tests/cpp/encode_dump.cpp"),
+                    "-o", str(exe)], check=True)
+    lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    A, B, bias, C, xf, scale = 0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000
+    expect = [
+        ane_amd.rec_dense_i8(50, 16, 128, 0.5, 0.25, False, A, B, bias, C),
+        ane_amd.rec_dense_i8(50, 128, 832, ctypes.c_float(1.0 / 255.0).value, 0.125, True, A, B, bias, C,
+                             unsigned_a=True),
+        ane_amd.rec_quantize(832 * 128, xf, A, scale),
+        ane_amd.rec_dequantize(256, 0.75, A, C),
+        ane_amd.rec_pack_b(832, 128, A, B),
+        ane_amd.rec_channelwise(7, 48, xf, A, scale),
+        ane_amd.rec_q8_0_gemv(4096, 14336, xf, B, C),
+        ane_amd.rec_dense_fused_i8(50, 128, 784, 1.0, True, xf, xf, C),
+    ]
+    assert lines == [e.hex() for e in expect]
+
+
+def test_encode_requires_typed_args():
+    with pytest.raises(TypeError):
+        encode(Op.dense_i8, 1, 2)
+    assert encode(Op.dense_fused_i8, i32(-1))[1:] == b"\xff\xff\xff\xff"
+    assert encode(Op.q8_0_gemv, u32(1), f32(1.0), boolean(True), ptr(7)) == (
+        bytes([0x57]) + b"\x01\0\0\0" + b"\0\0\x80\x3f" + b"\x01" + b"\x07" + b"\0" * 7)
+
+
+def _run_async(data: bytes):
+    L = ane_amd.lib()
+    buf = ctypes.create_string_buffer(data, len(data))
+    st = L.ane_stream_exec_async(buf, len(data), None)
+    return st, L.ane_last_error_message().decode()
+
+
+def test_decoder_unknown_opcode():
+    st, msg = _run_async(bytes([0x15]) + b"\0" * 40)  # dense_fp32: not on this path
+    assert st == 4 and "0x15" in msg
+
+
+def test_decoder_truncated_record():
+    rec = ane_amd.rec_dense_i8(16, 16, 64, 1.0, 1.0, False, 0, 0, 0, 0)
+    st, msg = _run_async(rec[:-3])
+    assert st == 5 and "truncated" in msg
+
+
+def test_decoder_stops_at_exit_opcode():
+    """Slot 0x00 of the jump table is .L_exit: bytes after it are not run."""
+    st, _ = _run_async(bytes([0x00, 0x15, 0x15]))
+    assert st == 0
+
+
+def test_decoder_null_operand():
+    st, msg = _run_async(ane_amd.rec_quantize(64, 0, 0, 0))
+    assert st == 2 and "null" in msg
+
+
+def test_empty_stream_is_ok():
+    st, _ = _run_async(b"")
+    assert st == 0

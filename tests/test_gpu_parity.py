@@ -1,0 +1,376 @@
+"""GPU parity: libane_amd.so (through the C ABI) against the CPU oracle on the
+same seeded inputs.  Integer/byte results and the fp32 outputs of the
+reference opcodes are compared bit for bit (the epilogues are single-rounding
+fp32 sequences, so bit equality is the bar; NaNs compare as NaN)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests import data
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def zeros(n, dtype):
+    import torch
+
+    return torch.zeros(n, dtype=dtype, device="cuda")
+
+
+def bits(a):
+    a = np.ascontiguousarray(a, F32)
+    return a.view(np.uint32)
+
+
+def assert_f32_identical(got, want):
+    got = np.asarray(got, F32)
+    want = np.asarray(want, F32)
+    assert got.shape == want.shape
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(bits(got)[~nan], bits(want)[~nan])
+
+
+# ---------------------------------------------------------------- MFMA core
+@pytest.mark.parametrize("M,N,K", [(1, 1, 16), (32, 32, 32), (50, 130, 784), (128, 128, 128),
+                                   (300, 200, 1008), (257, 129, 4096), (64, 512, 48)])
+def test_gemm_s8_i32_exact(ane, M, N, K):
+    import torch
+
+    g = np.random.default_rng(M + N + K)
+    A = g.integers(-128, 128, size=(M, K), dtype=np.int8)
+    Bt = g.integers(-128, 128, size=(N, K), dtype=np.int8)
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    ane.gemm_s8_i32(dev(A), dev(Bt), acc, M, N, K)
+    want = A.astype(np.int64) @ Bt.astype(np.int64).T
+    np.testing.assert_array_equal(host(acc), want.astype(np.int32))
+
+
+# ---------------------------------------------------------------- quantize
+@pytest.mark.parametrize("count", [1, 16, 17, 1000, 4096 + 5, 1 << 20])
+def test_quantize_opcode_parity(ane, oracle, count):
+    n = max(16, -(-count // 16) * 16)
+    x = np.random.default_rng(count).standard_normal(n).astype(F32) * F32(3)
+    x[:4] = [0.0, -0.0, 1e-41, -7.5]
+    q_ref, s_ref = oracle.quantize(x, count)
+    src, dst, sc = dev(x), zeros(n, ane_torch_int8()), zeros(1, ane_torch_f32())
+    ane.stream_exec(ane.rec_quantize(count, src, dst, sc))
+    np.testing.assert_array_equal(host(dst), q_ref)
+    assert host(sc)[0].tobytes() == F32(s_ref).tobytes()
+
+
+def ane_torch_int8():
+    import torch
+
+    return torch.int8
+
+
+def ane_torch_f32():
+    import torch
+
+    return torch.float32
+
+
+def test_quantize_host_scale_pointer(ane, oracle):
+    """The reference writes the scale through a host pointer
+    (tests/test_mnist_i8.cpp:307-308); a host scale_out is staged back."""
+    x = np.random.default_rng(1).standard_normal(4096).astype(F32)
+    q_ref, s_ref = oracle.quantize(x)
+    scale = np.zeros(1, F32)
+    dst = zeros(4096, ane_torch_int8())
+    ane.stream_exec(ane.rec_quantize(4096, dev(x), dst, scale.ctypes.data))
+    assert scale[0] == s_ref
+    np.testing.assert_array_equal(host(dst), q_ref)
+
+
+def test_quantize_nan_and_zero(ane):
+    x = np.ones(64, F32)
+    x[9] = np.nan
+    dst, sc = zeros(64, ane_torch_int8()), zeros(1, ane_torch_f32())
+    ane.stream_exec(ane.rec_quantize(64, dev(x), dst, sc))
+    assert np.isnan(host(sc)[0]) and not host(dst).any()
+    ane.stream_exec(ane.rec_quantize(64, dev(np.zeros(64, F32)), dst, sc))
+    assert host(sc)[0] == 1.0 and not host(dst).any()
+
+
+def test_quantize_exact_count_kernel_abi(ane, oracle):
+    x = np.random.default_rng(3).standard_normal(1003).astype(F32)
+    q_ref, s_ref = oracle.quantize_exact(x)
+    dst, sc = zeros(1003, ane_torch_int8()), zeros(1, ane_torch_f32())
+    ane.quantize_fp32_i8(dev(x), dst, sc, count=1003, pad16=False)
+    np.testing.assert_array_equal(host(dst), q_ref)
+    assert host(sc)[0] == s_ref
+
+
+def test_dequantize_parity(ane, oracle):
+    q = np.random.default_rng(2).integers(-128, 128, size=4096 + 16, dtype=np.int8)
+    out = zeros(q.size, ane_torch_f32())
+    ane.stream_exec(ane.rec_dequantize(q.size - 3, 0.0173, dev(q), out))
+    ref = oracle.dequantize(q, F32(0.0173), q.size - 3)
+    assert_f32_identical(host(out)[: ref.size], ref)
+
+
+def test_channelwise_parity(ane, oracle):
+    rows, cols = 33, 100
+    cpad = 112
+    x = np.random.default_rng(4).standard_normal(rows * cpad).astype(F32)
+    x[cpad * 5: cpad * 6] = 0.0
+    q_ref, s_ref = oracle.channelwise(x, rows, cols)
+    dst, sc = zeros(rows * cpad, ane_torch_int8()), zeros(rows, ane_torch_f32())
+    ane.stream_exec(ane.rec_channelwise(rows, cols, dev(x), dst, sc))
+    np.testing.assert_array_equal(host(dst), q_ref)
+    np.testing.assert_array_equal(host(sc), s_ref)
+
+
+@pytest.mark.parametrize("K,N", [(832, 128), (128, 16), (5, 17), (4096, 4096), (100, 10)])
+def test_pack_b_parity(ane, oracle, K, N):
+    B = np.random.default_rng(K + N).integers(-128, 128, size=(K, N), dtype=np.int8)
+    ref = oracle.pack_b(B, K, N)
+    dst = zeros(ref.size, ane_torch_int8())
+    ane.stream_exec(ane.rec_pack_b(K, N, dev(B), dst))
+    np.testing.assert_array_equal(host(dst), ref)
+
+
+# ---------------------------------------------------------------- dense_i8 / u8s8
+def _dense_inputs(M, N, K, seed, unsigned_a):
+    g = np.random.default_rng(seed)
+    Kp = -(-K // 64) * 64
+    Mp = max(16, -(-M // 16) * 16)
+    if unsigned_a:
+        A = g.integers(0, 256, size=(Mp, Kp), dtype=np.uint8)
+    else:
+        A = g.integers(-127, 128, size=(Mp, Kp), dtype=np.int8)
+    B = np.zeros((Kp, N), np.int8)
+    B[:K] = g.integers(-127, 128, size=(K, N), dtype=np.int8)
+    bias = g.standard_normal(max(N, 1)).astype(F32)
+    return A, B, bias, Mp, Kp
+
+
+@pytest.mark.parametrize("M,N,K,unsigned_a", [
+    (50, 128, 832, True), (50, 16, 128, False), (1, 10, 64, False), (17, 33, 100, False),
+    (16, 32, 64, True), (0, 5, 64, False), (200, 300, 1000, False), (129, 257, 4096, True),
+])
+def test_dense_i8_parity(ane, oracle, M, N, K, unsigned_a):
+    A, B, bias, Mp, Kp = _dense_inputs(M, N, K, M * 3 + N + K, unsigned_a)
+    Bp = oracle.pack_b(B, Kp, N)
+    dA, dBp, dbias = dev(A), dev(Bp), dev(bias)
+    for flags in (0, 1):
+        ref = oracle.dense_i8(M, N, K, F32(0.013), F32(0.021), flags, A, Bp, bias, unsigned_a)
+        C = zeros(Mp * N, ane_torch_f32())
+        ane.stream_exec(ane.rec_dense_i8(M, N, K, 0.013, 0.021, bool(flags), dA, dBp, dbias, C,
+                                         unsigned_a=unsigned_a))
+        assert_f32_identical(host(C).reshape(Mp, N), ref)
+
+
+def test_dense_i8_igemm_kat_on_gpu(ane):
+    """tests/test_remaining_ops.cpp:131-184 pattern, exact integers."""
+    M, N, K = 16, 32, 64
+    A = ((np.arange(M * K) % 11) - 5).astype(np.int8).reshape(M, K)
+    B = ((np.arange(K * N) % 13) - 6).astype(np.int8).reshape(K, N)
+    ref = (A.astype(np.int64) @ B.astype(np.int64)).astype(F32)
+    Bp = zeros(K * N * 2, ane_torch_int8())
+    ane.stream_exec(ane.rec_pack_b(K, N, dev(B), Bp))
+    C = zeros(M * N, ane_torch_f32())
+    ane.stream_exec(ane.rec_dense_i8(M, N, K, 1.0, 1.0, False, dev(A), Bp, dev(np.zeros(N, F32)), C))
+    np.testing.assert_array_equal(host(C).reshape(M, N), ref)
+
+
+def test_mnist_i8_composition(ane, oracle):
+    """The reference's int8 forward (tests/test_mnist_i8.cpp:198-207, 303-314):
+    quantize+pack W, dense_u8s8 on raw pixels, quantize hidden, dense_i8 with
+    the -1000 logit mask, as one multi-record stream."""
+    g = np.random.default_rng(12)
+    B, INP_K, HID, HID_K, OUT_PAD = 50, 832, 128, 128, 16
+    x_u8 = np.zeros((64, INP_K), np.uint8)
+    x_u8[:B, :784] = g.integers(0, 256, size=(B, 784))
+    W1 = np.zeros((INP_K, HID), F32)
+    W1[:784] = g.standard_normal((784, HID)) * 0.05
+    W2 = (g.standard_normal((HID_K, OUT_PAD)) * 0.05).astype(F32)
+    logit_bias = np.array([0] * 10 + [-1000.0] * 6, F32)
+    zero_bias = np.zeros(INP_K, F32)
+    # oracle
+    w1q, s1 = oracle.quantize(W1.ravel())
+    w1p = oracle.pack_b(w1q, INP_K, HID)
+    w2q, s2 = oracle.quantize(W2.ravel())
+    w2p = oracle.pack_b(w2q, HID_K, OUT_PAD)
+    h = oracle.dense_i8(B, HID, INP_K, F32(1 / 255), s1, 1, x_u8, w1p, zero_bias, unsigned_a=True)
+    hq, sh = oracle.quantize(h[:B].ravel(), B * HID_K)
+    hq_pad = np.zeros((64, HID_K), np.int8)
+    hq_pad[:B] = hq.reshape(B, HID_K)
+    logits = oracle.dense_i8(B, OUT_PAD, HID_K, sh, s2, 0, hq_pad, w2p, logit_bias)
+    # device, same call sequence
+    import torch
+
+    dW1, dW2 = dev(W1), dev(W2)
+    dw1q = zeros(INP_K * HID, torch.int8)
+    dw1p = zeros(oracle.packed_b_size(INP_K, HID), torch.int8)
+    dw2q = zeros(HID_K * OUT_PAD, torch.int8)
+    dw2p = zeros(oracle.packed_b_size(HID_K, OUT_PAD), torch.int8)
+    scales = zeros(3, torch.float32)
+    ane.stream_exec([
+        ane.rec_quantize(INP_K * HID, dW1, dw1q, scales.data_ptr()),
+        ane.rec_pack_b(INP_K, HID, dw1q, dw1p),
+        ane.rec_quantize(HID_K * OUT_PAD, dW2, dw2q, scales.data_ptr() + 4),
+        ane.rec_pack_b(HID_K, OUT_PAD, dw2q, dw2p),
+    ])
+    sc = host(scales)
+    assert sc[0] == s1 and sc[1] == s2
+    dh = zeros(64 * HID, torch.float32)
+    ane.stream_exec(ane.rec_dense_i8(B, HID, INP_K, 1 / 255, float(sc[0]), True, dev(x_u8), dw1p,
+                                     dev(zero_bias), dh, unsigned_a=True))
+    assert_f32_identical(host(dh).reshape(64, HID), h)
+    dhq = zeros(64 * HID_K, torch.int8)
+    sh_host = np.zeros(1, F32)
+    ane.stream_exec(ane.rec_quantize(B * HID_K, dh, dhq, sh_host.ctypes.data))
+    assert sh_host[0] == sh
+    dlog = zeros(64 * OUT_PAD, torch.float32)
+    ane.stream_exec(ane.rec_dense_i8(B, OUT_PAD, HID_K, float(sh_host[0]), float(sc[1]), False, dhq, dw2p,
+                                     dev(logit_bias), dlog))
+    assert_f32_identical(host(dlog).reshape(64, OUT_PAD), logits)
+
+
+# ---------------------------------------------------------------- dense_fused_i8
+def test_dense_fused_mnist_mlp(ane, oracle):
+    """Config 1: 50x784 -> 128 (ReLU) -> 10, through stream_exec."""
+    x, w1, w2 = data.mnist_inputs(seed=1)
+    h_ref = oracle.dense_fused_i8(50, 128, 784, F32(1.0), True, x, w1)
+    o_ref = oracle.dense_fused_i8(50, 10, 128, F32(1.0), False, h_ref, w2)
+    import torch
+
+    h = zeros(50 * 128, torch.float32)
+    o = zeros(50 * 10, torch.float32)
+    ane.stream_exec([ane.rec_dense_fused_i8(50, 128, 784, 1.0, True, dev(x), dev(w1), h),
+                     ane.rec_dense_fused_i8(50, 10, 128, 1.0, False, h, dev(w2), o)])
+    assert_f32_identical(host(h).reshape(50, 128), h_ref)
+    assert_f32_identical(host(o).reshape(50, 10), o_ref)
+
+
+@pytest.mark.parametrize("M,N,K,relu,scale", [(3, 5, 7, True, 1.0), (64, 64, 1, False, 2.5),
+                                              (1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0),
+                                              (129, 257, 1000, False, 0.75), (7, 9, 0, True, 1.0)])
+def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
+    A, B = data.gemm_inputs(M, N, K, seed=M + N + K)
+    ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
+    import torch
+
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, scale, relu, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
+def test_dense_fused_4096_cubed_sampled(ane, oracle):
+    """Config 2 at full size: both per-tensor scales exact, and a sample of
+    rows of C identical to the oracle's contraction of the oracle-quantized
+    operands (the full 4096^3 scalar product is too slow for a test)."""
+    import torch
+
+    M = N = K = 4096
+    A, B = data.gemm_inputs(M, N, K, seed=2)
+    qA, sa = oracle.quantize_exact(A.ravel())
+    qB, sb = oracle.quantize_exact(B.ravel())
+    C = zeros(M * N, torch.float32)
+    scales = zeros(2, torch.float32)
+    ane.dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C, scales_out=scales)
+    s = host(scales)
+    assert s[0] == sa and s[1] == sb
+    Ch = host(C).reshape(M, N)
+    oracle.set_threads(0)
+    try:
+        st = F32(F32(sa * sb) * F32(1.0))
+        for r0 in (0, 1337, 4088):
+            rows = oracle.dense_fused_rows(r0, r0 + 8, N, K, st, True, qA, qB)
+            assert_f32_identical(Ch[r0: r0 + 8], rows)
+    finally:
+        oracle.set_threads(1)
+    assert (Ch >= 0).all()
+
+
+# ---------------------------------------------------------------- Q8_0
+@pytest.mark.parametrize("M,K", [(1, 32), (3, 40), (4096, 4096), (14336, 4096), (4096, 14336), (77, 96)])
+def test_q8_0_gemv_r_parity(ane, oracle, M, K):
+    """Opcode 0x57 through stream_exec, bit-identical to the reference arithmetic."""
+    import torch
+
+    K32 = K - K % 32
+    W = data.q8_0_weights(M, K32, seed=M + K)
+    x = data.activations(1, K, seed=K)[0]
+    oracle.set_threads(0)
+    try:
+        ref = oracle.q8_0_gemv(M, K, x, W)
+    finally:
+        oracle.set_threads(1)
+    y = zeros(M, torch.float32)
+    ane.stream_exec(ane.rec_q8_0_gemv(M, K, dev(x), dev(W), y))
+    assert_f32_identical(host(y), ref)
+
+
+@pytest.mark.parametrize("N,K,T", [(4096, 4096, 1), (14336, 4096, 1), (4096, 14336, 1), (6144, 4096, 4),
+                                   (4096, 4096, 16), (1024, 4096, 64), (100, 96, 3), (5, 50, 2)])
+def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
+    import torch
+
+    W = data.q8_0_weights(N, K - K % 32, seed=N + K)
+    x = data.activations(T, K, seed=T + 100)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
+    finally:
+        oracle.set_threads(1)
+    y = zeros(T * N, torch.float32)
+    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
+    assert_f32_identical(host(y).reshape(T, N), ref)
+
+
+# ---------------------------------------------------------------- error paths
+def _hip():
+    return ctypes.CDLL("libamdhip64.so")
+
+
+def test_host_pointer_rejected(ane):
+    x = np.ones(64, F32)
+    q = np.zeros(64, np.int8)
+    with pytest.raises(ane.AneError) as e:
+        ane.stream_exec(ane.rec_quantize(64, x.ctypes.data, q.ctypes.data, 0))
+    assert e.value.status == 2
+
+
+def test_short_buffer_rejected(ane):
+    hip = _hip()
+    p = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(1024)) == 0
+    try:
+        import torch
+
+        dst = zeros(8192, torch.int8)
+        sc = zeros(1, torch.float32)
+        with pytest.raises(ane.AneError) as e:
+            ane.stream_exec(ane.rec_quantize(4096, p.value, dst, sc))
+        assert e.value.status == 3
+    finally:
+        hip.hipFree(p)
+
+
+def test_unknown_opcode_stops_stream(ane):
+    import torch
+
+    x = dev(np.ones(64, F32))
+    dst, sc = zeros(64, torch.int8), zeros(1, torch.float32)
+    with pytest.raises(ane.AneError) as e:
+        ane.stream_exec([bytes([0x15]), ane.rec_quantize(64, x, dst, sc)])
+    assert e.value.status == 4
+    assert not host(dst).any()
