@@ -75,6 +75,8 @@ EXPORTS = (
     "ane_hip_dense_i8",
     "ane_hip_dense_fused_i8_workspace_size",
     "ane_hip_dense_fused_i8",
+    "ane_hip_dense_fused_i8_quantize",
+    "ane_hip_dense_fused_i8_gemm",
     "ane_hip_gemm_s8_i32",
     "ane_hip_q8_0_gemv",
     "ane_hip_q8_0_mul_mat_workspace_size",
@@ -109,6 +111,10 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         _c.c_int,
         [_c.c_int32, _c.c_int32, _c.c_int32, _c.c_float, _c.c_int, _P, _P, _P, _P, _P, _c.c_size_t, _P],
     ),
+    "ane_hip_dense_fused_i8_quantize": (
+        _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _P, _P, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_dense_fused_i8_gemm": (
+        _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _c.c_float, _c.c_int, _P, _P, _c.c_size_t, _P]),
     "ane_hip_gemm_s8_i32": (
         _c.c_int,
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _c.c_uint32, _P, _c.c_uint32, _P, _P],
@@ -297,6 +303,18 @@ def dense_fused_i8(M, N, K, scale, relu, A, B, C, scales_out=None, workspace=Non
     ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=A.device)
     check(L.ane_hip_dense_fused_i8(M, N, K, scale, 1 if relu else 0, _p(A), _p(B), _p(C), _p(scales_out),
                                    _p(ws), wsb, _stream_handle(stream)), "dense_fused_i8")
+
+
+def dense_fused_i8_quantize(M, N, K, A, B, workspace, scales_out=None, stream=None):
+    check(lib().ane_hip_dense_fused_i8_quantize(M, N, K, _p(A), _p(B), _p(scales_out), _p(workspace),
+                                                workspace.numel(), _stream_handle(stream)),
+          "dense_fused_i8_quantize")
+
+
+def dense_fused_i8_gemm(M, N, K, scale, relu, C, workspace, stream=None):
+    check(lib().ane_hip_dense_fused_i8_gemm(M, N, K, scale, 1 if relu else 0, _p(C), _p(workspace),
+                                            workspace.numel(), _stream_handle(stream)),
+          "dense_fused_i8_gemm")
 
 
 def dense_fused_i8_workspace_size(M, N, K) -> int:

@@ -389,28 +389,47 @@ static uint32_t fused_blocks(uint64_t n) {
     return (uint32_t)b;
 }
 
-extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale, int relu,
-                                      const float* A, const float* B, float* C,
-                                      float* scales_out, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
+struct FusedLayout {
+    uint64_t Kp;
+    float* scales;
+    uint32_t* partials;
+    int8_t* qA;
+    int8_t* qBt;
+};
+
+static FusedLayout fused_layout(int32_t M, int32_t K, void* workspace) {
+    FusedLayout L;
+    L.Kp = fused_kp(K);
+    uint8_t* ws = (uint8_t*)workspace;
+    L.scales = (float*)ws;
+    L.partials = (uint32_t*)(ws + 256);
+    L.qA = (int8_t*)(ws + 256 + ceil_to((uint64_t)kFusedPartials * 2 * 4, 256));
+    L.qBt = L.qA + ceil_to((uint64_t)M * L.Kp, 256);
+    return L;
+}
+
+static int fused_check(int32_t M, int32_t N, int32_t K, const void* workspace, size_t workspace_bytes) {
     if (M < 0 || N < 0 || K < 0) return ANE_ERR_INVALID_ARG;
-    if (M == 0 || N == 0) return ANE_OK;
-    if (!C || (K > 0 && (!A || !B))) return ANE_ERR_BAD_POINTER;
     if (!workspace || !aligned16(workspace) ||
         workspace_bytes < ane_hip_dense_fused_i8_workspace_size(M, N, K))
         return ANE_ERR_WORKSPACE;
-    hipStream_t s = (hipStream_t)stream;
-    const uint64_t Kp = fused_kp(K);
-    uint8_t* ws = (uint8_t*)workspace;
-    float* scales = (float*)ws;
-    uint32_t* partials = (uint32_t*)(ws + 256);
-    int8_t* qA = (int8_t*)(ws + 256 + ceil_to((uint64_t)kFusedPartials * 2 * 4, 256));
-    int8_t* qBt = qA + ceil_to((uint64_t)M * Kp, 256);
+    return ANE_OK;
+}
 
+extern "C" int ane_hip_dense_fused_i8_quantize(int32_t M, int32_t N, int32_t K, const float* A,
+                                               const float* B, float* scales_out, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+    int st = fused_check(M, N, K, workspace, workspace_bytes);
+    if (st != ANE_OK) return st;
+    if (M == 0 || N == 0) return ANE_OK;
+    if (K > 0 && (!A || !B)) return ANE_ERR_BAD_POINTER;
+    hipStream_t s = (hipStream_t)stream;
+    const FusedLayout L = fused_layout(M, K, workspace);
+    const uint64_t Kp = L.Kp;
     const uint64_t nA = (uint64_t)M * (uint64_t)K, nB = (uint64_t)K * (uint64_t)N;
     const uint32_t nbA = fused_blocks(nA), nbB = fused_blocks(nB);
     hipLaunchKernelGGL(k_absmax_two, dim3(nbA + nbB), dim3(256), 0, s, A, nA, nbA, B, nB, nbB,
-                       partials);
+                       L.partials);
     uint64_t nqA = ((uint64_t)M * (Kp / 16) + 255) / 256;
     if (nqA > 2048) nqA = 2048;
     if (nqA < 1) nqA = 1;
@@ -418,33 +437,55 @@ extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float sca
     if (Kp > 0) {
         if (nqA + nqB > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
         hipLaunchKernelGGL(k_quantize_two, dim3((uint32_t)(nqA + nqB)), dim3(256), 0, s, A, B,
-                           (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, partials, nbA, nbB,
-                           (uint32_t)nqA, qA, qBt, scales);
+                           (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, L.partials, nbA, nbB,
+                           (uint32_t)nqA, L.qA, L.qBt, L.scales);
     } else {
         // K == 0: no operands to quantize; both scales are 1 (zero guard).
-        hipLaunchKernelGGL(k_quantize_two, dim3(2), dim3(256), 0, s, A, B, (uint32_t)M,
-                           (uint32_t)N, 0u, 0u, partials, nbA, nbB, 1u, qA, qBt, scales);
+        hipLaunchKernelGGL(k_quantize_two, dim3(2), dim3(256), 0, s, A, B, (uint32_t)M, (uint32_t)N,
+                           0u, 0u, L.partials, nbA, nbB, 1u, L.qA, L.qBt, L.scales);
     }
     ANE_HIP_CHECK_LAUNCH();
     if (scales_out) {
-        hipError_t e = hipMemcpyAsync(scales_out, scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
+        hipError_t e = hipMemcpyAsync(scales_out, L.scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return ANE_ERR_HIP;
     }
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, float scale, int relu,
+                                           float* C, const void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    int st = fused_check(M, N, K, workspace, workspace_bytes);
+    if (st != ANE_OK) return st;
+    if (M == 0 || N == 0) return ANE_OK;
+    if (!C) return ANE_ERR_BAD_POINTER;
+    const FusedLayout L = fused_layout(M, K, (void*)workspace);
     GemmParams p{};
-    p.A = qA;
-    p.lda = Kp;
-    p.B = qBt;
-    p.ldb = Kp;
+    p.A = L.qA;
+    p.lda = L.Kp;
+    p.B = L.qBt;
+    p.ldb = L.Kp;
     p.rowsA = (uint32_t)M;
     p.colsB = (uint32_t)N;
-    p.Kp = (uint32_t)Kp;
+    p.Kp = (uint32_t)L.Kp;
     p.Mout = (uint32_t)M;
     p.Nout = (uint32_t)N;
-    p.sdev = scales;
+    p.sdev = L.scales;
     p.smul = scale;
     p.bias = nullptr;
     p.lo = relu ? 0.0f : -3.40282347e+38f;
     p.C = C;
     p.ldc = (uint64_t)N;
-    return launch_gemm<kBTransposed, false>(p, s);
+    return launch_gemm<kBTransposed, false>(p, (hipStream_t)stream);
+}
+
+extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale, int relu,
+                                      const float* A, const float* B, float* C,
+                                      float* scales_out, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    if (M > 0 && N > 0 && !C) return ANE_ERR_BAD_POINTER;
+    int st = ane_hip_dense_fused_i8_quantize(M, N, K, A, B, scales_out, workspace, workspace_bytes,
+                                             stream);
+    if (st != ANE_OK) return st;
+    return ane_hip_dense_fused_i8_gemm(M, N, K, scale, relu, C, workspace, workspace_bytes, stream);
 }

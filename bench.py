@@ -1,0 +1,350 @@
+#!/usr/bin/env python3
+"""Benchmark of ane's quantized compute path on one MI355X.
+
+Headline (BASELINE.json metric, config 2): Op::dense_fused_i8 at
+M = N = K = 4096, scale 1.0, ReLU -- fp32 A and B quantized per tensor to
+int8, int8 x int8 -> int32 on MFMA, fused dequant/scale/ReLU epilogue.  One
+step = one full dense_fused_i8 call with A and B already resident in HBM.
+``value`` is 2*M*N*K / (time per step) in TOPS.
+
+Also reported (same JSON line):
+* ``roofline`` -- the dominant kernel (the MFMA contraction + epilogue),
+  timed alone with HIP events on its stream, against 5.0 POPS int8 dense.
+* ``q8_0_matvec`` -- config 3: Q8_0 matvec 14336x4096 ("G mode", x quantized
+  on the fly) and the reference-arithmetic opcode 0x57 ("R mode"), GB/s
+  against 8 TB/s, rotating >256 MB of weight copies so the Infinity Cache
+  cannot serve them.
+* ``cpu_baseline`` -- the scalar CPU restatement (oracle/) on a bounded
+  sample of the same workload, with the host thread count used.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "int8 GEMM TOPS (% MFMA peak) + q8_0 matvec GB/s (% HBM peak), 1 MI355X"
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POPS
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+PROFILES = ROOT / "profiles"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--M", type=int, default=4096)
+    ap.add_argument("--N", type=int, default=4096)
+    ap.add_argument("--K", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 matvec section")
+    ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
+    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy"], default=None,
+                    help="profiling mode: launch only this workload --steps times, print timing")
+    return ap.parse_args()
+
+
+def events_time(fn, reps: int, stream) -> float:
+    """Average milliseconds per call of fn() over reps calls, HIP events on stream."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def read_pmc_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary
+    (profiles/<name>), lines 'traffic_bytes_per_launch: <int>'."""
+    p = PROFILES / name
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build targets one GPU: the dense_fused_i8 and Q8_0 "
+                                   "kernels shard by rows with no reduction (see DESIGN.md); "
+                                   "run with --gpus 1"}), flush=True)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import ane_amd
+
+    ane_amd.require_gpu()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    M, N, K = args.M, args.N, args.K
+
+    # ------------------------------------------------------------ inputs
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    A = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
+    B = torch.randn((K, N), generator=g, device=dev, dtype=torch.float32)
+    C = torch.empty((M, N), device=dev, dtype=torch.float32)
+    wsb = ane_amd.dense_fused_i8_workspace_size(M, N, K)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    scales = torch.empty(2, dtype=torch.float32, device=dev)
+
+    def fused():
+        ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=stream)
+
+    def gemm_phase():
+        ane_amd.dense_fused_i8_gemm(M, N, K, 1.0, True, C, ws, stream=stream)
+
+    def quant_phase():
+        ane_amd.dense_fused_i8_quantize(M, N, K, A, B, ws, stream=stream)
+
+    ops = 2.0 * M * N * K
+
+    if args.only == "copy":
+        # Plain device copy of a known size: the reference reading for the
+        # FETCH_SIZE / WRITE_SIZE scale factors of the --pmc runs.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup):
+            dst.copy_(src)
+        ms = events_time(lambda: dst.copy_(src), args.steps, stream)
+        log(f"copy 256 MiB: {ms * 1e3:.2f} us/launch, {2 * (256 << 20) / ms / 1e6:.0f} GB/s")
+        return 0
+    if args.only in ("q8g", "q8r"):
+        return profile_q8(args, stream)
+
+    if args.only in ("gemm", "fused"):
+        fn = gemm_phase if args.only == "gemm" else fused
+        quant_phase()
+        for _ in range(args.warmup):
+            fn()
+        ms = events_time(fn, args.steps, stream)
+        log(f"{args.only}: {ms * 1e3:.2f} us/launch, {ops / ms / 1e9:.1f} TOPS")
+        return 0
+
+    # ------------------------------------------------------------ headline
+    log(f"dense_fused_i8 M={M} N={N} K={K}: warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        fused()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fused()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    value = ops / (ms_per_step * 1e-3) / 1e12
+    log(f"whole op: {ms_per_step * 1e3:.2f} us/step = {value:.1f} TOPS")
+
+    # ------------------------------------------------------------ kernel roofline
+    quant_phase()
+    for _ in range(5):
+        gemm_phase()
+    gemm_ms = events_time(gemm_phase, args.kernel_reps, stream)
+    gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
+    quant_ms = events_time(quant_phase, max(20, args.kernel_reps // 4), stream)
+    quant_bytes = 5.0 * (M * K + K * N)  # read fp32 once + write int8 (algorithmic)
+    log(f"MFMA kernel: {gemm_ms * 1e3:.2f} us = {gemm_tops:.1f} TOPS ({gemm_tops / PEAK_INT8_TOPS:.1%})")
+    log(f"quantize phase: {quant_ms * 1e3:.2f} us = {quant_bytes / quant_ms / 1e6:.0f} GB/s algorithmic")
+    roofline = {
+        "bound": "mfma",
+        "kernel": "k_gemm_i8<kBTransposed,false> (dense_fused_i8 contraction + epilogue)",
+        "achieved": round(gemm_tops, 2),
+        "peak": PEAK_INT8_TOPS,
+        "unit": "TOPS",
+        "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+        "algorithmic_per_launch": f"2*M*N*K = {int(ops)} int8 ops",
+        "avg_launch_us": round(gemm_ms * 1e3, 3),
+        "traffic": read_pmc_traffic("gemm_i8_4096_pmc.txt"),
+    }
+
+    # ------------------------------------------------------------ Q8_0 matvec
+    q8 = None
+    if not args.no_q8:
+        q8 = bench_q8(args, stream)
+
+    # ------------------------------------------------------------ CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(A, B, C, M, N, K)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: A, B ~ N(0,1) fp32 (seeded), quantized per tensor on the GPU each step",
+        "config": {"workload": f"dense_fused_i8 M={M} N={N} K={K} scale=1.0 relu (config 2)",
+                   "M": M, "N": N, "K": K},
+        "roofline": roofline,
+        "phases_us": {"quantize": round(quant_ms * 1e3, 2), "contraction": round(gemm_ms * 1e3, 2)},
+        "q8_0_matvec": q8,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def profile_q8(args, stream) -> int:
+    """Launch only the 14336x4096 Q8_0 matvec (G or R mode) --steps times."""
+    import numpy as np
+    import torch
+
+    import ane_amd
+    from tests import data
+
+    Nr, Kc = 14336, 4096
+    W0 = torch.from_numpy(data.q8_0_weights(Nr, Kc, seed=3)).cuda()
+    copies = 6
+    Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(data.activations(1, Kc, seed=4)).cuda()
+    y = torch.empty(Nr, device="cuda", dtype=torch.float32)
+    wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, 1), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def fn():
+        W = Ws[it[0] % copies]
+        it[0] += 1
+        if args.only == "q8g":
+            ane_amd.q8_0_mul_mat(Nr, Kc, 1, x, W, y, workspace=wsq, stream=stream)
+        else:
+            ane_amd.q8_0_gemv(Nr, Kc, x, W, y, stream=stream)
+
+    for _ in range(args.warmup):
+        fn()
+    ms = events_time(fn, args.steps, stream)
+    alg = Nr * (Kc // 32) * 34 + 4 * Kc + 4 * Nr
+    log(f"{args.only} {Nr}x{Kc}: {ms * 1e3:.2f} us/launch, {alg / ms / 1e6:.0f} GB/s")
+    return 0
+
+
+def bench_q8(args, stream) -> dict:
+    import numpy as np
+    import torch
+
+    import ane_amd
+    from tests import data
+
+    res = {}
+    shapes = [(14336, 4096), (4096, 4096), (4096, 14336)]
+    for (Nr, Kc) in shapes:
+        row_bytes = Kc // 32 * 34
+        wbytes = Nr * row_bytes
+        copies = max(2, int(np.ceil(300e6 / wbytes)))  # > 256 MB Infinity Cache
+        W0 = torch.from_numpy(data.q8_0_weights(Nr, Kc, seed=3)).cuda()
+        Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+        x = torch.from_numpy(data.activations(1, Kc, seed=4)).cuda()
+        y = torch.empty(Nr, device="cuda", dtype=torch.float32)
+        wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, 1), dtype=torch.uint8, device="cuda")
+        it = [0]
+
+        def g_mode():
+            W = Ws[it[0] % copies]
+            it[0] += 1
+            ane_amd.q8_0_mul_mat(Nr, Kc, 1, x, W, y, workspace=wsq, stream=stream)
+
+        def r_mode():
+            W = Ws[it[0] % copies]
+            it[0] += 1
+            ane_amd.q8_0_gemv(Nr, Kc, x, W, y, stream=stream)
+
+        alg = wbytes + 4 * Kc + 4 * Nr
+        entry = {"weights_bytes": wbytes, "algorithmic_bytes": alg, "rotating_copies": copies}
+        for name, fn in (("g_mode", g_mode), ("r_mode", r_mode)):
+            for _ in range(10):
+                fn()
+            ms = events_time(fn, args.kernel_reps, stream)
+            gbs = alg / (ms * 1e-3) / 1e9
+            entry[name] = {"us": round(ms * 1e3, 3), "GB_s": round(gbs, 1),
+                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+            log(f"q8_0 {name} {Nr}x{Kc}: {ms * 1e3:.2f} us = {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
+        res[f"{Nr}x{Kc}"] = entry
+        del Ws, W0
+        torch.cuda.empty_cache()
+    head = res["14336x4096"]["g_mode"]
+    return {
+        "workload": "Q8_0 matvec 14336x4096, x fp32 quantized to Q8_0 on the fly (G mode), config 3",
+        "value": head["GB_s"],
+        "unit": "GB/s",
+        "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": head["frac_hbm"],
+                     "algorithmic_per_launch": "N*(K/32)*34 + 4K + 4N bytes",
+                     "traffic": read_pmc_traffic("q8_0_matvec_14336x4096_pmc.txt")},
+        "shapes": res,
+    }
+
+
+def cpu_baseline(A, B, C, M, N, K) -> dict:
+    """Scalar oracle on the host: full per-tensor quantization of A and B,
+    then rows of the contraction until ~10 s of work; extrapolated to the
+    whole op.  Also checks the sampled rows against the GPU's C."""
+    import numpy as np
+
+    from tests import _oracle
+
+    oracle = _oracle.load()
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    An = A.cpu().numpy()
+    Bn = B.cpu().numpy()
+    t0 = time.perf_counter()
+    qA, sa = oracle.quantize_exact(An.ravel())
+    qB, sb = oracle.quantize_exact(Bn.ravel())
+    t_quant = time.perf_counter() - t0
+    s = np.float32(np.float32(sa * sb) * np.float32(1.0))
+    rows = 0
+    t_rows = 0.0
+    chunk = 64
+    sample_rows = []
+    while rows < M and t_rows < 10.0:
+        r1 = min(M, rows + chunk)
+        t1 = time.perf_counter()
+        out = oracle.dense_fused_rows(rows, r1, N, K, s, True, qA, qB)
+        t_rows += time.perf_counter() - t1
+        sample_rows.append((rows, out))
+        rows = r1
+    oracle.set_threads(1)
+    t_full = t_quant + t_rows * (M / rows)
+    tops = 2.0 * M * N * K / t_full / 1e12
+    Cg = C.cpu().numpy()
+    match = all(np.array_equal(Cg[r0:r0 + o.shape[0]].view(np.uint32), o.view(np.uint32))
+                for r0, o in sample_rows)
+    log(f"cpu baseline: {threads} threads, quantize {t_quant:.2f}s, {rows} rows in {t_rows:.2f}s "
+        f"-> {tops:.4f} TOPS (sampled rows bit-identical to GPU: {match})")
+    return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"oracle/ane_oracle.c (-O2, OpenMP over rows): quantize all of A and B "
+                      f"({t_quant:.2f} s) + {rows} of {M} rows of the int32 contraction and "
+                      f"epilogue ({t_rows:.2f} s), extrapolated to the full {M}x{N}x{K} op",
+            "gpu_rows_bit_identical": bool(match)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -125,6 +125,19 @@ int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
                            float* scales_out, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* The two phases of ane_hip_dense_fused_i8, for callers that quantize an
+ * operand pair once and run the contraction repeatedly (the reference's own
+ * quantize-once / reuse pattern, tests/test_mnist_i8.cpp:198-207, 415):
+ * _quantize writes both int8 operands and their scales into the workspace;
+ * _gemm reads them from the same workspace and writes C. */
+int ane_hip_dense_fused_i8_quantize(int32_t M, int32_t N, int32_t K,
+                                    const float* A, const float* B,
+                                    float* scales_out, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, float scale,
+                                int relu, float* C, const void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* Raw int32 accumulators of the int8 MFMA contraction (test/debug entry):
  * acc[i*N+j] = sum_{k<K} A[i*lda+k] * Bt[j*ldb+k], wrapping int32.
  * A and Bt are int8 row-major with K contiguous. */
