@@ -10,9 +10,11 @@
 // Tile: 128 x 128 output per 256-thread workgroup, K staged through LDS in
 // 128-byte slices, four waves each owning a 64 x 64 block of 2 x 2
 // v_mfma_i32_32x32x32_i8 tiles.  Both operand tiles sit in LDS as
-// [row][128 bytes] with the 16-byte chunk index XOR-swizzled by (row>>1)&7
-// so the ds_read_b128 of 16 consecutive rows hits 16 distinct bank groups.
-#include "common.hpp"
+// [row][128 bytes] with the 16-byte chunk index XOR-swizzled by
+// (row ^ row>>3) & 7 so the ds_read_b128 of 16 consecutive rows (one LDS
+// cycle: 64 banks x 4 bytes) hits 16 distinct bank groups.  Large shapes use the 256 x 256 kernel of
+// gemm_i8_tile256.hip instead.
+#include "gemm_i8.hpp"
 
 namespace ane {
 
@@ -21,27 +23,8 @@ constexpr int kGThreads = 256;
 
 enum BLayout : int { kBTransposed = 0, kBPanel = 1 };
 
-struct GemmParams {
-    const int8_t* A;      // row-major, K contiguous
-    uint64_t lda;         // bytes between rows of A
-    const int8_t* B;      // Bt (N x K, K contiguous) or SMOPA panels
-    uint64_t ldb;         // Bt: bytes between rows; panel: groups per panel (G)
-    uint32_t rowsA;       // rows of A that may be read (others read as 0)
-    uint32_t colsB;       // columns of B that may be read (others read as 0)
-    uint32_t Kp;          // contraction length, multiple of 16
-    uint32_t Mout, Nout;  // output rows / columns written
-    float s;              // epilogue multiplier (when sdev == nullptr)
-    const float* sdev;    // device {sa, sb}: s = (sa*sb)*smul
-    float smul;
-    const float* bias;    // fp32[Nout] or nullptr (adds +0.0f)
-    float lo;             // ReLU floor: +0 or -FLT_MAX
-    float* C;             // fp32 output, row stride ldc
-    uint64_t ldc;
-    int32_t* Craw;        // raw int32 output instead (debug entry)
-};
-
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
-    return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4);
+    return row * kBK + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
 }
 
 template <int BL, bool AU8>
@@ -302,6 +285,7 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
 template <int BL, bool AU8>
 static int launch_gemm(const GemmParams& p, hipStream_t s) {
     if (p.Mout == 0 || p.Nout == 0) return ANE_OK;
+    if (BL == kBTransposed && !AU8 && tile256_eligible(p)) return launch_gemm_tile256(p, s);
     dim3 grid((p.Nout + kBN - 1) / kBN, (p.Mout + kBM - 1) / kBM);
     if (grid.y > 65535) return ANE_ERR_INVALID_ARG;
     hipLaunchKernelGGL((k_gemm_i8<BL, AU8>), grid, dim3(kGThreads), 0, s, p);
@@ -370,7 +354,9 @@ extern "C" int ane_hip_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int
     return launch_gemm<kBTransposed, false>(p, (hipStream_t)stream);
 }
 
-static uint64_t fused_kp(int32_t K) { return ceil_to((uint64_t)(K > 0 ? K : 0), 16); }
+// The fused operands are laid out with K padded (zeros) to a multiple of 128
+// so both contraction kernels run whole 128-byte K slices.
+static uint64_t fused_kp(int32_t K) { return ceil_to((uint64_t)(K > 0 ? K : 0), 128); }
 
 extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K) {
     if (M < 0 || N < 0 || K < 0) return 0;

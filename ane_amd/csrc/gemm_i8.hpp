@@ -1,0 +1,33 @@
+// gemm_i8.hpp -- parameters shared by the int8 contraction kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace ane {
+
+struct GemmParams {
+    const int8_t* A;      // row-major, K contiguous
+    uint64_t lda;         // bytes between rows of A
+    const int8_t* B;      // Bt (N x K, K contiguous) or SMOPA panels
+    uint64_t ldb;         // Bt: bytes between rows; panel: groups per panel (G)
+    uint32_t rowsA;       // rows of A that may be read (others read as 0)
+    uint32_t colsB;       // columns of B that may be read (others read as 0)
+    uint32_t Kp;          // contraction length, multiple of 16
+    uint32_t Mout, Nout;  // output rows / columns written
+    float s;              // epilogue multiplier (when sdev == nullptr)
+    const float* sdev;    // device {sa, sb}: s = (sa*sb)*smul
+    float smul;
+    const float* bias;    // fp32[Nout] or nullptr (adds +0.0f)
+    float lo;             // ReLU floor: +0 or -FLT_MAX
+    float* C;             // fp32 output, row stride ldc
+    uint64_t ldc;
+    int32_t* Craw;        // raw int32 output instead (debug entry)
+};
+
+// 256 x 256 tile kernel (gemm_i8_tile256.hip): Bt layout, signed A, whole
+// 128-byte K slices, 16-byte aligned rows, and enough rows/columns to fill
+// 256-wide tiles reasonably.
+bool tile256_eligible(const GemmParams& p);
+int launch_gemm_tile256(const GemmParams& p, hipStream_t s);
+
+}  // namespace ane

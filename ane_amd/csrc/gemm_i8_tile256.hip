@@ -1,0 +1,369 @@
+// gemm_i8_tile256.hip -- the large-shape int8 contraction of dense_fused_i8
+// (and gemm_s8_i32): C[M x N] = epilogue(A[M x K] . Bt[N x K]^T), both
+// operands int8 row-major with K contiguous.
+//
+// Design (gfx950, one workgroup per CU):
+//  * 256 x 256 output tile.  NW waves (4 or 8) in a (NW/2) x 2 grid; a wave
+//    owns (256*2/NW) x 128 outputs = FM x 4 v_mfma_i32_32x32x32_i8
+//    accumulator blocks.  With 8 waves two share each SIMD, so one wave's
+//    barrier or LDS wait is covered by the other's MFMAs.
+//  * K advances in 64-byte slices through a 4-stage LDS ring (4 x 32 KB).
+//    Slice kt is computed from stage kt%4 while slices kt+1 and kt+2 are in
+//    flight; slice kt+2 goes into the stage of slice kt-2, which every wave
+//    finished reading before the barrier that preceded the last k-step of
+//    slice kt-1.  Slices are copied with buffer_load_dwordx4 ... lds (direct
+//    global -> LDS, no VGPR staging; rows past the operand's end and the
+//    out-of-range tail slices read as zeros through the buffer resource's
+//    range check, so every slice issues the same number of copies).  The
+//    copies are spread over the MFMAs so the vector-memory queue never
+//    stalls MFMA issue.
+//  * Synchronisation is s_waitcnt vmcnt + a bare s_barrier.  __syncthreads()
+//    would add a release fence, i.e. vmcnt(0), draining the slices that are
+//    meant to stay in flight.  The barrier for slice kt+1 is taken before the
+//    last k-step of slice kt, whose MFMAs then cover the LDS reads of slice
+//    kt+1's first fragments.
+//  * LDS layout per stage: [256 rows][64 bytes] for A then for Bt; the
+//    16-byte chunk c of row r sits in slot c ^ ((r ^ r>>2) & 3).  A
+//    ds_read_b128 serves 16 lanes (16 consecutive rows, same chunk) per LDS
+//    cycle (64 banks x 4 bytes); the swizzle gives them 16 distinct bank
+//    groups.  Each copy wave-instruction writes 1 KB of consecutive LDS, so
+//    the swizzle is applied on the global side.
+//  * Tiles are assigned XCD-major: dispatch round-robins workgroups over the
+//    8 XCDs, so workgroup w is remapped to logical tile (w%8)*(T/8) + w/8 and
+//    each XCD's L2 sees a compact 4 x 8 block of tiles.
+//  * Epilogue: fmaxA(fadd(fmul((float)acc, s), bias), lo), one rounding per
+//    operation, staged through LDS so each wave stores whole 512-byte row
+//    segments with 16-byte stores.
+#include "gemm_i8.hpp"
+
+namespace ane {
+namespace {
+
+#ifndef ANE_TILE256_WAVES
+#define ANE_TILE256_WAVES 8
+#endif
+
+constexpr int TM = 256, TN = 256;
+constexpr int TK = 64;                        // bytes of K per slice
+constexpr int STAGES = 4;                     // LDS ring depth
+constexpr int NW = ANE_TILE256_WAVES;         // waves per workgroup
+constexpr int kThreads = NW * 64;
+constexpr int WM = NW / 2;                    // waves along M
+constexpr int FM = TM / (WM * 32);            // 32x32 MFMA blocks per wave along M
+constexpr int FN = 4;                         // ... along N (wave spans 128 columns)
+constexpr int kChunks = TK / 16;              // 16-byte chunks per row
+constexpr int kStageA = TM * TK;
+constexpr int kStageB = TN * TK;
+constexpr int kStage = kStageA + kStageB;
+constexpr int kLdsBytes = STAGES * kStage;
+constexpr int kRowsPerDma = 1024 / TK;        // rows covered by one copy wave-instruction
+constexpr int kRowsPerWave = TM / NW;         // rows of A (and of Bt) each wave copies
+constexpr int kDmaPerWave = kRowsPerWave / kRowsPerDma;
+constexpr int kSteps = TK / 32;
+constexpr int kDmaPerStep = 2 * kDmaPerWave / kSteps;
+static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+static_assert(kLdsBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
+static_assert(kSteps % 2 == 0, "fragment double-buffering needs an even k-step count");
+static_assert(kDmaPerStep * kSteps == 2 * kDmaPerWave, "copies must split evenly over k-steps");
+// Epilogue staging: per wave EPR rows x 128 fp32 per pass, rows padded to
+// 544 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
+// store land in different bank halves).
+constexpr int kEpiRowBytes = 544;
+constexpr int EPR = NW == 4 ? 32 : 16;
+constexpr int kEpiWaveBytes = EPR * kEpiRowBytes;
+static_assert(NW * kEpiWaveBytes <= kLdsBytes, "epilogue staging does not fit");
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ uint32_t swz_g(uint32_t row) { return (row ^ (row >> 2)) & 3; }
+__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
+    return row * TK + ((chunk ^ swz_g(row)) << 4);
+}
+
+// Raw buffer resource over [base, base + bytes): loads past `bytes` return
+// zeros (checked per dword).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt with vmcnt = n and the LDS/export counters left unconstrained;
+// the "memory" clobber keeps the compiler from moving LDS reads across it.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt out of range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// Workgroup barrier without the release fence of __syncthreads() (see the
+// file comment).  LDS is coherent within the workgroup, so a wave's
+// completed copies (its vmcnt wait) plus s_barrier make them visible.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt lgkmcnt(0) only (LDS and scalar memory), leaving stores in flight.
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// One slice copy: wave w copies rows [w*kRowsPerWave, (w+1)*kRowsPerWave)
+// of the tile's A rows and of its Bt rows; wave-instruction i covers
+// kRowsPerDma rows (1 KB of consecutive LDS).  `live` false sends every lane
+// out of range: the copy then writes zeros without touching memory.
+struct SliceCopy {
+    __amdgpu_buffer_rsrc_t ra, rb;
+    int8_t* stage;
+    uint32_t wave, k0;
+    bool live;
+};
+
+template <int first, int count>
+__device__ __forceinline__ void issue_part(const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
+                                           const uint32_t (&offB)[kDmaPerWave]) {
+#pragma unroll
+    for (int d = first; d < first + count; d++) {
+        const int i = d % kDmaPerWave;
+        const bool isB = d >= kDmaPerWave;
+        int8_t* dst = c.stage + (c.wave * kRowsPerWave + i * kRowsPerDma) * TK + (isB ? kStageA : 0);
+        const uint32_t o = c.live ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isB ? c.rb : c.ra, (lds_ptr_t)dst, 16, o, 0, 0, 0);
+    }
+}
+
+struct Frags {
+    v4i a[FM], b[FN];
+};
+
+__device__ __forceinline__ void load_frags(const int8_t* stage, uint32_t rA, uint32_t rB,
+                                           uint32_t chunk, Frags& f) {
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++)
+        f.a[mi] = *reinterpret_cast<const v4i*>(stage + swz(rA + mi * 32, chunk));
+#pragma unroll
+    for (int ni = 0; ni < FN; ni++)
+        f.b[ni] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(rB + ni * 32, chunk));
+}
+
+__device__ __forceinline__ void mfmas(v16i (&acc)[FM][FN], const Frags& f) {
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+        for (int ni = 0; ni < FN; ni++)
+            acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+}
+
+// The MFMAs of one k-step with the LDS reads of the next k-step's fragments
+// and this k-step's share of slice copies spread between them;
+// sched_barrier keeps k-steps in order so consecutive MFMAs never
+// accumulate into the same registers.
+template <int ks>
+__device__ __forceinline__ void kstep(v16i (&acc)[FM][FN], const Frags& cur, Frags& nxt,
+                                      const int8_t* src, uint32_t rA, uint32_t rB, uint32_t chunk,
+                                      const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
+                                      const uint32_t (&offB)[kDmaPerWave]) {
+    constexpr int nM = FM * FN, nD = FM + FN, nV = kDmaPerStep;
+    load_frags(src, rA, rB, chunk, nxt);
+    issue_part<ks * kDmaPerStep, kDmaPerStep>(c, offA, offB);
+    mfmas(acc, cur);
+#pragma unroll
+    for (int i = 0; i < nM; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // 1 MFMA
+        if (i < nD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // 1 LDS read
+        if ((i * nV) / nM != ((i + 1) * nV) / nM)
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);               // 1 slice copy
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// One slice: its first k-step's fragments are in f0 (prefetched during the
+// previous slice).  Before the last k-step, `boundary()` makes the next
+// slice visible (copy wait + barrier); the last k-step then prefetches the
+// next slice's first fragments from `next_stage` into f0.
+template <int ks, typename Boundary>
+__device__ __forceinline__ void ksteps(v16i (&acc)[FM][FN], Frags& f0, Frags& f1, const int8_t* stage,
+                                       const int8_t* next_stage, uint32_t rA, uint32_t rB,
+                                       uint32_t chalf, const SliceCopy& c,
+                                       const uint32_t (&offA)[kDmaPerWave],
+                                       const uint32_t (&offB)[kDmaPerWave], Boundary boundary) {
+    if constexpr (ks < kSteps) {
+        constexpr bool last = ks + 1 == kSteps;
+        if constexpr (last) boundary();
+        const int8_t* src = last ? next_stage : stage;
+        const uint32_t chunk = last ? chalf : 2 * (ks + 1) + chalf;
+        if constexpr (ks % 2 == 0)
+            kstep<ks>(acc, f0, f1, src, rA, rB, chunk, c, offA, offB);
+        else
+            kstep<ks>(acc, f1, f0, src, rA, rB, chunk, c, offA, offB);
+        ksteps<ks + 1>(acc, f0, f1, stage, next_stage, rA, rB, chalf, c, offA, offB, boundary);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kLdsBytes];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // XCD-major tile order, then groups of 4 tile-rows.
+    const uint32_t total = tiles_m * tiles_n;
+    const uint32_t wg = blockIdx.x;
+    uint32_t logical = wg;
+    if ((total & 7) == 0) logical = (wg & 7) * (total >> 3) + (wg >> 3);
+    constexpr uint32_t GM = 4;
+    const uint32_t per_group = GM * tiles_n;
+    const uint32_t group = logical / per_group;
+    const uint32_t first_m = group * GM;
+    const uint32_t gm = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
+    const uint32_t in = logical % per_group;
+    const uint32_t row0 = (first_m + in % gm) * TM;
+    const uint32_t col0 = (in / gm) * TN;
+
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.rowsA * p.lda));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(p.colsB * p.ldb));
+    uint32_t offA[kDmaPerWave], offB[kDmaPerWave];
+    {
+        // lane l fills slot l % kChunks of row wave*kRowsPerWave + i*kRowsPerDma + l/kChunks
+        const uint32_t r = wave * kRowsPerWave + lane / kChunks;
+#pragma unroll
+        for (int i = 0; i < kDmaPerWave; i++) {
+            const uint32_t row = r + i * kRowsPerDma;
+            const uint32_t chunk = (lane % kChunks) ^ swz_g(row);
+            offA[i] = (row0 + row) * (uint32_t)p.lda + chunk * 16;
+            offB[i] = (col0 + row) * (uint32_t)p.ldb + chunk * 16;
+        }
+    }
+
+    const uint32_t wr0 = (wave >> 1) * (FM * 32);
+    const uint32_t wc0 = (wave & 1) * (FN * 32);
+    const uint32_t rA = wr0 + (lane & 31);
+    const uint32_t rB = wc0 + (lane & 31);
+    const uint32_t chalf = lane >> 5;
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    const uint32_t nk = p.Kp / TK;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const SliceCopy c{ra, rb, smem + s * kStage, wave, (uint32_t)s * TK, (uint32_t)s < nk};
+        issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
+    }
+    Frags f0, f1;
+    wait_vmcnt<2 * kDmaPerWave>();  // slice 0 landed (slice 1 may be in flight)
+    lds_barrier();
+    load_frags(smem, rA, rB, chalf, f0);
+
+    uint32_t st = 0;
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t st1 = st + 1 == STAGES ? 0 : st + 1;
+        const uint32_t st2 = st1 + 1 == STAGES ? 0 : st1 + 1;
+        const uint32_t k2 = kt + 2;
+        const SliceCopy c{ra, rb, smem + st2 * kStage, wave, k2 * TK, k2 < nk};
+        const bool more = kt + 1 < nk;
+        auto boundary = [&]() {
+            if (more) {
+                // slice kt+1 landed for this wave: the only younger copies are
+                // the ones of slice kt+2 issued in this slice's earlier k-steps
+                wait_vmcnt<(kSteps - 1) * kDmaPerStep>();
+                lds_barrier();
+            }
+        };
+        ksteps<0>(acc, f0, f1, smem + st * kStage, smem + (more ? st1 : st) * kStage, rA, rB, chalf,
+                  c, offA, offB, boundary);
+        st = st1;
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // all fragment reads done: the ring becomes epilogue staging
+
+    float s = p.s;
+    if (p.sdev) s = __fmul_rn(__fmul_rn(p.sdev[0], p.sdev[1]), p.smul);
+    float bj[FN];
+#pragma unroll
+    for (int ni = 0; ni < FN; ni++) {
+        const uint32_t j = col0 + wc0 + ni * 32 + (lane & 31);
+        bj[ni] = (p.bias && j < p.Nout) ? p.bias[j] : 0.0f;
+    }
+    int8_t* epi = smem + wave * kEpiWaveBytes;
+    const bool vec_ok =
+        (((uintptr_t)(p.Craw ? (void*)p.Craw : (void*)p.C)) & 15) == 0 && (p.ldc & 3) == 0;
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++) {
+#pragma unroll
+        for (int h = 0; h < 32 / EPR; h++) {
+            // rows [h*EPR, (h+1)*EPR) of the 32-row block mi -> LDS.  Lane l,
+            // register r of a 32x32 MFMA block holds row 8(r/4) + 4(l/32) +
+            // r%4, column l%32.
+#pragma unroll
+            for (int ni = 0; ni < FN; ni++) {
+#pragma unroll
+                for (int r = h * EPR / 2; r < (h + 1) * EPR / 2; r++) {
+                    const uint32_t lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) - h * EPR;
+                    const uint32_t lc = ni * 32 + (lane & 31);
+                    uint32_t bitsv;
+                    if (p.Craw) {
+                        bitsv = (uint32_t)acc[mi][ni][r];
+                    } else {
+                        const float f = __fadd_rn(__fmul_rn((float)acc[mi][ni][r], s), bj[ni]);
+                        bitsv = __float_as_uint(fmax_a(f, p.lo));
+                    }
+                    *reinterpret_cast<uint32_t*>(epi + lr * kEpiRowBytes + lc * 4) = bitsv;
+                }
+            }
+            wait_lgkmcnt0();
+            __builtin_amdgcn_wave_barrier();
+            // 16 B per lane: half-wave hw stores staged row 2q+hw, columns 4*(lane&31)..+3
+#pragma unroll
+            for (int q = 0; q < EPR / 2; q++) {
+                const uint32_t lr = 2 * q + (lane >> 5);
+                const uint32_t lc = 4 * (lane & 31);
+                const v4i v = *reinterpret_cast<const v4i*>(epi + lr * kEpiRowBytes + lc * 4);
+                const uint32_t i = row0 + wr0 + mi * 32 + h * EPR + lr;
+                const uint32_t j = col0 + wc0 + lc;
+                if (i >= p.Mout) continue;
+                uint32_t* dst = p.Craw ? reinterpret_cast<uint32_t*>(p.Craw) + (uint64_t)i * p.ldc + j
+                                       : reinterpret_cast<uint32_t*>(p.C) + (uint64_t)i * p.ldc + j;
+                if (vec_ok && j + 3 < p.Nout) {
+                    *reinterpret_cast<v4i*>(dst) = v;
+                } else {
+                    if (j + 0 < p.Nout) dst[0] = (uint32_t)v.x;
+                    if (j + 1 < p.Nout) dst[1] = (uint32_t)v.y;
+                    if (j + 2 < p.Nout) dst[2] = (uint32_t)v.z;
+                    if (j + 3 < p.Nout) dst[3] = (uint32_t)v.w;
+                }
+            }
+            wait_lgkmcnt0();  // staging reads done before the next pass overwrites them;
+            __builtin_amdgcn_wave_barrier();  // the global stores keep draining
+        }
+    }
+}
+
+}  // namespace
+
+bool tile256_eligible(const GemmParams& p) {
+    if (p.Mout < TM || p.Nout < TN) return false;
+    if (p.Kp == 0 || (p.Kp % TK) != 0) return false;
+    if ((p.lda & 15) || (p.ldb & 15)) return false;
+    if ((((uintptr_t)p.A) & 15) || (((uintptr_t)p.B) & 15)) return false;
+    if (p.rowsA < p.Mout || p.colsB < p.Nout) return false;
+    // buffer offsets are 32-bit and 0x80000000 marks an empty copy: every
+    // row of every tile, in range or not, stays below it
+    const uint64_t rows_a = ceil_to(p.Mout, TM) + TM, rows_b = ceil_to(p.Nout, TN) + TN;
+    if (rows_a * p.lda + p.Kp >= (1ull << 31) || rows_b * p.ldb + p.Kp >= (1ull << 31)) return false;
+    return true;
+}
+
+int launch_gemm_tile256(const GemmParams& p, hipStream_t s) {
+    const uint32_t tiles_m = (p.Mout + TM - 1) / TM;
+    const uint32_t tiles_n = (p.Nout + TN - 1) / TN;
+    const uint64_t total = (uint64_t)tiles_m * tiles_n;
+    if (total > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_gemm_i8_tile256, dim3((uint32_t)total), dim3(kThreads), 0, s, p, tiles_m,
+                       tiles_n);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+}  // namespace ane

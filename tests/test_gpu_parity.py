@@ -48,7 +48,10 @@ def assert_f32_identical(got, want):
 
 # ---------------------------------------------------------------- MFMA core
 @pytest.mark.parametrize("M,N,K", [(1, 1, 16), (32, 32, 32), (50, 130, 784), (128, 128, 128),
-                                   (300, 200, 1008), (257, 129, 4096), (64, 512, 48)])
+                                   (300, 200, 1008), (257, 129, 4096), (64, 512, 48),
+                                   # 256 x 256 tile kernel: full, partial and odd tile grids
+                                   (256, 256, 128), (1000, 600, 896), (513, 257, 4096),
+                                   (2048, 1536, 256), (768, 2304, 1152)])
 def test_gemm_s8_i32_exact(ane, M, N, K):
     import torch
 
@@ -262,7 +265,8 @@ def test_dense_fused_mnist_mlp(ane, oracle):
 
 @pytest.mark.parametrize("M,N,K,relu,scale", [(3, 5, 7, True, 1.0), (64, 64, 1, False, 2.5),
                                               (1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0),
-                                              (129, 257, 1000, False, 0.75), (7, 9, 0, True, 1.0)])
+                                              (129, 257, 1000, False, 0.75), (7, 9, 0, True, 1.0),
+                                              (300, 700, 333, True, 1.0), (1024, 512, 4096, False, 1.0)])
 def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
     A, B = data.gemm_inputs(M, N, K, seed=M + N + K)
     ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
