@@ -158,130 +158,6 @@ k_gemm_i8(GemmParams p) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// dense_fused_i8 operand preparation.
-
-constexpr uint32_t kFusedPartials = 1024;
-
-// Pass 1 over both tensors: blocks [0, nbA) reduce A, [nbA, nbA+nbB) reduce B.
-__global__ void __launch_bounds__(256)
-k_absmax_two(const float* __restrict__ A, uint64_t nA, uint32_t nbA,
-             const float* __restrict__ B, uint64_t nB, uint32_t nbB,
-             uint32_t* __restrict__ partials) {
-    __shared__ uint32_t red[4];
-    const bool isA = blockIdx.x < nbA;
-    const float* src = isA ? A : B;
-    const uint64_t n = isA ? nA : nB;
-    const uint32_t b = isA ? blockIdx.x : blockIdx.x - nbA;
-    const uint32_t nbk = isA ? nbA : nbB;
-    const uint64_t tid = (uint64_t)b * 256 + threadIdx.x;
-    const uint64_t stride = (uint64_t)nbk * 256;
-    uint32_t m = 0;
-    uint64_t head = 0;
-    if ((((uintptr_t)src) & 15) == 0) {
-        const uint64_t n4 = n >> 2;
-        const float4* s4 = reinterpret_cast<const float4*>(src);
-        for (uint64_t i = tid; i < n4; i += stride) {
-            float4 v = s4[i];
-            uint32_t a = abs_key(v.x), c = abs_key(v.y), d = abs_key(v.z), e = abs_key(v.w);
-            a = a > c ? a : c;
-            d = d > e ? d : e;
-            a = a > d ? a : d;
-            m = m > a ? m : a;
-        }
-        head = n4 << 2;
-    }
-    for (uint64_t i = head + tid; i < n; i += stride) {
-        uint32_t a = abs_key(src[i]);
-        m = m > a ? m : a;
-    }
-    m = block_max_u32_256(m, red);
-    if (threadIdx.x == 0) partials[blockIdx.x] = m;
-}
-
-__device__ __forceinline__ float fold_partials(const uint32_t* partials, uint32_t n,
-                                               uint32_t* red) {
-    uint32_t m = 0;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) {
-        uint32_t a = partials[i];
-        m = m > a ? m : a;
-    }
-    return __uint_as_float(block_max_u32_256(m, red));
-}
-
-// Pass 2: blocks [0, nqA) quantize A row-major into qA (M x Kp, zero k-pad);
-// blocks [nqA, ...) quantize 64 x 64 tiles of B transposed into qBt (N x Kp).
-__global__ void __launch_bounds__(256)
-k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_t M,
-               uint32_t N, uint32_t K, uint32_t Kp, const uint32_t* __restrict__ partials,
-               uint32_t nbA, uint32_t nbB, uint32_t nqA, int8_t* __restrict__ qA,
-               int8_t* __restrict__ qBt, float* __restrict__ scales) {
-    __shared__ uint32_t red[4];
-    __shared__ int8_t tileT[64][64 + 4];
-    const bool isA = blockIdx.x < nqA;
-    const float amax = isA ? fold_partials(partials, nbA, red)
-                           : fold_partials(partials + nbA, nbB, red);
-    float scale, inv;
-    quant_params(amax, scale, inv);
-    if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == nqA)) scales[isA ? 0 : 1] = scale;
-
-    if (isA) {
-        // 16 output bytes per thread; chunk index over M x (Kp/16).
-        const uint64_t chunks_per_row = Kp / 16;
-        const uint64_t total = (uint64_t)M * chunks_per_row;
-        const bool vec = ((K & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
-        for (uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x; c < total;
-             c += (uint64_t)nqA * 256) {
-            const uint64_t i = c / chunks_per_row;
-            const uint32_t k = (uint32_t)(c % chunks_per_row) * 16;
-            const float* src = A + i * K + k;
-            uint32_t w[4] = {0, 0, 0, 0};
-            if (vec && k + 16 <= K) {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float4 v = reinterpret_cast<const float4*>(src)[q];
-                    w[q] = (uint32_t)(quant1(v.x, inv) & 0xff) |
-                           ((uint32_t)(quant1(v.y, inv) & 0xff) << 8) |
-                           ((uint32_t)(quant1(v.z, inv) & 0xff) << 16) |
-                           ((uint32_t)(quant1(v.w, inv) & 0xff) << 24);
-                }
-            } else {
-                for (int e = 0; e < 16; e++)
-                    if (k + e < K) w[e >> 2] |= (uint32_t)(quant1(src[e], inv) & 0xff) << (8 * (e & 3));
-            }
-            *reinterpret_cast<uint4*>(qA + i * Kp + k) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-        return;
-    }
-    // B tile (k0, n0) of 64 x 64: read rows of B, write rows of qBt.
-    const uint32_t tb = blockIdx.x - nqA;
-    const uint32_t ntn = (N + 63) / 64;
-    const uint32_t k0 = (tb / ntn) * 64, n0 = (tb % ntn) * 64;
-    {
-        const uint32_t kk = threadIdx.x >> 2, nn = (threadIdx.x & 3) * 16;
-        const uint32_t gk = k0 + kk;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const uint32_t gn = n0 + nn + e;
-            int q = 0;
-            if (gk < K && gn < N) q = quant1(B[(uint64_t)gk * N + gn], inv);
-            tileT[nn + e][kk] = (int8_t)q;
-        }
-    }
-    __syncthreads();
-    {
-        const uint32_t nn = threadIdx.x >> 2, kc = (threadIdx.x & 3) * 16;
-        const uint32_t gn = n0 + nn, gk = k0 + kc;
-        if (gn < N && gk < Kp) {
-            uint32_t w[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                w[q] = *reinterpret_cast<const uint32_t*>(&tileT[nn][kc + 4 * q]);
-            *reinterpret_cast<uint4*>(qBt + (uint64_t)gn * Kp + gk) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-    }
-}
-
 template <int BL, bool AU8>
 static int launch_gemm(const GemmParams& p, hipStream_t s) {
     if (p.Mout == 0 || p.Nout == 0) return ANE_OK;
@@ -368,12 +244,6 @@ extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, in
     return (size_t)bytes;
 }
 
-static uint32_t fused_blocks(uint64_t n) {
-    uint64_t b = (n / 4 + 1024 - 1) / 1024;
-    if (b < 1) b = 1;
-    if (b > kFusedPartials) b = kFusedPartials;
-    return (uint32_t)b;
-}
 
 struct FusedLayout {
     uint64_t Kp;
@@ -412,25 +282,9 @@ extern "C" int ane_hip_dense_fused_i8_quantize(int32_t M, int32_t N, int32_t K, 
     hipStream_t s = (hipStream_t)stream;
     const FusedLayout L = fused_layout(M, K, workspace);
     const uint64_t Kp = L.Kp;
-    const uint64_t nA = (uint64_t)M * (uint64_t)K, nB = (uint64_t)K * (uint64_t)N;
-    const uint32_t nbA = fused_blocks(nA), nbB = fused_blocks(nB);
-    hipLaunchKernelGGL(k_absmax_two, dim3(nbA + nbB), dim3(256), 0, s, A, nA, nbA, B, nB, nbB,
-                       L.partials);
-    uint64_t nqA = ((uint64_t)M * (Kp / 16) + 255) / 256;
-    if (nqA > 2048) nqA = 2048;
-    if (nqA < 1) nqA = 1;
-    const uint64_t nqB = ((Kp + 63) / 64) * (((uint64_t)N + 63) / 64);
-    if (Kp > 0) {
-        if (nqA + nqB > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
-        hipLaunchKernelGGL(k_quantize_two, dim3((uint32_t)(nqA + nqB)), dim3(256), 0, s, A, B,
-                           (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, L.partials, nbA, nbB,
-                           (uint32_t)nqA, L.qA, L.qBt, L.scales);
-    } else {
-        // K == 0: no operands to quantize; both scales are 1 (zero guard).
-        hipLaunchKernelGGL(k_quantize_two, dim3(2), dim3(256), 0, s, A, B, (uint32_t)M, (uint32_t)N,
-                           0u, 0u, L.partials, nbA, nbB, 1u, L.qA, L.qBt, L.scales);
-    }
-    ANE_HIP_CHECK_LAUNCH();
+    st = launch_fused_quantize(A, B, (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, L.partials,
+                               L.qA, L.qBt, L.scales, s);
+    if (st != ANE_OK) return st;
     if (scales_out) {
         hipError_t e = hipMemcpyAsync(scales_out, L.scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return ANE_ERR_HIP;

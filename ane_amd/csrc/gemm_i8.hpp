@@ -24,6 +24,13 @@ struct GemmParams {
     int32_t* Craw;        // raw int32 output instead (debug entry)
 };
 
+// dense_fused_i8 operand preparation (quantize_fused.hip): absmax partials
+// (kFusedPartials per tensor), qA (M x Kp), qBt (N x Kp), scales {sa, sb}.
+constexpr uint32_t kFusedPartials = 1024;
+int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
+                          uint32_t Kp, uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales,
+                          hipStream_t s);
+
 // 256 x 256 tile kernel (gemm_i8_tile256.hip): Bt layout, signed A, whole
 // 128-byte K slices, 16-byte aligned rows, and enough rows/columns to fill
 // 256-wide tiles reasonably.

@@ -3,10 +3,10 @@
 // operands int8 row-major with K contiguous.
 //
 // Design (gfx950, one workgroup per CU):
-//  * 256 x 256 output tile.  NW waves (4 or 8) in a (NW/2) x 2 grid; a wave
-//    owns (256*2/NW) x 128 outputs = FM x 4 v_mfma_i32_32x32x32_i8
-//    accumulator blocks.  With 8 waves two share each SIMD, so one wave's
-//    barrier or LDS wait is covered by the other's MFMAs.
+//  * 256 x 256 output tile.  NW waves (4, 8 or 16) in a WM x WN grid; a
+//    wave owns FM x FN blocks of v_mfma_i32_32x32x32_i8 accumulators.  With
+//    8 or 16 waves, 2 or 4 share each SIMD, so one wave's barrier or LDS
+//    wait is covered by the others' MFMAs.
 //  * K advances in 64-byte slices through a 4-stage LDS ring (4 x 32 KB).
 //    Slice kt is computed from stage kt%4 while slices kt+1 and kt+2 are in
 //    flight; slice kt+2 goes into the stage of slice kt-2, which every wave
@@ -32,8 +32,8 @@
 //    8 XCDs, so workgroup w is remapped to logical tile (w%8)*(T/8) + w/8 and
 //    each XCD's L2 sees a compact 4 x 8 block of tiles.
 //  * Epilogue: fmaxA(fadd(fmul((float)acc, s), bias), lo), one rounding per
-//    operation, staged through LDS so each wave stores whole 512-byte row
-//    segments with 16-byte stores.
+//    operation, staged through LDS so each wave stores whole row segments
+//    with 16-byte stores.
 #include "gemm_i8.hpp"
 
 namespace ane {
@@ -48,9 +48,10 @@ constexpr int TK = 64;                        // bytes of K per slice
 constexpr int STAGES = 4;                     // LDS ring depth
 constexpr int NW = ANE_TILE256_WAVES;         // waves per workgroup
 constexpr int kThreads = NW * 64;
-constexpr int WM = NW / 2;                    // waves along M
+constexpr int WN = NW == 16 ? 4 : 2;          // waves along N
+constexpr int WM = NW / WN;                   // waves along M
 constexpr int FM = TM / (WM * 32);            // 32x32 MFMA blocks per wave along M
-constexpr int FN = 4;                         // ... along N (wave spans 128 columns)
+constexpr int FN = TN / (WN * 32);            // ... along N
 constexpr int kChunks = TK / 16;              // 16-byte chunks per row
 constexpr int kStageA = TM * TK;
 constexpr int kStageB = TN * TK;
@@ -61,15 +62,18 @@ constexpr int kRowsPerWave = TM / NW;         // rows of A (and of Bt) each wave
 constexpr int kDmaPerWave = kRowsPerWave / kRowsPerDma;
 constexpr int kSteps = TK / 32;
 constexpr int kDmaPerStep = 2 * kDmaPerWave / kSteps;
-static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
 static_assert(kLdsBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
 static_assert(kSteps % 2 == 0, "fragment double-buffering needs an even k-step count");
 static_assert(kDmaPerStep * kSteps == 2 * kDmaPerWave, "copies must split evenly over k-steps");
-// Epilogue staging: per wave EPR rows x 128 fp32 per pass, rows padded to
-// 544 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
-// store land in different bank halves).
-constexpr int kEpiRowBytes = 544;
+// Epilogue staging: per wave EPR rows x (FN*32) fp32 per pass, rows padded
+// by 32 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
+// staging write land in different bank halves).
+constexpr int kEpiCols = FN * 32;
+constexpr int kEpiRowBytes = kEpiCols * 4 + 32;
 constexpr int EPR = NW == 4 ? 32 : 16;
+constexpr int kLanesPerRow = kEpiCols / 4;     // 16-byte stores per staged row
+constexpr int kRowsPerStore = 64 / kLanesPerRow;
 constexpr int kEpiWaveBytes = EPR * kEpiRowBytes;
 static_assert(NW * kEpiWaveBytes <= kLdsBytes, "epilogue staging does not fit");
 
@@ -231,8 +235,8 @@ k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
         }
     }
 
-    const uint32_t wr0 = (wave >> 1) * (FM * 32);
-    const uint32_t wc0 = (wave & 1) * (FN * 32);
+    const uint32_t wr0 = (wave / WN) * (FM * 32);
+    const uint32_t wc0 = (wave % WN) * (FN * 32);
     const uint32_t rA = wr0 + (lane & 31);
     const uint32_t rB = wc0 + (lane & 31);
     const uint32_t chalf = lane >> 5;
@@ -314,11 +318,11 @@ k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
             }
             wait_lgkmcnt0();
             __builtin_amdgcn_wave_barrier();
-            // 16 B per lane: half-wave hw stores staged row 2q+hw, columns 4*(lane&31)..+3
+            // 16 B per lane: kLanesPerRow lanes cover one staged row
 #pragma unroll
-            for (int q = 0; q < EPR / 2; q++) {
-                const uint32_t lr = 2 * q + (lane >> 5);
-                const uint32_t lc = 4 * (lane & 31);
+            for (int q = 0; q < EPR / kRowsPerStore; q++) {
+                const uint32_t lr = kRowsPerStore * q + lane / kLanesPerRow;
+                const uint32_t lc = 4 * (lane % kLanesPerRow);
                 const v4i v = *reinterpret_cast<const v4i*>(epi + lr * kEpiRowBytes + lc * 4);
                 const uint32_t i = row0 + wr0 + mi * 32 + h * EPR + lr;
                 const uint32_t j = col0 + wc0 + lc;
