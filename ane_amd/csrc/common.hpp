@@ -86,6 +86,89 @@ __host__ __device__ inline uint64_t ceil_to(uint64_t x, uint64_t m) {
     return (x + m - 1) / m * m;
 }
 
+// ------------------------------------------------- DPP row permutations
+// v_mov_b32 with a DPP control: every lane reads the named lane of its own
+// 16-lane row (all rows and banks enabled, so every source is valid).
+enum : int {
+    kDppQuadXor1 = 0xB1,    // quad_perm [1,0,3,2]: lane ^ 1
+    kDppQuadXor2 = 0x4E,    // quad_perm [2,3,0,1]: lane ^ 2
+    kDppHalfMirror = 0x141, // lane i <-> 7-i within each 8 lanes
+    kDppRowMirror = 0x140,  // lane i <-> 15-i within each 16 lanes
+};
+
+template <int ctrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xf, 0xf, false);
+}
+template <int ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
+// SVE FADDV over 16 lanes (bytecode_interpreter.s:7059): the pairwise tree
+// ((((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)))+(((a8+a9)+...))).  Each step adds
+// the partner group's partial; after step k all lanes of a 2^k-group hold
+// bit-identical values (fp32 addition is commutative), so pairing lane i
+// with its mirror instead of i ^ 4 / i ^ 8 forms the same sums.  Every lane
+// of the 16-lane row ends with the full sum.
+__device__ __forceinline__ float faddv16(float v) {
+    v = v + dpp_f32<kDppQuadXor1>(v);
+    v = v + dpp_f32<kDppQuadXor2>(v);
+    v = v + dpp_f32<kDppHalfMirror>(v);
+    v = v + dpp_f32<kDppRowMirror>(v);
+    return v;
+}
+
+// max over each aligned group of 8 lanes.
+__device__ __forceinline__ uint32_t max8_u32(uint32_t m) {
+    uint32_t o = dpp_u32<kDppQuadXor1>(m);
+    m = m > o ? m : o;
+    o = dpp_u32<kDppQuadXor2>(m);
+    m = m > o ? m : o;
+    o = dpp_u32<kDppHalfMirror>(m);
+    return m > o ? m : o;
+}
+
+// Four quantized values packed little-endian into one dword.
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
+    return (uint32_t)(quant1(a, inv) & 0xff) | ((uint32_t)(quant1(b, inv) & 0xff) << 8) |
+           ((uint32_t)(quant1(c, inv) & 0xff) << 16) | ((uint32_t)(quant1(d, inv) & 0xff) << 24);
+}
+
+// ----------------------------------------------------------- LDS copy helpers
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Raw buffer resource over [base, base + bytes): loads past `bytes` return
+// zeros (checked per dword) without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// One buffer_load_dwordx4 ... lds: lane l's 16 bytes at `voffset` land at
+// LDS dst + 16*l (dst must be wave-uniform).
+__device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voffset, 0, 0, 0);
+}
+
+// s_waitcnt with vmcnt = n and the LDS/export counters left unconstrained;
+// the "memory" clobber keeps the compiler from moving LDS reads across it.
+// Vector-memory loads (including copies to LDS) complete in issue order.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt out of range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// Workgroup barrier without the release fence of __syncthreads(), which
+// would wait for every outstanding vector-memory operation (vmcnt(0)) and
+// so drain copies that are meant to stay in flight.  LDS is coherent within
+// the workgroup: a wave's completed copies (its vmcnt wait) or LDS writes
+// (its lgkmcnt wait) plus s_barrier make them visible to the others.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt lgkmcnt(0) only (LDS and scalar memory), leaving stores in flight.
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 }  // namespace ane
 
 #define ANE_HIP_CHECK_LAUNCH()                                   \

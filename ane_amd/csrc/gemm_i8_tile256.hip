@@ -77,34 +77,10 @@ constexpr int kRowsPerStore = 64 / kLanesPerRow;
 constexpr int kEpiWaveBytes = EPR * kEpiRowBytes;
 static_assert(NW * kEpiWaveBytes <= kLdsBytes, "epilogue staging does not fit");
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 __device__ __forceinline__ uint32_t swz_g(uint32_t row) { return (row ^ (row >> 2)) & 3; }
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
     return row * TK + ((chunk ^ swz_g(row)) << 4);
 }
-
-// Raw buffer resource over [base, base + bytes): loads past `bytes` return
-// zeros (checked per dword).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// s_waitcnt with vmcnt = n and the LDS/export counters left unconstrained;
-// the "memory" clobber keeps the compiler from moving LDS reads across it.
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt out of range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-}
-
-// Workgroup barrier without the release fence of __syncthreads() (see the
-// file comment).  LDS is coherent within the workgroup, so a wave's
-// completed copies (its vmcnt wait) plus s_barrier make them visible.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// s_waitcnt lgkmcnt(0) only (LDS and scalar memory), leaving stores in flight.
-__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // One slice copy: wave w copies rows [w*kRowsPerWave, (w+1)*kRowsPerWave)
 // of the tile's A rows and of its Bt rows; wave-instruction i covers
@@ -126,7 +102,7 @@ __device__ __forceinline__ void issue_part(const SliceCopy& c, const uint32_t (&
         const bool isB = d >= kDmaPerWave;
         int8_t* dst = c.stage + (c.wave * kRowsPerWave + i * kRowsPerDma) * TK + (isB ? kStageA : 0);
         const uint32_t o = c.live ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isB ? c.rb : c.ra, (lds_ptr_t)dst, 16, o, 0, 0, 0);
+        copy16_to_lds(isB ? c.rb : c.ra, dst, o);
     }
 }
 

@@ -1,27 +1,28 @@
 // q8_0.hip -- Q8_0 matrix-vector kernels (ggml block layout: fp16 d followed
-// by 32 int8 quants, 34 bytes per 32 weights, rows of K/32 blocks).
+// by 32 int8 quants, 34 bytes per 32 weights, rows of K/32 blocks;
+// API.md:598, bytecode_interpreter.s:7013, 7036-7056).
 //
 //   R mode  = the reference's q8_0_gemv (0x57, bytecode_interpreter.s:7010-7063):
-//             fp32 x, 16 fma lanes per row, FADDV tree; reproduced bit-exactly.
+//             fp32 x, 16 fma lanes per row (lane l takes elements l and 16+l
+//             of every block in order), FADDV tree; reproduced bit-exactly.
 //   G mode  = x quantized to Q8_0 per 32-block (0x19 arithmetic, fp32 scale),
 //             v_dot4 int8 block dots, 16 fp32 partials (block b -> partial
 //             b % 16, fmaf((float)isum, d_w*d_x, p)) combined by the same
 //             FADDV tree.  Serves GGML_OP_MUL_MAT for every token.
+//
+// Two implementations of each mode, bit-identical by construction:
+//  * streaming kernels (k_q8_0_stream), used when every row starts 16-byte
+//    aligned (nb % 8 == 0, W 16-byte aligned), the matrix is under 2 GB and
+//    the activations fit in LDS;
+//  * general kernels (k_q8_0_gemv_r, k_q8_0_quantize_x + k_q8_0_mul_mat_g)
+//    for everything else.
 #include "common.hpp"
 
 namespace ane {
+namespace {
 
+// ====================================================== general kernels
 constexpr int kRowsPerBlock = 16;  // 16 lanes per row, 256 threads
-
-__device__ __forceinline__ float faddv16(float v) {
-    // xor-butterfly over 16 lanes with offsets 1, 2, 4, 8: every lane ends
-    // with ((((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)))+(...)), the FADDV order.
-    v = v + __shfl_xor(v, 1, kWave);
-    v = v + __shfl_xor(v, 2, kWave);
-    v = v + __shfl_xor(v, 4, kWave);
-    v = v + __shfl_xor(v, 8, kWave);
-    return v;
-}
 
 __global__ void __launch_bounds__(256)
 k_q8_0_gemv_r(uint32_t M, uint32_t nb, const float* __restrict__ x,
@@ -63,12 +64,7 @@ k_q8_0_quantize_x(uint64_t nblocks, uint32_t nb, uint32_t K, const float* __rest
     quant_params(__uint_as_float(m), scale, inv);
     dx[b] = scale;
     uint32_t* q = reinterpret_cast<uint32_t*>(qx + b * 32);
-    for (int w = 0; w < 8; w++) {
-        q[w] = (uint32_t)(quant1(s[4 * w], inv) & 0xff) |
-               ((uint32_t)(quant1(s[4 * w + 1], inv) & 0xff) << 8) |
-               ((uint32_t)(quant1(s[4 * w + 2], inv) & 0xff) << 16) |
-               ((uint32_t)(quant1(s[4 * w + 3], inv) & 0xff) << 24);
-    }
+    for (int w = 0; w < 8; w++) q[w] = pack4(s[4 * w], s[4 * w + 1], s[4 * w + 2], s[4 * w + 3], inv);
 }
 
 constexpr int kTokChunk = 4;
@@ -115,6 +111,390 @@ k_q8_0_mul_mat_g(uint32_t N, uint32_t nb, uint32_t T, const int8_t* __restrict__
     }
 }
 
+// ====================================================== streaming kernels
+//  * Persistent grid: workgroups = CUs x occupancy, NW waves each.  Wave w
+//    owns the contiguous row range [w*N/Wt, (w+1)*N/Wt) of the Wt waves, so
+//    every wave streams the same number of bytes.
+//  * A wave walks its rows 4 at a time ("unit": one row per 16-lane group;
+//    in G mode lane l of a group owns blocks b = l mod 16, the partial order
+//    of the definition) and each unit in segments of SB blocks ("item").
+//    Items are copied global -> LDS with buffer_load_dwordx4 ... lds into a
+//    ring of S stages private to the wave: each copy wave-instruction moves
+//    1 KB of consecutive bytes of one or two rows, so HBM sees fully
+//    coalesced reads, and no VGPRs or workgroup barriers are spent on
+//    staging.  Item i+S-1 is issued before item i is computed; items past
+//    the end issue all-out-of-range copies so the s_waitcnt count is fixed.
+//  * Staged rows sit SB*17/8 + pad chunks apart, 16 or 48 dwords mod 64, so
+//    the four groups' block reads (dword offsets 17(l/2) + 8(l%2), distinct
+//    mod 16) never share an LDS bank.
+//  * A block b at byte 34b of its staged row is read as 9 aligned dwords
+//    from 34b - 2(b%2); v_perm_b32 realigns the scale and the 8 quant
+//    dwords (lanes of one parity share the selector, no branches).
+//  * G mode: each workgroup first quantizes the T activation rows into LDS
+//    (one 32-block per 8 lanes, 0x19 arithmetic); the halves of the 32-byte
+//    qx blocks are swapped on odd (b/8) so 16 lanes reading 16 blocks hit 16
+//    distinct bank quads.  R mode: x is copied to LDS as fp32.  The first
+//    batch of activation loads is issued ahead of the ring's first copies
+//    (vector-memory loads complete in issue order).
+constexpr int kUnitRows = 4;       // rows per wave pass (one per 16-lane group)
+constexpr uint32_t kXBatch = 8;    // activation float4 loads in flight per thread
+
+enum { kModeR = 0, kModeG = 1 };
+
+template <int SB>
+struct Seg {
+    static_assert(SB % 16 == 0, "segment length must be a multiple of 16 blocks");
+    static constexpr uint32_t kCpr = SB * 17 / 8;              // 16-byte chunks per row segment
+    static constexpr uint32_t kPad = SB == 32 ? 0 : 4;         // staged stride = 16 or 48 dwords mod 64
+    static constexpr uint32_t kRowChunks = kCpr + kPad;
+    static constexpr uint32_t kDma = (kUnitRows * kRowChunks + 63) / 64;
+    static constexpr uint32_t kStageBytes = kDma * 1024;
+};
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Per-lane byte offsets (relative to the item's first row) of the chunks a
+// full-segment item copies; 0x80000000 marks pad chunks.  Chunk c = lane +
+// 64 j is staged row c / kRowChunks, chunk c % kRowChunks.
+template <int SB>
+__device__ __forceinline__ void full_offsets(uint32_t lane, uint32_t rb, uint32_t (&off)[Seg<SB>::kDma]) {
+#pragma unroll
+    for (uint32_t j = 0; j < Seg<SB>::kDma; j++) {
+        const uint32_t c = j * 64 + lane;
+        const uint32_t g = c / Seg<SB>::kRowChunks, cc = c - g * Seg<SB>::kRowChunks;
+        off[j] = (g < kUnitRows && cc < Seg<SB>::kCpr) ? g * rb + cc * 16 : 0x80000000u;
+    }
+}
+
+// Copies one full-segment item: rows_live rows from byte `base` of W.  A
+// chunk is live iff its row is below rows_live, i.e. off < rows_live * rb
+// (pad offsets exceed every such bound).
+template <int SB>
+__device__ __forceinline__ void issue_full(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t base,
+                                           uint32_t rows_live, uint32_t rb,
+                                           const uint32_t (&off)[Seg<SB>::kDma]) {
+    const uint32_t lim = rows_live * rb;
+#pragma unroll
+    for (uint32_t j = 0; j < Seg<SB>::kDma; j++)
+        copy16_to_lds(w, stage + j * 1024, off[j] < lim ? base + off[j] : 0x80000000u);
+}
+
+// The last, shorter segment of a row (nb % SB blocks): staged stride
+// sbk*17/8 + pad chunks, offsets computed per call.
+template <int SB>
+__device__ __forceinline__ void issue_partial(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t lane,
+                                              uint32_t base, uint32_t rows_live, uint32_t rb,
+                                              uint32_t sbk) {
+    const uint32_t cpr = sbk * 17 / 8;
+    const uint32_t rc = cpr + Seg<SB>::kPad;
+#pragma unroll
+    for (uint32_t j = 0; j < Seg<SB>::kDma; j++) {
+        const uint32_t c = j * 64 + lane;
+        const uint32_t g = c / rc, cc = c - g * rc;
+        const bool live = g < rows_live && cc < cpr;
+        copy16_to_lds(w, stage + j * 1024, live ? base + g * rb + cc * 16 : 0x80000000u);
+    }
+}
+
+// Activation staging, in passes of one float4 per thread.
+//  G mode: pass p covers 32-blocks p*(THREADS/8) ... of the T x nb block
+//  grid (8 lanes per block); the 8 lanes reduce max|x|, quantize with the
+//  0x19 arithmetic and write 4 bytes each plus the fp32 scale.
+//  R mode: pass p covers float4s p*THREADS ... of x, copied as is.
+// Loads are four range-checked buffer_load_dword (any 4-byte alignment of
+// x and K; lanes past the end read zeros), issued unconditionally so the
+// loads of a batch and the ring copies after them are counted exactly by
+// the compiler's s_waitcnt placement.
+template <int MODE, int THREADS>
+struct XStage {
+    __amdgpu_buffer_rsrc_t xr;
+    uint32_t K, nb, T, n;  // n = blocks (G) or float4s (R)
+    int8_t* lds;
+    float* dxs;
+
+    static constexpr uint32_t kPerPass = MODE == kModeG ? THREADS / 8 : THREADS;
+
+    __device__ __forceinline__ uint32_t passes() const { return (n + kPerPass - 1) / kPerPass; }
+
+    __device__ __forceinline__ float4 load(uint32_t p) const {
+        uint32_t o = 0x80000000u;
+        if (MODE == kModeG) {
+            const uint32_t blk = p * kPerPass + (threadIdx.x >> 3);
+            const uint32_t t = T == 1 ? 0 : blk / nb, b = blk - t * nb;
+            if (blk < n) o = (t * K + b * 32 + (threadIdx.x & 7) * 4) * 4;
+        } else {
+            const uint32_t i = p * kPerPass + threadIdx.x;
+            if (i < n) o = 16 * i;
+        }
+        return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 4, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 8, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 12, 0, 0)));
+    }
+
+    __device__ __forceinline__ void store(uint32_t p, float4 f) const {
+        if (MODE == kModeG) {
+            const uint32_t blk = p * kPerPass + (threadIdx.x >> 3), part = threadIdx.x & 7;
+            const uint32_t m =
+                max8_u32(umax32(umax32(abs_key(f.x), abs_key(f.y)), umax32(abs_key(f.z), abs_key(f.w))));
+            float scale, inv;
+            quant_params(__uint_as_float(m), scale, inv);
+            if (blk < n) {
+                const uint32_t b = T == 1 ? blk : blk % nb;
+                const uint32_t half = (part >> 2) ^ ((b >> 3) & 1);
+                *reinterpret_cast<uint32_t*>(lds + (uint64_t)blk * 32 + 16 * half + 4 * (part & 3)) =
+                    pack4(f.x, f.y, f.z, f.w, inv);
+                if (part == 0) dxs[blk] = scale;
+            }
+        } else {
+            const uint32_t i = p * kPerPass + threadIdx.x;
+            if (i < n) reinterpret_cast<float4*>(lds)[i] = f;
+        }
+    }
+};
+
+// One G-mode block: isum of the staged block at rowp + 34b against each
+// token's quantized block gb, folded into p[t] with one fma.
+template <int TT>
+__device__ __forceinline__ void block_g(const int8_t* rowp, uint32_t b, uint32_t odd, uint32_t sel,
+                                        uint32_t ssel, uint32_t gb, const int8_t* qxs,
+                                        const float* dxs, uint32_t nb, uint32_t T, float (&p)[TT]) {
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(rowp + 34 * b - 2 * odd);
+    uint32_t D[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) D[i] = a[i];
+    const float dw = half_bits_to_float(__builtin_amdgcn_perm(D[1], D[0], ssel));
+    int q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = (int)__builtin_amdgcn_perm(D[i + 1], D[i], sel);
+    const uint32_t h = (gb >> 3) & 1;
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        if (TT == 1 || t < (int)T) {
+            const v4i* xb = reinterpret_cast<const v4i*>(qxs + ((uint64_t)t * nb + gb) * 32);
+            const v4i x0 = xb[h], x1 = xb[h ^ 1];
+            int isum = 0;
+            isum = __builtin_amdgcn_sdot4(q[0], x0.x, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[1], x0.y, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[2], x0.z, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[3], x0.w, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[4], x1.x, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[5], x1.y, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[6], x1.z, isum, false);
+            isum = __builtin_amdgcn_sdot4(q[7], x1.w, isum, false);
+            const float dd = __fmul_rn(dw, dxs[t * nb + gb]);
+            p[t] = __builtin_fmaf((float)isum, dd, p[t]);
+        }
+    }
+}
+
+// Blocks b = l, l+16, ... < sbk of one staged row, in increasing order.
+template <int SB, int TT, bool Full>
+__device__ __forceinline__ void compute_g(const int8_t* rowp, uint32_t l, uint32_t sbk, uint32_t gb0,
+                                          const int8_t* qxs, const float* dxs, uint32_t nb,
+                                          uint32_t T, float (&p)[TT]) {
+    const uint32_t odd = l & 1;
+    const uint32_t sel = odd ? 0x07060504u : 0x05040302u;   // quant dword i = bytes 2..5 / 4..7 of {D[i+1]:D[i]}
+    const uint32_t ssel = odd ? 0x0c0c0302u : 0x0c0c0100u;  // fp16 scale = bytes 0,1 / 2,3 of D[0]
+    if (Full) {
+#pragma unroll
+        for (uint32_t k = 0; k < SB / 16; k++)
+            block_g<TT>(rowp, l + 16 * k, odd, sel, ssel, gb0 + l + 16 * k, qxs, dxs, nb, T, p);
+    } else {
+        for (uint32_t b = l; b < sbk; b += 16) block_g<TT>(rowp, b, odd, sel, ssel, gb0 + b, qxs, dxs, nb, T, p);
+    }
+}
+
+// R mode: lane l takes bytes 2+l and 18+l of every block in order.
+__device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint32_t sbk, uint32_t gb0,
+                                           const float* xs, float acc) {
+#pragma unroll 8
+    for (uint32_t b = 0; b < sbk; b++) {
+        const int8_t* blk = rowp + 34 * b;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+        const float w0 = __fmul_rn((float)blk[2 + l], d);
+        const float w1 = __fmul_rn((float)blk[18 + l], d);
+        const float* xb = xs + (gb0 + b) * 32;
+        acc = __builtin_fmaf(w0, xb[l], acc);
+        acc = __builtin_fmaf(w1, xb[16 + l], acc);
+    }
+    return acc;
+}
+
+template <int MODE, int NW, int SB, int S, int TT>
+__global__ void __launch_bounds__(NW * 64)
+k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __restrict__ x,
+              const uint8_t* __restrict__ W, float* __restrict__ y, uint32_t total_waves) {
+    using G = Seg<SB>;
+    static_assert((S - 1) * G::kDma < 64, "copies in flight exceed the vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, grp = lane >> 4, l = lane & 15;
+    int8_t* ring = smem + wave * (S * G::kStageBytes);
+    int8_t* xlds = smem + NW * S * G::kStageBytes;
+
+    const uint32_t gw = blockIdx.x * NW + wave;
+    const uint32_t r0 = (uint32_t)(((uint64_t)gw * N) / total_waves);
+    const uint32_t r1 = (uint32_t)(((uint64_t)(gw + 1) * N) / total_waves);
+    const uint32_t nseg = (nb + SB - 1) / SB;
+    const uint32_t nitems = (r1 - r0 + kUnitRows - 1) / kUnitRows * nseg;
+    const uint32_t rb = nb * 34;
+    const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(W, N * rb);
+    uint32_t off[G::kDma];
+    full_offsets<SB>(lane, rb, off);
+
+    auto issue = [&](uint32_t i) {
+        const uint32_t u = i / nseg, s = i - u * nseg;
+        const uint32_t row0 = r0 + kUnitRows * u;
+        const uint32_t rows_live = i < nitems ? min((uint32_t)kUnitRows, r1 - row0) : 0u;
+        const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
+        int8_t* stage = ring + (i % S) * G::kStageBytes;
+        const uint32_t base = row0 * rb + s * (SB * 34);
+        if (sbk == (uint32_t)SB) issue_full<SB>(rsrc, stage, base, rows_live, rb, off);
+        else issue_partial<SB>(rsrc, stage, lane, base, rows_live, rb, sbk);
+    };
+
+    const int8_t* qxs = xlds;
+    float* dxs = reinterpret_cast<float*>(xlds + ceil_to((uint64_t)T * nb * 32, 16));
+    const float* xs = reinterpret_cast<const float*>(xlds);
+    const XStage<MODE, NW * 64> xst{make_rsrc(x, T * K * 4), K, nb, T, MODE == kModeG ? nb * T : nb * 8,
+                                    xlds, dxs};
+    const uint32_t npass = xst.passes();
+    float4 xv[kXBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
+#pragma unroll
+    for (int i = 0; i < S - 1; i++) issue(i);
+#pragma unroll
+    for (uint32_t k = 0; k < kXBatch; k++)
+        if (k < npass) xst.store(k, xv[k]);
+    for (uint32_t p0 = kXBatch; p0 < npass; p0 += kXBatch) {
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(p0 + k);
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++)
+            if (p0 + k < npass) xst.store(p0 + k, xv[k]);
+    }
+    wait_lgkmcnt0();
+    lds_barrier();
+
+    float p[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) p[t] = 0.0f;
+    for (uint32_t i = 0; i < nitems; i++) {
+        wait_lgkmcnt0();  // reads of the stage about to be refilled are done
+        issue(i + S - 1);
+        wait_vmcnt<(S - 1) * G::kDma>();  // item i has landed
+        const uint32_t u = i / nseg, s = i - u * nseg;
+        const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
+        const int8_t* rowp = ring + (i % S) * G::kStageBytes + grp * (sbk * 17 / 8 + G::kPad) * 16;
+        if (s == 0) {
+#pragma unroll
+            for (int t = 0; t < TT; t++) p[t] = 0.0f;
+        }
+        if (MODE == kModeG) {
+            if (sbk == (uint32_t)SB) compute_g<SB, TT, true>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
+            else compute_g<SB, TT, false>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
+        } else {
+            p[0] = compute_r(rowp, l, sbk, s * SB, xs, p[0]);
+        }
+        if (s == nseg - 1) {
+            const uint32_t row = r0 + kUnitRows * u + grp;
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                const float v = faddv16(p[t]);
+                if (l == 0 && row < r1 && (TT == 1 || t < (int)T)) y[(uint64_t)t * N + row] = v;
+            }
+        }
+    }
+    wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+}
+
+constexpr uint32_t kLdsLimit = 160 * 1024;
+constexpr int kMaxStreamTokens = 4;
+
+bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void* W) {
+    return nb > 0 && nb % 8 == 0 && (((uintptr_t)W) & 15) == 0 &&
+           (uint64_t)N * nb * 34 < 0x80000000ull && (uint64_t)T * K * 4 < 0x80000000ull;
+}
+
+template <int MODE, int NW, int SB, int S>
+uint64_t stream_lds(uint32_t nb, uint32_t T) {
+    const uint64_t xb = MODE == kModeG ? ceil_to((uint64_t)T * nb * 32, 16) + (uint64_t)T * nb * 4
+                                       : (uint64_t)nb * 32 * 4;
+    return (uint64_t)NW * S * Seg<SB>::kStageBytes + ceil_to(xb, 16);
+}
+
+int cu_count(int dev) {
+    static int cached[64];
+    if (dev < 0 || dev >= 64) return 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Launches one configuration if its LDS fits; returns -1 if it does not.
+// Occupancy is queried once per (device, LDS size).
+template <int MODE, int NW, int SB, int S, int TT>
+int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W,
+               float* y, hipStream_t s) {
+    const uint64_t lds64 = stream_lds<MODE, NW, SB, S>(nb, T);
+    if (lds64 > kLdsLimit) return -1;
+    const uint32_t lds = (uint32_t)lds64;
+    auto fn = k_q8_0_stream<MODE, NW, SB, S, TT>;
+    static int occ_cache[64];
+    static uint32_t occ_lds[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    if (occ_lds[dev] != lds) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return ANE_ERR_HIP;
+        int occ = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, NW * 64, lds) != hipSuccess || occ < 1)
+            return ANE_ERR_HIP;
+        occ_cache[dev] = occ;
+        occ_lds[dev] = lds;
+    }
+    const int cus = cu_count(dev);
+    if (cus <= 0) return ANE_ERR_HIP;
+    const uint64_t units = ((uint64_t)N + kUnitRows - 1) / kUnitRows;
+    uint64_t grid = (uint64_t)cus * occ_cache[dev];
+    const uint64_t need = (units + NW - 1) / NW;
+    if (grid > need) grid = need;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
+                       (const uint8_t*)W, y, (uint32_t)(grid * NW));
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+// Configurations in order of preference (waves per workgroup, blocks per
+// segment, ring stages); the first whose LDS fits is launched.
+#ifndef ANE_Q8_G_CFG
+#define ANE_Q8_G_CFG 8, 32, 2
+#endif
+template <int TT>
+int stream_g(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
+             hipStream_t s) {
+    int r = try_stream<kModeG, ANE_Q8_G_CFG, TT>(N, nb, K, T, x, W, y, s);
+    if (r < 0) r = try_stream<kModeG, 4, 32, 2, TT>(N, nb, K, T, x, W, y, s);
+    return r;
+}
+
+#ifndef ANE_Q8_R_CFG
+#define ANE_Q8_R_CFG 8, 32, 2
+#endif
+int stream_r(uint32_t N, uint32_t nb, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
+    int r = try_stream<kModeR, ANE_Q8_R_CFG, 1>(N, nb, K, 1, x, W, y, s);
+    if (r < 0) r = try_stream<kModeR, 4, 32, 2, 1>(N, nb, K, 1, x, W, y, s);
+    return r;
+}
+
+}  // namespace
 }  // namespace ane
 
 using namespace ane;
@@ -125,9 +505,14 @@ extern "C" int ane_hip_q8_0_gemv(uint32_t M, uint32_t K, const float* x, const v
     if (!y || ((K >> 5) && (!x || !W))) return ANE_ERR_BAD_POINTER;
     if ((((uintptr_t)W) & 1) != 0) return ANE_ERR_INVALID_ARG;
     const uint32_t nb = K >> 5;
+    hipStream_t s = (hipStream_t)stream;
+    if (stream_eligible(M, nb, K, 1, W)) {
+        const int r = stream_r(M, nb, K, x, W, y, s);
+        if (r >= 0) return r;
+    }
     const uint64_t grid = ((uint64_t)M + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipLaunchKernelGGL(k_q8_0_gemv_r, dim3((uint32_t)grid), dim3(256), 0, (hipStream_t)stream, M, nb,
-                       x, (const uint8_t*)W, y);
+    hipLaunchKernelGGL(k_q8_0_gemv_r, dim3((uint32_t)grid), dim3(256), 0, s, M, nb, x,
+                       (const uint8_t*)W, y);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -148,6 +533,11 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
         workspace_bytes < ane_hip_q8_0_mul_mat_workspace_size(K, T))
         return ANE_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
+    if (T <= kMaxStreamTokens && stream_eligible(N, nb, K, T, W)) {
+        const int r = T == 1 ? stream_g<1>(N, nb, K, T, x, W, y, s)
+                             : stream_g<kMaxStreamTokens>(N, nb, K, T, x, W, y, s);
+        if (r >= 0) return r;
+    }
     int8_t* qx = (int8_t*)workspace;
     float* dx = (float*)((uint8_t*)workspace + ceil_to((uint64_t)T * nb * 32, 256));
     const uint64_t nblocks = (uint64_t)T * nb;

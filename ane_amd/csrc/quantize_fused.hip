@@ -57,11 +57,6 @@ __device__ __forceinline__ float fold_partials(const uint32_t* partials, uint32_
     return __uint_as_float(block_max_u32_256(m, red));
 }
 
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
-    return (uint32_t)(quant1(a, inv) & 0xff) | ((uint32_t)(quant1(b, inv) & 0xff) << 8) |
-           ((uint32_t)(quant1(c, inv) & 0xff) << 16) | ((uint32_t)(quant1(d, inv) & 0xff) << 24);
-}
-
 // B tiles: 128 k x 64 n per block.
 constexpr int kBTK = 128, kBTN = 64;
 constexpr int kTileRowDw = kBTK / 4 + 1;  // dwords per transposed row (+1 pad)

@@ -305,7 +305,9 @@ def test_dense_fused_4096_cubed_sampled(ane, oracle):
 
 
 # ---------------------------------------------------------------- Q8_0
-@pytest.mark.parametrize("M,K", [(1, 32), (3, 40), (4096, 4096), (14336, 4096), (4096, 14336), (77, 96)])
+@pytest.mark.parametrize("M,K", [(1, 32), (3, 40), (4096, 4096), (14336, 4096), (4096, 14336), (77, 96),
+                                 # streaming kernel: partial last segment, ragged row split, K % 32 != 0
+                                 (1001, 2304), (5, 261), (4097, 512)])
 def test_q8_0_gemv_r_parity(ane, oracle, M, K):
     """Opcode 0x57 through stream_exec, bit-identical to the reference arithmetic."""
     import torch
@@ -324,7 +326,10 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
 
 
 @pytest.mark.parametrize("N,K,T", [(4096, 4096, 1), (14336, 4096, 1), (4096, 14336, 1), (6144, 4096, 4),
-                                   (4096, 4096, 16), (1024, 4096, 64), (100, 96, 3), (5, 50, 2)])
+                                   (4096, 4096, 16), (1024, 4096, 64), (100, 96, 3), (5, 50, 2),
+                                   # streaming kernel: partial segment, ragged rows, unaligned x rows, T 2..4
+                                   (1001, 2304, 1), (37, 261, 3), (4097, 512, 2), (28672, 4096, 4),
+                                   (3, 256, 1)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
@@ -338,6 +343,44 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     y = zeros(T * N, torch.float32)
     ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
     assert_f32_identical(host(y).reshape(T, N), ref)
+
+
+def test_q8_0_mul_mat_g_special_values(ane, oracle):
+    """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules per block)."""
+    import torch
+
+    N, K, T = 300, 1024, 2
+    W = data.q8_0_weights(N, K, seed=11)
+    x = data.activations(T, K, seed=12)
+    x[0, 0:32] = 0.0
+    x[0, 64] = np.nan
+    x[1, 100] = np.inf
+    x[1, 200] = -1e-40  # denormal
+    ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
+    y = zeros(T * N, torch.float32)
+    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
+    assert_f32_identical(host(y).reshape(T, N), ref)
+
+
+@pytest.mark.parametrize("mode", ["R", "G"])
+def test_q8_0_misaligned_weights(ane, oracle, mode):
+    """W starting 2 bytes into an allocation (rows not 16-byte aligned): general kernels."""
+    import torch
+
+    N, K = 513, 1024
+    W = data.q8_0_weights(N, K, seed=5)
+    x = data.activations(1, K, seed=6)[0]
+    buf = torch.zeros(W.size + 16, dtype=torch.uint8, device="cuda")
+    buf[2: 2 + W.size] = dev(W.reshape(-1))
+    Wv = buf[2: 2 + W.size]
+    y = zeros(N, torch.float32)
+    if mode == "R":
+        ref = oracle.q8_0_gemv(N, K, x, W)
+        ane.q8_0_gemv(N, K, dev(x), Wv, y)
+    else:
+        ref = oracle.q8_0_mul_mat_g(N, K, 1, x[None, :], W)[0]
+        ane.q8_0_mul_mat(N, K, 1, dev(x), Wv, y)
+    assert_f32_identical(host(y), ref)
 
 
 # ---------------------------------------------------------------- error paths
