@@ -72,6 +72,37 @@ def events_time(fn, reps: int, stream) -> float:
     return start.elapsed_time(stop) / reps
 
 
+def graph_time(fn_s, reps: int, rounds: int = 5) -> float:
+    """Median milliseconds per call of fn_s(stream): `reps` calls (fn_s may
+    rotate its inputs) are captured into one HIP graph on a side stream and
+    replayed `rounds` times on that stream between HIP events, so host
+    launch overhead is outside the timed region."""
+    import torch
+
+    gs = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(gs):
+        for _ in range(3):
+            fn_s(gs)
+        gs.synchronize()
+        with torch.cuda.graph(graph, stream=gs):
+            for _ in range(reps):
+                fn_s(gs)
+        graph.replay()
+        gs.synchronize()
+        times = []
+        for _ in range(rounds):
+            start = torch.cuda.Event(enable_timing=True)
+            stop = torch.cuda.Event(enable_timing=True)
+            start.record(gs)
+            graph.replay()
+            stop.record(gs)
+            stop.synchronize()
+            times.append(start.elapsed_time(stop) / reps)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def read_pmc_traffic(name: str):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary
     (profiles/<name>), lines 'traffic_bytes_per_launch: <int>'."""
@@ -110,14 +141,14 @@ def main() -> int:
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     scales = torch.empty(2, dtype=torch.float32, device=dev)
 
-    def fused():
-        ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=stream)
+    def fused(st=stream):
+        ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st)
 
-    def gemm_phase():
-        ane_amd.dense_fused_i8_gemm(M, N, K, 1.0, True, C, ws, stream=stream)
+    def gemm_phase(st=stream):
+        ane_amd.dense_fused_i8_gemm(M, N, K, 1.0, True, C, ws, stream=st)
 
-    def quant_phase():
-        ane_amd.dense_fused_i8_quantize(M, N, K, A, B, ws, stream=stream)
+    def quant_phase(st=stream):
+        ane_amd.dense_fused_i8_quantize(M, N, K, A, B, ws, stream=st)
 
     ops = 2.0 * M * N * K
 
@@ -159,17 +190,16 @@ def main() -> int:
 
     # ------------------------------------------------------------ kernel roofline
     quant_phase()
-    for _ in range(5):
-        gemm_phase()
-    gemm_ms = events_time(gemm_phase, args.kernel_reps, stream)
+    torch.cuda.synchronize()
+    gemm_ms = graph_time(gemm_phase, args.kernel_reps)
     gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
-    quant_ms = events_time(quant_phase, max(20, args.kernel_reps // 4), stream)
+    quant_ms = graph_time(quant_phase, max(20, args.kernel_reps // 4))
     quant_bytes = 5.0 * (M * K + K * N)  # read fp32 once + write int8 (algorithmic)
     log(f"MFMA kernel: {gemm_ms * 1e3:.2f} us = {gemm_tops:.1f} TOPS ({gemm_tops / PEAK_INT8_TOPS:.1%})")
     log(f"quantize phase: {quant_ms * 1e3:.2f} us = {quant_bytes / quant_ms / 1e6:.0f} GB/s algorithmic")
     roofline = {
         "bound": "mfma",
-        "kernel": "k_gemm_i8<kBTransposed,false> (dense_fused_i8 contraction + epilogue)",
+        "kernel": "k_gemm_tile256 (dense_fused_i8 contraction + fused dequant/scale/ReLU epilogue)",
         "achieved": round(gemm_tops, 2),
         "peak": PEAK_INT8_TOPS,
         "unit": "TOPS",
@@ -266,22 +296,20 @@ def bench_q8(args, stream) -> dict:
         wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, 1), dtype=torch.uint8, device="cuda")
         it = [0]
 
-        def g_mode():
+        def g_mode(st):
             W = Ws[it[0] % copies]
             it[0] += 1
-            ane_amd.q8_0_mul_mat(Nr, Kc, 1, x, W, y, workspace=wsq, stream=stream)
+            ane_amd.q8_0_mul_mat(Nr, Kc, 1, x, W, y, workspace=wsq, stream=st)
 
-        def r_mode():
+        def r_mode(st):
             W = Ws[it[0] % copies]
             it[0] += 1
-            ane_amd.q8_0_gemv(Nr, Kc, x, W, y, stream=stream)
+            ane_amd.q8_0_gemv(Nr, Kc, x, W, y, stream=st)
 
         alg = wbytes + 4 * Kc + 4 * Nr
         entry = {"weights_bytes": wbytes, "algorithmic_bytes": alg, "rotating_copies": copies}
         for name, fn in (("g_mode", g_mode), ("r_mode", r_mode)):
-            for _ in range(10):
-                fn()
-            ms = events_time(fn, args.kernel_reps, stream)
+            ms = graph_time(fn, 4 * copies)
             gbs = alg / (ms * 1e-3) / 1e9
             entry[name] = {"us": round(ms * 1e3, 3), "GB_s": round(gbs, 1),
                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
