@@ -59,7 +59,8 @@ STATUS = {
     8: "ANE_ERR_WORKSPACE",
 }
 
-# Symbols include/ane_hip.h declares; the library must export every one.
+# Symbols include/ane_hip.h and include/ggml-ane-hip.h declare; the library
+# must export every one.
 EXPORTS = (
     "stream_exec",
     "ane_last_error",
@@ -83,6 +84,15 @@ EXPORTS = (
     "ane_hip_q8_0_mul_mat",
     "ane_hip_device_check",
     "ane_hip_version",
+    # include/ggml-ane-hip.h
+    "ane_ggml_backend_name",
+    "ane_ggml_device_name",
+    "ane_ggml_backend_init",
+    "ane_ggml_backend_free",
+    "ane_ggml_backend_set_q8_mode",
+    "ane_ggml_supports_op",
+    "ane_ggml_compute_forward",
+    "ane_ggml_graph_compute",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -127,6 +137,14 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     ),
     "ane_hip_device_check": (_c.c_int, []),
     "ane_hip_version": (_c.c_char_p, []),
+    "ane_ggml_backend_name": (_c.c_char_p, []),
+    "ane_ggml_device_name": (_c.c_char_p, []),
+    "ane_ggml_backend_init": (_P, [_P]),
+    "ane_ggml_backend_free": (None, [_P]),
+    "ane_ggml_backend_set_q8_mode": (None, [_P, _c.c_int]),
+    "ane_ggml_supports_op": (_c.c_int, [_P]),
+    "ane_ggml_compute_forward": (_c.c_int, [_P, _P]),
+    "ane_ggml_graph_compute": (_c.c_int, [_P, _P, _c.c_int]),
 }
 
 
@@ -362,3 +380,87 @@ def require_gpu() -> None:
     st = lib().ane_hip_device_check()
     if st != 0:
         raise AneError(st, "no usable gfx950 device")
+
+
+# ---------------------------------------------------------------- ggml hook
+class GgmlType:
+    """ggml_type values the hook distinguishes (include/ggml-ane-hip.h)."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q8_0 = 8
+
+
+class GgmlOp:
+    NONE = 0
+    MUL_MAT = 1
+    OTHER = 2
+
+
+class GgmlTensor(ctypes.Structure):
+    """Mirror of struct ane_ggml_tensor (ggml's ne/nb/type/op/src/data)."""
+
+
+GgmlTensor._fields_ = [
+    ("type", ctypes.c_int32),
+    ("ne", ctypes.c_int64 * 4),
+    ("nb", ctypes.c_size_t * 4),
+    ("op", ctypes.c_int32),
+    ("src", ctypes.POINTER(GgmlTensor) * 10),
+    ("data", ctypes.c_void_p),
+]
+
+_TYPE_SIZE = {GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.Q8_0: (32, 34)}
+
+
+def ggml_tensor(type_, ne, data=None, nb=None, op=GgmlOp.NONE, src=()) -> GgmlTensor:
+    """A node with ggml's default (contiguous) strides unless nb is given."""
+    ne = list(ne) + [1] * (4 - len(ne))
+    t = GgmlTensor()
+    t.type = type_
+    t.op = op
+    for i in range(4):
+        t.ne[i] = ne[i]
+    if nb is None:
+        blk, size = _TYPE_SIZE[type_]
+        nb = [size, size * (ne[0] // blk)]
+        nb.append(nb[1] * ne[1])
+        nb.append(nb[2] * ne[2])
+    for i in range(4):
+        t.nb[i] = nb[i]
+    for i, s_ in enumerate(src):
+        t.src[i] = ctypes.pointer(s_)
+    t.data = _p(data) or None
+    return t
+
+
+class GgmlBackend:
+    """The backend instance of include/ggml-ane-hip.h (device workspace, stream)."""
+
+    def __init__(self, stream=None, q8_mode: int = 0):
+        self.L = lib()
+        self.h = self.L.ane_ggml_backend_init(_stream_handle(stream))
+        if not self.h:
+            raise AneError(6, "ane_ggml_backend_init failed")
+        self.L.ane_ggml_backend_set_q8_mode(self.h, q8_mode)
+
+    def supports(self, node: GgmlTensor) -> bool:
+        return bool(self.L.ane_ggml_supports_op(ctypes.byref(node)))
+
+    def compute(self, node: GgmlTensor) -> None:
+        check(self.L.ane_ggml_compute_forward(self.h, ctypes.byref(node)), "ane_ggml_compute_forward")
+
+    def graph_compute(self, nodes) -> None:
+        arr = (ctypes.POINTER(GgmlTensor) * len(nodes))(*[ctypes.pointer(n) for n in nodes])
+        check(self.L.ane_ggml_graph_compute(self.h, arr, len(nodes)), "ane_ggml_graph_compute")
+
+    def close(self) -> None:
+        if self.h:
+            self.L.ane_ggml_backend_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

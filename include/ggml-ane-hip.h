@@ -1,0 +1,99 @@
+/*
+ * ggml-ane-hip.h -- the ggml backend side of ane's quantized path on MI355X.
+ *
+ * The reference ships a ggml backend (src/ggml-backend/ggml-ane.h:20,
+ * ggml-ane.cpp) whose GGML_OP_MUL_MAT hook sends Q8_0 weights to q8_0_gemv
+ * (ggml-ane.cpp:119-154).  ggml itself is not vendored there and no version
+ * is pinned, so this header declares the minimal ggml subset the hook reads.
+ * Field names and meanings follow ggml's ggml_tensor: ne[] element counts
+ * and nb[] byte strides, innermost first; src[0] = weights, src[1] =
+ * activations.  Type values follow ggml's on-disk enum ggml_type.  It is an
+ * API-level shim: a maintainer plugging this backend into a real ggml build
+ * copies ggml_tensor's ne/nb/type/data/src into these fields per node.
+ *
+ * Compared with the reference hook, this backend:
+ *   - computes every token (ne11) and every broadcast batch (ne12, ne13),
+ *     where the reference computes token 0 only;
+ *   - honours nb[] strides: non-contiguous activation rows are gathered,
+ *     and non-contiguous output rows are scattered;
+ *   - runs on device memory with an explicit HIP stream.
+ */
+#ifndef GGML_ANE_HIP_H
+#define GGML_ANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ANE_GGML_MAX_DIMS 4
+#define ANE_GGML_MAX_SRC 10
+
+/* ggml_type values of the formats this hook distinguishes (ggml's enum). */
+enum ane_ggml_type {
+    ANE_GGML_TYPE_F32 = 0,
+    ANE_GGML_TYPE_F16 = 1,
+    ANE_GGML_TYPE_Q4_0 = 2,
+    ANE_GGML_TYPE_Q8_0 = 8
+};
+
+/* Operations the hook distinguishes.  ggml's numeric op values depend on the
+ * ggml version, so the caller translates its op into one of these. */
+enum ane_ggml_op {
+    ANE_GGML_OP_NONE = 0,
+    ANE_GGML_OP_MUL_MAT = 1,
+    ANE_GGML_OP_OTHER = 2 /* anything else: not supported by this backend */
+};
+
+/* Q8_0 arithmetic of MUL_MAT: G quantizes each activation row per 32-block
+ * and dots int8 x int8 (the default); R is the reference opcode 0x57's fp32
+ * arithmetic (bytecode_interpreter.s:7010-7063), one launch per token. */
+enum ane_ggml_q8_mode { ANE_GGML_Q8_G = 0, ANE_GGML_Q8_R = 1 };
+
+struct ane_ggml_tensor {
+    int32_t type;                                /* enum ane_ggml_type        */
+    int64_t ne[ANE_GGML_MAX_DIMS];               /* elements per dimension    */
+    size_t nb[ANE_GGML_MAX_DIMS];                /* bytes between elements    */
+    int32_t op;                                  /* enum ane_ggml_op          */
+    struct ane_ggml_tensor* src[ANE_GGML_MAX_SRC];
+    void* data;                                  /* device memory             */
+};
+
+typedef struct ane_ggml_backend* ane_ggml_backend_t;
+
+/* Replaces ggml_backend_ane_reg() (ggml-ane.h:20): name of the backend and
+ * of its single device ("ANE0" in the reference, ggml-ane.cpp:302-318). */
+const char* ane_ggml_backend_name(void);
+const char* ane_ggml_device_name(void);
+
+/* Backend instance: owns a grow-only device workspace; compute runs on
+ * `stream` (void* = hipStream_t, 0 = null stream).  Replaces
+ * ane_dev_init_backend / ane_backend_free (ggml-ane.cpp:332-357, 102-104). */
+ane_ggml_backend_t ane_ggml_backend_init(void* stream);
+void ane_ggml_backend_free(ane_ggml_backend_t backend);
+void ane_ggml_backend_set_q8_mode(ane_ggml_backend_t backend, int mode);
+
+/* Replaces ane_dev_supports_op (ggml-ane.cpp:363-368): 1 if this backend
+ * computes the node.  MUL_MAT: src0 Q8_0, src1 and dst F32, ne00 == ne10,
+ * ne0 == ne01, ne1 == ne11, src1/dst batches broadcastable over src0's
+ * (ne12 % ne02 == 0, ne13 % ne03 == 0), innermost strides equal to the
+ * element size, Q8_0 rows contiguous. */
+int ane_ggml_supports_op(const struct ane_ggml_tensor* node);
+
+/* Replaces ane_compute_forward for one node (ggml-ane.cpp:109-154).
+ * Asynchronous on the backend's stream; returns an ane_status. */
+int ane_ggml_compute_forward(ane_ggml_backend_t backend, const struct ane_ggml_tensor* node);
+
+/* Replaces ane_graph_compute (ggml-ane.cpp:287-299): computes the
+ * nodes in order, then synchronises the stream once.  Returns the status of
+ * the first failing node (ANE_ERR_INVALID_ARG for an unsupported one). */
+int ane_ggml_graph_compute(ane_ggml_backend_t backend, struct ane_ggml_tensor* const* nodes,
+                           int n_nodes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GGML_ANE_HIP_H */

@@ -1,6 +1,6 @@
 """The C-ABI boundary without a GPU: exports, byte encoding, decoder errors.
 
-Covers include/ane_hip.h (every declared function is exported by
+Covers include/ane_hip.h and include/ggml-ane-hip.h (every declared function is exported by
 libane_amd.so), the Python mirror of ane::dispatch against the C++ header
 (include/ane/ane.hpp compiled with g++), and the decoder's error paths that
 return before any HIP call.
@@ -17,14 +17,16 @@ import ane_amd
 from ane_amd import Op, boolean, encode, f32, i32, ptr, u32
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "ane_hip.h"
+HEADERS = [ROOT / "include" / "ane_hip.h", ROOT / "include" / "ggml-ane-hip.h"]
 
 
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(\w+)\s*\(", text, flags=re.M)
-    return sorted(set(n for n in names if n not in ("if", "defined")))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        text = re.sub(r"^\s*(?:struct|enum|typedef)\b.*?;", "", text, flags=re.S | re.M)
+        names |= set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(\w+)\s*\(", text, flags=re.M))
+    return sorted(n for n in names if n not in ("if", "defined"))
 
 
 def test_header_matches_python_export_list():
