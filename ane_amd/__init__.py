@@ -59,8 +59,8 @@ STATUS = {
     8: "ANE_ERR_WORKSPACE",
 }
 
-# Symbols include/ane_hip.h and include/ggml-ane-hip.h declare; the library
-# must export every one.
+# Symbols include/ane_hip.h, include/ggml-ane-hip.h and include/ane_decode.h
+# declare; the library must export every one.
 EXPORTS = (
     "stream_exec",
     "ane_last_error",
@@ -93,6 +93,14 @@ EXPORTS = (
     "ane_ggml_supports_op",
     "ane_ggml_compute_forward",
     "ane_ggml_graph_compute",
+    # include/ane_decode.h
+    "ane_decode_workspace_size",
+    "ane_decode_token",
+    "ane_hip_q8_0_matvec_fused",
+    "ane_hip_rope_kv_append",
+    "ane_hip_attention_workspace_size",
+    "ane_hip_attention_decode",
+    "ane_hip_silu_mul",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -145,6 +153,13 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_ggml_supports_op": (_c.c_int, [_P]),
     "ane_ggml_compute_forward": (_c.c_int, [_P, _P]),
     "ane_ggml_graph_compute": (_c.c_int, [_P, _P, _c.c_int]),
+    "ane_decode_workspace_size": (_c.c_size_t, [_P]),
+    "ane_decode_token": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_q8_0_matvec_fused": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _c.c_float, _P, _P, _P, _P]),
+    "ane_hip_rope_kv_append": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _P]),
+    "ane_hip_attention_workspace_size": (_c.c_size_t, [_P]),
+    "ane_hip_attention_decode": (_c.c_int, [_P, _P, _P, _P, _c.c_uint32, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_silu_mul": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
 }
 
 
@@ -464,3 +479,60 @@ class GgmlBackend:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------- decode step
+class DecodeConfig(ctypes.Structure):
+    """Mirror of struct ane_decode_config (include/ane_decode.h)."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_layers", "hidden", "ffn", "n_heads", "n_kv_heads",
+                                                "head_dim", "ctx")] + [("eps", ctypes.c_float)]
+
+
+class DecodeLayer(ctypes.Structure):
+    """Mirror of struct ane_decode_layer (device pointers)."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in ("w_qkv", "w_o", "w_gate_up", "w_down", "attn_norm",
+                                                "ffn_norm", "k_cache", "v_cache")]
+
+
+def rope_table(ctx: int, head_dim: int = 128, base: float = 500000.0):
+    """(cos, sin) of pos * base^(-2i/head_dim), fp32 [ctx][head_dim/2][2],
+    computed in float64 and rounded once."""
+    import numpy as np
+
+    i = np.arange(head_dim // 2, dtype=np.float64)
+    theta = np.power(base, -2.0 * i / head_dim)
+    ang = np.arange(ctx, dtype=np.float64)[:, None] * theta[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+def q8_0_matvec_fused(N, K, x, W, y, norm_w=None, eps=0.0, residual=None, stream=None):
+    check(lib().ane_hip_q8_0_matvec_fused(N, K, _p(x), _p(norm_w), eps, _p(W), _p(residual), _p(y),
+                                          _stream_handle(stream)), "q8_0_matvec_fused")
+
+
+def rope_kv_append(cfg, qkv, table, pos, k_cache, v_cache, stream=None):
+    check(lib().ane_hip_rope_kv_append(ctypes.byref(cfg), _p(qkv), _p(table), pos, _p(k_cache), _p(v_cache),
+                                       _stream_handle(stream)), "rope_kv_append")
+
+
+def attention_decode(cfg, q, k_cache, v_cache, length, out, workspace=None, stream=None):
+    import torch
+
+    L = lib()
+    wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
+    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    check(L.ane_hip_attention_decode(ctypes.byref(cfg), _p(q), _p(k_cache), _p(v_cache), length, _p(out), _p(ws),
+                                     wsb, _stream_handle(stream)), "attention_decode")
+
+
+def silu_mul(n, gu, h, stream=None):
+    check(lib().ane_hip_silu_mul(n, _p(gu), _p(h), _stream_handle(stream)), "silu_mul")
+
+
+def decode_token(cfg, layers, table, pos, x, workspace, stream=None):
+    """layers: a ctypes array of DecodeLayer (host memory)."""
+    L = lib()
+    check(L.ane_decode_token(ctypes.byref(cfg), layers, _p(table), pos, _p(x), _p(workspace),
+                             workspace.numel(), _stream_handle(stream)), "decode_token")

@@ -1,0 +1,315 @@
+// decode.hip -- single-token decode of a Llama-shaped model: the steps
+// around the Q8_0 matrix products (RoPE + KV append, GQA attention over the
+// fp16 cache, SiLU * up) and the per-token driver ane_decode_token.
+//
+// Matrix products go through ane_hip_q8_0_matvec_fused (q8_0.hip), which
+// fuses the RMSNorm of its input and the residual add of its output, so a
+// layer is seven launches: qkv, rope/append, attention partial, attention
+// combine, o (+residual), gate_up (norm fused), silu*up, down (+residual).
+//
+// Attention is split over the context in chunks of 128 positions
+// (flash-decoding): one workgroup per (kv head, chunk) reads that chunk's K
+// and V rows once for all G = n_heads / n_kv_heads query heads of the group,
+// keeps per-head running max / sum / output, and a combine kernel merges the
+// chunks with the usual exp(m_c - M) rescaling.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "../../include/ane_decode.h"
+#include "common.hpp"
+
+namespace ane {
+namespace {
+
+constexpr int kHD = 128;     // head_dim
+constexpr int kChunk = 128;  // context positions per attention workgroup
+constexpr int kGroup = 4;    // query heads per kv head (one wave each in the softmax)
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    const _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+// Threads [0, nq*64) rotate q pairs in place, [nq*64, (nq+nkv)*64) rotate k
+// pairs into the k cache, the next nkv*128 copy v into the v cache.
+__global__ void __launch_bounds__(256)
+k_rope_kv_append(float* __restrict__ qkv, uint32_t nq, uint32_t nkv, const float* __restrict__ cs,
+                 uint32_t pos, uint32_t ctx, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t qpairs = nq * (kHD / 2), kpairs = nkv * (kHD / 2), vel = nkv * kHD;
+    if (i < qpairs + kpairs) {
+        const bool isq = i < qpairs;
+        const uint32_t pi = isq ? i : i - qpairs;
+        const uint32_t head = pi / (kHD / 2), pr = pi % (kHD / 2);
+        float* src = qkv + (isq ? 0 : nq * kHD) + head * kHD + 2 * pr;
+        const float c = cs[2 * pr], s = cs[2 * pr + 1];
+        const float a = src[0], b = src[1];
+        const float o0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+        const float o1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+        if (isq) {
+            src[0] = o0;
+            src[1] = o1;
+        } else {
+            uint16_t* dst = kc + ((uint64_t)head * ctx + pos) * kHD + 2 * pr;
+            dst[0] = f32_to_f16_bits(o0);
+            dst[1] = f32_to_f16_bits(o1);
+        }
+    } else if (i < qpairs + kpairs + vel) {
+        const uint32_t vi = i - qpairs - kpairs;
+        const uint32_t head = vi / kHD, d = vi % kHD;
+        vc[((uint64_t)head * ctx + pos) * kHD + d] = f32_to_f16_bits(qkv[(nq + nkv) * kHD + vi]);
+    }
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// One workgroup (4 waves) per (kv head g, chunk c).
+//  scores: 16 lanes per position (8 dims each, one 16-byte K load), 4
+//          positions per wave per step, all 4 query heads of the group;
+//  softmax: wave w takes head w over the chunk's 128 positions;
+//  values: lane owns dims 2l, 2l+1; wave w sums positions 32w .. 32w+31;
+//          the four waves' partial outputs are added in LDS.
+__global__ void __launch_bounds__(256)
+k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+               const uint16_t* __restrict__ vc, uint32_t len, uint32_t ctx, uint32_t nch, float scale,
+               float* __restrict__ po, float* __restrict__ pml) {
+    __shared__ float sc[kGroup][kChunk];
+    __shared__ float red[4][kGroup][kHD];
+    const uint32_t g = blockIdx.x, c = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15;
+    const uint32_t j0 = c * kChunk;
+
+    float qv[kGroup][8];
+#pragma unroll
+    for (int h = 0; h < kGroup; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[h][e] = q[(g * kGroup + h) * kHD + sub * 8 + e];
+
+#pragma unroll 2
+    for (uint32_t st = 0; st < kChunk / 16; st++) {
+        const uint32_t jl = st * 16 + wave * 4 + (lane >> 4);
+        const uint32_t j = j0 + jl;
+        float kf[8];
+        if (j < len) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(kc + ((uint64_t)g * ctx + j) * kHD + sub * 8);
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kf[2 * e] = half_bits_to_float(w[e] & 0xffffu);
+                kf[2 * e + 1] = half_bits_to_float(w[e] >> 16);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) kf[e] = 0.0f;
+        }
+#pragma unroll
+        for (int h = 0; h < kGroup; h++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) d = __builtin_fmaf(qv[h][e], kf[e], d);
+            d = faddv16(d);
+            if (sub == 0) sc[h][jl] = j < len ? d * scale : -INFINITY;
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t h = wave;
+        const float a = sc[h][lane], b = sc[h][lane + 64];
+        const float m = wave_max_f32(fmaxf(a, b));  // finite: position j0 < len
+        const float pa = expf(a - m), pb = expf(b - m);
+        const float l = wave_sum_f32(pa + pb);
+        sc[h][lane] = pa;
+        sc[h][lane + 64] = pb;
+        if (lane == 0) {
+            pml[((g * kGroup + h) * nch + c) * 2] = m;
+            pml[((g * kGroup + h) * nch + c) * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+    float o[kGroup][2];
+#pragma unroll
+    for (int h = 0; h < kGroup; h++) o[h][0] = o[h][1] = 0.0f;
+    for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
+        const uint32_t jl = wave * (kChunk / 4) + jj, j = j0 + jl;
+        if (j >= len) break;  // uniform across the wave
+        const uint32_t raw = *reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + j) * kHD + 2 * lane);
+        const float v0 = half_bits_to_float(raw & 0xffffu), v1 = half_bits_to_float(raw >> 16);
+#pragma unroll
+        for (int h = 0; h < kGroup; h++) {
+            const float p = sc[h][jl];
+            o[h][0] = __builtin_fmaf(p, v0, o[h][0]);
+            o[h][1] = __builtin_fmaf(p, v1, o[h][1]);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < kGroup; h++) {
+        red[wave][h][2 * lane] = o[h][0];
+        red[wave][h][2 * lane + 1] = o[h][1];
+    }
+    __syncthreads();
+    {
+        const uint32_t h = wave;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const uint32_t d = 2 * lane + e;
+            po[((g * kGroup + h) * nch + c) * kHD + d] = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kHD)
+k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint32_t nch,
+               float* __restrict__ out) {
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float* ml = pml + (uint64_t)h * nch * 2;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nch; c++) M = fmaxf(M, ml[2 * c]);
+    float L = 0.0f, O = 0.0f;
+    for (uint32_t c = 0; c < nch; c++) {
+        const float w = expf(ml[2 * c] - M);
+        L = __builtin_fmaf(ml[2 * c + 1], w, L);
+        O = __builtin_fmaf(po[((uint64_t)h * nch + c) * kHD + d], w, O);
+    }
+    out[h * kHD + d] = O / L;
+}
+
+__global__ void __launch_bounds__(256)
+k_silu_mul(uint32_t n, const float* __restrict__ gu, float* __restrict__ h) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float g = gu[i], u = gu[n + i];
+    h[i] = (g / (1.0f + expf(-g))) * u;
+}
+
+bool cfg_ok(const ane_decode_config* c) {
+    return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
+           c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->hidden % 32 == 0 && c->ffn % 32 == 0 &&
+           (uint64_t)c->n_heads * kHD % 32 == 0;
+}
+
+uint32_t n_chunks(uint32_t len) { return (len + kChunk - 1) / kChunk; }
+
+struct DecodeWs {
+    float *qkv, *attn, *gu, *h;
+    void* att;
+    size_t attb;
+};
+
+size_t layout(const ane_decode_config* c, uint8_t* base, DecodeWs* w) {
+    const uint64_t nqkv = (uint64_t)(c->n_heads + 2 * c->n_kv_heads) * kHD;
+    size_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const size_t o = off;
+        off += ceil_to(bytes, 256);
+        return base ? base + o : nullptr;
+    };
+    float* qkv = reinterpret_cast<float*>(take(nqkv * 4));
+    float* attn = reinterpret_cast<float*>(take((uint64_t)c->n_heads * kHD * 4));
+    float* gu = reinterpret_cast<float*>(take((uint64_t)2 * c->ffn * 4));
+    float* h = reinterpret_cast<float*>(take((uint64_t)c->ffn * 4));
+    const size_t attb = ane_hip_attention_workspace_size(c);
+    void* att = take(attb);
+    if (w) *w = DecodeWs{qkv, attn, gu, h, att, attb};
+    return off;
+}
+
+}  // namespace
+}  // namespace ane
+
+using namespace ane;
+
+extern "C" int ane_hip_rope_kv_append(const ane_decode_config* cfg, float* qkv, const float* rope_table,
+                                      uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, void* stream) {
+    if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
+    if (!qkv || !rope_table || !k_cache || !v_cache) return ANE_ERR_BAD_POINTER;
+    if (pos >= cfg->ctx) return ANE_ERR_INVALID_ARG;
+    const uint64_t n = (uint64_t)(cfg->n_heads + cfg->n_kv_heads) * (kHD / 2) + (uint64_t)cfg->n_kv_heads * kHD;
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       qkv, cfg->n_heads, cfg->n_kv_heads, rope_table + (uint64_t)pos * kHD, pos, cfg->ctx,
+                       k_cache, v_cache);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" size_t ane_hip_attention_workspace_size(const ane_decode_config* cfg) {
+    if (!cfg) return 0;
+    const uint64_t nch = n_chunks(cfg->ctx);
+    return (size_t)(ceil_to((uint64_t)cfg->n_heads * nch * kHD * 4, 256) + ceil_to((uint64_t)cfg->n_heads * nch * 8, 256));
+}
+
+extern "C" int ane_hip_attention_decode(const ane_decode_config* cfg, const float* q, const uint16_t* k_cache,
+                                        const uint16_t* v_cache, uint32_t len, float* out, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
+    if (!q || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
+    if (len == 0 || len > cfg->ctx) return ANE_ERR_INVALID_ARG;
+    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ane_hip_attention_workspace_size(cfg))
+        return ANE_ERR_WORKSPACE;
+    const uint32_t nch = n_chunks(len);
+    const uint64_t nch_max = n_chunks(cfg->ctx);
+    float* po = static_cast<float*>(workspace);
+    float* pml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                          ceil_to((uint64_t)cfg->n_heads * nch_max * kHD * 4, 256));
+    hipStream_t s = (hipStream_t)stream;
+    const float scale = 1.0f / sqrtf((float)kHD);
+    hipLaunchKernelGGL(k_attn_partial, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, k_cache, v_cache, len,
+                       cfg->ctx, nch, scale, po, pml);
+    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, po, pml, nch, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream) {
+    if (n == 0) return ANE_OK;
+    if (!gu || !h) return ANE_ERR_BAD_POINTER;
+    hipLaunchKernelGGL(k_silu_mul, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, n, gu, h);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" size_t ane_decode_workspace_size(const ane_decode_config* cfg) {
+    if (!cfg_ok(cfg)) return 0;
+    return layout(cfg, nullptr, nullptr);
+}
+
+extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_layer* layers,
+                                const float* rope_table, uint32_t pos, float* x, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+    if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
+    if (!layers || !rope_table || !x) return ANE_ERR_BAD_POINTER;
+    if (pos >= cfg->ctx) return ANE_ERR_INVALID_ARG;
+    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < layout(cfg, nullptr, nullptr))
+        return ANE_ERR_WORKSPACE;
+    DecodeWs w;
+    layout(cfg, static_cast<uint8_t*>(workspace), &w);
+    const uint32_t H = cfg->hidden, F = cfg->ffn;
+    const uint32_t nq = cfg->n_heads * kHD;
+    const uint32_t nqkv = (cfg->n_heads + 2 * cfg->n_kv_heads) * kHD;
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
+        const ane_decode_layer& L = layers[l];
+        int st;
+        if ((st = ane_hip_q8_0_matvec_fused(nqkv, H, x, L.attn_norm, cfg->eps, L.w_qkv, nullptr, w.qkv, stream)))
+            return st;
+        if ((st = ane_hip_rope_kv_append(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, stream))) return st;
+        if ((st = ane_hip_attention_decode(cfg, w.qkv, L.k_cache, L.v_cache, pos + 1, w.attn, w.att, w.attb,
+                                           stream)))
+            return st;
+        if ((st = ane_hip_q8_0_matvec_fused(H, nq, w.attn, nullptr, 0.0f, L.w_o, x, x, stream))) return st;
+        if ((st = ane_hip_q8_0_matvec_fused(2 * F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, nullptr, w.gu, stream)))
+            return st;
+        if ((st = ane_hip_silu_mul(F, w.gu, w.h, stream))) return st;
+        if ((st = ane_hip_q8_0_matvec_fused(H, F, w.h, nullptr, 0.0f, L.w_down, x, x, stream))) return st;
+    }
+    return ANE_OK;
+}

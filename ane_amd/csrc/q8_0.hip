@@ -16,6 +16,7 @@
 //    the activations fit in LDS;
 //  * general kernels (k_q8_0_gemv_r, k_q8_0_quantize_x + k_q8_0_mul_mat_g)
 //    for everything else.
+#include "../../include/ane_decode.h"
 #include "common.hpp"
 
 namespace ane {
@@ -122,8 +123,9 @@ k_q8_0_mul_mat_g(uint32_t N, uint32_t nb, uint32_t T, const int8_t* __restrict__
 //    ring of S stages private to the wave: each copy wave-instruction moves
 //    1 KB of consecutive bytes of one or two rows, so HBM sees fully
 //    coalesced reads, and no VGPRs or workgroup barriers are spent on
-//    staging.  Item i+S-1 is issued before item i is computed; items past
-//    the end issue all-out-of-range copies so the s_waitcnt count is fixed.
+//    staging.  S items are issued before the activation prologue; after item
+//    i is computed its stage is refilled with item i+S.  Items past the end
+//    issue all-out-of-range copies so the s_waitcnt count is fixed.
 //  * Staged rows sit SB*17/8 + pad chunks apart, 16 or 48 dwords mod 64, so
 //    the four groups' block reads (dword offsets 17(l/2) + 8(l%2), distinct
 //    mod 16) never share an LDS bank.
@@ -141,15 +143,34 @@ constexpr uint32_t kXBatch = 8;    // activation float4 loads in flight per thre
 
 enum { kModeR = 0, kModeG = 1 };
 
+// LDS bytes of the activation region (G: qx then fp32 scales; R: fp32 x),
+// rounded to 16; the fp64 reduction slots of the norm fusion follow it.
+__host__ __device__ __forceinline__ uint32_t stream_x_bytes(int mode, uint32_t nb, uint32_t T) {
+    const uint64_t xb = mode == kModeG ? ceil_to((uint64_t)T * nb * 32, 16) + (uint64_t)T * nb * 4
+                                       : (uint64_t)nb * 32 * 4;
+    return (uint32_t)ceil_to(xb, 16);
+}
+
 template <int SB>
 struct Seg {
     static_assert(SB % 16 == 0, "segment length must be a multiple of 16 blocks");
     static constexpr uint32_t kCpr = SB * 17 / 8;              // 16-byte chunks per row segment
     static constexpr uint32_t kPad = SB == 32 ? 0 : 4;         // staged stride = 16 or 48 dwords mod 64
     static constexpr uint32_t kRowChunks = kCpr + kPad;
-    static constexpr uint32_t kDma = (kUnitRows * kRowChunks + 63) / 64;
-    static constexpr uint32_t kStageBytes = kDma * 1024;
+    static constexpr uint32_t kStageChunks = kUnitRows * kRowChunks;
+    static constexpr uint32_t kDma = (kStageChunks + 63) / 64;          // copy wave-instructions per item
+    static constexpr uint32_t kLastLanes = kStageChunks - 64 * (kDma - 1);  // lanes of the last one
+    static constexpr uint32_t kStageBytes = kStageChunks * 16;
 };
+
+// One copy wave-instruction j of an item: the last one runs only its first
+// kLastLanes lanes, so a stage holds exactly kStageChunks chunks.
+template <int SB>
+__device__ __forceinline__ void copy_chunk(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t j,
+                                           uint32_t lane, uint32_t voffset) {
+    if (Seg<SB>::kLastLanes == 64 || j + 1 < Seg<SB>::kDma || lane < Seg<SB>::kLastLanes)
+        copy16_to_lds(w, stage + j * 1024, voffset);
+}
 
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
@@ -170,13 +191,13 @@ __device__ __forceinline__ void full_offsets(uint32_t lane, uint32_t rb, uint32_
 // chunk is live iff its row is below rows_live, i.e. off < rows_live * rb
 // (pad offsets exceed every such bound).
 template <int SB>
-__device__ __forceinline__ void issue_full(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t base,
+__device__ __forceinline__ void issue_full(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t lane, uint32_t base,
                                            uint32_t rows_live, uint32_t rb,
                                            const uint32_t (&off)[Seg<SB>::kDma]) {
     const uint32_t lim = rows_live * rb;
 #pragma unroll
     for (uint32_t j = 0; j < Seg<SB>::kDma; j++)
-        copy16_to_lds(w, stage + j * 1024, off[j] < lim ? base + off[j] : 0x80000000u);
+        copy_chunk<SB>(w, stage, j, lane, off[j] < lim ? base + off[j] : 0x80000000u);
 }
 
 // The last, shorter segment of a row (nb % SB blocks): staged stride
@@ -192,7 +213,7 @@ __device__ __forceinline__ void issue_partial(__amdgpu_buffer_rsrc_t w, int8_t* 
         const uint32_t c = j * 64 + lane;
         const uint32_t g = c / rc, cc = c - g * rc;
         const bool live = g < rows_live && cc < cpr;
-        copy16_to_lds(w, stage + j * 1024, live ? base + g * rb + cc * 16 : 0x80000000u);
+        copy_chunk<SB>(w, stage, j, lane, live ? base + g * rb + cc * 16 : 0x80000000u);
     }
 }
 
@@ -230,6 +251,16 @@ struct XStage {
                            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 4, 0, 0)),
                            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 8, 0, 0)),
                            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 12, 0, 0)));
+    }
+
+    // G mode, one token: the norm weights at the same elements as load(p).
+    __device__ __forceinline__ float4 load_w(uint32_t p, __amdgpu_buffer_rsrc_t wr) const {
+        const uint32_t blk = p * kPerPass + (threadIdx.x >> 3);
+        const uint32_t o = blk < n ? (blk * 32 + (threadIdx.x & 7) * 4) * 4 : 0x80000000u;
+        return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, o + 4, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, o + 8, 0, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, o + 12, 0, 0)));
     }
 
     __device__ __forceinline__ void store(uint32_t p, float4 f) const {
@@ -321,12 +352,46 @@ __device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint3
     return acc;
 }
 
-template <int MODE, int NW, int SB, int S, int TT>
+// Optional fusions of the G-mode single-token kernel (the decode step):
+//  kFuseNorm: x' = fl(fl(x * inv) * w) with inv = 1 / sqrt(fl(fl(ss / K) + eps)),
+//    ss = sum of x^2 accumulated in fp64 (every x^2 is exact in fp64, so the
+//    fp32 value of ss / K does not depend on the summation order), then x' is
+//    quantized as usual;
+//  kFuseResidual: y[n] = fl(FADDV(p) + r[n]) (r may alias y: each row is read
+//    and written by the one lane that owns it).
+enum { kFuseNorm = 1, kFuseResidual = 2 };
+
+struct StreamFuse {
+    const float* norm_w;
+    float eps;
+    const float* residual;
+};
+
+template <int NW>
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    wait_lgkmcnt0();
+    lds_barrier();
+    double s = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) s += red[w];
+    return s;
+}
+
+__device__ __forceinline__ float rms_inv(double ss, uint32_t K, float eps) {
+    const float ms = (float)(ss / (double)K);
+    return 1.0f / sqrtf(ms + eps);
+}
+
+template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0>
 __global__ void __launch_bounds__(NW * 64)
 k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __restrict__ x,
-              const uint8_t* __restrict__ W, float* __restrict__ y, uint32_t total_waves) {
+              const uint8_t* __restrict__ W, float* y, uint32_t total_waves, StreamFuse fz) {
     using G = Seg<SB>;
-    static_assert((S - 1) * G::kDma < 64, "copies in flight exceed the vmcnt range");
+    static_assert(FUSE == 0 || (MODE == kModeG && TT == 1), "fusions are for the G-mode decode step");
+    static_assert(S * G::kDma < 64, "copies in flight exceed the vmcnt range");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, grp = lane >> 4, l = lane & 15;
@@ -350,7 +415,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
         const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
         int8_t* stage = ring + (i % S) * G::kStageBytes;
         const uint32_t base = row0 * rb + s * (SB * 34);
-        if (sbk == (uint32_t)SB) issue_full<SB>(rsrc, stage, base, rows_live, rb, off);
+        if (sbk == (uint32_t)SB) issue_full<SB>(rsrc, stage, lane, base, rows_live, rb, off);
         else issue_partial<SB>(rsrc, stage, lane, base, rows_live, rb, sbk);
     };
 
@@ -360,14 +425,44 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     const XStage<MODE, NW * 64> xst{make_rsrc(x, T * K * 4), K, nb, T, MODE == kModeG ? nb * T : nb * 8,
                                     xlds, dxs};
     const uint32_t npass = xst.passes();
+    // residual values of this wave's rows (at most 64, one per lane), loaded
+    // first so the epilogue never waits on the ring's copies
+    float rv = 0.0f;
+    if (FUSE & kFuseResidual) {
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(fz.residual, N * 4);
+        rv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, r0 + lane < r1 ? (r0 + lane) * 4 : 0x80000000u, 0, 0));
+    }
     float4 xv[kXBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
+    float4 wv[(FUSE & kFuseNorm) ? kXBatch : 1];
+    if (FUSE & kFuseNorm) {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(fz.norm_w, K * 4);
 #pragma unroll
-    for (int i = 0; i < S - 1; i++) issue(i);
+        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load_w(k, wr);
+    }
+#pragma unroll
+    for (int i = 0; i < S; i++) issue(i);
+    if (FUSE & kFuseNorm) {  // the host guarantees npass <= kXBatch
+        double ss = 0.0;
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 f = xv[k];  // lanes past the end hold zeros
+            ss += (double)f.x * f.x + (double)f.y * f.y + (double)f.z * f.z + (double)f.w * f.w;
+        }
+        ss = block_sum_f64<NW>(ss, reinterpret_cast<double*>(xlds + stream_x_bytes(MODE, nb, T)));
+        const float inv = rms_inv(ss, K, fz.eps);
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 f = xv[k], w4 = wv[k];
+            xv[k] = make_float4(__fmul_rn(__fmul_rn(f.x, inv), w4.x), __fmul_rn(__fmul_rn(f.y, inv), w4.y),
+                                __fmul_rn(__fmul_rn(f.z, inv), w4.z), __fmul_rn(__fmul_rn(f.w, inv), w4.w));
+        }
+    }
 #pragma unroll
     for (uint32_t k = 0; k < kXBatch; k++)
         if (k < npass) xst.store(k, xv[k]);
+    if (FUSE & kFuseResidual) asm volatile("" ::"v"(rv));  // its load completes here
     for (uint32_t p0 = kXBatch; p0 < npass; p0 += kXBatch) {
 #pragma unroll
         for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(p0 + k);
@@ -382,9 +477,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
 #pragma unroll
     for (int t = 0; t < TT; t++) p[t] = 0.0f;
     for (uint32_t i = 0; i < nitems; i++) {
-        wait_lgkmcnt0();  // reads of the stage about to be refilled are done
-        issue(i + S - 1);
-        wait_vmcnt<(S - 1) * G::kDma>();  // item i has landed
+        wait_vmcnt<(S - 1) * G::kDma>();  // item i has landed (items i+1 .. i+S-1 may be in flight)
         const uint32_t u = i / nseg, s = i - u * nseg;
         const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
         const int8_t* rowp = ring + (i % S) * G::kStageBytes + grp * (sbk * 17 / 8 + G::kPad) * 16;
@@ -402,10 +495,13 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
             const uint32_t row = r0 + kUnitRows * u + grp;
 #pragma unroll
             for (int t = 0; t < TT; t++) {
-                const float v = faddv16(p[t]);
+                float v = faddv16(p[t]);
+                if (FUSE & kFuseResidual) v = v + __shfl(rv, (int)(kUnitRows * u + grp), kWave);
                 if (l == 0 && row < r1 && (TT == 1 || t < (int)T)) y[(uint64_t)t * N + row] = v;
             }
         }
+        wait_lgkmcnt0();  // this stage's LDS reads are done before it is refilled
+        issue(i + S);
     }
     wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
 }
@@ -420,9 +516,7 @@ bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void
 
 template <int MODE, int NW, int SB, int S>
 uint64_t stream_lds(uint32_t nb, uint32_t T) {
-    const uint64_t xb = MODE == kModeG ? ceil_to((uint64_t)T * nb * 32, 16) + (uint64_t)T * nb * 4
-                                       : (uint64_t)nb * 32 * 4;
-    return (uint64_t)NW * S * Seg<SB>::kStageBytes + ceil_to(xb, 16);
+    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW;
 }
 
 int cu_count(int dev) {
@@ -438,13 +532,13 @@ int cu_count(int dev) {
 
 // Launches one configuration if its LDS fits; returns -1 if it does not.
 // Occupancy is queried once per (device, LDS size).
-template <int MODE, int NW, int SB, int S, int TT>
+template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0>
 int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W,
-               float* y, hipStream_t s) {
+               float* y, hipStream_t s, StreamFuse fz = StreamFuse{nullptr, 0.0f, nullptr}) {
     const uint64_t lds64 = stream_lds<MODE, NW, SB, S>(nb, T);
     if (lds64 > kLdsLimit) return -1;
     const uint32_t lds = (uint32_t)lds64;
-    auto fn = k_q8_0_stream<MODE, NW, SB, S, TT>;
+    auto fn = k_q8_0_stream<MODE, NW, SB, S, TT, FUSE>;
     static int occ_cache[64];
     static uint32_t occ_lds[64];
     int dev = 0;
@@ -466,8 +560,11 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     const uint64_t need = (units + NW - 1) / NW;
     if (grid > need) grid = need;
     if (grid < 1) grid = 1;
+    // the residual fusion holds one row per lane: at most 64 rows per wave
+    if ((FUSE & kFuseResidual) && ((uint64_t)N + grid * NW - 1) / (grid * NW) > 64) return -1;
+    if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
-                       (const uint8_t*)W, y, (uint32_t)(grid * NW));
+                       (const uint8_t*)W, y, (uint32_t)(grid * NW), fz);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -515,6 +612,23 @@ extern "C" int ane_hip_q8_0_gemv(uint32_t M, uint32_t K, const float* x, const v
                        (const uint8_t*)W, y);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
+}
+
+extern "C" int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x, const float* norm_w,
+                                         float eps, const void* W, const float* residual, float* y,
+                                         void* stream) {
+    if (N == 0) return ANE_OK;
+    const uint32_t nb = K >> 5;
+    if (!y || !x || !W || (K & 31)) return ANE_ERR_BAD_POINTER;
+    if (!stream_eligible(N, nb, K, 1, W)) return ANE_ERR_INVALID_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    const StreamFuse fz{norm_w, eps, residual};
+    int r;
+    if (norm_w && residual) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseNorm | kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
+    else if (norm_w) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseNorm>(N, nb, K, 1, x, W, y, s, fz);
+    else if (residual) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
+    else r = try_stream<kModeG, ANE_Q8_G_CFG, 1>(N, nb, K, 1, x, W, y, s);
+    return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {

@@ -1,0 +1,100 @@
+/*
+ * ane_decode.h -- single-token decode of a Llama-shaped model on MI355X with
+ * every matrix product on the Q8_0 kernels of ane_hip.h (G mode).
+ *
+ * This is the driver around the GGML_OP_MUL_MAT hook: the steps on either
+ * side of mul_mat in one decoder layer, as a ggml graph of a Llama model
+ * runs them (the reference has SME kernels for these steps:
+ * bytecode_interpreter.s:6508 rms_norm, 6617 silu, 6714 rope (adjacent
+ * pairs, out[2i] = in[2i] cos - in[2i+1] sin), 11657 flash_attention; its
+ * ggml backend routes MUL_MAT to the quantized path,
+ * src/ggml-backend/ggml-ane.cpp:119-154):
+ *
+ *   qkv  = W_qkv . q8(rmsnorm(x) * attn_norm)       fused norm prologue
+ *   rope(q, k) at pos; k, v -> fp16 KV cache at pos
+ *   attn = softmax(q k^T / sqrt(d)) v over positions 0..pos (GQA)
+ *   x    = x + W_o . q8(attn)                        fused residual epilogue
+ *   gu   = W_gate_up . q8(rmsnorm(x) * ffn_norm)     fused norm prologue
+ *   h    = silu(gate) * up
+ *   x    = x + W_down . q8(h)                        fused residual epilogue
+ *
+ * Layouts: weights are Q8_0 rows (ggml block layout) with the output
+ * features as rows: W_qkv rows [q heads | k heads | v heads], W_gate_up rows
+ * [gate | up].  KV cache: fp16 [n_kv_heads][ctx][head_dim].  RoPE table:
+ * fp32 [ctx][head_dim/2][2] = (cos, sin) of pos * base^(-2i/head_dim),
+ * applied to adjacent pairs (x[2i], x[2i+1]).  All pointers are device
+ * memory; the layer array itself is host memory.
+ */
+#ifndef ANE_DECODE_H
+#define ANE_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+struct ane_decode_config {
+    uint32_t n_layers;
+    uint32_t hidden;      /* model width (4096)                 */
+    uint32_t ffn;         /* feed-forward width (14336)         */
+    uint32_t n_heads;     /* query heads (32)                   */
+    uint32_t n_kv_heads;  /* key/value heads (8)                */
+    uint32_t head_dim;    /* 128 (the only supported value)     */
+    uint32_t ctx;         /* KV cache capacity in positions     */
+    float eps;            /* RMSNorm epsilon                    */
+};
+
+struct ane_decode_layer {
+    const void* w_qkv;      /* Q8_0 [(n_heads + 2 n_kv_heads) head_dim][hidden] */
+    const void* w_o;        /* Q8_0 [hidden][n_heads head_dim]                  */
+    const void* w_gate_up;  /* Q8_0 [2 ffn][hidden]                             */
+    const void* w_down;     /* Q8_0 [hidden][ffn]                               */
+    const float* attn_norm; /* [hidden]                                         */
+    const float* ffn_norm;  /* [hidden]                                         */
+    uint16_t* k_cache;      /* fp16 [n_kv_heads][ctx][head_dim]                 */
+    uint16_t* v_cache;      /* fp16 [n_kv_heads][ctx][head_dim]                 */
+};
+
+/* Device workspace bytes for ane_decode_token (256-byte aligned sections). */
+size_t ane_decode_workspace_size(const struct ane_decode_config* cfg);
+
+/* One token at position pos (< ctx) through every layer: x (fp32 [hidden],
+ * the residual stream) is updated in place, and k/v of pos are written into
+ * each layer's cache; positions 0..pos of the caches are attended to.
+ * Asynchronous on stream; returns an ane_status. */
+int ane_decode_token(const struct ane_decode_config* cfg, const struct ane_decode_layer* layers,
+                     const float* rope_table, uint32_t pos, float* x, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* The steps of ane_decode_token, for tests and for callers that schedule
+ * them differently.  All asynchronous on stream. */
+
+/* Q8_0 matvec (G mode, one token) with optional fusions: norm_w != NULL
+ * applies x' = x * inv_rms(x) * norm_w before quantizing (inv_rms =
+ * 1/sqrt(fl(fl(sum x^2 / K) + eps)), sum in fp64); residual != NULL adds
+ * residual[n] to each output (residual may equal y). */
+int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x, const float* norm_w, float eps,
+                              const void* W, const float* residual, float* y, void* stream);
+
+/* RoPE on the q and k heads of qkv (in place for q), then k and v of this
+ * position converted to fp16 into the caches. */
+int ane_hip_rope_kv_append(const struct ane_decode_config* cfg, float* qkv, const float* rope_table,
+                           uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, void* stream);
+
+/* out[h] = softmax(q[h] . K[g]^T / sqrt(head_dim)) V[g] over positions
+ * 0..len-1, g = h / (n_heads / n_kv_heads).  q: fp32 [n_heads][head_dim]. */
+size_t ane_hip_attention_workspace_size(const struct ane_decode_config* cfg);
+int ane_hip_attention_decode(const struct ane_decode_config* cfg, const float* q, const uint16_t* k_cache,
+                             const uint16_t* v_cache, uint32_t len, float* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* h[i] = silu(gu[i]) * gu[n + i], i < n. */
+int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ANE_DECODE_H */

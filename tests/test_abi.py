@@ -1,6 +1,6 @@
 """The C-ABI boundary without a GPU: exports, byte encoding, decoder errors.
 
-Covers include/ane_hip.h and include/ggml-ane-hip.h (every declared function is exported by
+Covers include/ane_hip.h, ggml-ane-hip.h and ane_decode.h (every declared function is exported by
 libane_amd.so), the Python mirror of ane::dispatch against the C++ header
 (include/ane/ane.hpp compiled with g++), and the decoder's error paths that
 return before any HIP call.
@@ -17,7 +17,7 @@ import ane_amd
 from ane_amd import Op, boolean, encode, f32, i32, ptr, u32
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADERS = [ROOT / "include" / "ane_hip.h", ROOT / "include" / "ggml-ane-hip.h"]
+HEADERS = [ROOT / "include" / "ane_hip.h", ROOT / "include" / "ggml-ane-hip.h", ROOT / "include" / "ane_decode.h"]
 
 
 def declared_functions() -> list[str]:

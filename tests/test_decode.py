@@ -1,0 +1,247 @@
+"""The decode step (include/ane_decode.h, ane_amd/csrc/decode.hip and the
+fused variants of the streaming Q8_0 kernel).
+
+Bit-exact against numpy + the oracle: the fused RMSNorm / residual matvec
+(fp32 ops and the G-mode definition), RoPE and the fp16 KV append.
+Tolerance against float64 references (the GPU uses expf): attention
+(rtol 2e-5, atol 1e-6), SiLU * up (rtol 1e-6), and a 2-layer model over
+several tokens (relative L2 error of the residual stream < 1e-3: a
+last-ulp difference after expf can move one activation across an int8
+rounding boundary of the next layer's quantizer).
+"""
+import ctypes
+import shutil
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import ane_amd
+from tests import data
+
+ROOT = Path(__file__).resolve().parents[1]
+F32 = np.float32
+
+
+# ------------------------------------------------------------------ references
+def np_rmsnorm(x, w, eps):
+    ss = np.sum(np.asarray(x, np.float64) ** 2)
+    ms = np.float32(ss / x.size)
+    inv = np.float32(1.0) / np.sqrt(np.float32(ms + np.float32(eps)))
+    return ((np.asarray(x, F32) * inv).astype(F32) * np.asarray(w, F32)).astype(F32)
+
+
+def np_rope(v, cs):
+    """v: [heads][128] fp32; cs: [64][2] fp32; adjacent pairs, fp32 ops."""
+    a, b = v[:, 0::2], v[:, 1::2]
+    c, s = cs[:, 0], cs[:, 1]
+    out = np.empty_like(v)
+    out[:, 0::2] = ((a * c).astype(F32) - (b * s).astype(F32)).astype(F32)
+    out[:, 1::2] = ((a * s).astype(F32) + (b * c).astype(F32)).astype(F32)
+    return out
+
+
+def np_attention(q, kc, vc, length, n_heads, n_kv):
+    """q [n_heads][128] fp32, caches fp16 [n_kv][ctx][128] -> fp64 softmax attention."""
+    G = n_heads // n_kv
+    out = np.zeros((n_heads, 128))
+    for h in range(n_heads):
+        g = h // G
+        k = kc[g, :length].astype(np.float64)
+        v = vc[g, :length].astype(np.float64)
+        s = k @ q[h].astype(np.float64) / np.sqrt(128.0)
+        p = np.exp(s - s.max())
+        out[h] = (p @ v) / p.sum()
+    return out
+
+
+def np_silu_mul(gu, n):
+    g = gu[:n].astype(np.float64)
+    return g / (1.0 + np.exp(-g)) * gu[n:2 * n].astype(np.float64)
+
+
+# ------------------------------------------------------------------ CPU
+def test_struct_layouts_match_c(tmp_path):
+    gcc = shutil.which("gcc")
+    if not gcc:
+        pytest.skip("gcc not available")
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "ane_decode.h"\n'
+        "int main(void) { printf(\"%zu %zu %zu %zu\\n\", sizeof(struct ane_decode_config),"
+        " offsetof(struct ane_decode_config, eps), sizeof(struct ane_decode_layer),"
+        " offsetof(struct ane_decode_layer, v_cache)); return 0; }\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    C, L = ane_amd.DecodeConfig, ane_amd.DecodeLayer
+    assert got == [ctypes.sizeof(C), C.eps.offset, ctypes.sizeof(L), L.v_cache.offset]
+
+
+def test_workspace_sizes():
+    L = ane_amd.lib()
+    cfg = ane_amd.DecodeConfig(32, 4096, 14336, 32, 8, 128, 4096, 1e-5)
+    assert L.ane_decode_workspace_size(ctypes.byref(cfg)) >= 4 * (6144 + 4096 + 2 * 14336 + 14336)
+    assert L.ane_hip_attention_workspace_size(ctypes.byref(cfg)) >= 32 * 32 * 128 * 4
+    bad = ane_amd.DecodeConfig(32, 4096, 14336, 32, 8, 64, 4096, 1e-5)  # head_dim 64 unsupported
+    assert L.ane_decode_workspace_size(ctypes.byref(bad)) == 0
+
+
+# ------------------------------------------------------------------ GPU
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,norm,resid", [(6144, 4096, True, False), (4096, 4096, False, True),
+                                            (4096, 14336, False, True), (28672, 4096, True, False),
+                                            (512, 1024, True, True), (300, 256, False, False)])
+def test_matvec_fused_exact(ane, oracle, N, K, norm, resid):
+    import torch
+
+    W = data.q8_0_weights(N, K, seed=N + K)
+    x = data.activations(1, K, seed=7)[0] * F32(3.0)
+    w = (1.0 + 0.1 * data.activations(1, K, seed=8)[0]).astype(F32)
+    r = data.activations(1, N, seed=9)[0]
+    eps = F32(1e-5)
+    xin = np_rmsnorm(x, w, eps) if norm else x
+    oracle.set_threads(0)
+    try:
+        ref = oracle.q8_0_mul_mat_g(N, K, 1, xin, W)[0]
+    finally:
+        oracle.set_threads(1)
+    if resid:
+        ref = (ref + r).astype(F32)
+    y = dev(r) if resid else torch.zeros(N, dtype=torch.float32, device="cuda")
+    ane.q8_0_matvec_fused(N, K, dev(x), dev(W), y, norm_w=dev(w) if norm else None, eps=float(eps),
+                          residual=y if resid else None)
+    assert host(y).tobytes() == ref.tobytes()
+
+
+@pytest.mark.gpu
+def test_rope_kv_append_exact(ane):
+    import torch
+
+    cfg = ane.DecodeConfig(1, 1024, 2048, 8, 2, 128, 16, 1e-5)
+    table = ane.rope_table(16)
+    qkv = data.activations(1, (8 + 4) * 128, seed=3)[0]
+    kc = torch.zeros((2, 16, 128), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((2, 16, 128), dtype=torch.float16, device="cuda")
+    qd = dev(qkv)
+    ane.rope_kv_append(cfg, qd, dev(table), 5, kc, vc)
+    q_ref = np_rope(qkv[:1024].reshape(8, 128), table[5])
+    k_ref = np_rope(qkv[1024:1280].reshape(2, 128), table[5]).astype(np.float16)
+    v_ref = qkv[1280:].reshape(2, 128).astype(np.float16)
+    got = host(qd)
+    assert got[:1024].tobytes() == q_ref.reshape(-1).tobytes()
+    assert got[1024:].tobytes() == qkv[1024:].tobytes()  # k and v stay unrotated in qkv
+    kh, vh = host(kc), host(vc)
+    assert kh[:, 5].tobytes() == k_ref.tobytes() and vh[:, 5].tobytes() == v_ref.tobytes()
+    assert not kh[:, :5].any() and not kh[:, 6:].any()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("length", [1, 100, 128, 129, 1000, 4096])
+def test_attention_decode(ane, length):
+    import torch
+
+    cfg = ane.DecodeConfig(1, 4096, 14336, 32, 8, 128, 4096, 1e-5)
+    g = np.random.default_rng(length)
+    kc = g.standard_normal((8, 4096, 128)).astype(np.float16)
+    vc = g.standard_normal((8, 4096, 128)).astype(np.float16)
+    q = (g.standard_normal((32, 128)) * 2.0).astype(F32)
+    out = torch.zeros(32 * 128, dtype=torch.float32, device="cuda")
+    ane.attention_decode(cfg, dev(q), dev(kc), dev(vc), length, out)
+    ref = np_attention(q, kc, vc, length, 32, 8)
+    np.testing.assert_allclose(host(out).reshape(32, 128), ref, rtol=2e-5, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_silu_mul(ane):
+    import torch
+
+    n = 14336
+    gu = (data.activations(1, 2 * n, seed=4)[0] * 4.0).astype(F32)
+    h = torch.zeros(n, dtype=torch.float32, device="cuda")
+    ane.silu_mul(n, dev(gu), h)
+    np.testing.assert_allclose(host(h), np_silu_mul(gu, n), rtol=1e-6, atol=1e-30)
+
+
+def small_model(seed=0, layers=2, hidden=512, ffn=1024, n_heads=8, n_kv=2, ctx=64):
+    g = np.random.default_rng(seed)
+    nqkv = (n_heads + 2 * n_kv) * 128
+    m = []
+    for l in range(layers):
+        m.append({
+            "w_qkv": data.q8_0_weights(nqkv, hidden, seed=100 * l + 1),
+            "w_o": data.q8_0_weights(hidden, n_heads * 128, seed=100 * l + 2),
+            "w_gate_up": data.q8_0_weights(2 * ffn, hidden, seed=100 * l + 3),
+            "w_down": data.q8_0_weights(hidden, ffn, seed=100 * l + 4),
+            "attn_norm": (1.0 + 0.1 * g.standard_normal(hidden)).astype(F32),
+            "ffn_norm": (1.0 + 0.1 * g.standard_normal(hidden)).astype(F32),
+        })
+    return m
+
+
+def np_decode_token(oracle, cfg, m, caches, table, pos, x):
+    H, F, nh, nkv = cfg.hidden, cfg.ffn, cfg.n_heads, cfg.n_kv_heads
+    nq = nh * 128
+    for l, L in enumerate(m):
+        kc, vc = caches[l]
+        xn = np_rmsnorm(x, L["attn_norm"], cfg.eps)
+        qkv = oracle.q8_0_mul_mat_g((nh + 2 * nkv) * 128, H, 1, xn, L["w_qkv"])[0]
+        q = np_rope(qkv[:nq].reshape(nh, 128), table[pos])
+        kc[:, pos] = np_rope(qkv[nq:nq + nkv * 128].reshape(nkv, 128), table[pos]).astype(np.float16)
+        vc[:, pos] = qkv[nq + nkv * 128:].reshape(nkv, 128).astype(np.float16)
+        attn = np_attention(q, kc, vc, pos + 1, nh, nkv).astype(F32).reshape(-1)
+        x = (x + oracle.q8_0_mul_mat_g(H, nq, 1, attn, L["w_o"])[0]).astype(F32)
+        xn = np_rmsnorm(x, L["ffn_norm"], cfg.eps)
+        gu = oracle.q8_0_mul_mat_g(2 * F, H, 1, xn, L["w_gate_up"])[0]
+        h = np_silu_mul(gu, F).astype(F32)
+        x = (x + oracle.q8_0_mul_mat_g(H, F, 1, h, L["w_down"])[0]).astype(F32)
+    return x
+
+
+@pytest.mark.gpu
+def test_decode_tokens_small_model(ane, oracle):
+    import torch
+
+    cfg = ane.DecodeConfig(2, 512, 1024, 8, 2, 128, 64, 1e-5)
+    m = small_model()
+    table = ane.rope_table(64)
+    keep = []
+    layers = (ane.DecodeLayer * cfg.n_layers)()
+    dev_caches = []
+    for l, L in enumerate(m):
+        t = {k: dev(v) for k, v in L.items()}
+        kc = torch.zeros((2, 64, 128), dtype=torch.float16, device="cuda")
+        vc = torch.zeros((2, 64, 128), dtype=torch.float16, device="cuda")
+        keep += [t, kc, vc]
+        dev_caches.append((kc, vc))
+        layers[l] = ane.DecodeLayer(*[t[k].data_ptr() for k in ("w_qkv", "w_o", "w_gate_up", "w_down",
+                                                                  "attn_norm", "ffn_norm")],
+                                    kc.data_ptr(), vc.data_ptr())
+    ws = torch.empty(ane.lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
+    x0 = data.activations(5, 512, seed=21).astype(F32)
+    xd = torch.zeros(512, dtype=torch.float32, device="cuda")
+    tab = dev(table)
+    np_caches = [(np.zeros((2, 64, 128), np.float16), np.zeros((2, 64, 128), np.float16)) for _ in m]
+    for pos in range(5):
+        xd.copy_(dev(x0[pos]))
+        ane.decode_token(cfg, layers, tab, pos, xd, ws)
+        ref = np_decode_token(oracle, cfg, m, np_caches, table, pos, x0[pos])
+        got = host(xd)
+        err = np.linalg.norm(got.astype(np.float64) - ref) / np.linalg.norm(ref)
+        assert err < 1e-3, (pos, err)
+        if pos == 0:  # first layer, first token: every step before attention is exact
+            assert host(dev_caches[0][0])[:, 0].tobytes() == np_caches[0][0][:, 0].tobytes()
