@@ -101,6 +101,8 @@ EXPORTS = (
     "ane_hip_attention_workspace_size",
     "ane_hip_attention_decode",
     "ane_hip_silu_mul",
+    "ane_hip_q8_0_matvec_silu",
+    "ane_hip_attention_decode_rope",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -160,6 +162,8 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_hip_attention_workspace_size": (_c.c_size_t, [_P]),
     "ane_hip_attention_decode": (_c.c_int, [_P, _P, _P, _P, _c.c_uint32, _P, _P, _c.c_size_t, _P]),
     "ane_hip_silu_mul": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
+    "ane_hip_q8_0_matvec_silu": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
+    "ane_hip_attention_decode_rope": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _P, _P, _c.c_size_t, _P]),
 }
 
 
@@ -525,6 +529,21 @@ def attention_decode(cfg, q, k_cache, v_cache, length, out, workspace=None, stre
     ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=q.device)
     check(L.ane_hip_attention_decode(ctypes.byref(cfg), _p(q), _p(k_cache), _p(v_cache), length, _p(out), _p(ws),
                                      wsb, _stream_handle(stream)), "attention_decode")
+
+
+def q8_0_matvec_silu(N, K, gu, W, y, residual=None, stream=None):
+    check(lib().ane_hip_q8_0_matvec_silu(N, K, _p(gu), _p(W), _p(residual), _p(y), _stream_handle(stream)),
+          "q8_0_matvec_silu")
+
+
+def attention_decode_rope(cfg, qkv, table, pos, k_cache, v_cache, out, workspace=None, stream=None):
+    import torch
+
+    L = lib()
+    wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
+    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=qkv.device)
+    check(L.ane_hip_attention_decode_rope(ctypes.byref(cfg), _p(qkv), _p(table), pos, _p(k_cache), _p(v_cache),
+                                          _p(out), _p(ws), wsb, _stream_handle(stream)), "attention_decode_rope")
 
 
 def silu_mul(n, gu, h, stream=None):

@@ -4,8 +4,9 @@
 //
 // Matrix products go through ane_hip_q8_0_matvec_fused (q8_0.hip), which
 // fuses the RMSNorm of its input and the residual add of its output, so a
-// layer is seven launches: qkv, rope/append, attention partial, attention
-// combine, o (+residual), gate_up (norm fused), silu*up, down (+residual).
+// layer is six launches: qkv (norm fused), attention partial (RoPE and the
+// KV append fused), attention combine, o (+residual), gate_up (norm fused),
+// down (SiLU * up fused into its activation prologue, +residual).
 //
 // Attention is split over the context in chunks of 128 positions
 // (flash-decoding): one workgroup per (kv head, chunk) reads that chunk's K
@@ -74,44 +75,93 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
-// One workgroup (4 waves) per (kv head g, chunk c).
+// One workgroup (4 waves) per (kv head g, chunk c).  Every K and V load of
+// the chunk is issued up front (positions past `len` read a clamped valid
+// row and get probability 0), so a workgroup waits on memory about twice.
 //  scores: 16 lanes per position (8 dims each, one 16-byte K load), 4
 //          positions per wave per step, all 4 query heads of the group;
 //  softmax: wave w takes head w over the chunk's 128 positions;
 //  values: lane owns dims 2l, 2l+1; wave w sums positions 32w .. 32w+31;
 //          the four waves' partial outputs are added in LDS.
+// ROPE: q and k come unrotated from qkv and are rotated here with the
+// table row of `pos` (the same fp32 operations as k_rope_kv_append); the
+// workgroup holding position pos = len-1 uses k and v of pos from qkv
+// (rounded to fp16, as the cache holds them) and writes them to the caches.
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& o0, float& o1) {
+    o0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    o1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+}
+
+template <bool ROPE>
 __global__ void __launch_bounds__(256)
-k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-               const uint16_t* __restrict__ vc, uint32_t len, uint32_t ctx, uint32_t nch, float scale,
+k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16_t* kc, uint16_t* vc,
+               uint32_t len, uint32_t ctx, uint32_t nq, uint32_t nkv, uint32_t nch, float scale,
                float* __restrict__ po, float* __restrict__ pml) {
     __shared__ float sc[kGroup][kChunk];
     __shared__ float red[4][kGroup][kHD];
     const uint32_t g = blockIdx.x, c = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15;
     const uint32_t j0 = c * kChunk;
+    const uint32_t pos = len - 1;
 
+    // ---- issue every K and V load of the chunk
+    uint4 kraw[kChunk / 16];
+#pragma unroll
+    for (uint32_t st = 0; st < kChunk / 16; st++) {
+        const uint32_t j = j0 + st * 16 + wave * 4 + (lane >> 4);
+        const uint32_t jc = j < len ? j : len - 1;
+        kraw[st] = *reinterpret_cast<const uint4*>(kc + ((uint64_t)g * ctx + jc) * kHD + sub * 8);
+    }
+    uint32_t vraw[kChunk / 4];
+#pragma unroll
+    for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
+        const uint32_t j = j0 + wave * (kChunk / 4) + jj;
+        const uint32_t jc = j < len ? j : len - 1;
+        vraw[jj] = *reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + jc) * kHD + 2 * lane);
+    }
+
+    // ---- q of the group's heads, dims sub*8 .. sub*8+7
     float qv[kGroup][8];
 #pragma unroll
-    for (int h = 0; h < kGroup; h++)
+    for (int h = 0; h < kGroup; h++) {
+        const float* qh = q + (g * kGroup + h) * kHD + sub * 8;
 #pragma unroll
-        for (int e = 0; e < 8; e++) qv[h][e] = q[(g * kGroup + h) * kHD + sub * 8 + e];
+        for (int e = 0; e < 8; e += 2) {
+            if (ROPE) {
+                const uint32_t pr = sub * 4 + e / 2;
+                rope_pair(qh[e], qh[e + 1], cs[2 * pr], cs[2 * pr + 1], qv[h][e], qv[h][e + 1]);
+            } else {
+                qv[h][e] = qh[e];
+                qv[h][e + 1] = qh[e + 1];
+            }
+        }
+    }
 
-#pragma unroll 2
+    // ---- scores
+#pragma unroll
     for (uint32_t st = 0; st < kChunk / 16; st++) {
         const uint32_t jl = st * 16 + wave * 4 + (lane >> 4);
         const uint32_t j = j0 + jl;
-        float kf[8];
-        if (j < len) {
-            const uint4 raw = *reinterpret_cast<const uint4*>(kc + ((uint64_t)g * ctx + j) * kHD + sub * 8);
-            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint4 raw = kraw[st];
+        if (ROPE && j == pos) {  // k of this token: rotate, round to fp16, store to the cache
+            const float* kh = q + nq * kHD + g * kHD + sub * 8;
+            uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                kf[2 * e] = half_bits_to_float(w[e] & 0xffffu);
-                kf[2 * e + 1] = half_bits_to_float(w[e] >> 16);
+                const uint32_t pr = sub * 4 + e;
+                float o0, o1;
+                rope_pair(kh[2 * e], kh[2 * e + 1], cs[2 * pr], cs[2 * pr + 1], o0, o1);
+                w[e] = (uint32_t)f32_to_f16_bits(o0) | ((uint32_t)f32_to_f16_bits(o1) << 16);
             }
-        } else {
+            raw = make_uint4(w[0], w[1], w[2], w[3]);
+            *reinterpret_cast<uint4*>(kc + ((uint64_t)g * ctx + pos) * kHD + sub * 8) = raw;
+        }
+        const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+        float kf[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = 0.0f;
+        for (int e = 0; e < 4; e++) {
+            kf[2 * e] = half_bits_to_float(wd[e] & 0xffffu);
+            kf[2 * e + 1] = half_bits_to_float(wd[e] >> 16);
         }
 #pragma unroll
         for (int h = 0; h < kGroup; h++) {
@@ -137,14 +187,25 @@ k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ kc,
         }
     }
     __syncthreads();
+
+    // ---- values
     float o[kGroup][2];
 #pragma unroll
     for (int h = 0; h < kGroup; h++) o[h][0] = o[h][1] = 0.0f;
+#pragma unroll
     for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
         const uint32_t jl = wave * (kChunk / 4) + jj, j = j0 + jl;
-        if (j >= len) break;  // uniform across the wave
-        const uint32_t raw = *reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + j) * kHD + 2 * lane);
-        const float v0 = half_bits_to_float(raw & 0xffffu), v1 = half_bits_to_float(raw >> 16);
+        uint32_t raw = vraw[jj];
+        if (ROPE && j == pos) {  // v of this token, rounded to fp16, stored to the cache
+            const float* vh = q + (nq + nkv) * kHD + g * kHD + 2 * lane;
+            raw = (uint32_t)f32_to_f16_bits(vh[0]) | ((uint32_t)f32_to_f16_bits(vh[1]) << 16);
+            *reinterpret_cast<uint32_t*>(vc + ((uint64_t)g * ctx + pos) * kHD + 2 * lane) = raw;
+        }
+        // past len: probability 0 and value 0 (the clamped row may be the
+        // one being written, or hold non-finite fp16 that 0 * v would keep)
+        const bool live = j < len;
+        const float v0 = live ? half_bits_to_float(raw & 0xffffu) : 0.0f;
+        const float v1 = live ? half_bits_to_float(raw >> 16) : 0.0f;
 #pragma unroll
         for (int h = 0; h < kGroup; h++) {
             const float p = sc[h][jl];
@@ -168,19 +229,44 @@ k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ kc,
     }
 }
 
+// One workgroup per query head: the chunks' (max, sum) go through LDS, then
+// every thread reads its dimension of all chunks' outputs at once.
+constexpr uint32_t kMaxChunks = 512;  // contexts up to 65536 positions
+
 __global__ void __launch_bounds__(kHD)
 k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint32_t nch,
                float* __restrict__ out) {
+    __shared__ float wsh[kMaxChunks];
+    __shared__ float red[2][kHD / 64];
     const uint32_t h = blockIdx.x, d = threadIdx.x;
     const float* ml = pml + (uint64_t)h * nch * 2;
     float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; c++) M = fmaxf(M, ml[2 * c]);
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t c = 0; c < nch; c++) {
+    for (uint32_t c = d; c < nch; c += kHD) M = fmaxf(M, ml[2 * c]);
+    M = wave_max_f32(M);
+    if ((d & 63) == 0) red[0][d >> 6] = M;
+    __syncthreads();
+    M = fmaxf(red[0][0], red[0][1]);
+    float L = 0.0f;
+    for (uint32_t c = d; c < nch; c += kHD) {
         const float w = expf(ml[2 * c] - M);
+        wsh[c] = w;
         L = __builtin_fmaf(ml[2 * c + 1], w, L);
-        O = __builtin_fmaf(po[((uint64_t)h * nch + c) * kHD + d], w, O);
     }
+    L = wave_sum_f32(L);
+    if ((d & 63) == 0) red[1][d >> 6] = L;
+    __syncthreads();
+    L = red[1][0] + red[1][1];
+    float O = 0.0f;
+    const float* pd = po + (uint64_t)h * nch * kHD + d;
+    uint32_t c = 0;
+    for (; c + 8 <= nch; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = pd[(uint64_t)(c + k) * kHD];
+#pragma unroll
+        for (int k = 0; k < 8; k++) O = __builtin_fmaf(v[k], wsh[c + k], O);
+    }
+    for (; c < nch; c++) O = __builtin_fmaf(pd[(uint64_t)c * kHD], wsh[c], O);
     out[h * kHD + d] = O / L;
 }
 
@@ -193,7 +279,7 @@ k_silu_mul(uint32_t n, const float* __restrict__ gu, float* __restrict__ h) {
 }
 
 bool cfg_ok(const ane_decode_config* c) {
-    return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
+    return c && c->head_dim == kHD && c->ctx <= kMaxChunks * kChunk && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
            c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->hidden % 32 == 0 && c->ffn % 32 == 0 &&
            (uint64_t)c->n_heads * kHD % 32 == 0;
 }
@@ -263,8 +349,32 @@ extern "C" int ane_hip_attention_decode(const ane_decode_config* cfg, const floa
                                           ceil_to((uint64_t)cfg->n_heads * nch_max * kHD * 4, 256));
     hipStream_t s = (hipStream_t)stream;
     const float scale = 1.0f / sqrtf((float)kHD);
-    hipLaunchKernelGGL(k_attn_partial, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, k_cache, v_cache, len,
-                       cfg->ctx, nch, scale, po, pml);
+    hipLaunchKernelGGL(k_attn_partial<false>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, nullptr,
+                       const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache), len, cfg->ctx,
+                       cfg->n_heads, cfg->n_kv_heads, nch, scale, po, pml);
+    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, po, pml, nch, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_attention_decode_rope(const ane_decode_config* cfg, const float* qkv, const float* rope_table,
+                                             uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
+                                             void* workspace, size_t workspace_bytes, void* stream) {
+    if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
+    if (!qkv || !rope_table || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
+    if (pos >= cfg->ctx) return ANE_ERR_INVALID_ARG;
+    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ane_hip_attention_workspace_size(cfg))
+        return ANE_ERR_WORKSPACE;
+    const uint32_t len = pos + 1, nch = n_chunks(len);
+    const uint64_t nch_max = n_chunks(cfg->ctx);
+    float* po = static_cast<float*>(workspace);
+    float* pml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                          ceil_to((uint64_t)cfg->n_heads * nch_max * kHD * 4, 256));
+    hipStream_t s = (hipStream_t)stream;
+    const float scale = 1.0f / sqrtf((float)kHD);
+    hipLaunchKernelGGL(k_attn_partial<true>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, qkv,
+                       rope_table + (uint64_t)pos * kHD, k_cache, v_cache, len, cfg->ctx, cfg->n_heads,
+                       cfg->n_kv_heads, nch, scale, po, pml);
     hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, po, pml, nch, out);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
@@ -301,15 +411,13 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
         int st;
         if ((st = ane_hip_q8_0_matvec_fused(nqkv, H, x, L.attn_norm, cfg->eps, L.w_qkv, nullptr, w.qkv, stream)))
             return st;
-        if ((st = ane_hip_rope_kv_append(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, stream))) return st;
-        if ((st = ane_hip_attention_decode(cfg, w.qkv, L.k_cache, L.v_cache, pos + 1, w.attn, w.att, w.attb,
-                                           stream)))
+        if ((st = ane_hip_attention_decode_rope(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, w.attn, w.att,
+                                                w.attb, stream)))
             return st;
         if ((st = ane_hip_q8_0_matvec_fused(H, nq, w.attn, nullptr, 0.0f, L.w_o, x, x, stream))) return st;
         if ((st = ane_hip_q8_0_matvec_fused(2 * F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, nullptr, w.gu, stream)))
             return st;
-        if ((st = ane_hip_silu_mul(F, w.gu, w.h, stream))) return st;
-        if ((st = ane_hip_q8_0_matvec_fused(H, F, w.h, nullptr, 0.0f, L.w_down, x, x, stream))) return st;
+        if ((st = ane_hip_q8_0_matvec_silu(H, F, w.gu, L.w_down, x, x, stream))) return st;
     }
     return ANE_OK;
 }

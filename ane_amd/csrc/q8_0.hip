@@ -237,15 +237,16 @@ struct XStage {
 
     __device__ __forceinline__ uint32_t passes() const { return (n + kPerPass - 1) / kPerPass; }
 
-    __device__ __forceinline__ float4 load(uint32_t p) const {
+    // shift: extra bytes added to the offset (the up half of gate|up).
+    __device__ __forceinline__ float4 load(uint32_t p, uint32_t shift = 0) const {
         uint32_t o = 0x80000000u;
         if (MODE == kModeG) {
             const uint32_t blk = p * kPerPass + (threadIdx.x >> 3);
             const uint32_t t = T == 1 ? 0 : blk / nb, b = blk - t * nb;
-            if (blk < n) o = (t * K + b * 32 + (threadIdx.x & 7) * 4) * 4;
+            if (blk < n) o = (t * K + b * 32 + (threadIdx.x & 7) * 4) * 4 + shift;
         } else {
             const uint32_t i = p * kPerPass + threadIdx.x;
-            if (i < n) o = 16 * i;
+            if (i < n) o = 16 * i + shift;
         }
         return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0)),
                            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, o + 4, 0, 0)),
@@ -359,7 +360,11 @@ __device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint3
 //    quantized as usual;
 //  kFuseResidual: y[n] = fl(FADDV(p) + r[n]) (r may alias y: each row is read
 //    and written by the one lane that owns it).
-enum { kFuseNorm = 1, kFuseResidual = 2 };
+//  kFuseSiluMul: the input is gate|up (2K floats) and the row quantized is
+//    x[i] = (g / (1 + expf(-g))) * u with g = in[i], u = in[K + i].
+enum { kFuseNorm = 1, kFuseResidual = 2, kFuseSiluMul = 4 };
+
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
 struct StreamFuse {
     const float* norm_w;
@@ -422,8 +427,8 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     const int8_t* qxs = xlds;
     float* dxs = reinterpret_cast<float*>(xlds + ceil_to((uint64_t)T * nb * 32, 16));
     const float* xs = reinterpret_cast<const float*>(xlds);
-    const XStage<MODE, NW * 64> xst{make_rsrc(x, T * K * 4), K, nb, T, MODE == kModeG ? nb * T : nb * 8,
-                                    xlds, dxs};
+    const XStage<MODE, NW * 64> xst{make_rsrc(x, ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4), K, nb, T,
+                                    MODE == kModeG ? nb * T : nb * 8, xlds, dxs};
     const uint32_t npass = xst.passes();
     // residual values of this wave's rows (at most 64, one per lane), loaded
     // first so the epilogue never waits on the ring's copies
@@ -435,14 +440,25 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     float4 xv[kXBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
-    float4 wv[(FUSE & kFuseNorm) ? kXBatch : 1];
+    float4 wv[(FUSE & (kFuseNorm | kFuseSiluMul)) ? kXBatch : 1];
     if (FUSE & kFuseNorm) {
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(fz.norm_w, K * 4);
 #pragma unroll
         for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load_w(k, wr);
     }
+    if (FUSE & kFuseSiluMul) {
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(k, K * 4);  // up
+    }
 #pragma unroll
     for (int i = 0; i < S; i++) issue(i);
+    if (FUSE & kFuseSiluMul) {
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 g = xv[k], u = wv[k];
+            xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
+        }
+    }
     if (FUSE & kFuseNorm) {  // the host guarantees npass <= kXBatch
         double ss = 0.0;
 #pragma unroll
@@ -562,7 +578,7 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     if (grid < 1) grid = 1;
     // the residual fusion holds one row per lane: at most 64 rows per wave
     if ((FUSE & kFuseResidual) && ((uint64_t)N + grid * NW - 1) / (grid * NW) > 64) return -1;
-    if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
+    if ((FUSE & (kFuseNorm | kFuseSiluMul)) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
                        (const uint8_t*)W, y, (uint32_t)(grid * NW), fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -628,6 +644,20 @@ extern "C" int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x,
     else if (norm_w) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseNorm>(N, nb, K, 1, x, W, y, s, fz);
     else if (residual) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
     else r = try_stream<kModeG, ANE_Q8_G_CFG, 1>(N, nb, K, 1, x, W, y, s);
+    return r < 0 ? ANE_ERR_INVALID_ARG : r;
+}
+
+extern "C" int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu, const void* W,
+                                        const float* residual, float* y, void* stream) {
+    if (N == 0) return ANE_OK;
+    const uint32_t nb = K >> 5;
+    if (!y || !gu || !W || (K & 31)) return ANE_ERR_BAD_POINTER;
+    if (!stream_eligible(N, nb, K, 2, W)) return ANE_ERR_INVALID_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    const StreamFuse fz{nullptr, 0.0f, residual};
+    const int r = residual
+        ? try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseSiluMul | kFuseResidual>(N, nb, K, 1, gu, W, y, s, fz)
+        : try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseSiluMul>(N, nb, K, 1, gu, W, y, s, fz);
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 

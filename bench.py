@@ -51,9 +51,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--N", type=int, default=4096)
     ap.add_argument("--K", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 matvec section")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 matvec / mul_mat sections")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the dense_fused_i8 M sweep")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
+    ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
-    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode"], default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
 
@@ -164,6 +167,9 @@ def main() -> int:
         return 0
     if args.only in ("q8g", "q8r"):
         return profile_q8(args, stream)
+    if args.only == "decode":
+        bench_decode(args)
+        return 0
 
     if args.only in ("gemm", "fused"):
         fn = gemm_phase if args.only == "gemm" else fused
@@ -211,8 +217,12 @@ def main() -> int:
 
     # ------------------------------------------------------------ Q8_0 matvec
     q8 = None
+    mul_mat = None
     if not args.no_q8:
         q8 = bench_q8(args, stream)
+        mul_mat = bench_mul_mat(args)
+    m_sweep = bench_m_sweep(args, N, K) if not args.no_sweep else None
+    decode = bench_decode(args) if not args.no_decode else None
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
@@ -237,6 +247,9 @@ def main() -> int:
         "roofline": roofline,
         "phases_us": {"quantize": round(quant_ms * 1e3, 2), "contraction": round(gemm_ms * 1e3, 2)},
         "q8_0_matvec": q8,
+        "q8_0_mul_mat_config4": mul_mat,
+        "dense_fused_m_sweep": m_sweep,
+        "decode_config5": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -328,6 +341,162 @@ def bench_q8(args, stream) -> dict:
                      "traffic": read_pmc_traffic("q8_0_matvec_14336x4096_pmc.txt")},
         "shapes": res,
     }
+
+
+def bench_mul_mat(args) -> dict:
+    """Config 4: Q8_0 mul_mat (the ggml MUL_MAT hook's kernel, G mode) at the
+    Llama-3-8B projections for T = 1, 4, 16, 64 tokens.  GB/s counts the
+    weights once plus x and y, as the algorithmic traffic of one call."""
+    import numpy as np
+    import torch
+
+    import ane_amd
+    from tests import data
+
+    res = {}
+    for name, (Nr, Kc) in (("qkv", (6144, 4096)), ("o", (4096, 4096)), ("gate_up", (28672, 4096)),
+                           ("down", (4096, 14336))):
+        wbytes = Nr * (Kc // 32) * 34
+        copies = max(2, int(np.ceil(300e6 / wbytes)))
+        W0 = torch.from_numpy(data.q8_0_weights(Nr, Kc, seed=5)).cuda()
+        Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+        entry = {}
+        for T in (1, 4, 16, 64):
+            x = torch.from_numpy(data.activations(T, Kc, seed=6)).cuda()
+            y = torch.empty(T * Nr, device="cuda", dtype=torch.float32)
+            wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, T), dtype=torch.uint8, device="cuda")
+            it = [0]
+
+            def fn(st):
+                W = Ws[it[0] % copies]
+                it[0] += 1
+                ane_amd.q8_0_mul_mat(Nr, Kc, T, x, W, y, workspace=wsq, stream=st)
+
+            ms = graph_time(fn, 2 * copies)
+            alg = wbytes + 4 * T * (Kc + Nr)
+            entry[f"T{T}"] = {"us": round(ms * 1e3, 2), "GB_s": round(alg / ms / 1e6, 1),
+                              "TOPS": round(2.0 * T * Nr * Kc / ms / 1e9, 2)}
+            log(f"mul_mat {name} {Nr}x{Kc} T={T}: {ms * 1e3:.2f} us = {alg / ms / 1e6:.0f} GB/s")
+        res[f"{name} {Nr}x{Kc}"] = entry
+        del Ws, W0
+        torch.cuda.empty_cache()
+    return {"workload": "config 4: Q8_0 mul_mat G mode, Llama-3-8B projections, T tokens",
+            "unit": "us per call", "shapes": res}
+
+
+def q8_0_random_device(N: int, K: int, gen) -> "torch.Tensor":
+    """Q8_0 rows generated on the GPU, distributed as config 3: qs ~ U{-127..127},
+    d = fp16(|N(0, 0.01)|).  Returns uint8 [N, K/32*34]."""
+    import torch
+
+    nb = K // 32
+    W = torch.empty((N, nb, 34), dtype=torch.uint8, device="cuda")
+    d = (torch.randn((N, nb), generator=gen, device="cuda") * 0.01).abs().half()
+    W[:, :, :2] = d.view(torch.uint8).view(N, nb, 2)
+    W[:, :, 2:] = torch.randint(-127, 128, (N, nb, 32), generator=gen, device="cuda",
+                                dtype=torch.int8).view(torch.uint8)
+    return W.view(N, nb * 34)
+
+
+def bench_decode(args) -> dict:
+    """Config 5: one decode token of a random-init Llama-3-8B-shaped model
+    (hidden 4096, FFN 14336, 32 q / 8 kv heads of 128, fp16 KV at context
+    4096, Q8_0 weights) through ane_decode_token; every matrix product runs
+    on the Q8_0 streaming kernel.  The token is captured once as a HIP graph
+    (7 launches per layer) and replayed; mul_mat share = the same graph's
+    matrix products alone / the whole token."""
+    import ctypes
+
+    import torch
+
+    import ane_amd
+
+    H, F, NH, NKV, HD, CTX = 4096, 14336, 32, 8, 128, 4096
+    nl = args.layers
+    cfg = ane_amd.DecodeConfig(nl, H, F, NH, NKV, HD, CTX, 1e-5)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    keep = []
+    layers = (ane_amd.DecodeLayer * nl)()
+    wbytes = 0
+    for l in range(nl):
+        t = {"w_qkv": q8_0_random_device((NH + 2 * NKV) * HD, H, gen), "w_o": q8_0_random_device(H, NH * HD, gen),
+             "w_gate_up": q8_0_random_device(2 * F, H, gen), "w_down": q8_0_random_device(H, F, gen),
+             "attn_norm": 1.0 + 0.1 * torch.randn(H, generator=gen, device="cuda"),
+             "ffn_norm": 1.0 + 0.1 * torch.randn(H, generator=gen, device="cuda"),
+             "k_cache": torch.randn((NKV, CTX, HD), generator=gen, device="cuda").half(),
+             "v_cache": torch.randn((NKV, CTX, HD), generator=gen, device="cuda").half()}
+        wbytes += sum(t[k].numel() for k in ("w_qkv", "w_o", "w_gate_up", "w_down"))
+        keep.append(t)
+        layers[l] = ane_amd.DecodeLayer(*[t[k].data_ptr() for k in ("w_qkv", "w_o", "w_gate_up", "w_down",
+                                                                      "attn_norm", "ffn_norm", "k_cache",
+                                                                      "v_cache")])
+    table = torch.from_numpy(ane_amd.rope_table(CTX)).cuda()
+    ws = torch.empty(ane_amd.lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
+    x = torch.randn(H, generator=gen, device="cuda")
+    pos = CTX - 1  # attend over the full 4096-position context
+    torch.cuda.synchronize()
+
+    def token(st):
+        ane_amd.decode_token(cfg, layers, table, pos, x, ws, stream=st)
+
+    nqkv = (NH + 2 * NKV) * HD
+    scratch = torch.empty(2 * F, device="cuda")
+    xin = torch.randn(F, generator=gen, device="cuda")
+
+    resid = torch.randn(H, generator=gen, device="cuda")
+
+    def matmuls_only(st):  # the token's four products with the same fusions
+        for t in keep:
+            ane_amd.q8_0_matvec_fused(nqkv, H, xin, t["w_qkv"], scratch, norm_w=t["attn_norm"], eps=1e-5, stream=st)
+            ane_amd.q8_0_matvec_fused(H, NH * HD, xin, t["w_o"], resid, residual=resid, stream=st)
+            ane_amd.q8_0_matvec_fused(2 * F, H, xin, t["w_gate_up"], scratch, norm_w=t["ffn_norm"], eps=1e-5,
+                                      stream=st)
+            ane_amd.q8_0_matvec_fused(H, F, xin, t["w_down"], resid, residual=resid, stream=st)
+
+    tok_ms = graph_time(token, 3)
+    mm_ms = graph_time(matmuls_only, 3)
+    kv_bytes = nl * 2 * NKV * CTX * HD * 2
+    tok_s = 1e3 / tok_ms
+    log(f"decode (config 5, {nl} layers, ctx {CTX}): {tok_ms * 1e3:.1f} us/token = {tok_s:.1f} tok/s; "
+        f"mul_mat {mm_ms * 1e3:.1f} us ({mm_ms / tok_ms:.1%}); weights+KV {(wbytes + kv_bytes) / tok_ms / 1e6:.0f} GB/s")
+    res = {"workload": f"config 5: decode 1 token, Llama-3-8B shapes, {nl} layers, Q8_0 weights, fp16 KV ctx {CTX}",
+           "tok_s": round(tok_s, 1), "us_per_token": round(tok_ms * 1e3, 1),
+           "mul_mat_us": round(mm_ms * 1e3, 1), "mul_mat_share": round(mm_ms / tok_ms, 4),
+           "weights_bytes": int(wbytes), "kv_bytes": int(kv_bytes),
+           "GB_s_weights_plus_kv": round((wbytes + kv_bytes) / tok_ms / 1e6, 1),
+           "upper_bound_tok_s_at_8TBs": round(8e12 / (wbytes + kv_bytes), 1)}
+    del keep
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_m_sweep(args, N, K) -> dict:
+    """Config 2's M sweep: whole dense_fused_i8 (quantize + contraction) at
+    M in {1, 16, 128, 1024}, N = K = 4096."""
+    import torch
+
+    import ane_amd
+
+    out = {}
+    for M in (1, 16, 128, 1024):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(2)
+        A = torch.randn((M, K), generator=g, device="cuda", dtype=torch.float32)
+        B = torch.randn((K, N), generator=g, device="cuda", dtype=torch.float32)
+        C = torch.empty((M, N), device="cuda", dtype=torch.float32)
+        ws = torch.empty(ane_amd.dense_fused_i8_workspace_size(M, N, K), dtype=torch.uint8, device="cuda")
+
+        def fn(st):
+            ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st)
+
+        ms = graph_time(fn, 20)
+        ops = 2.0 * M * N * K
+        alg = 4.0 * (M * K + K * N + M * N)
+        out[f"M{M}"] = {"us": round(ms * 1e3, 2), "TOPS": round(ops / ms / 1e9, 2),
+                        "GB_s_fp32_io": round(alg / ms / 1e6, 1)}
+        log(f"dense_fused_i8 M={M}: {ms * 1e3:.2f} us = {ops / ms / 1e9:.1f} TOPS")
+    return {"workload": "config 2 M sweep: dense_fused_i8 M x 4096 x 4096, whole op", "shapes": out}
 
 
 def cpu_baseline(A, B, C, M, N, K) -> dict:

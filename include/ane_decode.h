@@ -11,12 +11,11 @@
  * src/ggml-backend/ggml-ane.cpp:119-154):
  *
  *   qkv  = W_qkv . q8(rmsnorm(x) * attn_norm)       fused norm prologue
- *   rope(q, k) at pos; k, v -> fp16 KV cache at pos
- *   attn = softmax(q k^T / sqrt(d)) v over positions 0..pos (GQA)
+ *   attn = softmax(rope(q) rope(k)^T / sqrt(d)) v over positions 0..pos (GQA),
+ *          k, v of pos appended to the fp16 cache      one fused kernel + combine
  *   x    = x + W_o . q8(attn)                        fused residual epilogue
  *   gu   = W_gate_up . q8(rmsnorm(x) * ffn_norm)     fused norm prologue
- *   h    = silu(gate) * up
- *   x    = x + W_down . q8(h)                        fused residual epilogue
+ *   x    = x + W_down . q8(silu(gate) * up)          fused prologue and epilogue
  *
  * Layouts: weights are Q8_0 rows (ggml block layout) with the output
  * features as rows: W_qkv rows [q heads | k heads | v heads], W_gate_up rows
@@ -78,6 +77,12 @@ int ane_decode_token(const struct ane_decode_config* cfg, const struct ane_decod
 int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x, const float* norm_w, float eps,
                               const void* W, const float* residual, float* y, void* stream);
 
+/* y = W . q8(silu(gu[0..K)) * gu[K..2K)) (+ residual), silu(g) = g / (1 + e^-g):
+ * the down projection with SiLU * up fused into its activation prologue;
+ * bit-identical to ane_hip_silu_mul followed by ane_hip_q8_0_matvec_fused. */
+int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu, const void* W, const float* residual,
+                             float* y, void* stream);
+
 /* RoPE on the q and k heads of qkv (in place for q), then k and v of this
  * position converted to fp16 into the caches. */
 int ane_hip_rope_kv_append(const struct ane_decode_config* cfg, float* qkv, const float* rope_table,
@@ -89,6 +94,13 @@ size_t ane_hip_attention_workspace_size(const struct ane_decode_config* cfg);
 int ane_hip_attention_decode(const struct ane_decode_config* cfg, const float* q, const uint16_t* k_cache,
                              const uint16_t* v_cache, uint32_t len, float* out, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* ane_hip_attention_decode at len = pos + 1 on unrotated q and k: RoPE of q
+ * and k (as ane_hip_rope_kv_append) and the fp16 append of k and v at pos
+ * happen inside the attention kernel; same results, one launch fewer. */
+int ane_hip_attention_decode_rope(const struct ane_decode_config* cfg, const float* qkv, const float* rope_table,
+                                  uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, float* out, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* h[i] = silu(gu[i]) * gu[n + i], i < n. */
 int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream);

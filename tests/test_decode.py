@@ -245,3 +245,50 @@ def test_decode_tokens_small_model(ane, oracle):
         assert err < 1e-3, (pos, err)
         if pos == 0:  # first layer, first token: every step before attention is exact
             assert host(dev_caches[0][0])[:, 0].tobytes() == np_caches[0][0][:, 0].tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos", [0, 5, 127, 128, 300])
+def test_attention_rope_fused_matches_separate(ane, pos):
+    """RoPE + append inside the attention kernel == rope_kv_append then attention,
+    bit for bit; non-finite garbage at and past pos in the cache is never used."""
+    import torch
+
+    cfg = ane.DecodeConfig(1, 4096, 14336, 32, 8, 128, 512, 1e-5)
+    table = dev(ane.rope_table(512))
+    g = np.random.default_rng(pos)
+    qkv = (g.standard_normal(48 * 128) * 2).astype(F32)
+    kc = g.standard_normal((8, 512, 128)).astype(np.float16)
+    vc = g.standard_normal((8, 512, 128)).astype(np.float16)
+    kc[:, pos:] = np.inf
+    vc[:, pos:] = np.nan
+    k1, v1, k2, v2 = dev(kc), dev(vc), dev(kc), dev(vc)
+    q1 = dev(qkv)
+    out1 = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    out2 = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    ane.rope_kv_append(cfg, q1, table, pos, k1, v1)
+    ane.attention_decode(cfg, q1, k1, v1, pos + 1, out1)
+    ane.attention_decode_rope(cfg, dev(qkv), table, pos, k2, v2, out2)
+    o1, o2 = host(out1), host(out2)
+    assert np.isfinite(o2).all()
+    assert o1.tobytes() == o2.tobytes()
+    assert host(k1)[:, :pos + 1].tobytes() == host(k2)[:, :pos + 1].tobytes()
+    assert host(v1)[:, :pos + 1].tobytes() == host(v2)[:, :pos + 1].tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("resid", [False, True])
+def test_matvec_silu_matches_separate(ane, resid):
+    import torch
+
+    N, F = 4096, 14336
+    W = dev(data.q8_0_weights(N, F, seed=41))
+    gu = dev((data.activations(1, 2 * F, seed=42)[0] * 3).astype(F32))
+    r = data.activations(1, N, seed=43)[0]
+    h = torch.zeros(F, dtype=torch.float32, device="cuda")
+    y1 = dev(r) if resid else torch.zeros(N, dtype=torch.float32, device="cuda")
+    y2 = dev(r) if resid else torch.zeros(N, dtype=torch.float32, device="cuda")
+    ane.silu_mul(F, gu, h)
+    ane.q8_0_matvec_fused(N, F, h, W, y1, residual=y1 if resid else None)
+    ane.q8_0_matvec_silu(N, F, gu, W, y2, residual=y2 if resid else None)
+    assert host(y1).tobytes() == host(y2).tobytes()
