@@ -585,25 +585,33 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     return ANE_OK;
 }
 
-// Configurations in order of preference (waves per workgroup, blocks per
-// segment, ring stages); the first whose LDS fits is launched.
-#ifndef ANE_Q8_G_CFG
-#define ANE_Q8_G_CFG 8, 32, 2
+// Configuration choice (waves per workgroup, blocks per segment, ring
+// stages).  A wave takes whole 4-row units, so a matrix with few units per
+// CU runs the 4-wave configuration: the 8-wave one would
+// leave CUs idle (4096 rows = 1024 units = 128 eight-wave workgroups).
+// Otherwise the 8-wave configuration (two workgroups per CU).  The first
+// configuration whose LDS fits is launched.
+#ifndef ANE_Q8_SMALL_UNITS_PER_CU
+#define ANE_Q8_SMALL_UNITS_PER_CU 12
 #endif
-template <int TT>
-int stream_g(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
-             hipStream_t s) {
-    int r = try_stream<kModeG, ANE_Q8_G_CFG, TT>(N, nb, K, T, x, W, y, s);
-    if (r < 0) r = try_stream<kModeG, 4, 32, 2, TT>(N, nb, K, T, x, W, y, s);
-    return r;
-}
+#ifndef ANE_Q8_SMALL_CFG
+#define ANE_Q8_SMALL_CFG 4, 32, 2
+#endif
+#ifndef ANE_Q8_LARGE_CFG
+#define ANE_Q8_LARGE_CFG 8, 32, 2
+#endif
 
-#ifndef ANE_Q8_R_CFG
-#define ANE_Q8_R_CFG 8, 32, 2
-#endif
-int stream_r(uint32_t N, uint32_t nb, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
-    int r = try_stream<kModeR, ANE_Q8_R_CFG, 1>(N, nb, K, 1, x, W, y, s);
-    if (r < 0) r = try_stream<kModeR, 4, 32, 2, 1>(N, nb, K, 1, x, W, y, s);
+template <int MODE, int TT, int FUSE = 0>
+int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
+                hipStream_t s, StreamFuse fz = StreamFuse{nullptr, 0.0f, nullptr}) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
+    const uint64_t units = ((uint64_t)N + kUnitRows - 1) / kUnitRows;
+    int r = -1;
+    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU)
+        r = try_stream<MODE, ANE_Q8_SMALL_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+    if (r < 0) r = try_stream<MODE, ANE_Q8_LARGE_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+    if (r < 0) r = try_stream<MODE, 4, 32, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
     return r;
 }
 
@@ -620,7 +628,7 @@ extern "C" int ane_hip_q8_0_gemv(uint32_t M, uint32_t K, const float* x, const v
     const uint32_t nb = K >> 5;
     hipStream_t s = (hipStream_t)stream;
     if (stream_eligible(M, nb, K, 1, W)) {
-        const int r = stream_r(M, nb, K, x, W, y, s);
+        const int r = stream_auto<kModeR, 1>(M, nb, K, 1, x, W, y, s);
         if (r >= 0) return r;
     }
     const uint64_t grid = ((uint64_t)M + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -640,10 +648,10 @@ extern "C" int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x,
     hipStream_t s = (hipStream_t)stream;
     const StreamFuse fz{norm_w, eps, residual};
     int r;
-    if (norm_w && residual) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseNorm | kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
-    else if (norm_w) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseNorm>(N, nb, K, 1, x, W, y, s, fz);
-    else if (residual) r = try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
-    else r = try_stream<kModeG, ANE_Q8_G_CFG, 1>(N, nb, K, 1, x, W, y, s);
+    if (norm_w && residual) r = stream_auto<kModeG, 1, kFuseNorm | kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
+    else if (norm_w) r = stream_auto<kModeG, 1, kFuseNorm>(N, nb, K, 1, x, W, y, s, fz);
+    else if (residual) r = stream_auto<kModeG, 1, kFuseResidual>(N, nb, K, 1, x, W, y, s, fz);
+    else r = stream_auto<kModeG, 1>(N, nb, K, 1, x, W, y, s);
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 
@@ -656,8 +664,8 @@ extern "C" int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu,
     hipStream_t s = (hipStream_t)stream;
     const StreamFuse fz{nullptr, 0.0f, residual};
     const int r = residual
-        ? try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseSiluMul | kFuseResidual>(N, nb, K, 1, gu, W, y, s, fz)
-        : try_stream<kModeG, ANE_Q8_G_CFG, 1, kFuseSiluMul>(N, nb, K, 1, gu, W, y, s, fz);
+        ? stream_auto<kModeG, 1, kFuseSiluMul | kFuseResidual>(N, nb, K, 1, gu, W, y, s, fz)
+        : stream_auto<kModeG, 1, kFuseSiluMul>(N, nb, K, 1, gu, W, y, s, fz);
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 
@@ -678,8 +686,8 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
         return ANE_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
     if (T <= kMaxStreamTokens && stream_eligible(N, nb, K, T, W)) {
-        const int r = T == 1 ? stream_g<1>(N, nb, K, T, x, W, y, s)
-                             : stream_g<kMaxStreamTokens>(N, nb, K, T, x, W, y, s);
+        const int r = T == 1 ? stream_auto<kModeG, 1>(N, nb, K, T, x, W, y, s)
+                             : stream_auto<kModeG, kMaxStreamTokens>(N, nb, K, T, x, W, y, s);
         if (r >= 0) return r;
     }
     int8_t* qx = (int8_t*)workspace;
