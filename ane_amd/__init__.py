@@ -526,7 +526,7 @@ def attention_decode(cfg, q, k_cache, v_cache, length, out, workspace=None, stre
 
     L = lib()
     wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
-    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    ws = workspace if workspace is not None else torch.zeros(wsb, dtype=torch.uint8, device=q.device)
     check(L.ane_hip_attention_decode(ctypes.byref(cfg), _p(q), _p(k_cache), _p(v_cache), length, _p(out), _p(ws),
                                      wsb, _stream_handle(stream)), "attention_decode")
 
@@ -541,13 +541,20 @@ def attention_decode_rope(cfg, qkv, table, pos, k_cache, v_cache, out, workspace
 
     L = lib()
     wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
-    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=qkv.device)
+    ws = workspace if workspace is not None else torch.zeros(wsb, dtype=torch.uint8, device=qkv.device)
     check(L.ane_hip_attention_decode_rope(ctypes.byref(cfg), _p(qkv), _p(table), pos, _p(k_cache), _p(v_cache),
                                           _p(out), _p(ws), wsb, _stream_handle(stream)), "attention_decode_rope")
 
 
 def silu_mul(n, gu, h, stream=None):
     check(lib().ane_hip_silu_mul(n, _p(gu), _p(h), _stream_handle(stream)), "silu_mul")
+
+
+def decode_workspace(cfg, device="cuda"):
+    """A device workspace for decode_token."""
+    import torch
+
+    return torch.zeros(lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device=device)
 
 
 def decode_token(cfg, layers, table, pos, x, workspace, stream=None):

@@ -23,7 +23,11 @@ namespace ane {
 namespace {
 
 constexpr int kHD = 128;     // head_dim
-constexpr int kChunk = 128;  // context positions per attention workgroup
+#ifndef ANE_ATTN_CHUNK
+#define ANE_ATTN_CHUNK 64
+#endif
+constexpr int kChunk = ANE_ATTN_CHUNK;  // context positions per attention workgroup
+static_assert(kChunk % 16 == 0 && kChunk <= 128, "chunk: a multiple of 16 positions, at most 128");
 constexpr int kGroup = 4;    // query heads per kv head (one wave each in the softmax)
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
@@ -64,39 +68,59 @@ k_rope_kv_append(float* __restrict__ qkv, uint32_t nq, uint32_t nkv, const float
     }
 }
 
+// Wave-wide max / sum: DPP within each 16-lane row, then the four row
+// results read out with v_readlane (no LDS round trips).
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppRowMirror>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    v = faddv16(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
-// One workgroup (4 waves) per (kv head g, chunk c).  Every K and V load of
-// the chunk is issued up front (positions past `len` read a clamped valid
-// row and get probability 0), so a workgroup waits on memory about twice.
+// One workgroup (4 waves) per (kv head g, chunk c of kChunk positions).
+//  loads: the small operands first (q slices, RoPE row, this token's k and v
+//         slices), then every K and V row of the chunk (positions past `len`
+//         read a clamped valid row; their probability and value are zeroed),
+//         all unconditional, so scores start once K has landed while V is
+//         still in flight;
 //  scores: 16 lanes per position (8 dims each, one 16-byte K load), 4
 //          positions per wave per step, all 4 query heads of the group;
-//  softmax: wave w takes head w over the chunk's 128 positions;
-//  values: lane owns dims 2l, 2l+1; wave w sums positions 32w .. 32w+31;
-//          the four waves' partial outputs are added in LDS.
-// ROPE: q and k come unrotated from qkv and are rotated here with the
-// table row of `pos` (the same fp32 operations as k_rope_kv_append); the
-// workgroup holding position pos = len-1 uses k and v of pos from qkv
-// (rounded to fp16, as the cache holds them) and writes them to the caches.
+//  softmax: wave w takes head w over the chunk's positions;
+//  values: lane owns dims 2l, 2l+1; wave w sums a quarter of the positions;
+//          the four waves' partial outputs are added in LDS;
+//  output: (max, sum, unnormalised output) of the chunk per head, merged by
+//          k_attn_combine with exp(m_c - M) rescaling.
+// ROPE: q and k come unrotated from qkv and are rotated here with the table
+// row of `pos` (the same fp32 operations as k_rope_kv_append); position pos
+// = len-1 uses this token's k and v (rounded to fp16, as the cache holds
+// them), which the workgroup holding pos also writes to the caches.
 __device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& o0, float& o1) {
     o0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
     o1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
 }
 
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+}
+
 template <bool ROPE>
 __global__ void __launch_bounds__(256)
-k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16_t* kc, uint16_t* vc,
-               uint32_t len, uint32_t ctx, uint32_t nq, uint32_t nkv, uint32_t nch, float scale,
-               float* __restrict__ po, float* __restrict__ pml) {
+k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t* kc, uint16_t* vc,
+            uint32_t len, uint32_t ctx, uint32_t nq, uint32_t nkv, uint32_t nch, float scale,
+            float* __restrict__ po, float* __restrict__ pml) {
     __shared__ float sc[kGroup][kChunk];
     __shared__ float red[4][kGroup][kHD];
     const uint32_t g = blockIdx.x, c = blockIdx.y;
@@ -104,7 +128,26 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
     const uint32_t j0 = c * kChunk;
     const uint32_t pos = len - 1;
 
-    // ---- issue every K and V load of the chunk
+    // ---- small operands
+    float4 qa[kGroup], qb[kGroup];
+#pragma unroll
+    for (int h = 0; h < kGroup; h++) {
+        const float* qh = q + (g * kGroup + h) * kHD + sub * 8;
+        qa[h] = *reinterpret_cast<const float4*>(qh);
+        qb[h] = *reinterpret_cast<const float4*>(qh + 4);
+    }
+    float4 csa = make_float4(0, 0, 0, 0), csb = csa, ka = csa, kb = csa;
+    float2 vv = make_float2(0, 0);
+    if (ROPE) {
+        csa = *reinterpret_cast<const float4*>(cs + 8 * sub);      // (cos, sin) of pairs 4sub, 4sub+1
+        csb = *reinterpret_cast<const float4*>(cs + 8 * sub + 4);  // pairs 4sub+2, 4sub+3
+        const float* kh = q + nq * kHD + g * kHD + sub * 8;
+        ka = *reinterpret_cast<const float4*>(kh);
+        kb = *reinterpret_cast<const float4*>(kh + 4);
+        vv = *reinterpret_cast<const float2*>(q + (nq + nkv) * kHD + g * kHD + 2 * lane);
+    }
+
+    // ---- every K and V row of the chunk
     uint4 kraw[kChunk / 16];
 #pragma unroll
     for (uint32_t st = 0; st < kChunk / 16; st++) {
@@ -120,21 +163,32 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
         vraw[jj] = *reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + jc) * kHD + 2 * lane);
     }
 
-    // ---- q of the group's heads, dims sub*8 .. sub*8+7
+    // ---- q (rotated), and this token's k and v as fp16
     float qv[kGroup][8];
 #pragma unroll
     for (int h = 0; h < kGroup; h++) {
-        const float* qh = q + (g * kGroup + h) * kHD + sub * 8;
+        const float in[8] = {qa[h].x, qa[h].y, qa[h].z, qa[h].w, qb[h].x, qb[h].y, qb[h].z, qb[h].w};
+        if (ROPE) {
+            rope_pair(in[0], in[1], csa.x, csa.y, qv[h][0], qv[h][1]);
+            rope_pair(in[2], in[3], csa.z, csa.w, qv[h][2], qv[h][3]);
+            rope_pair(in[4], in[5], csb.x, csb.y, qv[h][4], qv[h][5]);
+            rope_pair(in[6], in[7], csb.z, csb.w, qv[h][6], qv[h][7]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            if (ROPE) {
-                const uint32_t pr = sub * 4 + e / 2;
-                rope_pair(qh[e], qh[e + 1], cs[2 * pr], cs[2 * pr + 1], qv[h][e], qv[h][e + 1]);
-            } else {
-                qv[h][e] = qh[e];
-                qv[h][e + 1] = qh[e + 1];
-            }
+            for (int e = 0; e < 8; e++) qv[h][e] = in[e];
         }
+    }
+    uint4 kpos = make_uint4(0, 0, 0, 0);
+    uint32_t vpos = 0;
+    if (ROPE) {
+        float k[8];
+        rope_pair(ka.x, ka.y, csa.x, csa.y, k[0], k[1]);
+        rope_pair(ka.z, ka.w, csa.z, csa.w, k[2], k[3]);
+        rope_pair(kb.x, kb.y, csb.x, csb.y, k[4], k[5]);
+        rope_pair(kb.z, kb.w, csb.z, csb.w, k[6], k[7]);
+        kpos = make_uint4(pack_f16x2(k[0], k[1]), pack_f16x2(k[2], k[3]), pack_f16x2(k[4], k[5]),
+                          pack_f16x2(k[6], k[7]));
+        vpos = pack_f16x2(vv.x, vv.y);
     }
 
     // ---- scores
@@ -142,20 +196,9 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
     for (uint32_t st = 0; st < kChunk / 16; st++) {
         const uint32_t jl = st * 16 + wave * 4 + (lane >> 4);
         const uint32_t j = j0 + jl;
-        uint4 raw = kraw[st];
-        if (ROPE && j == pos) {  // k of this token: rotate, round to fp16, store to the cache
-            const float* kh = q + nq * kHD + g * kHD + sub * 8;
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t pr = sub * 4 + e;
-                float o0, o1;
-                rope_pair(kh[2 * e], kh[2 * e + 1], cs[2 * pr], cs[2 * pr + 1], o0, o1);
-                w[e] = (uint32_t)f32_to_f16_bits(o0) | ((uint32_t)f32_to_f16_bits(o1) << 16);
-            }
-            raw = make_uint4(w[0], w[1], w[2], w[3]);
-            *reinterpret_cast<uint4*>(kc + ((uint64_t)g * ctx + pos) * kHD + sub * 8) = raw;
-        }
+        const bool here = ROPE && j == pos;
+        const uint4 raw = here ? kpos : kraw[st];
+        if (here) *reinterpret_cast<uint4*>(kc + ((uint64_t)g * ctx + pos) * kHD + sub * 8) = kpos;
         const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
         float kf[8];
 #pragma unroll
@@ -175,12 +218,13 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
     __syncthreads();
     {
         const uint32_t h = wave;
-        const float a = sc[h][lane], b = sc[h][lane + 64];
+        const float a = lane < kChunk ? sc[h][lane] : -INFINITY;
+        const float b = lane + 64 < kChunk ? sc[h][lane + 64] : -INFINITY;
         const float m = wave_max_f32(fmaxf(a, b));  // finite: position j0 < len
         const float pa = expf(a - m), pb = expf(b - m);
         const float l = wave_sum_f32(pa + pb);
-        sc[h][lane] = pa;
-        sc[h][lane + 64] = pb;
+        if (lane < kChunk) sc[h][lane] = pa;
+        if (lane + 64 < kChunk) sc[h][lane + 64] = pb;
         if (lane == 0) {
             pml[((g * kGroup + h) * nch + c) * 2] = m;
             pml[((g * kGroup + h) * nch + c) * 2 + 1] = l;
@@ -195,14 +239,10 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
 #pragma unroll
     for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
         const uint32_t jl = wave * (kChunk / 4) + jj, j = j0 + jl;
-        uint32_t raw = vraw[jj];
-        if (ROPE && j == pos) {  // v of this token, rounded to fp16, stored to the cache
-            const float* vh = q + (nq + nkv) * kHD + g * kHD + 2 * lane;
-            raw = (uint32_t)f32_to_f16_bits(vh[0]) | ((uint32_t)f32_to_f16_bits(vh[1]) << 16);
-            *reinterpret_cast<uint32_t*>(vc + ((uint64_t)g * ctx + pos) * kHD + 2 * lane) = raw;
-        }
-        // past len: probability 0 and value 0 (the clamped row may be the
-        // one being written, or hold non-finite fp16 that 0 * v would keep)
+        const bool here = ROPE && j == pos;
+        const uint32_t raw = here ? vpos : vraw[jj];
+        if (here) *reinterpret_cast<uint32_t*>(vc + ((uint64_t)g * ctx + pos) * kHD + 2 * lane) = vpos;
+        // past len: value 0 as well (the clamped row may hold non-finite fp16)
         const bool live = j < len;
         const float v0 = live ? half_bits_to_float(raw & 0xffffu) : 0.0f;
         const float v1 = live ? half_bits_to_float(raw >> 16) : 0.0f;
@@ -221,25 +261,23 @@ k_attn_partial(const float* __restrict__ q, const float* __restrict__ cs, uint16
     __syncthreads();
     {
         const uint32_t h = wave;
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const uint32_t d = 2 * lane + e;
-            po[((g * kGroup + h) * nch + c) * kHD + d] = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
-        }
+        float2 r;
+        r.x = red[0][h][2 * lane] + red[1][h][2 * lane] + red[2][h][2 * lane] + red[3][h][2 * lane];
+        r.y = red[0][h][2 * lane + 1] + red[1][h][2 * lane + 1] + red[2][h][2 * lane + 1] + red[3][h][2 * lane + 1];
+        *reinterpret_cast<float2*>(po + ((g * kGroup + h) * nch + c) * kHD + 2 * lane) = r;
     }
 }
 
-// One workgroup per query head: the chunks' (max, sum) go through LDS, then
-// every thread reads its dimension of all chunks' outputs at once.
-constexpr uint32_t kMaxChunks = 512;  // contexts up to 65536 positions
-
+// One workgroup per query head merges the chunks: (max, sum) pairs through
+// LDS, then every thread reads its dimension of up to 32 chunks at once.
 __global__ void __launch_bounds__(kHD)
 k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint32_t nch,
                float* __restrict__ out) {
-    __shared__ float wsh[kMaxChunks];
+    __shared__ float wsh[32];
     __shared__ float red[2][kHD / 64];
     const uint32_t h = blockIdx.x, d = threadIdx.x;
     const float* ml = pml + (uint64_t)h * nch * 2;
+    const float* pd = po + (uint64_t)h * nch * kHD + d;
     float M = -INFINITY;
     for (uint32_t c = d; c < nch; c += kHD) M = fmaxf(M, ml[2 * c]);
     M = wave_max_f32(M);
@@ -247,28 +285,24 @@ k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint
     __syncthreads();
     M = fmaxf(red[0][0], red[0][1]);
     float L = 0.0f;
-    for (uint32_t c = d; c < nch; c += kHD) {
-        const float w = expf(ml[2 * c] - M);
-        wsh[c] = w;
-        L = __builtin_fmaf(ml[2 * c + 1], w, L);
-    }
+    for (uint32_t c = d; c < nch; c += kHD) L = __builtin_fmaf(ml[2 * c + 1], expf(ml[2 * c] - M), L);
     L = wave_sum_f32(L);
     if ((d & 63) == 0) red[1][d >> 6] = L;
-    __syncthreads();
-    L = red[1][0] + red[1][1];
     float O = 0.0f;
-    const float* pd = po + (uint64_t)h * nch * kHD + d;
-    uint32_t c = 0;
-    for (; c + 8 <= nch; c += 8) {
-        float v[8];
+    for (uint32_t c0 = 0; c0 < nch; c0 += 32) {
+        __syncthreads();
+        if (d < 32) wsh[d] = c0 + d < nch ? expf(ml[2 * (c0 + d)] - M) : 0.0f;
+        float v[32];  // chunks past nch read chunk nch-1 (finite) and get weight 0
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = pd[(uint64_t)(c + k) * kHD];
+        for (int k = 0; k < 32; k++) v[k] = pd[(uint64_t)min(c0 + k, nch - 1) * kHD];
+        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < 8; k++) O = __builtin_fmaf(v[k], wsh[c + k], O);
+        for (int k = 0; k < 32; k++) O = __builtin_fmaf(v[k], wsh[k], O);
     }
-    for (; c < nch; c++) O = __builtin_fmaf(pd[(uint64_t)c * kHD], wsh[c], O);
+    L = red[1][0] + red[1][1];
     out[h * kHD + d] = O / L;
 }
+
 
 __global__ void __launch_bounds__(256)
 k_silu_mul(uint32_t n, const float* __restrict__ gu, float* __restrict__ h) {
@@ -279,12 +313,51 @@ k_silu_mul(uint32_t n, const float* __restrict__ gu, float* __restrict__ h) {
 }
 
 bool cfg_ok(const ane_decode_config* c) {
-    return c && c->head_dim == kHD && c->ctx <= kMaxChunks * kChunk && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
+    return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
            c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->hidden % 32 == 0 && c->ffn % 32 == 0 &&
            (uint64_t)c->n_heads * kHD % 32 == 0;
 }
 
 uint32_t n_chunks(uint32_t len) { return (len + kChunk - 1) / kChunk; }
+
+// Attention workspace: partial outputs [n_heads][nch][head_dim], then
+// (max, sum) [n_heads][nch][2].
+struct AttnWs {
+    float* po;
+    float* pml;
+};
+
+size_t attn_layout(const ane_decode_config* cfg, void* base, AttnWs* w) {
+    const uint64_t nch = n_chunks(cfg->ctx);
+    const size_t a = ceil_to((uint64_t)cfg->n_heads * nch * kHD * 4, 256);
+    const size_t b = ceil_to((uint64_t)cfg->n_heads * nch * 8, 256);
+    if (w && base) {
+        uint8_t* p = static_cast<uint8_t*>(base);
+        *w = AttnWs{reinterpret_cast<float*>(p), reinterpret_cast<float*>(p + a)};
+    }
+    return a + b;
+}
+
+int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, const float* table_row,
+                     uint16_t* k_cache, uint16_t* v_cache, uint32_t len, float* out, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < attn_layout(cfg, nullptr, nullptr))
+        return ANE_ERR_WORKSPACE;
+    AttnWs w;
+    attn_layout(cfg, workspace, &w);
+    const uint32_t nch = n_chunks(len);
+    const float scale = 1.0f / sqrtf((float)kHD);
+    hipStream_t s = (hipStream_t)stream;
+    if (rope)
+        hipLaunchKernelGGL(k_attention<true>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, table_row, k_cache,
+                           v_cache, len, cfg->ctx, cfg->n_heads, cfg->n_kv_heads, nch, scale, w.po, w.pml);
+    else
+        hipLaunchKernelGGL(k_attention<false>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, table_row, k_cache,
+                           v_cache, len, cfg->ctx, cfg->n_heads, cfg->n_kv_heads, nch, scale, w.po, w.pml);
+    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, w.po, w.pml, nch, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
 
 struct DecodeWs {
     float *qkv, *attn, *gu, *h;
@@ -329,9 +402,8 @@ extern "C" int ane_hip_rope_kv_append(const ane_decode_config* cfg, float* qkv, 
 }
 
 extern "C" size_t ane_hip_attention_workspace_size(const ane_decode_config* cfg) {
-    if (!cfg) return 0;
-    const uint64_t nch = n_chunks(cfg->ctx);
-    return (size_t)(ceil_to((uint64_t)cfg->n_heads * nch * kHD * 4, 256) + ceil_to((uint64_t)cfg->n_heads * nch * 8, 256));
+    if (!cfg_ok(cfg)) return 0;
+    return attn_layout(cfg, nullptr, nullptr);
 }
 
 extern "C" int ane_hip_attention_decode(const ane_decode_config* cfg, const float* q, const uint16_t* k_cache,
@@ -340,21 +412,8 @@ extern "C" int ane_hip_attention_decode(const ane_decode_config* cfg, const floa
     if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
     if (!q || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
     if (len == 0 || len > cfg->ctx) return ANE_ERR_INVALID_ARG;
-    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ane_hip_attention_workspace_size(cfg))
-        return ANE_ERR_WORKSPACE;
-    const uint32_t nch = n_chunks(len);
-    const uint64_t nch_max = n_chunks(cfg->ctx);
-    float* po = static_cast<float*>(workspace);
-    float* pml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                          ceil_to((uint64_t)cfg->n_heads * nch_max * kHD * 4, 256));
-    hipStream_t s = (hipStream_t)stream;
-    const float scale = 1.0f / sqrtf((float)kHD);
-    hipLaunchKernelGGL(k_attn_partial<false>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, nullptr,
-                       const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache), len, cfg->ctx,
-                       cfg->n_heads, cfg->n_kv_heads, nch, scale, po, pml);
-    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, po, pml, nch, out);
-    ANE_HIP_CHECK_LAUNCH();
-    return ANE_OK;
+    return attention_launch(cfg, false, q, nullptr, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache),
+                            len, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ane_hip_attention_decode_rope(const ane_decode_config* cfg, const float* qkv, const float* rope_table,
@@ -363,21 +422,8 @@ extern "C" int ane_hip_attention_decode_rope(const ane_decode_config* cfg, const
     if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
     if (!qkv || !rope_table || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
     if (pos >= cfg->ctx) return ANE_ERR_INVALID_ARG;
-    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ane_hip_attention_workspace_size(cfg))
-        return ANE_ERR_WORKSPACE;
-    const uint32_t len = pos + 1, nch = n_chunks(len);
-    const uint64_t nch_max = n_chunks(cfg->ctx);
-    float* po = static_cast<float*>(workspace);
-    float* pml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                          ceil_to((uint64_t)cfg->n_heads * nch_max * kHD * 4, 256));
-    hipStream_t s = (hipStream_t)stream;
-    const float scale = 1.0f / sqrtf((float)kHD);
-    hipLaunchKernelGGL(k_attn_partial<true>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, qkv,
-                       rope_table + (uint64_t)pos * kHD, k_cache, v_cache, len, cfg->ctx, cfg->n_heads,
-                       cfg->n_kv_heads, nch, scale, po, pml);
-    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, po, pml, nch, out);
-    ANE_HIP_CHECK_LAUNCH();
-    return ANE_OK;
+    return attention_launch(cfg, true, qkv, rope_table + (uint64_t)pos * kHD, k_cache, v_cache, pos + 1, out,
+                            workspace, workspace_bytes, stream);
 }
 
 extern "C" int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream) {

@@ -432,7 +432,7 @@ def bench_decode(args) -> dict:
                                                                       "attn_norm", "ffn_norm", "k_cache",
                                                                       "v_cache")])
     table = torch.from_numpy(ane_amd.rope_table(CTX)).cuda()
-    ws = torch.empty(ane_amd.lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
+    ws = ane_amd.decode_workspace(cfg)
     x = torch.randn(H, generator=gen, device="cuda")
     pos = CTX - 1  # attend over the full 4096-position context
     torch.cuda.synchronize()

@@ -89,7 +89,9 @@ int ane_hip_rope_kv_append(const struct ane_decode_config* cfg, float* qkv, cons
                            uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, void* stream);
 
 /* out[h] = softmax(q[h] . K[g]^T / sqrt(head_dim)) V[g] over positions
- * 0..len-1, g = h / (n_heads / n_kv_heads).  q: fp32 [n_heads][head_dim]. */
+ * 0..len-1, g = h / (n_heads / n_kv_heads).  q: fp32 [n_heads][head_dim].
+ * Two launches: per (kv head, chunk of the context) partial results, then a
+ * merge per query head. */
 size_t ane_hip_attention_workspace_size(const struct ane_decode_config* cfg);
 int ane_hip_attention_decode(const struct ane_decode_config* cfg, const float* q, const uint16_t* k_cache,
                              const uint16_t* v_cache, uint32_t len, float* out, void* workspace,

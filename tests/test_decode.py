@@ -161,9 +161,15 @@ def test_attention_decode(ane, length):
     vc = g.standard_normal((8, 4096, 128)).astype(np.float16)
     q = (g.standard_normal((32, 128)) * 2.0).astype(F32)
     out = torch.zeros(32 * 128, dtype=torch.float32, device="cuda")
-    ane.attention_decode(cfg, dev(q), dev(kc), dev(vc), length, out)
+    ws = torch.zeros(ane.lib().ane_hip_attention_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    ane.attention_decode(cfg, qd, kd, vd, length, out, workspace=ws)
     ref = np_attention(q, kc, vc, length, 32, 8)
-    np.testing.assert_allclose(host(out).reshape(32, 128), ref, rtol=2e-5, atol=1e-6)
+    first = host(out).reshape(32, 128)
+    np.testing.assert_allclose(first, ref, rtol=2e-5, atol=1e-6)
+    out.zero_()
+    ane.attention_decode(cfg, qd, kd, vd, length, out, workspace=ws)  # the same workspace again
+    assert host(out).reshape(32, 128).tobytes() == first.tobytes()
 
 
 @pytest.mark.gpu
@@ -232,6 +238,7 @@ def test_decode_tokens_small_model(ane, oracle):
                                                                   "attn_norm", "ffn_norm")],
                                     kc.data_ptr(), vc.data_ptr())
     ws = torch.empty(ane.lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
+    ws.fill_(0xAB)  # no initialisation is needed
     x0 = data.activations(5, 512, seed=21).astype(F32)
     xd = torch.zeros(512, dtype=torch.float32, device="cuda")
     tab = dev(table)
