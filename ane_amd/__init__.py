@@ -103,6 +103,8 @@ EXPORTS = (
     "ane_hip_silu_mul",
     "ane_hip_q8_0_matvec_silu",
     "ane_hip_attention_decode_rope",
+    "ane_hip_q8_0_matvec_q8",
+    "ane_hip_silu_mul_quant",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -163,7 +165,9 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_hip_attention_decode": (_c.c_int, [_P, _P, _P, _P, _c.c_uint32, _P, _P, _c.c_size_t, _P]),
     "ane_hip_silu_mul": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
     "ane_hip_q8_0_matvec_silu": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
-    "ane_hip_attention_decode_rope": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_attention_decode_rope": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _P, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_q8_0_matvec_q8": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
+    "ane_hip_silu_mul_quant": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
 }
 
 
@@ -536,18 +540,33 @@ def q8_0_matvec_silu(N, K, gu, W, y, residual=None, stream=None):
           "q8_0_matvec_silu")
 
 
-def attention_decode_rope(cfg, qkv, table, pos, k_cache, v_cache, out, workspace=None, stream=None):
+def attention_decode_rope(cfg, qkv, table, pos, k_cache, v_cache, out, workspace=None, stream=None, out_q8=None):
     import torch
 
     L = lib()
     wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
     ws = workspace if workspace is not None else torch.zeros(wsb, dtype=torch.uint8, device=qkv.device)
     check(L.ane_hip_attention_decode_rope(ctypes.byref(cfg), _p(qkv), _p(table), pos, _p(k_cache), _p(v_cache),
-                                          _p(out), _p(ws), wsb, _stream_handle(stream)), "attention_decode_rope")
+                                          _p(out), _p(out_q8), _p(ws), wsb, _stream_handle(stream)),
+          "attention_decode_rope")
 
 
 def silu_mul(n, gu, h, stream=None):
     check(lib().ane_hip_silu_mul(n, _p(gu), _p(h), _stream_handle(stream)), "silu_mul")
+
+
+def q8_act_bytes(n):
+    """Bytes of the Q8 activation form of n values: qx [n/32][32] int8, then dx [n/32] fp32."""
+    return n // 32 * 36
+
+
+def silu_mul_quant(n, gu, xq, stream=None):
+    check(lib().ane_hip_silu_mul_quant(n, _p(gu), _p(xq), _stream_handle(stream)), "silu_mul_quant")
+
+
+def q8_0_matvec_q8(N, K, xq, W, y, residual=None, stream=None):
+    check(lib().ane_hip_q8_0_matvec_q8(N, K, _p(xq), _p(W), _p(residual), _p(y), _stream_handle(stream)),
+          "q8_0_matvec_q8")
 
 
 def decode_workspace(cfg, device="cuda"):

@@ -129,6 +129,11 @@ __device__ __forceinline__ uint32_t max8_u32(uint32_t m) {
     return m > o ? m : o;
 }
 
+// SiLU(g) * u = (g / (1 + e^-g)) * u, the one definition every fused and
+// unfused SiLU step uses (bytecode_interpreter.s:6617 computes the sigmoid
+// with an exp approximation; fp32 expf here).
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
 // Four quantized values packed little-endian into one dword.
 __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
     return (uint32_t)(quant1(a, inv) & 0xff) | ((uint32_t)(quant1(b, inv) & 0xff) << 8) |
@@ -148,6 +153,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // LDS dst + 16*l (dst must be wave-uniform).
 __device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voffset, 0, 0, 0);
+}
+
+// One buffer_load_dword ... lds: lane l's dword at `voffset` lands at LDS
+// dst + 4*l.
+__device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 4, voffset, 0, 0, 0);
 }
 
 // s_waitcnt with vmcnt = n and the LDS/export counters left unconstrained;

@@ -272,7 +272,7 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
 // LDS, then every thread reads its dimension of up to 32 chunks at once.
 __global__ void __launch_bounds__(kHD)
 k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint32_t nch,
-               float* __restrict__ out) {
+               float* __restrict__ out, uint8_t* __restrict__ q8, uint32_t nq) {
     __shared__ float wsh[32];
     __shared__ float red[2][kHD / 64];
     const uint32_t h = blockIdx.x, d = threadIdx.x;
@@ -300,16 +300,51 @@ k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint
         for (int k = 0; k < 32; k++) O = __builtin_fmaf(v[k], wsh[k], O);
     }
     L = red[1][0] + red[1][1];
-    out[h * kHD + d] = O / L;
+    const float v = O / L;
+    out[h * kHD + d] = v;
+    if (q8) {  // the 32-blocks of the output, quantized as the G-mode staging would
+        uint32_t m = abs_key(v);
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) {
+            const uint32_t o = __shfl_xor(m, off, kWave);
+            m = m > o ? m : o;
+        }
+        float bs, inv;
+        quant_params(__uint_as_float(m), bs, inv);
+        const uint32_t i = h * kHD + d;
+        q8[i] = (uint8_t)quant1(v, inv);
+        if ((d & 31) == 0) reinterpret_cast<float*>(q8 + nq)[i >> 5] = bs;
+    }
 }
-
 
 __global__ void __launch_bounds__(256)
 k_silu_mul(uint32_t n, const float* __restrict__ gu, float* __restrict__ h) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float g = gu[i], u = gu[n + i];
-    h[i] = (g / (1.0f + expf(-g))) * u;
+    h[i] = silu_mul1(gu[i], gu[n + i]);
+}
+
+// h = silu(g) * u quantized to Q8 activation blocks: 8 lanes per 32-block,
+// a float4 each (the arithmetic of the G-mode staging).  xq: qx [nb][32],
+// then dx [nb] fp32.
+__global__ void __launch_bounds__(256)
+k_silu_mul_quant(uint32_t nb, const float* __restrict__ gu, uint8_t* __restrict__ xq) {
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x, blk = t >> 3, part = t & 7;
+    const uint32_t n = nb * 32;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(gu, 2 * n * 4);
+    const uint32_t o = blk < nb ? (blk * 32 + part * 4) * 4 : 0x80000000u;  // whole 8-lane groups stay active
+    float h[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        h[e] = silu_mul1(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4 * e, 0, 0)),
+                         __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4 * e + n * 4, 0, 0)));
+    const uint32_t m = max8_u32(max(max(abs_key(h[0]), abs_key(h[1])), max(abs_key(h[2]), abs_key(h[3]))));
+    float bs, inv;
+    quant_params(__uint_as_float(m), bs, inv);
+    if (blk < nb) {
+        reinterpret_cast<uint32_t*>(xq)[blk * 8 + part] = pack4(h[0], h[1], h[2], h[3], inv);
+        if (part == 0) reinterpret_cast<float*>(xq + n)[blk] = bs;
+    }
 }
 
 bool cfg_ok(const ane_decode_config* c) {
@@ -339,8 +374,9 @@ size_t attn_layout(const ane_decode_config* cfg, void* base, AttnWs* w) {
 }
 
 int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, const float* table_row,
-                     uint16_t* k_cache, uint16_t* v_cache, uint32_t len, float* out, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     uint16_t* k_cache, uint16_t* v_cache, uint32_t len, float* out, void* out_q8,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+    if (out_q8 && (((uintptr_t)out_q8) & 15)) return ANE_ERR_INVALID_ARG;
     if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < attn_layout(cfg, nullptr, nullptr))
         return ANE_ERR_WORKSPACE;
     AttnWs w;
@@ -354,13 +390,15 @@ int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, co
     else
         hipLaunchKernelGGL(k_attention<false>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, table_row, k_cache,
                            v_cache, len, cfg->ctx, cfg->n_heads, cfg->n_kv_heads, nch, scale, w.po, w.pml);
-    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, w.po, w.pml, nch, out);
+    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, w.po, w.pml, nch, out,
+                       static_cast<uint8_t*>(out_q8), cfg->n_heads * kHD);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
 
 struct DecodeWs {
-    float *qkv, *attn, *gu, *h;
+    float *qkv, *attn, *gu;
+    uint8_t *attn_q8, *h_q8;  // Q8 activation blocks: qx [nb][32], then dx [nb]
     void* att;
     size_t attb;
 };
@@ -376,10 +414,11 @@ size_t layout(const ane_decode_config* c, uint8_t* base, DecodeWs* w) {
     float* qkv = reinterpret_cast<float*>(take(nqkv * 4));
     float* attn = reinterpret_cast<float*>(take((uint64_t)c->n_heads * kHD * 4));
     float* gu = reinterpret_cast<float*>(take((uint64_t)2 * c->ffn * 4));
-    float* h = reinterpret_cast<float*>(take((uint64_t)c->ffn * 4));
+    uint8_t* attn_q8 = take((uint64_t)c->n_heads * kHD / 32 * 36);
+    uint8_t* h_q8 = take((uint64_t)c->ffn / 32 * 36);
     const size_t attb = ane_hip_attention_workspace_size(c);
     void* att = take(attb);
-    if (w) *w = DecodeWs{qkv, attn, gu, h, att, attb};
+    if (w) *w = DecodeWs{qkv, attn, gu, attn_q8, h_q8, att, attb};
     return off;
 }
 
@@ -413,23 +452,34 @@ extern "C" int ane_hip_attention_decode(const ane_decode_config* cfg, const floa
     if (!q || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
     if (len == 0 || len > cfg->ctx) return ANE_ERR_INVALID_ARG;
     return attention_launch(cfg, false, q, nullptr, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache),
-                            len, out, workspace, workspace_bytes, stream);
+                            len, out, nullptr, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ane_hip_attention_decode_rope(const ane_decode_config* cfg, const float* qkv, const float* rope_table,
                                              uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
-                                             void* workspace, size_t workspace_bytes, void* stream) {
+                                             void* out_q8, void* workspace, size_t workspace_bytes, void* stream) {
     if (!cfg_ok(cfg)) return ANE_ERR_INVALID_ARG;
     if (!qkv || !rope_table || !k_cache || !v_cache || !out) return ANE_ERR_BAD_POINTER;
     if (pos >= cfg->ctx) return ANE_ERR_INVALID_ARG;
     return attention_launch(cfg, true, qkv, rope_table + (uint64_t)pos * kHD, k_cache, v_cache, pos + 1, out,
-                            workspace, workspace_bytes, stream);
+                            out_q8, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream) {
     if (n == 0) return ANE_OK;
     if (!gu || !h) return ANE_ERR_BAD_POINTER;
     hipLaunchKernelGGL(k_silu_mul, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, n, gu, h);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_silu_mul_quant(uint32_t n, const float* gu, void* xq, void* stream) {
+    if (n == 0) return ANE_OK;
+    if (!gu || !xq) return ANE_ERR_BAD_POINTER;
+    if ((n & 31) || (((uintptr_t)xq) & 15)) return ANE_ERR_INVALID_ARG;
+    const uint32_t nb = n >> 5;
+    hipLaunchKernelGGL(k_silu_mul_quant, dim3((nb * 8 + 255) / 256), dim3(256), 0, (hipStream_t)stream, nb, gu,
+                       static_cast<uint8_t*>(xq));
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -457,13 +507,14 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
         int st;
         if ((st = ane_hip_q8_0_matvec_fused(nqkv, H, x, L.attn_norm, cfg->eps, L.w_qkv, nullptr, w.qkv, stream)))
             return st;
-        if ((st = ane_hip_attention_decode_rope(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, w.attn, w.att,
-                                                w.attb, stream)))
+        if ((st = ane_hip_attention_decode_rope(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, w.attn,
+                                                w.attn_q8, w.att, w.attb, stream)))
             return st;
-        if ((st = ane_hip_q8_0_matvec_fused(H, nq, w.attn, nullptr, 0.0f, L.w_o, x, x, stream))) return st;
+        if ((st = ane_hip_q8_0_matvec_q8(H, nq, w.attn_q8, L.w_o, x, x, stream))) return st;
         if ((st = ane_hip_q8_0_matvec_fused(2 * F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, nullptr, w.gu, stream)))
             return st;
-        if ((st = ane_hip_q8_0_matvec_silu(H, F, w.gu, L.w_down, x, x, stream))) return st;
+        if ((st = ane_hip_silu_mul_quant(F, w.gu, w.h_q8, stream))) return st;
+        if ((st = ane_hip_q8_0_matvec_q8(H, F, w.h_q8, L.w_down, x, x, stream))) return st;
     }
     return ANE_OK;
 }

@@ -285,36 +285,56 @@ struct XStage {
     }
 };
 
+// The staged block at rowp + 34b: its fp16 scale as fp32 and its 32 quants
+// as 8 dwords (bytes realigned with v_perm_b32).
+struct StagedBlock {
+    float dw;
+    int q[8];
+};
+
+__device__ __forceinline__ StagedBlock load_block(const int8_t* rowp, uint32_t b, uint32_t odd, uint32_t sel,
+                                                  uint32_t ssel) {
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(rowp + 34 * b - 2 * odd);
+    uint32_t D[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) D[i] = a[i];
+    StagedBlock r;
+    r.dw = half_bits_to_float(__builtin_amdgcn_perm(D[1], D[0], ssel));
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = (int)__builtin_amdgcn_perm(D[i + 1], D[i], sel);
+    return r;
+}
+
+// isum of a staged block against the quantized activation block at xb32
+// (32 bytes, halves swapped when h = 1).
+__device__ __forceinline__ int block_isum(const StagedBlock& w, const int8_t* xb32, uint32_t h) {
+    const v4i* xb = reinterpret_cast<const v4i*>(xb32);
+    const v4i x0 = xb[h], x1 = xb[h ^ 1];
+    int isum = 0;
+    isum = __builtin_amdgcn_sdot4(w.q[0], x0.x, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[1], x0.y, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[2], x0.z, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[3], x0.w, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[4], x1.x, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[5], x1.y, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[6], x1.z, isum, false);
+    isum = __builtin_amdgcn_sdot4(w.q[7], x1.w, isum, false);
+    return isum;
+}
+
 // One G-mode block: isum of the staged block at rowp + 34b against each
 // token's quantized block gb, folded into p[t] with one fma.
 template <int TT>
 __device__ __forceinline__ void block_g(const int8_t* rowp, uint32_t b, uint32_t odd, uint32_t sel,
                                         uint32_t ssel, uint32_t gb, const int8_t* qxs,
                                         const float* dxs, uint32_t nb, uint32_t T, float (&p)[TT]) {
-    const uint32_t* a = reinterpret_cast<const uint32_t*>(rowp + 34 * b - 2 * odd);
-    uint32_t D[9];
-#pragma unroll
-    for (int i = 0; i < 9; i++) D[i] = a[i];
-    const float dw = half_bits_to_float(__builtin_amdgcn_perm(D[1], D[0], ssel));
-    int q[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = (int)__builtin_amdgcn_perm(D[i + 1], D[i], sel);
+    const StagedBlock w = load_block(rowp, b, odd, sel, ssel);
     const uint32_t h = (gb >> 3) & 1;
 #pragma unroll
     for (int t = 0; t < TT; t++) {
         if (TT == 1 || t < (int)T) {
-            const v4i* xb = reinterpret_cast<const v4i*>(qxs + ((uint64_t)t * nb + gb) * 32);
-            const v4i x0 = xb[h], x1 = xb[h ^ 1];
-            int isum = 0;
-            isum = __builtin_amdgcn_sdot4(q[0], x0.x, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[1], x0.y, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[2], x0.z, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[3], x0.w, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[4], x1.x, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[5], x1.y, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[6], x1.z, isum, false);
-            isum = __builtin_amdgcn_sdot4(q[7], x1.w, isum, false);
-            const float dd = __fmul_rn(dw, dxs[t * nb + gb]);
+            const int isum = block_isum(w, qxs + ((uint64_t)t * nb + gb) * 32, h);
+            const float dd = __fmul_rn(w.dw, dxs[t * nb + gb]);
             p[t] = __builtin_fmaf((float)isum, dd, p[t]);
         }
     }
@@ -359,12 +379,12 @@ __device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint3
 //    fp32 value of ss / K does not depend on the summation order), then x' is
 //    quantized as usual;
 //  kFuseResidual: y[n] = fl(FADDV(p) + r[n]) (r may alias y: each row is read
-//    and written by the one lane that owns it).
+//    by the wave that owns it, into LDS, before that wave writes it).
 //  kFuseSiluMul: the input is gate|up (2K floats) and the row quantized is
 //    x[i] = (g / (1 + expf(-g))) * u with g = in[i], u = in[K + i].
-enum { kFuseNorm = 1, kFuseResidual = 2, kFuseSiluMul = 4 };
-
-__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+//  kFusePreQuant: the input is already quantized (qx [nb][32] int8, then dx
+//    [nb] fp32, as the staging would have produced it) and is copied into LDS.
+enum { kFuseNorm = 1, kFuseResidual = 2, kFuseSiluMul = 4, kFusePreQuant = 8 };
 
 struct StreamFuse {
     const float* norm_w;
@@ -388,6 +408,100 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
 __device__ __forceinline__ float rms_inv(double ss, uint32_t K, float eps) {
     const float ms = (float)(ss / (double)K);
     return 1.0f / sqrtf(ms + eps);
+}
+
+// The prologue of the streaming kernels: copies the residual of rows
+// r0 .. r1-1 (at most 64, one per lane) into this wave's LDS slot rres,
+// issues the activation loads (and those of the norm weights or the up
+// half), then ring_start() to put the first RING weight copies in flight
+// behind them, applies the fusions, stores x into LDS and waits for every
+// wave.
+template <int MODE, int NW, int FUSE, int RING, class Start>
+__device__ __forceinline__ void stream_prologue(const XStage<MODE, NW * 64>& xst, const StreamFuse& fz,
+                                                uint32_t N, uint32_t r0, uint32_t r1, double* red, float* rres,
+                                                Start&& ring_start) {
+    static_assert(!(FUSE & kFusePreQuant) || !(FUSE & (kFuseNorm | kFuseSiluMul)),
+                  "a pre-quantized input takes no activation fusion");
+    const uint32_t npass = xst.passes();
+    const uint32_t lane = threadIdx.x & 63;
+    if (FUSE & kFuseResidual) {  // issued first: every later wait covers it
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(fz.residual, N * 4);
+        copy4_to_lds(rr, rres, r0 + lane < r1 ? (r0 + lane) * 4 : 0x80000000u);
+    }
+    if (FUSE & kFusePreQuant) {
+        // 16-byte chunks: 2nb of qx (the halves of block b swapped on odd b/8,
+        // as XStage::store writes them), then nb/4 of dx
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const uint32_t nq = 2 * xst.nb, nchunks = nq + xst.nb / 4;
+        for (uint32_t c0 = wave * 64; c0 < nchunks; c0 += NW * 64) {
+            const uint32_t c = c0 + lane, b = c >> 1;
+            const uint32_t src = c < nq ? (2 * b + ((c & 1) ^ ((b >> 3) & 1))) * 16 : c * 16;
+            if (c < nchunks) copy16_to_lds(xst.xr, xst.lds + c0 * 16, src);
+        }
+        ring_start();
+        wait_vmcnt<RING>();  // the activation copies have landed (the ring's may be in flight)
+        lds_barrier();
+        return;
+    }
+    float4 xv[kXBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
+    float4 wv[(FUSE & (kFuseNorm | kFuseSiluMul)) ? kXBatch : 1];
+    if (FUSE & kFuseNorm) {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(fz.norm_w, xst.K * 4);
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load_w(k, wr);
+    }
+    if (FUSE & kFuseSiluMul) {
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(k, xst.K * 4);  // up
+    }
+    ring_start();
+    if (FUSE & kFuseSiluMul) {
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 g = xv[k], u = wv[k];
+            xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
+        }
+    }
+    if (FUSE & kFuseNorm) {  // the host guarantees npass <= kXBatch for this fusion
+        double ss = 0.0;
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 f = xv[k];  // lanes past the end hold zeros
+            ss += (double)f.x * f.x + (double)f.y * f.y + (double)f.z * f.z + (double)f.w * f.w;
+        }
+        ss = block_sum_f64<NW>(ss, red);
+        const float inv = rms_inv(ss, xst.K, fz.eps);
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) {
+            const float4 f = xv[k], w4 = wv[k];
+            xv[k] = make_float4(__fmul_rn(__fmul_rn(f.x, inv), w4.x), __fmul_rn(__fmul_rn(f.y, inv), w4.y),
+                                __fmul_rn(__fmul_rn(f.z, inv), w4.z), __fmul_rn(__fmul_rn(f.w, inv), w4.w));
+        }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kXBatch; k++)
+        if (k < npass) xst.store(k, xv[k]);
+    for (uint32_t p0 = kXBatch; p0 < npass; p0 += kXBatch) {  // SiLU*up is elementwise: any K
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(p0 + k);
+        if (FUSE & kFuseSiluMul) {
+#pragma unroll
+            for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(p0 + k, xst.K * 4);
+#pragma unroll
+            for (uint32_t k = 0; k < kXBatch; k++) {
+                const float4 g = xv[k], u = wv[k];
+                xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z),
+                                    silu_mul1(g.w, u.w));
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kXBatch; k++)
+            if (p0 + k < npass) xst.store(p0 + k, xv[k]);
+    }
+    wait_lgkmcnt0();
+    lds_barrier();
 }
 
 template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0>
@@ -427,67 +541,15 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     const int8_t* qxs = xlds;
     float* dxs = reinterpret_cast<float*>(xlds + ceil_to((uint64_t)T * nb * 32, 16));
     const float* xs = reinterpret_cast<const float*>(xlds);
-    const XStage<MODE, NW * 64> xst{make_rsrc(x, ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4), K, nb, T,
-                                    MODE == kModeG ? nb * T : nb * 8, xlds, dxs};
-    const uint32_t npass = xst.passes();
-    // residual values of this wave's rows (at most 64, one per lane), loaded
-    // first so the epilogue never waits on the ring's copies
-    float rv = 0.0f;
-    if (FUSE & kFuseResidual) {
-        const __amdgpu_buffer_rsrc_t rr = make_rsrc(fz.residual, N * 4);
-        rv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, r0 + lane < r1 ? (r0 + lane) * 4 : 0x80000000u, 0, 0));
-    }
-    float4 xv[kXBatch];
+    const uint32_t xbytes = (FUSE & kFusePreQuant) ? nb * 36 : ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4;
+    const XStage<MODE, NW * 64> xst{make_rsrc(x, xbytes), K, nb, T, MODE == kModeG ? nb * T : nb * 8, xlds, dxs};
+    const auto ring_start = [&] {
 #pragma unroll
-    for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
-    float4 wv[(FUSE & (kFuseNorm | kFuseSiluMul)) ? kXBatch : 1];
-    if (FUSE & kFuseNorm) {
-        const __amdgpu_buffer_rsrc_t wr = make_rsrc(fz.norm_w, K * 4);
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load_w(k, wr);
-    }
-    if (FUSE & kFuseSiluMul) {
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(k, K * 4);  // up
-    }
-#pragma unroll
-    for (int i = 0; i < S; i++) issue(i);
-    if (FUSE & kFuseSiluMul) {
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
-            const float4 g = xv[k], u = wv[k];
-            xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
-        }
-    }
-    if (FUSE & kFuseNorm) {  // the host guarantees npass <= kXBatch
-        double ss = 0.0;
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
-            const float4 f = xv[k];  // lanes past the end hold zeros
-            ss += (double)f.x * f.x + (double)f.y * f.y + (double)f.z * f.z + (double)f.w * f.w;
-        }
-        ss = block_sum_f64<NW>(ss, reinterpret_cast<double*>(xlds + stream_x_bytes(MODE, nb, T)));
-        const float inv = rms_inv(ss, K, fz.eps);
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
-            const float4 f = xv[k], w4 = wv[k];
-            xv[k] = make_float4(__fmul_rn(__fmul_rn(f.x, inv), w4.x), __fmul_rn(__fmul_rn(f.y, inv), w4.y),
-                                __fmul_rn(__fmul_rn(f.z, inv), w4.z), __fmul_rn(__fmul_rn(f.w, inv), w4.w));
-        }
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < kXBatch; k++)
-        if (k < npass) xst.store(k, xv[k]);
-    if (FUSE & kFuseResidual) asm volatile("" ::"v"(rv));  // its load completes here
-    for (uint32_t p0 = kXBatch; p0 < npass; p0 += kXBatch) {
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(p0 + k);
-#pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++)
-            if (p0 + k < npass) xst.store(p0 + k, xv[k]);
-    }
-    wait_lgkmcnt0();
-    lds_barrier();
+        for (int i = 0; i < S; i++) issue(i);
+    };
+    double* red = reinterpret_cast<double*>(xlds + stream_x_bytes(MODE, nb, T));
+    float* rres = reinterpret_cast<float*>(red + NW) + wave * 64;
+    stream_prologue<MODE, NW, FUSE, S * G::kDma>(xst, fz, N, r0, r1, red, rres, ring_start);
 
     float p[TT];
 #pragma unroll
@@ -512,7 +574,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 float v = faddv16(p[t]);
-                if (FUSE & kFuseResidual) v = v + __shfl(rv, (int)(kUnitRows * u + grp), kWave);
+                if (FUSE & kFuseResidual) v = v + rres[kUnitRows * u + grp];
                 if (l == 0 && row < r1 && (TT == 1 || t < (int)T)) y[(uint64_t)t * N + row] = v;
             }
         }
@@ -532,7 +594,7 @@ bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void
 
 template <int MODE, int NW, int SB, int S>
 uint64_t stream_lds(uint32_t nb, uint32_t T) {
-    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW;
+    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW + 256 * NW;
 }
 
 int cu_count(int dev) {
@@ -578,7 +640,8 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     if (grid < 1) grid = 1;
     // the residual fusion holds one row per lane: at most 64 rows per wave
     if ((FUSE & kFuseResidual) && ((uint64_t)N + grid * NW - 1) / (grid * NW) > 64) return -1;
-    if ((FUSE & (kFuseNorm | kFuseSiluMul)) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
+    // the norm fusion holds all of x in registers until the sum of squares is known
+    if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
                        (const uint8_t*)W, y, (uint32_t)(grid * NW), fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -655,6 +718,19 @@ extern "C" int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x,
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 
+extern "C" int ane_hip_q8_0_matvec_q8(uint32_t N, uint32_t K, const void* xq, const void* W,
+                                      const float* residual, float* y, void* stream) {
+    if (N == 0) return ANE_OK;
+    const uint32_t nb = K >> 5;
+    if (!y || !xq || !W || (K & 31)) return ANE_ERR_BAD_POINTER;
+    if ((((uintptr_t)xq) & 15) || !stream_eligible(N, nb, K, 1, W)) return ANE_ERR_INVALID_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    const float* xf = static_cast<const float*>(xq);
+    const StreamFuse fz{nullptr, 0.0f, residual};
+    const int r = residual ? stream_auto<kModeG, 1, kFusePreQuant | kFuseResidual>(N, nb, K, 1, xf, W, y, s, fz)
+                           : stream_auto<kModeG, 1, kFusePreQuant>(N, nb, K, 1, xf, W, y, s, fz);
+    return r < 0 ? ANE_ERR_INVALID_ARG : r;
+}
 extern "C" int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu, const void* W,
                                         const float* residual, float* y, void* stream) {
     if (N == 0) return ANE_OK;

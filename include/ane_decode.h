@@ -12,10 +12,16 @@
  *
  *   qkv  = W_qkv . q8(rmsnorm(x) * attn_norm)       fused norm prologue
  *   attn = softmax(rope(q) rope(k)^T / sqrt(d)) v over positions 0..pos (GQA),
- *          k, v of pos appended to the fp16 cache      one fused kernel + combine
+ *          k, v of pos appended to the fp16 cache      one fused kernel + combine,
+ *                                                    which also emits q8(attn)
  *   x    = x + W_o . q8(attn)                        fused residual epilogue
  *   gu   = W_gate_up . q8(rmsnorm(x) * ffn_norm)     fused norm prologue
- *   x    = x + W_down . q8(silu(gate) * up)          fused prologue and epilogue
+ *   h    = q8(silu(gate) * up)                       one small kernel
+ *   x    = x + W_down . h                            fused residual epilogue
+ *
+ * q8(v) is the Q8 activation form of the G mode: per 32-block, amax/127 as
+ * the fp32 scale and the values rounded to int8 (bytecode_interpreter.s
+ * 0x19 arithmetic), stored as qx [K/32][32] int8 followed by dx [K/32] fp32.
  *
  * Layouts: weights are Q8_0 rows (ggml block layout) with the output
  * features as rows: W_qkv rows [q heads | k heads | v heads], W_gate_up rows
@@ -77,6 +83,12 @@ int ane_decode_token(const struct ane_decode_config* cfg, const struct ane_decod
 int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x, const float* norm_w, float eps,
                               const void* W, const float* residual, float* y, void* stream);
 
+/* y = W . xq (+ residual) with xq already in the Q8 activation form (16-byte
+ * aligned, K/32 * 36 bytes); bit-identical to ane_hip_q8_0_matvec_fused on
+ * the fp32 vector xq was quantized from. */
+int ane_hip_q8_0_matvec_q8(uint32_t N, uint32_t K, const void* xq, const void* W, const float* residual,
+                           float* y, void* stream);
+
 /* y = W . q8(silu(gu[0..K)) * gu[K..2K)) (+ residual), silu(g) = g / (1 + e^-g):
  * the down projection with SiLU * up fused into its activation prologue;
  * bit-identical to ane_hip_silu_mul followed by ane_hip_q8_0_matvec_fused. */
@@ -99,13 +111,18 @@ int ane_hip_attention_decode(const struct ane_decode_config* cfg, const float* q
 
 /* ane_hip_attention_decode at len = pos + 1 on unrotated q and k: RoPE of q
  * and k (as ane_hip_rope_kv_append) and the fp16 append of k and v at pos
- * happen inside the attention kernel; same results, one launch fewer. */
+ * happen inside the attention kernel; same results, one launch fewer.
+ * out_q8 (optional, 16-byte aligned): out in the Q8 activation form too. */
 int ane_hip_attention_decode_rope(const struct ane_decode_config* cfg, const float* qkv, const float* rope_table,
-                                  uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, float* out, void* workspace,
-                                  size_t workspace_bytes, void* stream);
+                                  uint32_t pos, uint16_t* k_cache, uint16_t* v_cache, float* out, void* out_q8,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* h[i] = silu(gu[i]) * gu[n + i], i < n. */
 int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream);
+
+/* xq = q8(h) for h as ane_hip_silu_mul computes it (n % 32 == 0, xq 16-byte
+ * aligned, n/32 * 36 bytes). */
+int ane_hip_silu_mul_quant(uint32_t n, const float* gu, void* xq, void* stream);
 
 #ifdef __cplusplus
 }

@@ -105,7 +105,11 @@ def host(t):
 @pytest.mark.gpu
 @pytest.mark.parametrize("N,K,norm,resid", [(6144, 4096, True, False), (4096, 4096, False, True),
                                             (4096, 14336, False, True), (28672, 4096, True, False),
-                                            (512, 1024, True, True), (300, 256, False, False)])
+                                            (512, 1024, True, True), (300, 256, False, False),
+                                            # split-K: a last workgroup with a 2-row unit and an empty
+                                            # slot; 8 items per wave; 4 items per wave
+                                            (4098, 2048, True, True), (4100, 16384, False, True),
+                                            (1030, 8192, True, False)])
 def test_matvec_fused_exact(ane, oracle, N, K, norm, resid):
     import torch
 
@@ -256,9 +260,10 @@ def test_decode_tokens_small_model(ane, oracle):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("pos", [0, 5, 127, 128, 300])
-def test_attention_rope_fused_matches_separate(ane, pos):
+def test_attention_rope_fused_matches_separate(ane, oracle, pos):
     """RoPE + append inside the attention kernel == rope_kv_append then attention,
-    bit for bit; non-finite garbage at and past pos in the cache is never used."""
+    bit for bit; non-finite garbage at and past pos in the cache is never used;
+    the Q8 form of the output is the oracle's quantization of it."""
     import torch
 
     cfg = ane.DecodeConfig(1, 4096, 14336, 32, 8, 128, 512, 1e-5)
@@ -275,10 +280,13 @@ def test_attention_rope_fused_matches_separate(ane, pos):
     out2 = torch.zeros(4096, dtype=torch.float32, device="cuda")
     ane.rope_kv_append(cfg, q1, table, pos, k1, v1)
     ane.attention_decode(cfg, q1, k1, v1, pos + 1, out1)
-    ane.attention_decode_rope(cfg, dev(qkv), table, pos, k2, v2, out2)
+    q8 = torch.full((ane.q8_act_bytes(4096),), 0x55, dtype=torch.uint8, device="cuda")
+    ane.attention_decode_rope(cfg, dev(qkv), table, pos, k2, v2, out2, out_q8=q8)
     o1, o2 = host(out1), host(out2)
     assert np.isfinite(o2).all()
     assert o1.tobytes() == o2.tobytes()
+    qx, dx = oracle.q8_0_quantize_x(4096, o2)
+    assert host(q8).tobytes() == qx.tobytes() + dx.tobytes()
     assert host(k1)[:, :pos + 1].tobytes() == host(k2)[:, :pos + 1].tobytes()
     assert host(v1)[:, :pos + 1].tobytes() == host(v2)[:, :pos + 1].tobytes()
 
@@ -299,3 +307,46 @@ def test_matvec_silu_matches_separate(ane, resid):
     ane.q8_0_matvec_fused(N, F, h, W, y1, residual=y1 if resid else None)
     ane.q8_0_matvec_silu(N, F, gu, W, y2, residual=y2 if resid else None)
     assert host(y1).tobytes() == host(y2).tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [14336, 96, 8224])
+def test_silu_mul_quant_exact(ane, oracle, n):
+    """silu_mul_quant == the oracle's Q8 activation quantization of silu_mul's output."""
+    import torch
+
+    gu = dev((data.activations(1, 2 * n, seed=n)[0] * 3).astype(F32))
+    gu_h = host(gu)
+    gu_h[5] = 0.0
+    gu_h[n + 37: n + 69] = 0.0  # an all-zero block (scale 1)
+    gu = dev(gu_h)
+    h = torch.zeros(n, dtype=torch.float32, device="cuda")
+    xq = torch.full((ane.q8_act_bytes(n),), 0x55, dtype=torch.uint8, device="cuda")
+    ane.silu_mul(n, gu, h)
+    ane.silu_mul_quant(n, gu, xq)
+    qx, dx = oracle.q8_0_quantize_x(n, host(h))
+    assert host(xq).tobytes() == qx.tobytes() + dx.tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,resid", [(4096, 14336, True), (4096, 4096, True), (28672, 4096, False),
+                                       (301, 256, True), (6, 1024, False)])
+def test_matvec_q8_exact(ane, oracle, N, K, resid):
+    """A pre-quantized activation gives the oracle's G-mode result bit for bit."""
+    import torch
+
+    W = data.q8_0_weights(N, K, seed=N + 3 * K)
+    x = data.activations(1, K, seed=11)[0] * F32(2.5)
+    qx, dx = oracle.q8_0_quantize_x(K, x)
+    xq = dev(np.frombuffer(qx.tobytes() + dx.tobytes(), np.uint8).copy())
+    r = data.activations(1, N, seed=12)[0]
+    oracle.set_threads(0)
+    try:
+        ref = oracle.q8_0_mul_mat_g(N, K, 1, x, W)[0]
+    finally:
+        oracle.set_threads(1)
+    if resid:
+        ref = (ref + r).astype(F32)
+    y = dev(r) if resid else torch.zeros(N, dtype=torch.float32, device="cuda")
+    ane.q8_0_matvec_q8(N, K, xq, dev(W), y, residual=y if resid else None)
+    assert host(y).tobytes() == ref.tobytes()
