@@ -268,42 +268,47 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
     }
 }
 
-// One workgroup per query head merges the chunks: (max, sum) pairs through
-// LDS, then every thread reads its dimension of up to 32 chunks at once.
+// One workgroup per query head merges the chunks in one round trip: every
+// thread issues the loads of its dimension for up to 64 chunks before the
+// (max, sum) pairs are read; both waves reduce the pairs (M, then
+// L = sum l_c e^(m_c - M)) on their own, and wave 0 publishes the weights
+// e^(m_c - M) in LDS.
 __global__ void __launch_bounds__(kHD)
 k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint32_t nch,
                float* __restrict__ out, uint8_t* __restrict__ q8, uint32_t nq) {
-    __shared__ float wsh[32];
-    __shared__ float red[2][kHD / 64];
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    extern __shared__ float wsh[];  // [nch rounded up to 64]
+    const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63;
     const float* ml = pml + (uint64_t)h * nch * 2;
     const float* pd = po + (uint64_t)h * nch * kHD + d;
+    float v[64];  // chunks past nch read chunk nch-1 (finite) and get weight 0
+#pragma unroll
+    for (int k = 0; k < 64; k++) v[k] = pd[(uint64_t)min((uint32_t)k, nch - 1) * kHD];
     float M = -INFINITY;
-    for (uint32_t c = d; c < nch; c += kHD) M = fmaxf(M, ml[2 * c]);
+    for (uint32_t c = lane; c < nch; c += 64) M = fmaxf(M, ml[2 * c]);
     M = wave_max_f32(M);
-    if ((d & 63) == 0) red[0][d >> 6] = M;
-    __syncthreads();
-    M = fmaxf(red[0][0], red[0][1]);
     float L = 0.0f;
-    for (uint32_t c = d; c < nch; c += kHD) L = __builtin_fmaf(ml[2 * c + 1], expf(ml[2 * c] - M), L);
-    L = wave_sum_f32(L);
-    if ((d & 63) == 0) red[1][d >> 6] = L;
-    float O = 0.0f;
-    for (uint32_t c0 = 0; c0 < nch; c0 += 32) {
-        __syncthreads();
-        if (d < 32) wsh[d] = c0 + d < nch ? expf(ml[2 * (c0 + d)] - M) : 0.0f;
-        float v[32];  // chunks past nch read chunk nch-1 (finite) and get weight 0
-#pragma unroll
-        for (int k = 0; k < 32; k++) v[k] = pd[(uint64_t)min(c0 + k, nch - 1) * kHD];
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 32; k++) O = __builtin_fmaf(v[k], wsh[k], O);
+    for (uint32_t c = lane; c < nch; c += 64) {
+        const float w = expf(ml[2 * c] - M);
+        L = __builtin_fmaf(ml[2 * c + 1], w, L);
+        if (d < 64) wsh[c] = w;
     }
-    L = red[1][0] + red[1][1];
-    const float v = O / L;
-    out[h * kHD + d] = v;
+    const uint32_t nch64 = (nch + 63) & ~63u;  // wsh is sized in whole batches of 64; the tail weighs 0
+    if (d < 64 && nch + lane < nch64) wsh[nch + lane] = 0.0f;
+    L = wave_sum_f32(L);
+    __syncthreads();
+    float O = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 64; k++) O = __builtin_fmaf(v[k], wsh[k], O);
+    for (uint32_t c0 = 64; c0 < nch; c0 += 64) {  // contexts past 64 chunks
+#pragma unroll
+        for (int k = 0; k < 64; k++) v[k] = pd[(uint64_t)min(c0 + k, nch - 1) * kHD];
+#pragma unroll
+        for (int k = 0; k < 64; k++) O = __builtin_fmaf(v[k], wsh[c0 + k], O);
+    }
+    const float r = O / L;
+    out[h * kHD + d] = r;
     if (q8) {  // the 32-blocks of the output, quantized as the G-mode staging would
-        uint32_t m = abs_key(v);
+        uint32_t m = abs_key(r);
 #pragma unroll
         for (int off = 16; off >= 1; off >>= 1) {
             const uint32_t o = __shfl_xor(m, off, kWave);
@@ -312,7 +317,7 @@ k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, uint
         float bs, inv;
         quant_params(__uint_as_float(m), bs, inv);
         const uint32_t i = h * kHD + d;
-        q8[i] = (uint8_t)quant1(v, inv);
+        q8[i] = (uint8_t)quant1(r, inv);
         if ((d & 31) == 0) reinterpret_cast<float*>(q8 + nq)[i >> 5] = bs;
     }
 }
@@ -349,7 +354,8 @@ k_silu_mul_quant(uint32_t nb, const float* __restrict__ gu, uint8_t* __restrict_
 
 bool cfg_ok(const ane_decode_config* c) {
     return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
-           c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->hidden % 32 == 0 && c->ffn % 32 == 0 &&
+           c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->ctx <= (1u << 20) && c->hidden % 32 == 0 &&
+           c->ffn % 32 == 0 &&
            (uint64_t)c->n_heads * kHD % 32 == 0;
 }
 
@@ -390,7 +396,7 @@ int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, co
     else
         hipLaunchKernelGGL(k_attention<false>, dim3(cfg->n_kv_heads, nch), dim3(256), 0, s, q, table_row, k_cache,
                            v_cache, len, cfg->ctx, cfg->n_heads, cfg->n_kv_heads, nch, scale, w.po, w.pml);
-    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), 0, s, w.po, w.pml, nch, out,
+    hipLaunchKernelGGL(k_attn_combine, dim3(cfg->n_heads), dim3(kHD), ((nch + 63) & ~63u) * 4, s, w.po, w.pml, nch, out,
                        static_cast<uint8_t*>(out_q8), cfg->n_heads * kHD);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;

@@ -47,7 +47,7 @@ struct ane_decode_config {
     uint32_t n_heads;     /* query heads (32)                   */
     uint32_t n_kv_heads;  /* key/value heads (8)                */
     uint32_t head_dim;    /* 128 (the only supported value)     */
-    uint32_t ctx;         /* KV cache capacity in positions     */
+    uint32_t ctx;         /* KV cache capacity in positions (at most 2^20) */
     float eps;            /* RMSNorm epsilon                    */
 };
 

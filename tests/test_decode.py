@@ -155,14 +155,16 @@ def test_rope_kv_append_exact(ane):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("length", [1, 100, 128, 129, 1000, 4096])
-def test_attention_decode(ane, length):
+@pytest.mark.parametrize("length,ctx", [(1, 4096), (100, 4096), (128, 4096), (129, 4096), (1000, 4096),
+                                        (4096, 4096), (5000, 8192), (8192, 8192)])
+def test_attention_decode(ane, length, ctx):
+    """Against a float64 softmax; contexts past 64 chunks take the merge's second batch."""
     import torch
 
-    cfg = ane.DecodeConfig(1, 4096, 14336, 32, 8, 128, 4096, 1e-5)
+    cfg = ane.DecodeConfig(1, 4096, 14336, 32, 8, 128, ctx, 1e-5)
     g = np.random.default_rng(length)
-    kc = g.standard_normal((8, 4096, 128)).astype(np.float16)
-    vc = g.standard_normal((8, 4096, 128)).astype(np.float16)
+    kc = g.standard_normal((8, ctx, 128)).astype(np.float16)
+    vc = g.standard_normal((8, ctx, 128)).astype(np.float16)
     q = (g.standard_normal((32, 128)) * 2.0).astype(F32)
     out = torch.zeros(32 * 128, dtype=torch.float32, device="cuda")
     ws = torch.zeros(ane.lib().ane_hip_attention_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device="cuda")
