@@ -36,7 +36,20 @@ class Op(enum.IntEnum):
     quantize_fp32_i8_channelwise = 0x1C
     dense_u8s8 = 0x1E
     q8_0_gemv = 0x57
+    q4_0_gemv = 0x58
+    q4_k_gemv = 0x75
+    q2_k_gemv = 0x76
+    q3_k_gemv = 0x77
+    q5_k_gemv = 0x78
+    q6_k_gemv = 0x79
+    get_rows_q8_0 = 0x7C
+    get_rows_q4_0 = 0x7D
     dense_fused_i8 = 0x80
+
+
+# R-mode GEMV formats besides Q8_0: name -> (bytes, values) per (super-)block
+QFORMATS = {"q4_0": (18, 32), "q4_k": (144, 256), "q2_k": (84, 256), "q3_k": (110, 256),
+            "q5_k": (176, 256), "q6_k": (210, 256)}
 
 
 class AneError(RuntimeError):
@@ -80,6 +93,14 @@ EXPORTS = (
     "ane_hip_dense_fused_i8_gemm",
     "ane_hip_gemm_s8_i32",
     "ane_hip_q8_0_gemv",
+    "ane_hip_q4_0_gemv",
+    "ane_hip_q4_k_gemv",
+    "ane_hip_q2_k_gemv",
+    "ane_hip_q3_k_gemv",
+    "ane_hip_q5_k_gemv",
+    "ane_hip_q6_k_gemv",
+    "ane_hip_get_rows_q8_0",
+    "ane_hip_get_rows_q4_0",
     "ane_hip_q8_0_mul_mat_workspace_size",
     "ane_hip_q8_0_mul_mat",
     "ane_hip_device_check",
@@ -142,6 +163,9 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _c.c_uint32, _P, _c.c_uint32, _P, _P],
     ),
     "ane_hip_q8_0_gemv": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]),
+    **{f"ane_hip_{f}_gemv": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]) for f in QFORMATS},
+    "ane_hip_get_rows_q8_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
+    "ane_hip_get_rows_q4_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
     "ane_hip_q8_0_mul_mat_workspace_size": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),
     "ane_hip_q8_0_mul_mat": (
         _c.c_int,
@@ -277,6 +301,16 @@ def rec_q8_0_gemv(M, K, x, W, y) -> bytes:
     return encode(Op.q8_0_gemv, u32(M), u32(K), ptr(x), ptr(W), ptr(y))
 
 
+def rec_q_gemv(fmt, M, K, x, W, y) -> bytes:
+    """Record of one of the QFORMATS GEMVs (same layout as q8_0_gemv)."""
+    return encode(Op[f"{fmt}_gemv"], u32(M), u32(K), ptr(x), ptr(W), ptr(y))
+
+
+def rec_get_rows(fmt, n_rows, dim, table, indices, out) -> bytes:
+    """get_rows_q8_0 / get_rows_q4_0 record: [n_rows:u32][dim:u32][table][indices][out]."""
+    return encode(Op[f"get_rows_{fmt}"], u32(n_rows), u32(dim), ptr(table), ptr(indices), ptr(out))
+
+
 def rec_dense_fused_i8(M, N, K, scale, relu, A, B, C) -> bytes:
     return encode(Op.dense_fused_i8, i32(M), i32(N), i32(K), f32(scale), boolean(relu), ptr(A), ptr(B),
                   ptr(C))
@@ -371,6 +405,22 @@ def q8_0_gemv(M, K, x, W, y, stream=None):
     check(lib().ane_hip_q8_0_gemv(M, K, _p(x), _p(W), _p(y), _stream_handle(stream)), "q8_0_gemv")
 
 
+def q_gemv(fmt, M, K, x, W, y, stream=None):
+    """y = W x for W in one of QFORMATS (the reference's R-mode arithmetic)."""
+    if fmt not in QFORMATS:
+        raise ValueError(f"unknown format {fmt!r}")
+    check(getattr(lib(), f"ane_hip_{fmt}_gemv")(M, K, _p(x), _p(W), _p(y), _stream_handle(stream)),
+          f"{fmt}_gemv")
+
+
+def get_rows(fmt, n_rows, dim, table, table_rows, indices, out, stream=None):
+    """out[r] = dequantized table row indices[r] (fmt "q8_0" or "q4_0")."""
+    if fmt not in ("q8_0", "q4_0"):
+        raise ValueError(f"unknown format {fmt!r}")
+    check(getattr(lib(), f"ane_hip_get_rows_{fmt}")(n_rows, dim, _p(table), table_rows, _p(indices), _p(out),
+                                                     _stream_handle(stream)), f"get_rows_{fmt}")
+
+
 def q8_0_mul_mat_workspace_size(K, T) -> int:
     return int(lib().ane_hip_q8_0_mul_mat_workspace_size(K, T))
 
@@ -433,7 +483,7 @@ GgmlTensor._fields_ = [
     ("data", ctypes.c_void_p),
 ]
 
-_TYPE_SIZE = {GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.Q8_0: (32, 34)}
+_TYPE_SIZE = {GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.Q4_0: (32, 18), GgmlType.Q8_0: (32, 34)}
 
 
 def ggml_tensor(type_, ne, data=None, nb=None, op=GgmlOp.NONE, src=()) -> GgmlTensor:

@@ -1,6 +1,6 @@
 // ggml_backend.hip -- the GGML_OP_MUL_MAT hook of ane's ggml backend
 // (reference src/ggml-backend/ggml-ane.cpp:109-154, 287-299, 363-368) on the
-// Q8_0 kernels of q8_0.hip.
+// Q8_0 kernels of q8_0.hip and the Q4_0 GEMV of qformats.hip.
 //
 // dst[i3][i2][i1][i0] = sum_k src0[i3/r3][i2/r2][i0][k] * src1[i3][i2][i1][k]
 // with r2 = ne12/ne02, r3 = ne13/ne03 (ggml's broadcast of the weights over
@@ -60,9 +60,10 @@ const ane_ggml_tensor* src_of(const ane_ggml_tensor* t, int i) { return t ? t->s
 bool mul_mat_supported(const ane_ggml_tensor* d) {
     const ane_ggml_tensor* a = src_of(d, 0);
     const ane_ggml_tensor* b = src_of(d, 1);
-    if (!a || !b || d->type != ANE_GGML_TYPE_F32 || a->type != ANE_GGML_TYPE_Q8_0 ||
-        b->type != ANE_GGML_TYPE_F32)
+    if (!a || !b || d->type != ANE_GGML_TYPE_F32 ||
+        (a->type != ANE_GGML_TYPE_Q8_0 && a->type != ANE_GGML_TYPE_Q4_0) || b->type != ANE_GGML_TYPE_F32)
         return false;
+    const size_t bb = a->type == ANE_GGML_TYPE_Q8_0 ? 34 : 18;  // bytes per 32-weight block
     for (int i = 0; i < 4; i++)
         if (d->ne[i] < 0 || a->ne[i] < 0 || b->ne[i] < 0) return false;
     const int64_t K = a->ne[0];
@@ -71,8 +72,8 @@ bool mul_mat_supported(const ane_ggml_tensor* d) {
         return false;
     if (a->ne[2] == 0 || a->ne[3] == 0 || b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0)
         return false;
-    // innermost strides: one Q8_0 block (34 bytes) / one float; weight rows packed
-    if (a->nb[0] != 34 || a->nb[1] != (size_t)(K / 32) * 34 || b->nb[0] != 4 || d->nb[0] != 4)
+    // innermost strides: one block / one float; weight rows packed
+    if (a->nb[0] != bb || a->nb[1] != (size_t)(K / 32) * bb || b->nb[0] != 4 || d->nb[0] != 4)
         return false;
     if (d->ne[0] > 0xffffffffLL || K > 0xffffffffLL) return false;
     return true;
@@ -95,12 +96,15 @@ bool ensure_ws(ane_ggml_backend* be, size_t bytes) {
     return true;
 }
 
-// One Q8_0 call over T rows: x rows `xs` bytes apart, y rows `ys` bytes apart.
-int mul_mat_rows(ane_ggml_backend* be, uint32_t N, uint32_t K, uint32_t T, const void* W,
+// One weight matrix over T rows: x rows `xs` bytes apart, y rows `ys` bytes
+// apart.  Q8_0 in the backend's mode; Q4_0 with the reference's q4_0_gemv
+// arithmetic (its only one) for every row.
+int mul_mat_rows(ane_ggml_backend* be, int type, uint32_t N, uint32_t K, uint32_t T, const void* W,
                  const uint8_t* x, uint64_t xs, uint8_t* y, uint64_t ys) {
     if (T == 0 || N == 0) return ANE_OK;
     const bool xc = xs == (uint64_t)K * 4, yc = ys == (uint64_t)N * 4;
-    const size_t qws = be->q8_mode == ANE_GGML_Q8_G ? ane_hip_q8_0_mul_mat_workspace_size(K, T) : 0;
+    const bool g = type == ANE_GGML_TYPE_Q8_0 && be->q8_mode == ANE_GGML_Q8_G;
+    const size_t qws = g ? ane_hip_q8_0_mul_mat_workspace_size(K, T) : 0;
     const size_t xoff = ceil_to(qws, 256);
     const size_t xbytes = xc ? 0 : ceil_to((uint64_t)T * K * 4, 256);
     const size_t yoff = xoff + xbytes;
@@ -116,11 +120,12 @@ int mul_mat_rows(ane_ggml_backend* be, uint32_t N, uint32_t K, uint32_t T, const
     }
     float* yp = yc ? reinterpret_cast<float*>(y) : reinterpret_cast<float*>(ws + yoff);
     int st = ANE_OK;
-    if (be->q8_mode == ANE_GGML_Q8_G) {
+    if (g) {
         st = ane_hip_q8_0_mul_mat(N, K, T, xp, W, yp, ws, qws, be->stream);
     } else {
+        const auto gemv = type == ANE_GGML_TYPE_Q8_0 ? ane_hip_q8_0_gemv : ane_hip_q4_0_gemv;
         for (uint32_t t = 0; t < T && st == ANE_OK; t++)
-            st = ane_hip_q8_0_gemv(N, K, xp + (uint64_t)t * K, W, yp + (uint64_t)t * N, be->stream);
+            st = gemv(N, K, xp + (uint64_t)t * K, W, yp + (uint64_t)t * N, be->stream);
     }
     if (st != ANE_OK) return st;
     if (!yc) {
@@ -149,13 +154,13 @@ int mul_mat(ane_ggml_backend* be, const ane_ggml_tensor* d) {
                            (B3 == 1 || d->nb[3] == (size_t)(T * B2) * d->nb[1]);
     const int64_t rows = T * B2 * B3;
     if (w_shared && x_uniform && y_uniform && rows <= 0xffffffffLL)
-        return mul_mat_rows(be, N, K, (uint32_t)rows, a->data, x0, b->nb[1], y0, d->nb[1]);
+        return mul_mat_rows(be, a->type, N, K, (uint32_t)rows, a->data, x0, b->nb[1], y0, d->nb[1]);
     if (T > 0xffffffffLL) return ANE_ERR_INVALID_ARG;
     for (int64_t i3 = 0; i3 < B3; i3++) {
         for (int64_t i2 = 0; i2 < B2; i2++) {
             const uint8_t* W = static_cast<const uint8_t*>(a->data) + (i2 / r2) * a->nb[2] + (i3 / r3) * a->nb[3];
-            const int st = mul_mat_rows(be, N, K, (uint32_t)T, W, x0 + i2 * b->nb[2] + i3 * b->nb[3], b->nb[1],
-                                        y0 + i2 * d->nb[2] + i3 * d->nb[3], d->nb[1]);
+            const int st = mul_mat_rows(be, a->type, N, K, (uint32_t)T, W, x0 + i2 * b->nb[2] + i3 * b->nb[3],
+                                        b->nb[1], y0 + i2 * d->nb[2] + i3 * d->nb[3], d->nb[1]);
             if (st != ANE_OK) return st;
         }
     }

@@ -1,0 +1,316 @@
+// qformats.hip -- the reference's other weight formats: Q4_0 and the K-quant
+// GEMVs (R mode: fp32 x, the handler's 16 fma lanes per row and FADDV tree)
+// and the Q8_0 / Q4_0 row gathers.
+//
+//   0x58 q4_0_gemv      bytecode_interpreter.s:7071-7126    18 B / 32 values
+//   0x75 q4_k_gemv      :11024-11131                         144 B / 256
+//   0x76 q2_k_gemv      :11146-11222                         84 B / 256
+//   0x77 q3_k_gemv      :11236-11358                         110 B / 256
+//   0x78 q5_k_gemv      :11372-11483                         176 B / 256
+//   0x79 q6_k_gemv      :11498-11626                         210 B / 256
+//   0x7C get_rows_q8_0  :12363-12408
+//   0x7D get_rows_q4_0  :12419-12469
+//
+// GEMV layout on the GPU: a workgroup of 256 threads takes 16 rows, one per
+// 16-lane group, lane l of a row carrying the handler's lane l.  A group
+// streams its row in stages of P super-blocks: 16-byte range-checked buffer
+// loads of the 16-byte-aligned window around the stage (any row alignment,
+// the window never leaves the pointer's 16-byte granule at the front and
+// reads zeros past the matrix's last dword), two stages in flight in registers, each stage
+// written to the group's own LDS window and decoded from there with byte
+// reads.  x is staged in LDS in chunks of 8192 values shared by the 16 rows.
+#include "../../include/ane_hip.h"
+#include "common.hpp"
+
+namespace ane {
+namespace {
+
+__device__ __forceinline__ uint32_t lu8(const uint8_t* p) { return *p; }
+__device__ __forceinline__ uint32_t lu16(const uint8_t* p) { return lu8(p) | (lu8(p + 1) << 8); }
+__device__ __forceinline__ uint32_t lu32(const uint8_t* p) { return lu16(p) | (lu16(p + 2) << 16); }
+__device__ __forceinline__ float lh(const uint8_t* p) { return half_bits_to_float(lu16(p)); }
+
+// Q4_K / Q5_K 6-bit (scale, min) of sub-block j (bytecode_interpreter.s:11064-11089).
+__device__ __forceinline__ void scale_min6(const uint8_t* s, int j, uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = lu8(s + j) & 63u;
+        m = lu8(s + j + 4) & 63u;
+    } else {
+        sc = (lu8(s + j + 4) & 15u) | ((lu8(s + j - 4) >> 6) << 4);
+        m = (lu8(s + j + 4) >> 4) | ((lu8(s + j) >> 6) << 4);
+    }
+}
+
+// Each format: kBytes / kValues per super-block (a Q4_0 block counts as one),
+// kStage super-blocks per stage, and acc(s, xs, l, acc): lane l's fmas over
+// the super-block at LDS s with its inputs at LDS xs, in the handler's order.
+struct Q40 {
+    static constexpr uint32_t kBytes = 18, kValues = 32, kStage = 32;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s);
+        const uint32_t b = lu8(s + 2 + l);
+        a = __builtin_fmaf(__fmul_rn((float)((int)(b & 15u) - 8), d), xs[l], a);
+        a = __builtin_fmaf(__fmul_rn((float)((int)(b >> 4) - 8), d), xs[16 + l], a);
+    }
+};
+
+struct Q4K {
+    static constexpr uint32_t kBytes = 144, kValues = 256, kStage = 4;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s), nmin = -lh(s + 2);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t sc, m;
+            scale_min6(s + 4, j, sc, m);
+            const float ds = __fmul_rn(d, (float)sc), dm = __fmul_rn(nmin, (float)m);
+            const uint32_t b = lu8(s + 16 + 16 * j + l);
+            a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)(b & 15u), ds), dm), xs[32 * j + l], a);
+            a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)(b >> 4), ds), dm), xs[32 * j + 16 + l], a);
+        }
+    }
+};
+
+struct Q2K {
+    static constexpr uint32_t kBytes = 84, kValues = 256, kStage = 4;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s + 80), nmin = -lh(s + 82);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t scb = lu8(s + j);
+            const float ds = __fmul_rn(d, (float)(scb & 15u)), dm = __fmul_rn(nmin, (float)(scb >> 4));
+            const uint32_t q = (lu32(s + 16 + 4 * j) >> (2 * l)) & 3u;
+            a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)q, ds), dm), xs[16 * j + l], a);
+        }
+    }
+};
+
+// The second half of each sub-block first shifts its qs word right by the bit
+// pattern of the lane's first-half input (SVE LSR: amounts >= 32 give 0), as
+// the handler does with the register its input load reused (:11323-11329).
+struct Q3K {
+    static constexpr uint32_t kBytes = 110, kValues = 256, kStage = 4;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s + 108);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t sc = j < 4 ? (lu8(s + 96 + j) & 63u)
+                                      : ((lu8(s + 100 + j) & 15u) | ((lu8(s + 92 + j) >> 6) << 4));
+            const float ds = __fmul_rn(d, (float)((int)sc - 32));
+            const float xa = xs[32 * j + l];
+            const uint32_t qa = lu32(s + 32 + 8 * j), ha = lu16(s + 4 * j);
+            const int q0 = (int)(((qa >> (2 * l)) & 3u) | (((ha >> l) & 1u) << 2));
+            a = __builtin_fmaf(__fmul_rn((float)(q0 - 4), ds), xa, a);
+            const uint32_t sh = __float_as_uint(xa);
+            const uint32_t qb = sh >= 32u ? 0u : lu32(s + 36 + 8 * j) >> sh;
+            const uint32_t hb = lu16(s + 4 * j + 2);
+            const int q1 = (int)(((qb >> (2 * l)) & 3u) | (((hb >> l) & 1u) << 2));
+            a = __builtin_fmaf(__fmul_rn((float)(q1 - 4), ds), xs[32 * j + 16 + l], a);
+        }
+    }
+};
+
+struct Q5K {
+    static constexpr uint32_t kBytes = 176, kValues = 256, kStage = 4;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s), nmin = -lh(s + 2);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t sc, m;
+            scale_min6(s + 4, j, sc, m);
+            const float ds = __fmul_rn(d, (float)sc), dm = __fmul_rn(nmin, (float)m);
+            const uint32_t b = lu8(s + 48 + 16 * j + l), h = lu32(s + 16 + 4 * j);
+            const uint32_t q0 = (b & 15u) | ((((h & 0xffffu) >> l) & 1u) << 4);
+            const uint32_t q1 = (b >> 4) | ((((h >> 16) >> l) & 1u) << 4);
+            a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)q0, ds), dm), xs[32 * j + l], a);
+            a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)q1, ds), dm), xs[32 * j + 16 + l], a);
+        }
+    }
+};
+
+struct Q6K {
+    static constexpr uint32_t kBytes = 210, kValues = 256, kStage = 4;
+    __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
+        const float d = lh(s + 208);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float ds = __fmul_rn(d, (float)(int8_t)lu8(s + 192 + j));
+            const uint32_t byte = lu8(s + 8 * j + (l >> 1));
+            const uint32_t nib = (l & 1) ? (byte >> 4) : (byte & 15u);
+            const int q = (int)(nib | (((lu32(s + 128 + 4 * j) >> (2 * l)) & 3u) << 4));
+            a = __builtin_fmaf(__fmul_rn((float)(q - 32), ds), xs[16 * j + l], a);
+        }
+    }
+};
+
+constexpr uint32_t kRowsPerWg = 16;
+constexpr uint32_t kXChunk = 8192;  // x values staged per pass
+
+template <class F>
+struct Stage {
+    // 16-byte loads per lane covering a stage's window (<= 15 bytes of lead-in)
+    static constexpr uint32_t kLoads = (F::kStage * F::kBytes + 15 + 255) / 256;
+    static constexpr uint32_t kWindow = kLoads * 256;
+};
+
+template <class F>
+__global__ void __launch_bounds__(256)
+k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const uint8_t* Wa, uint32_t off,
+        uint32_t wbytes, float* __restrict__ y) {
+    using St = Stage<F>;
+    __shared__ __attribute__((aligned(16))) uint8_t win_all[kRowsPerWg][St::kWindow];
+    __shared__ float xs[kXChunk];
+    const uint32_t g = threadIdx.x >> 4, l = threadIdx.x & 15;
+    const uint32_t r = blockIdx.x * kRowsPerWg + g;
+    const bool live = r < M;
+    uint8_t* win = win_all[g];
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(Wa, wbytes);
+    const uint64_t rb = (uint64_t)nsb * F::kBytes;
+    const uint64_t row0 = off + (live ? r : 0) * rb;  // byte of the row in the rsrc
+    const uint32_t nst = (nsb + F::kStage - 1) / F::kStage;
+    constexpr uint32_t kChunkSb = kXChunk / F::kValues;  // super-blocks per x chunk
+    static_assert(kChunkSb % (2 * F::kStage) == 0, "x chunks start on the even stages the loop restages at");
+
+    auto load = [&](uint4 (&v)[St::kLoads], uint32_t st) {
+        const uint64_t b = row0 + (uint64_t)st * F::kStage * F::kBytes;
+        const uint32_t w0 = (uint32_t)(b & ~(uint64_t)15);
+#pragma unroll
+        for (uint32_t i = 0; i < St::kLoads; i++) {
+            const uint32_t o = (live && st < nst) ? w0 + 256 * i + 16 * l : 0x80000000u;
+            v[i] = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 4, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 8, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 12, 0, 0));
+        }
+    };
+    auto run = [&](const uint4 (&v)[St::kLoads], uint32_t st, float& acc) {
+#pragma unroll
+        for (uint32_t i = 0; i < St::kLoads; i++) *reinterpret_cast<uint4*>(win + 256 * i + 16 * l) = v[i];
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t lead = (uint32_t)((row0 + (uint64_t)st * F::kStage * F::kBytes) & 15);
+        const uint32_t sb0 = st * F::kStage;
+#pragma unroll
+        for (uint32_t p = 0; p < F::kStage; p++)
+            if (sb0 + p < nsb) F::acc(win + lead + p * F::kBytes, xs + ((sb0 + p) % kChunkSb) * F::kValues, l, acc);
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    float acc = 0.0f;
+    uint4 va[St::kLoads], vb[St::kLoads];
+    load(va, 0);
+    load(vb, 1);
+    for (uint32_t st = 0; st < nst; st += 2) {
+        if ((st * F::kStage) % kChunkSb == 0) {  // next x chunk (every group is at the same stage)
+            __syncthreads();
+            const uint32_t k0 = st * F::kStage * F::kValues;
+            for (uint32_t i = threadIdx.x; i < kXChunk; i += 256) xs[i] = k0 + i < K ? x[k0 + i] : 0.0f;
+            __syncthreads();
+        }
+        run(va, st, acc);
+        load(va, st + 2);
+        if (st + 1 < nst) {
+            run(vb, st + 1, acc);
+            load(vb, st + 3);
+        }
+    }
+    const float v = faddv16(acc);
+    if (live && l == 0) y[r] = v;
+}
+
+// 8 lanes per 32-block, 4 outputs each, over a flat grid of every output
+// row; rows whose index is past table_rows are written as zeros.
+template <bool Q4>
+__global__ void __launch_bounds__(256)
+k_get_rows(uint32_t n_rows, uint32_t nb, const uint8_t* __restrict__ table, uint64_t table_rows,
+           const uint32_t* __restrict__ idx, float* __restrict__ out) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t rb = (uint64_t)nb * 8;  // threads per output row
+    if (t >= rb * n_rows) return;
+    const uint32_t r = (uint32_t)(t / rb), blk = (uint32_t)(t - (uint64_t)r * rb) >> 3, part = t & 7;
+    const uint32_t row = idx[r];
+    float* o = out + ((uint64_t)r * nb + blk) * 32 + part * 4;
+    if (row >= table_rows) {
+        o[0] = o[1] = o[2] = o[3] = 0.0f;
+        return;
+    }
+    constexpr uint32_t kB = Q4 ? 18 : 34;
+    const uint8_t* b = table + ((uint64_t)row * nb + blk) * kB;
+    const float d = half_bits_to_float((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t i = part * 4 + e;  // element of the block
+        float v;
+        if (Q4) {
+            const uint32_t q = b[2 + (i & 15)];
+            v = __fmul_rn((float)((int)(i < 16 ? (q & 15u) : (q >> 4)) - 8), d);
+        } else {
+            v = __fmul_rn((float)(int8_t)b[2 + i], d);
+        }
+        o[e] = v;
+    }
+}
+
+template <class F>
+int qgemv_launch(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    if (M == 0) return ANE_OK;
+    const uint32_t nsb = K / F::kValues;  // the handlers ignore a remainder (K >> 5 / K >> 8)
+    if (!y || (nsb && (!x || !W))) return ANE_ERR_BAD_POINTER;
+    const uintptr_t wp = reinterpret_cast<uintptr_t>(W);
+    const uint32_t off = (uint32_t)(wp & 15);
+    const uint64_t bytes = off + (uint64_t)M * nsb * F::kBytes + 512;  // + the last window's over-read
+    if (bytes >= 0x80000000ull) return ANE_ERR_INVALID_ARG;
+    // the range ends on a dword boundary: the range check drops a whole dword
+    // that crosses its end, and the bytes up to the boundary share the last
+    // byte's 4-byte granule (so its page)
+    const uint32_t range = (uint32_t)((off + (uint64_t)M * nsb * F::kBytes + 3) & ~(uint64_t)3);
+    hipLaunchKernelGGL(k_qgemv<F>, dim3((M + kRowsPerWg - 1) / kRowsPerWg), dim3(256), 0, (hipStream_t)stream, M,
+                       nsb, K, x, reinterpret_cast<const uint8_t*>(wp - off), off, range, y);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+template <bool Q4>
+int get_rows_launch(uint32_t n_rows, uint32_t dim, const void* table, uint64_t table_rows, const uint32_t* indices,
+                    float* out, void* stream) {
+    if (n_rows == 0 || dim < 32) return ANE_OK;
+    if (!table || !indices || !out) return ANE_ERR_BAD_POINTER;
+    if (dim & 31) return ANE_ERR_INVALID_ARG;
+    const uint32_t nb = dim >> 5;
+    const uint64_t blocks = ((uint64_t)n_rows * nb * 8 + 255) / 256;
+    if (blocks > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_get_rows<Q4>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, n_rows, nb,
+                       static_cast<const uint8_t*>(table), table_rows, indices, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+}  // namespace
+}  // namespace ane
+
+using namespace ane;
+
+extern "C" int ane_hip_q4_0_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q40>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_q4_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q4K>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_q2_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q2K>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_q3_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q3K>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_q5_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q5K>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_q6_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    return qgemv_launch<Q6K>(M, K, x, W, y, stream);
+}
+extern "C" int ane_hip_get_rows_q8_0(uint32_t n_rows, uint32_t dim, const void* table, uint64_t table_rows,
+                                     const uint32_t* indices, float* out, void* stream) {
+    return get_rows_launch<false>(n_rows, dim, table, table_rows, indices, out, stream);
+}
+extern "C" int ane_hip_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const void* table, uint64_t table_rows,
+                                     const uint32_t* indices, float* out, void* stream) {
+    return get_rows_launch<true>(n_rows, dim, table, table_rows, indices, out, stream);
+}

@@ -21,6 +21,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 #include <map>
 #include <mutex>
 #include <string>
@@ -312,6 +313,72 @@ int op_dense_fused(Reader& r, hipStream_t s) {
                       "dense_fused_i8");
 }
 
+// 0x58, 0x75-0x79 [M:u32][K:u32][x][W][y]: the other weight formats' GEMVs
+// (bytecode_interpreter.s:7071-7079, 11024-11032 and the same prologue in
+// each K-quant handler).
+struct QGemv {
+    uint8_t op;
+    const char* name;
+    uint32_t bytes, values;
+    int (*fn)(uint32_t, uint32_t, const float*, const void*, float*, void*);
+};
+const QGemv kQGemv[] = {
+    {ANE_OP_Q4_0_GEMV, "q4_0_gemv", 18, 32, ane_hip_q4_0_gemv},
+    {ANE_OP_Q4_K_GEMV, "q4_k_gemv", 144, 256, ane_hip_q4_k_gemv},
+    {ANE_OP_Q2_K_GEMV, "q2_k_gemv", 84, 256, ane_hip_q2_k_gemv},
+    {ANE_OP_Q3_K_GEMV, "q3_k_gemv", 110, 256, ane_hip_q3_k_gemv},
+    {ANE_OP_Q5_K_GEMV, "q5_k_gemv", 176, 256, ane_hip_q5_k_gemv},
+    {ANE_OP_Q6_K_GEMV, "q6_k_gemv", 210, 256, ane_hip_q6_k_gemv},
+};
+
+int op_q_gemv(Reader& r, hipStream_t s, const QGemv& f) {
+    const uint32_t M = r.get<uint32_t>();
+    const uint32_t K = r.get<uint32_t>();
+    const float* x = r.ptr<const float>();
+    const void* W = r.ptr<const void>();
+    float* y = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "%s record truncated", f.name);
+    if (M == 0) return ANE_OK;
+    const uint64_t nsb = K / f.values;
+    CHECK(check_range(x, nsb * f.values * 4, f.name, false, nullptr));
+    CHECK(check_range(W, (uint64_t)M * nsb * f.bytes, f.name, false, nullptr));
+    CHECK(check_range(y, (uint64_t)M * 4, f.name, false, nullptr));
+    return hip_status(f.fn(M, K, x, W, y, s), f.name);
+}
+
+// 0x7C / 0x7D [n_rows:u32][dim:u32][table][indices][out]
+// (bytecode_interpreter.s:12363-12370, 12419-12426).  The indices are read
+// back (after the stream's earlier work) to check every row against the
+// table's allocation, which the reference does not do.
+int op_get_rows(Reader& r, hipStream_t s, bool q4) {
+    const char* name = q4 ? "get_rows_q4_0" : "get_rows_q8_0";
+    const uint32_t n = r.get<uint32_t>();
+    const uint32_t dim = r.get<uint32_t>();
+    const void* table = r.ptr<const void>();
+    const uint32_t* idx = r.ptr<const uint32_t>();
+    float* out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "%s record truncated", name);
+    const uint64_t nb = dim >> 5;
+    if (n == 0 || nb == 0) return ANE_OK;
+    if (dim & 31) return fail(ANE_ERR_INVALID_ARG, "%s: dim %u is not a multiple of 32", name, dim);
+    CHECK(check_range(idx, (uint64_t)n * 4, name, false, nullptr));
+    CHECK(check_range(out, (uint64_t)n * nb * 32 * 4, name, false, nullptr));
+    CHECK(check_range(table, 1, name, false, nullptr));
+    std::vector<uint32_t> h(n);
+    if (hipStreamSynchronize(s) != hipSuccess || hipMemcpy(h.data(), idx, (size_t)n * 4, hipMemcpyDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ANE_ERR_HIP, "%s: reading the indices failed", name);
+    }
+    uint32_t mx = 0;
+    for (uint32_t v : h) mx = v > mx ? v : mx;
+    const uint64_t rb = nb * (q4 ? 18 : 34);
+    CHECK(check_range(table, ((uint64_t)mx + 1) * rb, name, false, nullptr));
+    const uint64_t rows = (uint64_t)mx + 1;
+    return hip_status(q4 ? ane_hip_get_rows_q4_0(n, dim, table, rows, idx, out, s)
+                         : ane_hip_get_rows_q8_0(n, dim, table, rows, idx, out, s),
+                      name);
+}
+
 int run(const uint8_t* data, size_t size, hipStream_t s) {
     t_message.clear();
     if (size && !data) return fail(ANE_ERR_BAD_POINTER, "stream is null");
@@ -331,11 +398,21 @@ int run(const uint8_t* data, size_t size, hipStream_t s) {
             case ANE_OP_DENSE_U8S8: st = op_dense(r, s, true); break;
             case ANE_OP_Q8_0_GEMV: st = op_q8_0_gemv(r, s); break;
             case ANE_OP_DENSE_FUSED_I8: st = op_dense_fused(r, s); break;
-            default:
+            case ANE_OP_GET_ROWS_Q8_0: st = op_get_rows(r, s, false); break;
+            case ANE_OP_GET_ROWS_Q4_0: st = op_get_rows(r, s, true); break;
+            default: {
+                const QGemv* f = nullptr;
+                for (const QGemv& q : kQGemv)
+                    if (q.op == op) f = &q;
+                if (f) {
+                    st = op_q_gemv(r, s, *f);
+                    break;
+                }
                 return fail(ANE_ERR_UNKNOWN_OPCODE,
                             "opcode 0x%02x at byte %zu is not part of the quantized path served by "
                             "this build",
                             op, at);
+            }
         }
         if (st != ANE_OK) {
             if (t_message.empty()) fail(st, "record at byte %zu failed", at);

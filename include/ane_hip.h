@@ -54,6 +54,14 @@ enum ane_status {
 #define ANE_OP_QUANTIZE_FP32_I8_CHANNELWISE 0x1C
 #define ANE_OP_DENSE_U8S8 0x1E
 #define ANE_OP_Q8_0_GEMV 0x57
+#define ANE_OP_Q4_0_GEMV 0x58
+#define ANE_OP_Q4_K_GEMV 0x75
+#define ANE_OP_Q2_K_GEMV 0x76
+#define ANE_OP_Q3_K_GEMV 0x77
+#define ANE_OP_Q5_K_GEMV 0x78
+#define ANE_OP_Q6_K_GEMV 0x79
+#define ANE_OP_GET_ROWS_Q8_0 0x7C
+#define ANE_OP_GET_ROWS_Q4_0 0x7D
 #define ANE_OP_DENSE_FUSED_I8 0x80 /* README.md:84-97; absent from the reference enum */
 
 /* ------------------------------------------------- reference boundary */
@@ -159,6 +167,36 @@ size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T);
 int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,
                          const void* W, float* y, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* The other weight formats, "R mode" like 0x57: fp32 x, y[m] = FADDV16 of
+ * the handler's 16 fma lanes, bit-identical to the reference's arithmetic.
+ * W: M rows of K/values blocks, any alignment; a remainder of K is ignored
+ * as the handlers ignore it.
+ *   0x58 q4_0_gemv  bytecode_interpreter.s:7071-7126  18-byte blocks of 32
+ *   0x75 q4_k_gemv  :11024-11131  144-byte super-blocks of 256
+ *   0x76 q2_k_gemv  :11146-11222  84
+ *   0x77 q3_k_gemv  :11236-11358  110 (the second half of each sub-block
+ *        decodes its 2-bit fields from the qs word shifted right by the bit
+ *        pattern of the matching first-half input, as the handler does,
+ *        :11323-11329: no shift for +0.0, zero fields for normal inputs)
+ *   0x78 q5_k_gemv  :11372-11483  176
+ *   0x79 q6_k_gemv  :11498-11626  210 */
+int ane_hip_q4_0_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+int ane_hip_q4_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+int ane_hip_q2_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+int ane_hip_q3_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+int ane_hip_q5_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+int ane_hip_q6_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream);
+
+/* 0x7C get_rows_q8_0 / 0x7D get_rows_q4_0 (bytecode_interpreter.s:12363-12408,
+ * 12419-12469): out row r (dim fp32, rows contiguous) = table row indices[r]
+ * dequantized.  dim % 32 == 0.  table_rows bounds the indices (the reference
+ * reads past its table instead): a row whose index is >= table_rows is
+ * written as zeros. */
+int ane_hip_get_rows_q8_0(uint32_t n_rows, uint32_t dim, const void* table, uint64_t table_rows,
+                          const uint32_t* indices, float* out, void* stream);
+int ane_hip_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const void* table, uint64_t table_rows,
+                          const uint32_t* indices, float* out, void* stream);
 
 /* Library/device information: returns ANE_OK if a gfx950 device is usable. */
 int ane_hip_device_check(void);

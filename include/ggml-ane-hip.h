@@ -2,8 +2,8 @@
  * ggml-ane-hip.h -- the ggml backend side of ane's quantized path on MI355X.
  *
  * The reference ships a ggml backend (src/ggml-backend/ggml-ane.h:20,
- * ggml-ane.cpp) whose GGML_OP_MUL_MAT hook sends Q8_0 weights to q8_0_gemv
- * (ggml-ane.cpp:119-154).  ggml itself is not vendored there and no version
+ * ggml-ane.cpp) whose GGML_OP_MUL_MAT hook sends Q8_0 and Q4_0 weights to
+ * q8_0_gemv / q4_0_gemv (ggml-ane.cpp:119-154).  ggml itself is not vendored there and no version
  * is pinned, so this header declares the minimal ggml subset the hook reads.
  * Field names and meanings follow ggml's ggml_tensor: ne[] element counts
  * and nb[] byte strides, innermost first; src[0] = weights, src[1] =
@@ -76,10 +76,12 @@ void ane_ggml_backend_free(ane_ggml_backend_t backend);
 void ane_ggml_backend_set_q8_mode(ane_ggml_backend_t backend, int mode);
 
 /* Replaces ane_dev_supports_op (ggml-ane.cpp:363-368): 1 if this backend
- * computes the node.  MUL_MAT: src0 Q8_0, src1 and dst F32, ne00 == ne10,
+ * computes the node.  MUL_MAT: src0 Q8_0 or Q4_0 (the reference's routing,
+ * ggml-ane.cpp:135-146; Q4_0 in its q4_0_gemv arithmetic for every token),
+ * src1 and dst F32, ne00 == ne10,
  * ne0 == ne01, ne1 == ne11, src1/dst batches broadcastable over src0's
  * (ne12 % ne02 == 0, ne13 % ne03 == 0), innermost strides equal to the
- * element size, Q8_0 rows contiguous. */
+ * element size, weight rows contiguous. */
 int ane_ggml_supports_op(const struct ane_ggml_tensor* node);
 
 /* Replaces ane_compute_forward for one node (ggml-ane.cpp:109-154).

@@ -337,3 +337,276 @@ void oracle_q8_0_mul_mat_g(uint32_t N, uint32_t K, uint32_t T, const float* x,
     free(qx);
     free(dx);
 }
+
+/* ------------------------------------------------------------ other Q formats
+ * The reference's per-format GEMVs share the 0x57 skeleton: 16 fp32 lanes per
+ * row, lane l accumulating with fmla in the order the handler visits the
+ * elements, then the FADDV tree.  Only the unpacking differs. */
+
+static inline float h2f(const uint8_t* p) { return oracle_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+static inline uint32_t ld16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+static inline uint32_t ld32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+/* SVE LSR (vectors): shift amounts >= the element size give 0. */
+static inline uint32_t lsr_sve(uint32_t v, uint32_t sh) { return sh >= 32 ? 0u : v >> sh; }
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* 0x58  bytecode_interpreter.s:7071-7126. */
+void oracle_q4_0_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nb = K >> 5; /* :7081 lsr #5 */
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nb * 18;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t* blk = row + b * 18;
+            float d = h2f(blk); /* :7094-7095 */
+            for (int l = 0; l < 16; l++) { /* low nibbles, :7101-7108 */
+                float w = (float)((int)(blk[2 + l] & 15) - 8) * d;
+                acc[l] = fmaf(w, x[32 * b + l], acc[l]);
+            }
+            for (int l = 0; l < 16; l++) { /* high nibbles, :7110-7117 */
+                float w = (float)((int)(blk[2 + l] >> 4) - 8) * d;
+                acc[l] = fmaf(w, x[32 * b + 16 + l], acc[l]);
+            }
+        }
+        y[mm] = faddv16(acc); /* :7123 */
+    }
+}
+
+/* The 6-bit (scale, min) pair of sub-block j from the 12-byte array of Q4_K
+ * and Q5_K (bytecode_interpreter.s:11064-11089, 11406-11427). */
+static void kq_scale_min(const uint8_t* s, int j, uint32_t* sc, uint32_t* m) {
+    if (j < 4) {
+        *sc = s[j] & 63u;
+        *m = s[j + 4] & 63u;
+    } else {
+        *sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+        *m = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+}
+
+/* 0x75  bytecode_interpreter.s:11024-11131: 144-byte super-blocks
+ * [d][dmin][scales 12][qs 128]; sub-block j (32 values) takes qs[16j+l]:
+ * low nibble -> element 32j+l, high nibble -> 32j+16+l;
+ * w = fl(fl(q * fl(d*sc)) + fl(-dmin*m)). */
+void oracle_q4_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nsb = K >> 8; /* :11035 lsr #8 */
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nsb * 144;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = row + sb * 144;
+            const float* xs = x + 256 * sb;
+            float d = h2f(blk), nmin = -h2f(blk + 2); /* :11045-11049 fneg */
+            for (int j = 0; j < 8; j++) {
+                uint32_t sc, m;
+                kq_scale_min(blk + 4, j, &sc, &m);
+                float ds = d * (float)sc, dm = nmin * (float)m; /* :11092-11097 */
+                const uint8_t* q = blk + 16 + 16 * j;
+                for (int l = 0; l < 16; l++) { /* :11104-11112 */
+                    float t = (float)(q[l] & 15) * ds;
+                    float w = t + dm;
+                    acc[l] = fmaf(w, xs[32 * j + l], acc[l]);
+                }
+                for (int l = 0; l < 16; l++) { /* :11114-11121 */
+                    float t = (float)(q[l] >> 4) * ds;
+                    float w = t + dm;
+                    acc[l] = fmaf(w, xs[32 * j + 16 + l], acc[l]);
+                }
+            }
+        }
+        y[mm] = faddv16(acc); /* :11129 */
+    }
+}
+
+/* 0x76  bytecode_interpreter.s:11146-11222: 84-byte super-blocks
+ * [scales 16][qs 64][d][dmin]; 16 sub-blocks of 16 values; element 16j+l
+ * = bits 2l..2l+1 of the little-endian word qs[4j..4j+3];
+ * w = fl(fl(q * fl(d*(sc&15))) + fl(-dmin*(sc>>4))). */
+void oracle_q2_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nsb = K >> 8;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nsb * 84;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = row + sb * 84;
+            const float* xs = x + 256 * sb;
+            float d = h2f(blk + 80), nmin = -h2f(blk + 82); /* :11169-11174 */
+            for (int j = 0; j < 16; j++) {
+                uint32_t sc = blk[j] & 15u, m = (uint32_t)(blk[j] >> 4); /* :11180-11182 */
+                float ds = d * (float)sc, dm = nmin * (float)m;
+                uint32_t q32 = ld32(blk + 16 + 4 * j); /* :11193 */
+                for (int l = 0; l < 16; l++) { /* :11203-11212 */
+                    float t = (float)((q32 >> (2 * l)) & 3u) * ds;
+                    float w = t + dm;
+                    acc[l] = fmaf(w, xs[16 * j + l], acc[l]);
+                }
+            }
+        }
+        y[mm] = faddv16(acc); /* :11220 */
+    }
+}
+
+/* 0x77  bytecode_interpreter.s:11236-11358: 110-byte super-blocks
+ * [hmask 32][qs 64][scales 12][d]; sub-block j (32 values): signed scale
+ * sc-32 (sc 6 bits, low four sub-blocks scales[j]&63, high four rebuilt as
+ * for Q4_K); element 32j+l: 2 bits from the word qs[8j..], high bit l of the
+ * halfword hmask[4j..]; element 32j+16+l: the word qs[8j+4..] and halfword
+ * hmask[4j+2..], w = fl((q - 4) * fl(d*(sc-32))).
+ * The second half reproduces the handler as it runs: its first shift
+ * (:11329, lsr z0, z0, z1) uses z1 after :11323 reloaded it with the first
+ * half's inputs, so the word is first shifted right by the bit pattern of
+ * x[32j+l] (0 for +0.0, small for tiny denormals, everything else >= 32 and
+ * so a zero field) before the 2l shift. */
+void oracle_q3_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nsb = K >> 8;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nsb * 110;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = row + sb * 110;
+            const uint8_t *hm = blk, *qs = blk + 32, *s = blk + 96;
+            const float* xs = x + 256 * sb;
+            float d = h2f(blk + 108); /* :11260-11261 */
+            for (int j = 0; j < 8; j++) {
+                uint32_t sc = j < 4 ? (s[j] & 63u) : ((s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4));
+                float ds = d * (float)((int)sc - 32); /* :11288-11290 */
+                uint32_t qa = ld32(qs + 8 * j), ha = ld16(hm + 4 * j);
+                for (int l = 0; l < 16; l++) { /* :11297-11325 */
+                    int q = (int)(((qa >> (2 * l)) & 3u) | (((ha >> l) & 1u) << 2));
+                    float w = (float)(q - 4) * ds;
+                    acc[l] = fmaf(w, xs[32 * j + l], acc[l]);
+                }
+                uint32_t qb = ld32(qs + 8 * j + 4), hb = ld16(hm + 4 * j + 2);
+                for (int l = 0; l < 16; l++) { /* :11327-11348 */
+                    uint32_t v = lsr_sve(qb, fbits(xs[32 * j + l]));
+                    int q = (int)(((v >> (2 * l)) & 3u) | (((hb >> l) & 1u) << 2));
+                    float w = (float)(q - 4) * ds;
+                    acc[l] = fmaf(w, xs[32 * j + 16 + l], acc[l]);
+                }
+            }
+        }
+        y[mm] = faddv16(acc); /* :11356 */
+    }
+}
+
+/* 0x78  bytecode_interpreter.s:11372-11483: 176-byte super-blocks
+ * [d][dmin][scales 12][qh 32][qs 128]; sub-block j: qs[16j+l] low nibble |
+ * bit l of qh word j << 4 -> element 32j+l, high nibble | bit 16+l << 4 ->
+ * element 32j+16+l; w = fl(fl(q * fl(d*sc)) + fl(-dmin*m)). */
+void oracle_q5_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nsb = K >> 8;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nsb * 176;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = row + sb * 176;
+            const float* xs = x + 256 * sb;
+            float d = h2f(blk), nmin = -h2f(blk + 2); /* :11393-11398 */
+            for (int j = 0; j < 8; j++) {
+                uint32_t sc, m;
+                kq_scale_min(blk + 4, j, &sc, &m);
+                float ds = d * (float)sc, dm = nmin * (float)m; /* :11428-11433 */
+                const uint8_t* q = blk + 48 + 16 * j;
+                uint32_t h = ld32(blk + 16 + 4 * j); /* :11444 */
+                for (int l = 0; l < 16; l++) { /* :11436-11458 */
+                    uint32_t qv = (q[l] & 15u) | ((((h & 0xffffu) >> l) & 1u) << 4);
+                    float t = (float)qv * ds;
+                    float w = t + dm;
+                    acc[l] = fmaf(w, xs[32 * j + l], acc[l]);
+                }
+                for (int l = 0; l < 16; l++) { /* :11460-11476 */
+                    uint32_t qv = (uint32_t)(q[l] >> 4) | ((((h >> 16) >> l) & 1u) << 4);
+                    float t = (float)qv * ds;
+                    float w = t + dm;
+                    acc[l] = fmaf(w, xs[32 * j + 16 + l], acc[l]);
+                }
+            }
+        }
+        y[mm] = faddv16(acc); /* :11481 */
+    }
+}
+
+/* 0x79  bytecode_interpreter.s:11498-11626: 210-byte super-blocks
+ * [ql 128][qh 64][scales 16 int8][d]; 16 sub-blocks of 16 values; element
+ * 16j+n = nibble n of ql[8j..8j+7] (low nibble of byte n/2 for even n, high
+ * for odd) | bits 2n..2n+1 of the word qh[4j..] << 4, centred by 32;
+ * w = fl((q - 32) * fl(d*sc)); the even and odd lanes are zipped back into
+ * element order before the fmla (:11609-11613). */
+void oracle_q6_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y) {
+    size_t nsb = K >> 8;
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long mm = 0; mm < (long)M; mm++) {
+        const uint8_t* row = W + (size_t)mm * nsb * 210;
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = row + sb * 210;
+            const float* xs = x + 256 * sb;
+            float d = h2f(blk + 208); /* :11522-11523 */
+            for (int j = 0; j < 16; j++) {
+                float ds = d * (float)(int8_t)blk[192 + j]; /* :11530-11532 */
+                uint32_t h = ld32(blk + 128 + 4 * j); /* :11560 */
+                for (int n = 0; n < 16; n++) {
+                    uint8_t byte = blk[8 * j + (n >> 1)];
+                    uint32_t nib = (n & 1) ? (uint32_t)(byte >> 4) : (uint32_t)(byte & 15);
+                    int q = (int)(nib | (((h >> (2 * n)) & 3u) << 4));
+                    float w = (float)(q - 32) * ds;
+                    acc[n] = fmaf(w, xs[16 * j + n], acc[n]);
+                }
+            }
+        }
+        y[mm] = faddv16(acc); /* :11622 */
+    }
+}
+
+/* 0x7C  bytecode_interpreter.s:12363-12408: out row r = dequantized Q8_0 row
+ * indices[r] (u32), dim/32 blocks of 34 bytes: out = fl((float)q * d). */
+void oracle_get_rows_q8_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, const uint32_t* indices,
+                          float* out) {
+    size_t nb = dim >> 5, rb = nb * 34;
+    for (size_t r = 0; r < n_rows; r++) {
+        const uint8_t* row = table + (size_t)indices[r] * rb;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t* blk = row + b * 34;
+            float d = h2f(blk);
+            for (int q = 0; q < 32; q++) out[r * nb * 32 + b * 32 + q] = (float)(int8_t)blk[2 + q] * d;
+        }
+    }
+}
+
+/* 0x7D  bytecode_interpreter.s:12419-12469: Q4_0 rows of 18-byte blocks;
+ * element i = (qs[i] & 15) - 8, element 16+i = (qs[i] >> 4) - 8, times d. */
+void oracle_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, const uint32_t* indices,
+                          float* out) {
+    size_t nb = dim >> 5, rb = nb * 18;
+    for (size_t r = 0; r < n_rows; r++) {
+        const uint8_t* row = table + (size_t)indices[r] * rb;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t* blk = row + b * 18;
+            float d = h2f(blk);
+            float* o = out + r * nb * 32 + b * 32;
+            for (int i = 0; i < 16; i++) {
+                o[i] = (float)((int)(blk[2 + i] & 15) - 8) * d;
+                o[16 + i] = (float)((int)(blk[2 + i] >> 4) - 8) * d;
+            }
+        }
+    }
+}

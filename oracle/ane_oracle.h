@@ -116,6 +116,30 @@ void oracle_q8_0_quantize_x(uint32_t K, const float* x, int8_t* qx, float* dx);
 void oracle_q8_0_mul_mat_g(uint32_t N, uint32_t K, uint32_t T, const float* x,
                            const uint8_t* W, float* y);
 
+/* The other weight formats of the reference, all "R mode" (fp32 x, 16 fma
+ * lanes per row in the handler's element order, FADDV tree), y[0..M):
+ *   0x58 q4_0_gemv  bytecode_interpreter.s:7071-7126   18 B / 32 values
+ *   0x75 q4_k_gemv  :11024-11131                        144 B / 256
+ *   0x76 q2_k_gemv  :11146-11222                        84 B / 256
+ *   0x77 q3_k_gemv  :11236-11358 (with the handler's second-half shift by
+ *                   the first half's input bits, :11323-11329)   110 B / 256
+ *   0x78 q5_k_gemv  :11372-11483                        176 B / 256
+ *   0x79 q6_k_gemv  :11498-11626                        210 B / 256 */
+void oracle_q4_0_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+void oracle_q4_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+void oracle_q2_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+void oracle_q3_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+void oracle_q5_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+void oracle_q6_k_gemv(uint32_t M, uint32_t K, const float* x, const uint8_t* W, float* y);
+
+/* 0x7C / 0x7D  bytecode_interpreter.s:12363-12408, 12419-12469: gather
+ * n_rows rows (u32 indices) of a Q8_0 / Q4_0 table of dim-wide rows and
+ * dequantize them to fp32, out rows contiguous. */
+void oracle_get_rows_q8_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, const uint32_t* indices,
+                          float* out);
+void oracle_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, const uint32_t* indices,
+                          float* out);
+
 /* IEEE half -> float (exact), as fcvt s, h. */
 float oracle_f16_to_f32(uint16_t h);
 

@@ -15,6 +15,10 @@ ORACLE_SO = ROOT / "oracle" / "libane_oracle.so"
 
 _lib = None
 
+# weight formats with an R-mode GEMV besides Q8_0: name -> (bytes, values) per block
+QFORMATS = {"q4_0": (18, 32), "q4_k": (144, 256), "q2_k": (84, 256), "q3_k": (110, 256),
+            "q5_k": (176, 256), "q6_k": (210, 256)}
+
 
 def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
@@ -45,7 +49,11 @@ class Oracle:
             "oracle_q8_0_quantize_x": (None, [c.c_uint32, P, P, P]),
             "oracle_q8_0_mul_mat_g": (None, [c.c_uint32, c.c_uint32, c.c_uint32, P, P, P]),
             "oracle_f16_to_f32": (c.c_float, [c.c_uint16]),
+            "oracle_get_rows_q8_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_get_rows_q4_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
         }
+        for fmt in QFORMATS:
+            sig[f"oracle_{fmt}_gemv"] = (None, [c.c_uint32, c.c_uint32, P, P, P])
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
             fn.restype = res
@@ -151,6 +159,21 @@ class Oracle:
         y = np.zeros((max(T, 1), max(N, 1)), np.float32)
         self.lib.oracle_q8_0_mul_mat_g(N, K, T, _p(x), _p(W), _p(y))
         return y[:T, :N]
+
+    def q_gemv(self, fmt, M, K, x, W):
+        """R-mode GEMV of one of QFORMATS (q4_0, q4_k, q2_k, q3_k, q5_k, q6_k)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        y = np.zeros(max(M, 1), np.float32)
+        getattr(self.lib, f"oracle_{fmt}_gemv")(M, K, _p(x), _p(W), _p(y))
+        return y[:M]
+
+    def get_rows(self, fmt, n_rows, dim, table, indices):
+        table = np.ascontiguousarray(table, dtype=np.uint8)
+        idx = np.ascontiguousarray(indices, dtype=np.uint32)
+        out = np.zeros((max(n_rows, 1), max(dim // 32 * 32, 1)), np.float32)
+        getattr(self.lib, f"oracle_get_rows_{fmt}")(n_rows, dim, _p(table), _p(idx), _p(out))
+        return out[:n_rows, : dim // 32 * 32]
 
     def f16_to_f32(self, h: int) -> float:
         return self.lib.oracle_f16_to_f32(h)

@@ -44,5 +44,24 @@ def q8_0_weights(N: int, K: int, seed: int = 3) -> np.ndarray:
     return W.reshape(N, nb * 34)
 
 
+# byte offsets of the fp16 fields of one block of each R-mode format (the
+# layouts of bytecode_interpreter.s:7071-7126 and 11024-11626)
+Q_BLOCK = {"q4_0": (18, 32, (0,)), "q4_k": (144, 256, (0, 2)), "q2_k": (84, 256, (80, 82)),
+           "q3_k": (110, 256, (108,)), "q5_k": (176, 256, (0, 2)), "q6_k": (210, 256, (208,))}
+
+
+def q_weights(fmt: str, N: int, K: int, seed: int = 5) -> np.ndarray:
+    """N rows of K/values blocks of format fmt: random quant and scale bytes,
+    the fp16 super-scales (d, dmin) = fp16(|N(0, 0.01)|).  Shape (N, row bytes)."""
+    g = rng(seed)
+    nbytes, nvals, fp16_at = Q_BLOCK[fmt]
+    nb = K // nvals
+    W = g.integers(0, 256, size=(N, nb, nbytes), dtype=np.uint8)
+    for off in fp16_at:
+        d = np.abs(g.standard_normal((N, nb)) * 0.01).astype(np.float16)
+        W[:, :, off:off + 2] = d.view(np.uint8).reshape(N, nb, 2)
+    return W.reshape(N, nb * nbytes)
+
+
 def activations(T: int, K: int, seed: int = 4) -> np.ndarray:
     return rng(seed).standard_normal((T, K), dtype=np.float32)

@@ -22,9 +22,9 @@ ROOT = Path(__file__).resolve().parents[1]
 F32 = np.float32
 
 
-def mul_mat_node(N, K, T, B2=1, B3=1, A2=1, A3=1, nb1=None, nb_dst1=None):
+def mul_mat_node(N, K, T, B2=1, B3=1, A2=1, A3=1, nb1=None, nb_dst1=None, q4=False):
     """A MUL_MAT node with null data pointers (layout only)."""
-    a = ggml_tensor(GgmlType.Q8_0, [K, N, A2, A3])
+    a = ggml_tensor(GgmlType.Q4_0 if q4 else GgmlType.Q8_0, [K, N, A2, A3])
     xs = nb1 or 4 * K
     b = ggml_tensor(GgmlType.F32, [K, T, B2, B3], nb=[4, xs, xs * T, xs * T * B2])
     ys = nb_dst1 or 4 * N
@@ -82,6 +82,11 @@ def test_supports_op_decisions():
     _, _, d = mul_mat_node(300, 512, 1)
     d.op = GgmlOp.OTHER
     assert sup(d) == 0
+    a, b, d = mul_mat_node(300, 512, 3, q4=True)
+    assert sup(d) == 1                       # Q4_0 weights (18-byte blocks)
+    a.nb[0] = 34
+    d.src[0] = ctypes.pointer(a)
+    assert sup(d) == 0                       # Q4_0 with Q8_0 strides
 
 
 def test_unsupported_node_is_rejected_without_gpu():
@@ -199,3 +204,31 @@ def test_ggml_graph_two_nodes(ane, oracle):
     y_ref = oracle.q8_0_mul_mat_g(N, H, T, h_ref, W2)
     assert host(h).tobytes() == h_ref.tobytes()
     assert host(y).tobytes() == y_ref.tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B2,A2", [(1, 1), (4, 2)])
+def test_ggml_mul_mat_q4_0_all_tokens(ane, oracle, B2, A2):
+    """Q4_0 weights: every token, in the reference's q4_0_gemv arithmetic."""
+    import torch
+
+    N, K, T = 260, 1024, 5
+    W = np.stack([data.q_weights("q4_0", N, K, seed=60 + i) for i in range(A2)])
+    X = data.activations(B2 * T, K, seed=61).reshape(B2, T, K)
+    Y = torch.zeros((B2, T, N), dtype=torch.float32, device="cuda")
+    Wd, Xd = dev(W), dev(X)  # the nodes hold raw pointers: keep the tensors alive
+    a = ggml_tensor(GgmlType.Q4_0, [K, N, A2], data=Wd)
+    b = ggml_tensor(GgmlType.F32, [K, T, B2], data=Xd)
+    d = ggml_tensor(GgmlType.F32, [N, T, B2], data=Y, op=GgmlOp.MUL_MAT, src=(a, b))
+    assert a.nb[0] == 18 and a.nb[1] == K // 32 * 18
+    be = ane_amd.GgmlBackend()
+    try:
+        assert be.supports(d)
+        be.graph_compute([d])
+    finally:
+        be.close()
+    got = host(Y)
+    for i2 in range(B2):
+        for t in range(T):
+            ref = oracle.q_gemv("q4_0", N, K, X[i2, t], W[i2 // (B2 // A2)])
+            assert got[i2, t].tobytes() == ref.tobytes(), (i2, t)
