@@ -56,7 +56,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
-    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode"], default=None,
+    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats"], default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
 
@@ -120,7 +120,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build targets one GPU: the dense_fused_i8 and Q8_0 "
-                                   "kernels shard by rows with no reduction (see DESIGN.md); "
+                                   "kernels shard by rows with no reduction; "
                                    "run with --gpus 1"}), flush=True)
         return 2
 
@@ -167,6 +167,9 @@ def main() -> int:
         return 0
     if args.only in ("q8g", "q8r"):
         return profile_q8(args, stream)
+    if args.only == "qformats":
+        bench_qformats(args)
+        return 0
     if args.only == "decode":
         bench_decode(args)
         return 0
@@ -221,6 +224,7 @@ def main() -> int:
     if not args.no_q8:
         q8 = bench_q8(args, stream)
         mul_mat = bench_mul_mat(args)
+    qformats = bench_qformats(args) if not args.no_q8 else None
     m_sweep = bench_m_sweep(args, N, K) if not args.no_sweep else None
     decode = bench_decode(args) if not args.no_decode else None
 
@@ -248,6 +252,7 @@ def main() -> int:
         "phases_us": {"quantize": round(quant_ms * 1e3, 2), "contraction": round(gemm_ms * 1e3, 2)},
         "q8_0_matvec": q8,
         "q8_0_mul_mat_config4": mul_mat,
+        "other_formats_gemv": qformats,
         "dense_fused_m_sweep": m_sweep,
         "decode_config5": decode,
         "cpu_baseline": cpu,
@@ -446,13 +451,20 @@ def bench_decode(args) -> dict:
 
     resid = torch.randn(H, generator=gen, device="cuda")
 
+    # pre-quantized activations for the o and down products (their inputs
+    # arrive in the Q8 activation form in the token)
+    xq_o = torch.zeros(ane_amd.q8_act_bytes(NH * HD), dtype=torch.uint8, device="cuda")
+    xq_d = torch.zeros(ane_amd.q8_act_bytes(F), dtype=torch.uint8, device="cuda")
+    ane_amd.silu_mul_quant(NH * HD, torch.randn(2 * NH * HD, generator=gen, device="cuda"), xq_o)
+    ane_amd.silu_mul_quant(F, torch.randn(2 * F, generator=gen, device="cuda"), xq_d)
+
     def matmuls_only(st):  # the token's four products with the same fusions
         for t in keep:
             ane_amd.q8_0_matvec_fused(nqkv, H, xin, t["w_qkv"], scratch, norm_w=t["attn_norm"], eps=1e-5, stream=st)
-            ane_amd.q8_0_matvec_fused(H, NH * HD, xin, t["w_o"], resid, residual=resid, stream=st)
+            ane_amd.q8_0_matvec_q8(H, NH * HD, xq_o, t["w_o"], resid, residual=resid, stream=st)
             ane_amd.q8_0_matvec_fused(2 * F, H, xin, t["w_gate_up"], scratch, norm_w=t["ffn_norm"], eps=1e-5,
                                       stream=st)
-            ane_amd.q8_0_matvec_fused(H, F, xin, t["w_down"], resid, residual=resid, stream=st)
+            ane_amd.q8_0_matvec_q8(H, F, xq_d, t["w_down"], resid, residual=resid, stream=st)
 
     tok_ms = graph_time(token, 3)
     mm_ms = graph_time(matmuls_only, 3)
@@ -469,6 +481,43 @@ def bench_decode(args) -> dict:
     del keep
     torch.cuda.empty_cache()
     return res
+
+
+def bench_qformats(args) -> dict:
+    """The other weight formats' R-mode GEMVs (q4_0, q4_k, q2_k, q3_k, q5_k,
+    q6_k) at 14336x4096, rotating weight copies past the Infinity Cache.
+    GB/s counts the weight bytes once plus x and y."""
+    import numpy as np
+    import torch
+
+    import ane_amd
+    from tests import data
+
+    Nr, Kc = 14336, 4096
+    x = torch.from_numpy(data.activations(1, Kc, seed=4)[0]).cuda()
+    y = torch.empty(Nr, device="cuda", dtype=torch.float32)
+    res = {}
+    for fmt, (bb, nv) in ane_amd.QFORMATS.items():
+        W0 = torch.from_numpy(data.q_weights(fmt, Nr, Kc, seed=3)).cuda()
+        wbytes = W0.numel()
+        copies = max(2, int(np.ceil(300e6 / wbytes)))
+        Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+        it = [0]
+
+        def fn(st):
+            W = Ws[it[0] % copies]
+            it[0] += 1
+            ane_amd.q_gemv(fmt, Nr, Kc, x, W, y, stream=st)
+
+        ms = graph_time(fn, 2 * copies)
+        alg = wbytes + 4 * (Kc + Nr)
+        gbs = alg / ms / 1e6
+        res[fmt] = {"us": round(ms * 1e3, 2), "weights_bytes": wbytes, "GB_s": round(gbs, 1),
+                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"{fmt}_gemv {Nr}x{Kc}: {ms * 1e3:.2f} us = {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
+        del Ws, W0
+        torch.cuda.empty_cache()
+    return {"workload": f"R-mode GEMV {Nr}x{Kc} per weight format, fp32 x", "shapes": res}
 
 
 def bench_m_sweep(args, N, K) -> dict:
