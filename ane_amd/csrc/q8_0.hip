@@ -678,6 +678,172 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     return r;
 }
 
+// ====================================================== MFMA mul_mat (T > 4)
+// G mode for 5+ tokens.  One v_mfma_i32_16x16x32_i8 is exactly one Q8_0
+// block's isum for a tile of 16 weight rows x 16 tokens (K = 32 = one
+// block), so the matrix cores produce the integer dots and the fp32 part
+// stays the definition's: lane (g, t) holds the tile's rows 4g..4g+3 for
+// token t, folds each block b into p[b % 16][i] = fmaf((float)isum,
+// fl(d_w * d_x), p[b % 16][i]) in increasing b, and ends with the FADDV tree
+// over its 16 partials in registers.
+//
+// One wave per tile, no barriers: each wave streams its tile through a
+// private LDS ring of S stages, a stage being 16 blocks of the 16 weight
+// rows (34-byte blocks, rows 35 chunks apart), of the 16 tokens' quantized
+// activations (rows 34 chunks apart) and of their 16 x 16 fp32 scales, all
+// copied global -> LDS with buffer_load_dwordx4 ... lds.  The waves of a
+// workgroup take the token tiles of one row tile, so the weight rows come
+// from HBM once and from L2 for the others.
+constexpr uint32_t kMmaSb = 16;                        // blocks per stage
+constexpr uint32_t kMmaWRowChunks = kMmaSb * 17 / 8 + 1;  // 34 + 1 pad
+constexpr uint32_t kMmaXRowChunks = kMmaSb * 2 + 2;       // 32 + 2 pad
+constexpr uint32_t kMmaWChunks = 16 * kMmaWRowChunks;     // 560
+constexpr uint32_t kMmaXChunks = 16 * kMmaXRowChunks;     // 544
+constexpr uint32_t kMmaDChunks = 16 * kMmaSb * 4 / 16;    // 64: 16 tokens x 16 fp32
+constexpr uint32_t kMmaDmaW = (kMmaWChunks + 63) / 64;    // 9
+constexpr uint32_t kMmaDmaX = (kMmaXChunks + 63) / 64;    // 9
+constexpr uint32_t kMmaDma = kMmaDmaW + kMmaDmaX + 1;     // copy instructions per stage
+constexpr uint32_t kMmaStageBytes = (kMmaWChunks + kMmaXChunks + kMmaDChunks) * 16;
+
+template <int NW, int S>
+__global__ void __launch_bounds__(NW * 64)
+k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, const uint8_t* __restrict__ qws,
+           uint32_t dx_off, float* __restrict__ y) {
+    static_assert((S - 1) * kMmaDma < 64, "copies in flight exceed the vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    int8_t* ring = smem + wave * (S * kMmaStageBytes);
+
+    const uint32_t tt = (T + 15) / 16;
+    const uint32_t gw = blockIdx.x * NW + wave;
+    const uint32_t row0 = (gw / tt) * 16, t0 = (gw % tt) * 16;
+    const bool live = row0 < N;  // waves past the last tile copy nothing and store nothing
+    const uint32_t rb = nb * 34;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W, N * rb);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(qws, dx_off + T * nb * 4);
+    const uint32_t nst = nb / kMmaSb;
+
+    // per-lane source offsets of each copy at stage 0 (0x80000000: pad, dead
+    // row or token, which read as zero) and the stride they advance by
+    uint32_t ow[kMmaDmaW], ox[kMmaDmaX], od;
+#pragma unroll
+    for (uint32_t j = 0; j < kMmaDmaW; j++) {
+        const uint32_t c = 64 * j + lane, r = c / kMmaWRowChunks, sub = c - r * kMmaWRowChunks;
+        ow[j] = (live && r < 16 && sub < kMmaSb * 17 / 8 && row0 + r < N) ? (row0 + r) * rb + 16 * sub : 0x80000000u;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kMmaDmaX; j++) {
+        const uint32_t c = 64 * j + lane, t = c / kMmaXRowChunks, sub = c - t * kMmaXRowChunks;
+        ox[j] = (live && t < 16 && sub < 2 * kMmaSb && t0 + t < T) ? (t0 + t) * nb * 32 + 16 * sub : 0x80000000u;
+    }
+    {
+        const uint32_t t = lane >> 2, sub = lane & 3;  // 16 tokens x 4 chunks of 4 scales
+        od = (live && t0 + t < T) ? dx_off + (t0 + t) * nb * 4 + 16 * sub : 0x80000000u;
+    }
+    auto issue = [&](uint32_t s) {
+        int8_t* st = ring + (s % S) * kMmaStageBytes;
+        const bool on = s < nst;
+#pragma unroll
+        for (uint32_t j = 0; j < kMmaDmaW; j++)
+            if (kMmaWChunks % 64 == 0 || j + 1 < kMmaDmaW || lane < kMmaWChunks % 64)
+                copy16_to_lds(wr, st + 1024 * j, on && ow[j] != 0x80000000u ? ow[j] + s * (kMmaSb * 34) : 0x80000000u);
+#pragma unroll
+        for (uint32_t j = 0; j < kMmaDmaX; j++)
+            if (kMmaXChunks % 64 == 0 || j + 1 < kMmaDmaX || lane < kMmaXChunks % 64)
+                copy16_to_lds(xr, st + kMmaWChunks * 16 + 1024 * j,
+                              on && ox[j] != 0x80000000u ? ox[j] + s * (kMmaSb * 32) : 0x80000000u);
+        copy16_to_lds(xr, st + (kMmaWChunks + kMmaXChunks) * 16,
+                      on && od != 0x80000000u ? od + s * (kMmaSb * 4) : 0x80000000u);
+    };
+
+    float p[16][4];
+#pragma unroll
+    for (int b = 0; b < 16; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) p[b][i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++) issue(s);
+    for (uint32_t s = 0; s < nst; s++) {
+        wait_vmcnt<(S - 1) * kMmaDma>();  // stage s has landed
+        const int8_t* st = ring + (s % S) * kMmaStageBytes;
+        const int8_t* wa = st + c16 * (kMmaWRowChunks * 16);                      // A: weight row c16
+        const int8_t* xb = st + kMmaWChunks * 16 + c16 * (kMmaXRowChunks * 16);   // B: token c16
+        const float* dxs = reinterpret_cast<const float*>(st + (kMmaWChunks + kMmaXChunks) * 16) + c16 * kMmaSb;
+#pragma unroll
+        for (uint32_t bb = 0; bb < kMmaSb; bb++) {
+            // A operand: quants 8g..8g+7 of row c16's block bb (bytes 34bb + 2 + 8g ..)
+            const uint32_t o = 34 * bb + 2 + 8 * g;  // 4-byte aligned iff bb is odd
+            const uint32_t* a32 = reinterpret_cast<const uint32_t*>(wa + (o & ~3u));
+            uint32_t a0, a1;
+            if (bb & 1) {
+                a0 = a32[0];
+                a1 = a32[1];
+            } else {
+                const uint32_t d0 = a32[0], d1 = a32[1], d2 = a32[2];
+                a0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                a1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+            }
+            const uint64_t av = (uint64_t)a0 | ((uint64_t)a1 << 32);
+            const uint64_t bv = *reinterpret_cast<const uint64_t*>(xb + 32 * bb + 8 * g);
+            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)av, (long)bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const float dx = dxs[bb];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {  // output row 4g + i of the tile, token c16
+                const uint16_t dwb = *reinterpret_cast<const uint16_t*>(st + (4 * g + i) * (kMmaWRowChunks * 16) + 34 * bb);
+                const float dd = __fmul_rn(half_bits_to_float(dwb), dx);
+                p[bb][i] = __builtin_fmaf((float)acc[i], dd, p[bb][i]);
+            }
+        }
+        wait_lgkmcnt0();  // this stage's LDS reads are done before it is refilled
+        issue(s + S);
+    }
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float t8[8], t4[4];
+#pragma unroll
+        for (int l = 0; l < 8; l++) t8[l] = p[2 * l][i] + p[2 * l + 1][i];
+#pragma unroll
+        for (int l = 0; l < 4; l++) t4[l] = t8[2 * l] + t8[2 * l + 1];
+        const float v = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+        const uint32_t row = row0 + 4 * g + i, t = t0 + c16;
+        if (live && row < N && t < T) y[(uint64_t)t * N + row] = v;
+    }
+}
+
+constexpr int kMmaNW = 4, kMmaS = 2;
+
+// The MFMA path: rows 16-byte aligned (as the streaming kernels need) and
+// whole 16-block stages.  x is quantized into the workspace first.
+int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
+                void* workspace, hipStream_t s) {
+    int8_t* qx = (int8_t*)workspace;
+    const uint64_t dx_off = ceil_to((uint64_t)T * nb * 32, 256);
+    float* dx = (float*)((uint8_t*)workspace + dx_off);
+    if (dx_off + (uint64_t)T * nb * 4 >= 0x80000000ull) return -1;
+    const uint64_t nblocks = (uint64_t)T * nb;
+    hipLaunchKernelGGL(k_q8_0_quantize_x, dim3((uint32_t)((nblocks + 255) / 256)), dim3(256), 0, s, nblocks, nb, K,
+                       x, qx, dx);
+    auto fn = k_q8_0_mma<kMmaNW, kMmaS>;
+    const uint32_t lds = kMmaNW * kMmaS * kMmaStageBytes;
+    static uint32_t attr_set[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    if (!attr_set[dev]) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return ANE_ERR_HIP;
+        attr_set[dev] = 1;
+    }
+    const uint64_t waves = (uint64_t)((N + 15) / 16) * ((T + 15) / 16);
+    const uint64_t grid = (waves + kMmaNW - 1) / kMmaNW;
+    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(kMmaNW * 64), lds, s, N, nb, T, (const uint8_t*)W,
+                       (const uint8_t*)workspace, (uint32_t)dx_off, y);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
 }  // namespace
 }  // namespace ane
 
@@ -764,6 +930,10 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
     if (T <= kMaxStreamTokens && stream_eligible(N, nb, K, T, W)) {
         const int r = T == 1 ? stream_auto<kModeG, 1>(N, nb, K, T, x, W, y, s)
                              : stream_auto<kModeG, kMaxStreamTokens>(N, nb, K, T, x, W, y, s);
+        if (r >= 0) return r;
+    }
+    if (T > kMaxStreamTokens && nb % kMmaSb == 0 && stream_eligible(N, nb, K, T, W)) {
+        const int r = mma_mul_mat(N, nb, K, T, x, W, y, workspace, s);
         if (r >= 0) return r;
     }
     int8_t* qx = (int8_t*)workspace;

@@ -329,7 +329,11 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    (4096, 4096, 16), (1024, 4096, 64), (100, 96, 3), (5, 50, 2),
                                    # streaming kernel: partial segment, ragged rows, unaligned x rows, T 2..4
                                    (1001, 2304, 1), (37, 261, 3), (4097, 512, 2), (28672, 4096, 4),
-                                   (3, 256, 1)])
+                                   (3, 256, 1),
+                                   # MFMA kernel (T > 4, K % 512 == 0): ragged row and token tiles,
+                                   # several stages, T past 64
+                                   (300, 512, 5), (17, 4096, 17), (4096, 14336, 16), (2000, 8192, 33),
+                                   (64, 1024, 100), (6144, 4096, 64)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
@@ -345,11 +349,13 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     assert_f32_identical(host(y).reshape(T, N), ref)
 
 
-def test_q8_0_mul_mat_g_special_values(ane, oracle):
-    """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules per block)."""
+@pytest.mark.parametrize("T", [2, 20])
+def test_q8_0_mul_mat_g_special_values(ane, oracle, T):
+    """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules
+    per block), on the streaming (T = 2) and MFMA (T = 20) kernels."""
     import torch
 
-    N, K, T = 300, 1024, 2
+    N, K = 300, 1024
     W = data.q8_0_weights(N, K, seed=11)
     x = data.activations(T, K, seed=12)
     x[0, 0:32] = 0.0
