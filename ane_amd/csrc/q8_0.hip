@@ -10,10 +10,11 @@
 //             b % 16, fmaf((float)isum, d_w*d_x, p)) combined by the same
 //             FADDV tree.  Serves GGML_OP_MUL_MAT for every token.
 //
-// Two implementations of each mode, bit-identical by construction:
-//  * streaming kernels (k_q8_0_stream), used when every row starts 16-byte
-//    aligned (nb % 8 == 0, W 16-byte aligned), the matrix is under 2 GB and
-//    the activations fit in LDS;
+// Implementations, bit-identical by construction:
+//  * streaming kernels (k_q8_0_stream), R and G mode for up to 4 tokens,
+//    used when every row starts 16-byte aligned (nb % 8 == 0, W 16-byte
+//    aligned), the matrix is under 2 GB and the activations fit in LDS;
+//  * the MFMA kernel (k_q8_0_mma), G mode for 5+ tokens when nb % 16 == 0;
 //  * general kernels (k_q8_0_gemv_r, k_q8_0_quantize_x + k_q8_0_mul_mat_g)
 //    for everything else.
 #include "../../include/ane_decode.h"
@@ -416,7 +417,7 @@ __device__ __forceinline__ float rms_inv(double ss, uint32_t K, float eps) {
 // half), then ring_start() to put the first RING weight copies in flight
 // behind them, applies the fusions, stores x into LDS and waits for every
 // wave.
-template <int MODE, int NW, int FUSE, int RING, class Start>
+template <int MODE, int NW, int FUSE, int RING, int XB, class Start>
 __device__ __forceinline__ void stream_prologue(const XStage<MODE, NW * 64>& xst, const StreamFuse& fz,
                                                 uint32_t N, uint32_t r0, uint32_t r1, double* red, float* rres,
                                                 Start&& ring_start) {
@@ -443,68 +444,68 @@ __device__ __forceinline__ void stream_prologue(const XStage<MODE, NW * 64>& xst
         lds_barrier();
         return;
     }
-    float4 xv[kXBatch];
+    float4 xv[XB];
 #pragma unroll
-    for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(k);
-    float4 wv[(FUSE & (kFuseNorm | kFuseSiluMul)) ? kXBatch : 1];
+    for (uint32_t k = 0; k < XB; k++) xv[k] = xst.load(k);
+    float4 wv[(FUSE & (kFuseNorm | kFuseSiluMul)) ? XB : 1];
     if (FUSE & kFuseNorm) {
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(fz.norm_w, xst.K * 4);
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load_w(k, wr);
+        for (uint32_t k = 0; k < XB; k++) wv[k] = xst.load_w(k, wr);
     }
     if (FUSE & kFuseSiluMul) {
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(k, xst.K * 4);  // up
+        for (uint32_t k = 0; k < XB; k++) wv[k] = xst.load(k, xst.K * 4);  // up
     }
     ring_start();
     if (FUSE & kFuseSiluMul) {
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
+        for (uint32_t k = 0; k < XB; k++) {
             const float4 g = xv[k], u = wv[k];
             xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
         }
     }
-    if (FUSE & kFuseNorm) {  // the host guarantees npass <= kXBatch for this fusion
+    if (FUSE & kFuseNorm) {  // the host guarantees npass <= XB for this fusion
         double ss = 0.0;
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
+        for (uint32_t k = 0; k < XB; k++) {
             const float4 f = xv[k];  // lanes past the end hold zeros
             ss += (double)f.x * f.x + (double)f.y * f.y + (double)f.z * f.z + (double)f.w * f.w;
         }
         ss = block_sum_f64<NW>(ss, red);
         const float inv = rms_inv(ss, xst.K, fz.eps);
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) {
+        for (uint32_t k = 0; k < XB; k++) {
             const float4 f = xv[k], w4 = wv[k];
             xv[k] = make_float4(__fmul_rn(__fmul_rn(f.x, inv), w4.x), __fmul_rn(__fmul_rn(f.y, inv), w4.y),
                                 __fmul_rn(__fmul_rn(f.z, inv), w4.z), __fmul_rn(__fmul_rn(f.w, inv), w4.w));
         }
     }
 #pragma unroll
-    for (uint32_t k = 0; k < kXBatch; k++)
+    for (uint32_t k = 0; k < XB; k++)
         if (k < npass) xst.store(k, xv[k]);
-    for (uint32_t p0 = kXBatch; p0 < npass; p0 += kXBatch) {  // SiLU*up is elementwise: any K
+    for (uint32_t p0 = XB; p0 < npass; p0 += XB) {  // SiLU*up is elementwise: any K
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++) xv[k] = xst.load(p0 + k);
+        for (uint32_t k = 0; k < XB; k++) xv[k] = xst.load(p0 + k);
         if (FUSE & kFuseSiluMul) {
 #pragma unroll
-            for (uint32_t k = 0; k < kXBatch; k++) wv[k] = xst.load(p0 + k, xst.K * 4);
+            for (uint32_t k = 0; k < XB; k++) wv[k] = xst.load(p0 + k, xst.K * 4);
 #pragma unroll
-            for (uint32_t k = 0; k < kXBatch; k++) {
+            for (uint32_t k = 0; k < XB; k++) {
                 const float4 g = xv[k], u = wv[k];
                 xv[k] = make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z),
                                     silu_mul1(g.w, u.w));
             }
         }
 #pragma unroll
-        for (uint32_t k = 0; k < kXBatch; k++)
+        for (uint32_t k = 0; k < XB; k++)
             if (p0 + k < npass) xst.store(p0 + k, xv[k]);
     }
     wait_lgkmcnt0();
     lds_barrier();
 }
 
-template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0>
+template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0, int XB = kXBatch>
 __global__ void __launch_bounds__(NW * 64)
 k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __restrict__ x,
               const uint8_t* __restrict__ W, float* y, uint32_t total_waves, StreamFuse fz) {
@@ -549,7 +550,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     };
     double* red = reinterpret_cast<double*>(xlds + stream_x_bytes(MODE, nb, T));
     float* rres = reinterpret_cast<float*>(red + NW) + wave * 64;
-    stream_prologue<MODE, NW, FUSE, S * G::kDma>(xst, fz, N, r0, r1, red, rres, ring_start);
+    stream_prologue<MODE, NW, FUSE, S * G::kDma, XB>(xst, fz, N, r0, r1, red, rres, ring_start);
 
     float p[TT];
 #pragma unroll
@@ -610,13 +611,13 @@ int cu_count(int dev) {
 
 // Launches one configuration if its LDS fits; returns -1 if it does not.
 // Occupancy is queried once per (device, LDS size).
-template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0>
+template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0, int XB = kXBatch>
 int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W,
                float* y, hipStream_t s, StreamFuse fz = StreamFuse{nullptr, 0.0f, nullptr}) {
     const uint64_t lds64 = stream_lds<MODE, NW, SB, S>(nb, T);
     if (lds64 > kLdsLimit) return -1;
     const uint32_t lds = (uint32_t)lds64;
-    auto fn = k_q8_0_stream<MODE, NW, SB, S, TT, FUSE>;
+    auto fn = k_q8_0_stream<MODE, NW, SB, S, TT, FUSE, XB>;
     static int occ_cache[64];
     static uint32_t occ_lds[64];
     int dev = 0;
@@ -641,7 +642,7 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     // the residual fusion holds one row per lane: at most 64 rows per wave
     if ((FUSE & kFuseResidual) && ((uint64_t)N + grid * NW - 1) / (grid * NW) > 64) return -1;
     // the norm fusion holds all of x in registers until the sum of squares is known
-    if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > kXBatch) return -1;
+    if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > XB) return -1;
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
                        (const uint8_t*)W, y, (uint32_t)(grid * NW), fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -664,6 +665,12 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
 #define ANE_Q8_LARGE_CFG 8, 32, 2
 #endif
 
+template <int NW, int SB, int S>
+struct SmallCfg {
+    static constexpr int kNw = NW;
+};
+using Q8SmallCfg = SmallCfg<ANE_Q8_SMALL_CFG>;
+
 template <int MODE, int TT, int FUSE = 0>
 int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
                 hipStream_t s, StreamFuse fz = StreamFuse{nullptr, 0.0f, nullptr}) {
@@ -671,8 +678,17 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t units = ((uint64_t)N + kUnitRows - 1) / kUnitRows;
     int r = -1;
-    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU)
-        r = try_stream<MODE, ANE_Q8_SMALL_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) {
+        // a plain single-token product whose activation needs 9-16 passes
+        // loads all of it before the ring's copies (one batch of 16)
+        constexpr int kSmallNw = Q8SmallCfg::kNw;
+        const uint64_t per_pass = MODE == kModeG ? kSmallNw * 64 / 8 : kSmallNw * 64;
+        const uint64_t npass = ((MODE == kModeG ? (uint64_t)nb * T : (uint64_t)nb * 8) + per_pass - 1) / per_pass;
+        if (FUSE == 0 && TT == 1 && npass > kXBatch && npass <= 2 * kXBatch)
+            r = try_stream<MODE, ANE_Q8_SMALL_CFG, TT, FUSE, 2 * kXBatch>(N, nb, K, T, x, W, y, s, fz);
+        else
+            r = try_stream<MODE, ANE_Q8_SMALL_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+    }
     if (r < 0) r = try_stream<MODE, ANE_Q8_LARGE_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
     if (r < 0) r = try_stream<MODE, 4, 32, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
     return r;
