@@ -699,100 +699,140 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
 // block's isum for a tile of 16 weight rows x 16 tokens (K = 32 = one
 // block), so the matrix cores produce the integer dots and the fp32 part
 // stays the definition's: lane (g, t) holds the tile's rows 4g..4g+3 for
-// token t, folds each block b into p[b % 16][i] = fmaf((float)isum,
-// fl(d_w * d_x), p[b % 16][i]) in increasing b, and ends with the FADDV tree
-// over its 16 partials in registers.
+// token t, folds block b into p[b % 16][i] = fmaf((float)isum,
+// fl(d_w * d_x), p[b % 16][i]) in increasing b, and the row result is the
+// FADDV tree over the 16 partials.
 //
-// One wave per tile, no barriers: each wave streams its tile through a
-// private LDS ring of S stages, a stage being 16 blocks of the 16 weight
-// rows (34-byte blocks, rows 35 chunks apart), of the 16 tokens' quantized
-// activations (rows 34 chunks apart) and of their 16 x 16 fp32 scales, all
-// copied global -> LDS with buffer_load_dwordx4 ... lds.  The waves of a
-// workgroup take the token tiles of one row tile, so the weight rows come
-// from HBM once and from L2 for the others.
-constexpr uint32_t kMmaSb = 16;                        // blocks per stage
+// A workgroup of RT x TT x KS waves takes RT row tiles x TT token tiles.
+// They share a ring of S stages in LDS; a stage is 16 blocks of the RT*16
+// weight rows (34-byte blocks, rows 35 chunks apart), of the TT*16 tokens'
+// quantized activations (rows 34 chunks apart) and of their fp32 scales,
+// copied global -> LDS with buffer_load_dwordx4 ... lds.  The copy
+// instructions of a stage are dealt round-robin to the waves (a wave with
+// fewer real ones copies zeros into its own trash slot, so every wave
+// issues the same count and the s_waitcnt immediates stay exact); each
+// stage ends with s_waitcnt + s_barrier.
+//
+// KS > 1 splits the 16 blocks of a stage among KS waves of the same tile by
+// residue: wave ks computes blocks b with (b % 16) / (16 / KS) == ks, so each
+// of the 16 fp32 chains stays inside one wave in its own order, and the
+// partials only meet, through LDS, for the final FADDV tree.
+constexpr uint32_t kMmaSb = 16;                           // blocks per stage
 constexpr uint32_t kMmaWRowChunks = kMmaSb * 17 / 8 + 1;  // 34 + 1 pad
 constexpr uint32_t kMmaXRowChunks = kMmaSb * 2 + 2;       // 32 + 2 pad
-constexpr uint32_t kMmaWChunks = 16 * kMmaWRowChunks;     // 560
-constexpr uint32_t kMmaXChunks = 16 * kMmaXRowChunks;     // 544
-constexpr uint32_t kMmaDChunks = 16 * kMmaSb * 4 / 16;    // 64: 16 tokens x 16 fp32
-constexpr uint32_t kMmaDmaW = (kMmaWChunks + 63) / 64;    // 9
-constexpr uint32_t kMmaDmaX = (kMmaXChunks + 63) / 64;    // 9
-constexpr uint32_t kMmaDma = kMmaDmaW + kMmaDmaX + 1;     // copy instructions per stage
-constexpr uint32_t kMmaStageBytes = (kMmaWChunks + kMmaXChunks + kMmaDChunks) * 16;
+constexpr uint32_t kMmaDTokChunks = kMmaSb * 4 / 16;      // 4: 16 fp32 scales per token
 
-template <int NW, int S>
-__global__ void __launch_bounds__(NW * 64)
+template <int RT, int TT, int KS>
+struct MmaLayout {
+    static constexpr int kNw = RT * TT * KS;
+    static constexpr uint32_t kWChunks = RT * 16 * kMmaWRowChunks;
+    static constexpr uint32_t kXChunks = TT * 16 * kMmaXRowChunks;
+    static constexpr uint32_t kDChunks = TT * 16 * kMmaDTokChunks;
+    static constexpr uint32_t kWInstr = (kWChunks + 63) / 64, kXInstr = (kXChunks + 63) / 64,
+                              kDInstr = (kDChunks + 63) / 64;
+    // copy slots per wave (instructions dealt round-robin)
+    static constexpr uint32_t kWSlots = (kWInstr + kNw - 1) / kNw, kXSlots = (kXInstr + kNw - 1) / kNw,
+                              kDSlots = (kDInstr + kNw - 1) / kNw;
+    static constexpr uint32_t kSlots = kWSlots + kXSlots + kDSlots;  // copy instructions per wave per stage
+    static constexpr uint32_t kXOff = kWChunks * 16, kDOff = kXOff + kXChunks * 16;
+    static constexpr uint32_t kStageBytes = kDOff + kDChunks * 16;
+};
+
+template <int RT, int TT, int KS, int S>
+__global__ void __launch_bounds__(RT * TT * KS * 64)
 k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, const uint8_t* __restrict__ qws,
-           uint32_t dx_off, float* __restrict__ y) {
-    static_assert((S - 1) * kMmaDma < 64, "copies in flight exceed the vmcnt range");
+           uint32_t dx_off, uint32_t n_ttiles, float* __restrict__ y) {
+    using L = MmaLayout<RT, TT, KS>;
+    constexpr int NW = L::kNw;
+    constexpr uint32_t kSbw = kMmaSb / KS;  // blocks of a stage per wave
+    static_assert(kMmaSb % KS == 0, "KS divides the 16 residues");
+    static_assert((S - 1) * L::kSlots < 64, "copies in flight exceed the vmcnt range");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t* trash = smem + S * L::kStageBytes;  // 1 KB per wave for padding copies
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    int8_t* ring = smem + wave * (S * kMmaStageBytes);
+    const uint32_t ks = wave % KS, tt = (wave / KS) % TT, rt = wave / (KS * TT);
 
-    const uint32_t tt = (T + 15) / 16;
-    const uint32_t gw = blockIdx.x * NW + wave;
-    const uint32_t row0 = (gw / tt) * 16, t0 = (gw % tt) * 16;
-    const bool live = row0 < N;  // waves past the last tile copy nothing and store nothing
+    // workgroup tile: row tiles [rbase, rbase + RT), token tiles [tbase, tbase + TT)
+    const uint32_t wg_t = blockIdx.x % ((n_ttiles + TT - 1) / TT), wg_r = blockIdx.x / ((n_ttiles + TT - 1) / TT);
+    const uint32_t row_base = wg_r * RT * 16, tok_base = wg_t * TT * 16;
     const uint32_t rb = nb * 34;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(W, N * rb);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(qws, dx_off + T * nb * 4);
     const uint32_t nst = nb / kMmaSb;
 
-    // per-lane source offsets of each copy at stage 0 (0x80000000: pad, dead
-    // row or token, which read as zero) and the stride they advance by
-    uint32_t ow[kMmaDmaW], ox[kMmaDmaX], od;
+    // per-slot source offsets at stage 0 (0x80000000: pad, dead row or token)
+    uint32_t ow[L::kWSlots], ox[L::kXSlots], od[L::kDSlots];
 #pragma unroll
-    for (uint32_t j = 0; j < kMmaDmaW; j++) {
-        const uint32_t c = 64 * j + lane, r = c / kMmaWRowChunks, sub = c - r * kMmaWRowChunks;
-        ow[j] = (live && r < 16 && sub < kMmaSb * 17 / 8 && row0 + r < N) ? (row0 + r) * rb + 16 * sub : 0x80000000u;
+    for (uint32_t q = 0; q < L::kWSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, r = c / kMmaWRowChunks, sub = c - r * kMmaWRowChunks;
+        const uint32_t row = row_base + r;
+        ow[q] = (c < L::kWChunks && sub < kMmaSb * 17 / 8 && row < N) ? row * rb + 16 * sub : 0x80000000u;
     }
 #pragma unroll
-    for (uint32_t j = 0; j < kMmaDmaX; j++) {
-        const uint32_t c = 64 * j + lane, t = c / kMmaXRowChunks, sub = c - t * kMmaXRowChunks;
-        ox[j] = (live && t < 16 && sub < 2 * kMmaSb && t0 + t < T) ? (t0 + t) * nb * 32 + 16 * sub : 0x80000000u;
+    for (uint32_t q = 0; q < L::kXSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, t = c / kMmaXRowChunks, sub = c - t * kMmaXRowChunks;
+        const uint32_t tok = tok_base + t;
+        ox[q] = (c < L::kXChunks && sub < 2 * kMmaSb && tok < T) ? tok * nb * 32 + 16 * sub : 0x80000000u;
     }
-    {
-        const uint32_t t = lane >> 2, sub = lane & 3;  // 16 tokens x 4 chunks of 4 scales
-        od = (live && t0 + t < T) ? dx_off + (t0 + t) * nb * 4 + 16 * sub : 0x80000000u;
+#pragma unroll
+    for (uint32_t q = 0; q < L::kDSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, t = c / kMmaDTokChunks, sub = c - t * kMmaDTokChunks;
+        const uint32_t tok = tok_base + t;
+        od[q] = (c < L::kDChunks && tok < T) ? dx_off + tok * nb * 4 + 16 * sub : 0x80000000u;
     }
+    // one copy slot: instruction i of a region if it exists (lanes past the
+    // region's last chunk masked; lane 0 is always live), else zeros into trash
+    auto slot = [&](__amdgpu_buffer_rsrc_t r, int8_t* region, uint32_t ninstr, uint32_t nchunks, uint32_t q,
+                    uint32_t src) {
+        const uint32_t i = q * NW + wave;
+        if (i < ninstr) {
+            if (nchunks % 64 == 0 || i + 1 < ninstr || lane < nchunks % 64) copy16_to_lds(r, region + 1024 * i, src);
+        } else {
+            copy16_to_lds(r, trash + 1024 * wave, 0x80000000u);
+        }
+    };
     auto issue = [&](uint32_t s) {
-        int8_t* st = ring + (s % S) * kMmaStageBytes;
+        int8_t* st = smem + (s % S) * L::kStageBytes;
         const bool on = s < nst;
 #pragma unroll
-        for (uint32_t j = 0; j < kMmaDmaW; j++)
-            if (kMmaWChunks % 64 == 0 || j + 1 < kMmaDmaW || lane < kMmaWChunks % 64)
-                copy16_to_lds(wr, st + 1024 * j, on && ow[j] != 0x80000000u ? ow[j] + s * (kMmaSb * 34) : 0x80000000u);
+        for (uint32_t q = 0; q < L::kWSlots; q++)
+            slot(wr, st, L::kWInstr, L::kWChunks, q,
+                 on && ow[q] != 0x80000000u ? ow[q] + s * (kMmaSb * 34) : 0x80000000u);
 #pragma unroll
-        for (uint32_t j = 0; j < kMmaDmaX; j++)
-            if (kMmaXChunks % 64 == 0 || j + 1 < kMmaDmaX || lane < kMmaXChunks % 64)
-                copy16_to_lds(xr, st + kMmaWChunks * 16 + 1024 * j,
-                              on && ox[j] != 0x80000000u ? ox[j] + s * (kMmaSb * 32) : 0x80000000u);
-        copy16_to_lds(xr, st + (kMmaWChunks + kMmaXChunks) * 16,
-                      on && od != 0x80000000u ? od + s * (kMmaSb * 4) : 0x80000000u);
+        for (uint32_t q = 0; q < L::kXSlots; q++)
+            slot(xr, st + L::kXOff, L::kXInstr, L::kXChunks, q,
+                 on && ox[q] != 0x80000000u ? ox[q] + s * (kMmaSb * 32) : 0x80000000u);
+#pragma unroll
+        for (uint32_t q = 0; q < L::kDSlots; q++)
+            slot(xr, st + L::kDOff, L::kDInstr, L::kDChunks, q,
+                 on && od[q] != 0x80000000u ? od[q] + s * (kMmaSb * 4) : 0x80000000u);
     };
 
-    float p[16][4];
+    float p[kSbw][4];
 #pragma unroll
-    for (int b = 0; b < 16; b++)
+    for (uint32_t b = 0; b < kSbw; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++) p[b][i] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < S; s++) issue(s);
+    for (int s = 0; s < S - 1; s++) issue(s);
     for (uint32_t s = 0; s < nst; s++) {
-        wait_vmcnt<(S - 1) * kMmaDma>();  // stage s has landed
-        const int8_t* st = ring + (s % S) * kMmaStageBytes;
-        const int8_t* wa = st + c16 * (kMmaWRowChunks * 16);                      // A: weight row c16
-        const int8_t* xb = st + kMmaWChunks * 16 + c16 * (kMmaXRowChunks * 16);   // B: token c16
-        const float* dxs = reinterpret_cast<const float*>(st + (kMmaWChunks + kMmaXChunks) * 16) + c16 * kMmaSb;
+        wait_vmcnt<(S - 2) * L::kSlots>();  // this wave's copies of stage s have landed
+        __builtin_amdgcn_s_barrier();       // everyone's have; everyone is done with stage s-1
+        issue(s + S - 1);                    // refills the slot of stage s-1
+        const int8_t* st = smem + (s % S) * L::kStageBytes;
+        const int8_t* wa = st + (rt * 16 + c16) * (kMmaWRowChunks * 16);                  // A: weight row
+        const int8_t* xb = st + L::kXOff + (tt * 16 + c16) * (kMmaXRowChunks * 16);      // B: token
+        const float* dxs = reinterpret_cast<const float*>(st + L::kDOff) + (tt * 16 + c16) * kMmaSb;
+        const int8_t* wrow = st + (rt * 16 + 4 * g) * (kMmaWRowChunks * 16);             // rows 4g.. for d_w
 #pragma unroll
-        for (uint32_t bb = 0; bb < kMmaSb; bb++) {
-            // A operand: quants 8g..8g+7 of row c16's block bb (bytes 34bb + 2 + 8g ..)
-            const uint32_t o = 34 * bb + 2 + 8 * g;  // 4-byte aligned iff bb is odd
+        for (uint32_t j = 0; j < kSbw; j++) {
+            const uint32_t bb = ks * kSbw + j;  // block of the stage; b % 16 == bb
+            const uint32_t o = 34 * bb + 2 + 8 * g;
             const uint32_t* a32 = reinterpret_cast<const uint32_t*>(wa + (o & ~3u));
             uint32_t a0, a1;
-            if (bb & 1) {
+            static_assert(kSbw % 2 == 0, "bb and j share their parity");
+            if (j & 1) {  // 34bb + 2 is 4-byte aligned for odd bb
                 a0 = a32[0];
                 a1 = a32[1];
             } else {
@@ -806,43 +846,67 @@ k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             const float dx = dxs[bb];
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // output row 4g + i of the tile, token c16
-                const uint16_t dwb = *reinterpret_cast<const uint16_t*>(st + (4 * g + i) * (kMmaWRowChunks * 16) + 34 * bb);
-                const float dd = __fmul_rn(half_bits_to_float(dwb), dx);
-                p[bb][i] = __builtin_fmaf((float)acc[i], dd, p[bb][i]);
+                const uint16_t dwb = *reinterpret_cast<const uint16_t*>(wrow + i * (kMmaWRowChunks * 16) + 34 * bb);
+                p[j][i] = __builtin_fmaf((float)acc[i], __fmul_rn(half_bits_to_float(dwb), dx), p[j][i]);
             }
         }
-        wait_lgkmcnt0();  // this stage's LDS reads are done before it is refilled
-        issue(s + S);
     }
     wait_vmcnt<0>();
+    const uint32_t row0 = row_base + rt * 16, t0 = tok_base + tt * 16;
+    if (KS > 1) {
+        // partials [tile][residue][lane][4] over the ring; wave ks holds residues ks*kSbw ..
+        __syncthreads();
+        float4* ex = reinterpret_cast<float4*>(smem) + (uint64_t)(rt * TT + tt) * 16 * 64;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float t8[8], t4[4];
+        for (uint32_t j = 0; j < kSbw; j++)
+            ex[(ks * kSbw + j) * 64 + lane] = make_float4(p[j][0], p[j][1], p[j][2], p[j][3]);
+        __syncthreads();
+        if (ks == 0) {
+            float q[16][4];
 #pragma unroll
-        for (int l = 0; l < 8; l++) t8[l] = p[2 * l][i] + p[2 * l + 1][i];
+            for (int r = 0; r < 16; r++) {
+                const float4 v = ex[r * 64 + lane];
+                q[r][0] = v.x;
+                q[r][1] = v.y;
+                q[r][2] = v.z;
+                q[r][3] = v.w;
+            }
 #pragma unroll
-        for (int l = 0; l < 4; l++) t4[l] = t8[2 * l] + t8[2 * l + 1];
-        const float v = (t4[0] + t4[1]) + (t4[2] + t4[3]);
-        const uint32_t row = row0 + 4 * g + i, t = t0 + c16;
-        if (live && row < N && t < T) y[(uint64_t)t * N + row] = v;
+            for (int i = 0; i < 4; i++) {
+                float t8[8], t4[4];
+#pragma unroll
+                for (int l = 0; l < 8; l++) t8[l] = q[2 * l][i] + q[2 * l + 1][i];
+#pragma unroll
+                for (int l = 0; l < 4; l++) t4[l] = t8[2 * l] + t8[2 * l + 1];
+                const float v = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+                const uint32_t row = row0 + 4 * g + i, t = t0 + c16;
+                if (row < N && t < T) y[(uint64_t)t * N + row] = v;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float t8[8], t4[4];
+#pragma unroll
+            for (int l = 0; l < 8; l++) t8[l] = p[2 * l][i] + p[2 * l + 1][i];
+#pragma unroll
+            for (int l = 0; l < 4; l++) t4[l] = t8[2 * l] + t8[2 * l + 1];
+            const float v = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+            const uint32_t row = row0 + 4 * g + i, t = t0 + c16;
+            if (row < N && t < T) y[(uint64_t)t * N + row] = v;
+        }
     }
 }
 
-constexpr int kMmaNW = 4, kMmaS = 2;
-
-// The MFMA path: rows 16-byte aligned (as the streaming kernels need) and
-// whole 16-block stages.  x is quantized into the workspace first.
-int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
-                void* workspace, hipStream_t s) {
-    int8_t* qx = (int8_t*)workspace;
-    const uint64_t dx_off = ceil_to((uint64_t)T * nb * 32, 256);
-    float* dx = (float*)((uint8_t*)workspace + dx_off);
-    if (dx_off + (uint64_t)T * nb * 4 >= 0x80000000ull) return -1;
-    const uint64_t nblocks = (uint64_t)T * nb;
-    hipLaunchKernelGGL(k_q8_0_quantize_x, dim3((uint32_t)((nblocks + 255) / 256)), dim3(256), 0, s, nblocks, nb, K,
-                       x, qx, dx);
-    auto fn = k_q8_0_mma<kMmaNW, kMmaS>;
-    const uint32_t lds = kMmaNW * kMmaS * kMmaStageBytes;
+template <int RT, int TT, int KS, int S>
+int mma_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* ws, uint32_t dx_off, float* y,
+               hipStream_t s) {
+    using L = MmaLayout<RT, TT, KS>;
+    const uint64_t ring = (uint64_t)S * L::kStageBytes;
+    const uint64_t exch = KS > 1 ? (uint64_t)RT * TT * 16 * 64 * 16 : 0;
+    const uint32_t lds = (uint32_t)((ring > exch ? ring : exch) + 1024 * L::kNw);
+    if (lds > kLdsLimit) return -1;
+    auto fn = k_q8_0_mma<RT, TT, KS, S>;
     static uint32_t attr_set[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
@@ -852,12 +916,43 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
             return ANE_ERR_HIP;
         attr_set[dev] = 1;
     }
-    const uint64_t waves = (uint64_t)((N + 15) / 16) * ((T + 15) / 16);
-    const uint64_t grid = (waves + kMmaNW - 1) / kMmaNW;
-    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(kMmaNW * 64), lds, s, N, nb, T, (const uint8_t*)W,
-                       (const uint8_t*)workspace, (uint32_t)dx_off, y);
+    const uint32_t rtiles = (N + 15) / 16, ttiles = (T + 15) / 16;
+    const uint64_t grid = (uint64_t)((rtiles + RT - 1) / RT) * ((ttiles + TT - 1) / TT);
+    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(L::kNw * 64), lds, s, N, nb, T, (const uint8_t*)W,
+                       (const uint8_t*)ws, dx_off, ttiles, y);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
+}
+
+// The MFMA path: rows 16-byte aligned (as the streaming kernels need) and
+// whole 16-block stages.  x is quantized into the workspace first.
+int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
+                void* workspace, hipStream_t s) {
+    int8_t* qx = (int8_t*)workspace;
+    const uint64_t dx_off = ceil_to((uint64_t)T * nb * 32, 256);
+    float* dx = (float*)((uint8_t*)workspace + dx_off);
+    if (dx_off + (uint64_t)T * nb * 4 >= 0x80000000ull) return -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
+    const uint64_t cus = cu_count(dev);
+    const uint64_t nblocks = (uint64_t)T * nb;
+    hipLaunchKernelGGL(k_q8_0_quantize_x, dim3((uint32_t)((nblocks + 255) / 256)), dim3(256), 0, s, nblocks, nb, K,
+                       x, qx, dx);
+    ANE_HIP_CHECK_LAUNCH();
+    const uint64_t tiles = (uint64_t)((N + 15) / 16) * ((T + 15) / 16);
+    const uint32_t ttiles = (T + 15) / 16;
+    const bool few = tiles < 4 * cus;  // fewer than 4 tiles per CU
+    const uint32_t dxo = (uint32_t)dx_off;
+    int r;
+    // shapes measured on the config-4 projections (6144/4096/28672/4096 rows,
+    // K 4096/14336, T 16 and 64): split-K over residues pays wherever it
+    // keeps a workgroup's LDS small enough for 16+ waves per CU
+    if (ttiles == 1)
+        r = few ? mma_launch<1, 1, 8, 2>(N, nb, T, W, workspace, dxo, y, s)
+                : mma_launch<2, 1, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
+    else
+        r = mma_launch<1, 2, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
+    return r;
 }
 
 }  // namespace

@@ -333,7 +333,9 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # MFMA kernel (T > 4, K % 512 == 0): ragged row and token tiles,
                                    # several stages, T past 64
                                    (300, 512, 5), (17, 4096, 17), (4096, 14336, 16), (2000, 8192, 33),
-                                   (64, 1024, 100), (6144, 4096, 64)])
+                                   (64, 1024, 100), (6144, 4096, 64),
+                                   # the workgroup shapes for many tiles: 4x1 + split 2, 4x2, 2x3
+                                   (28672, 512, 16), (8192, 1024, 32), (6000, 512, 40)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
