@@ -125,6 +125,7 @@ EXPORTS = (
     "ane_hip_q8_0_matvec_silu",
     "ane_hip_attention_decode_rope",
     "ane_hip_q8_0_matvec_q8",
+    "ane_hip_q8_0_gate_up_silu_quant",
     "ane_hip_silu_mul_quant",
 )
 
@@ -191,6 +192,7 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_hip_q8_0_matvec_silu": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
     "ane_hip_attention_decode_rope": (_c.c_int, [_P, _P, _P, _c.c_uint32, _P, _P, _P, _P, _P, _c.c_size_t, _P]),
     "ane_hip_q8_0_matvec_q8": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
+    "ane_hip_q8_0_gate_up_silu_quant": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _c.c_float, _P, _P, _P]),
     "ane_hip_silu_mul_quant": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
 }
 
@@ -612,6 +614,21 @@ def q8_act_bytes(n):
 
 def silu_mul_quant(n, gu, xq, stream=None):
     check(lib().ane_hip_silu_mul_quant(n, _p(gu), _p(xq), _stream_handle(stream)), "silu_mul_quant")
+
+
+def q8_0_gate_up_silu_quant(F, K, x, norm_w, W, xq, eps=1e-5, stream=None):
+    """xq = q8(silu(gate) * up) of the gate|up product (rows interleaved in 32-row groups)."""
+    check(lib().ane_hip_q8_0_gate_up_silu_quant(F, K, _p(x), _p(norm_w), float(eps), _p(W), _p(xq),
+                                                 _stream_handle(stream)), "q8_0_gate_up_silu_quant")
+
+
+def interleave_gate_up(W_gate, W_up):
+    """Rows of the decode step's w_gate_up: gate and up in alternating 32-row groups."""
+    import numpy as np
+
+    F = W_gate.shape[0]
+    assert W_up.shape == W_gate.shape and F % 32 == 0
+    return np.stack([W_gate.reshape(F // 32, 32, -1), W_up.reshape(F // 32, 32, -1)], axis=1).reshape(2 * F, -1)
 
 
 def q8_0_matvec_q8(N, K, xq, W, y, residual=None, stream=None):

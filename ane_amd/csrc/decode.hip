@@ -2,16 +2,20 @@
 // around the Q8_0 matrix products (RoPE + KV append, GQA attention over the
 // fp16 cache, SiLU * up) and the per-token driver ane_decode_token.
 //
-// Matrix products go through ane_hip_q8_0_matvec_fused (q8_0.hip), which
-// fuses the RMSNorm of its input and the residual add of its output, so a
-// layer is six launches: qkv (norm fused), attention partial (RoPE and the
-// KV append fused), attention combine, o (+residual), gate_up (norm fused),
-// down (SiLU * up fused into its activation prologue, +residual).
+// Matrix products run on the Q8_0 streaming kernel of q8_0.hip with the
+// steps around them fused in, so a layer is six launches:
+//   qkv       RMSNorm in the activation prologue
+//   attention partial: RoPE of q and k and the fp16 KV append fused
+//   attention merge, which also writes the output's Q8 activation form
+//   o         on that Q8 form, residual add in the epilogue
+//   gate|up   RMSNorm prologue, SiLU * up quantized to the Q8 form in the
+//             epilogue (gate and up rows interleaved in 32-row groups)
+//   down      on that Q8 form, residual add in the epilogue
 //
-// Attention is split over the context in chunks of 128 positions
+// Attention is split over the context in chunks of ANE_ATTN_CHUNK positions
 // (flash-decoding): one workgroup per (kv head, chunk) reads that chunk's K
 // and V rows once for all G = n_heads / n_kv_heads query heads of the group,
-// keeps per-head running max / sum / output, and a combine kernel merges the
+// keeps per-head max / sum / output, and the merge kernel combines the
 // chunks with the usual exp(m_c - M) rescaling.
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -403,7 +407,7 @@ int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, co
 }
 
 struct DecodeWs {
-    float *qkv, *attn, *gu;
+    float *qkv, *attn;
     uint8_t *attn_q8, *h_q8;  // Q8 activation blocks: qx [nb][32], then dx [nb]
     void* att;
     size_t attb;
@@ -419,12 +423,11 @@ size_t layout(const ane_decode_config* c, uint8_t* base, DecodeWs* w) {
     };
     float* qkv = reinterpret_cast<float*>(take(nqkv * 4));
     float* attn = reinterpret_cast<float*>(take((uint64_t)c->n_heads * kHD * 4));
-    float* gu = reinterpret_cast<float*>(take((uint64_t)2 * c->ffn * 4));
     uint8_t* attn_q8 = take((uint64_t)c->n_heads * kHD / 32 * 36);
     uint8_t* h_q8 = take((uint64_t)c->ffn / 32 * 36);
     const size_t attb = ane_hip_attention_workspace_size(c);
     void* att = take(attb);
-    if (w) *w = DecodeWs{qkv, attn, gu, attn_q8, h_q8, att, attb};
+    if (w) *w = DecodeWs{qkv, attn, attn_q8, h_q8, att, attb};
     return off;
 }
 
@@ -517,9 +520,8 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
                                                 w.attn_q8, w.att, w.attb, stream)))
             return st;
         if ((st = ane_hip_q8_0_matvec_q8(H, nq, w.attn_q8, L.w_o, x, x, stream))) return st;
-        if ((st = ane_hip_q8_0_matvec_fused(2 * F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, nullptr, w.gu, stream)))
+        if ((st = ane_hip_q8_0_gate_up_silu_quant(F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, w.h_q8, stream)))
             return st;
-        if ((st = ane_hip_silu_mul_quant(F, w.gu, w.h_q8, stream))) return st;
         if ((st = ane_hip_q8_0_matvec_q8(H, F, w.h_q8, L.w_down, x, x, stream))) return st;
     }
     return ANE_OK;

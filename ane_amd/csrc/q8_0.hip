@@ -385,7 +385,12 @@ __device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint3
 //    x[i] = (g / (1 + expf(-g))) * u with g = in[i], u = in[K + i].
 //  kFusePreQuant: the input is already quantized (qx [nb][32] int8, then dx
 //    [nb] fp32, as the staging would have produced it) and is copied into LDS.
-enum { kFuseNorm = 1, kFuseResidual = 2, kFuseSiluMul = 4, kFusePreQuant = 8 };
+//  kFuseSiluQuant: the rows are gate|up interleaved in 32-row groups (rows
+//    64k..64k+31 = gate 32k.., rows 64k+32..64k+63 = up 32k..); a workgroup
+//    owns one 64-row group, keeps its outputs in LDS and writes
+//    q8(silu(gate) * up) for those 32 values: one block of the Q8 activation
+//    form (qx at y, dx at y + N/2 bytes), as ane_hip_silu_mul_quant would.
+enum { kFuseNorm = 1, kFuseResidual = 2, kFuseSiluMul = 4, kFusePreQuant = 8, kFuseSiluQuant = 16 };
 
 struct StreamFuse {
     const float* norm_w;
@@ -519,8 +524,11 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     int8_t* xlds = smem + NW * S * G::kStageBytes;
 
     const uint32_t gw = blockIdx.x * NW + wave;
-    const uint32_t r0 = (uint32_t)(((uint64_t)gw * N) / total_waves);
-    const uint32_t r1 = (uint32_t)(((uint64_t)(gw + 1) * N) / total_waves);
+    static_assert(!(FUSE & kFuseSiluQuant) || (64 / NW) % kUnitRows == 0, "whole units per wave");
+    const uint32_t r0 = (FUSE & kFuseSiluQuant) ? blockIdx.x * 64 + wave * (64 / NW)
+                                                : (uint32_t)(((uint64_t)gw * N) / total_waves);
+    const uint32_t r1 = (FUSE & kFuseSiluQuant) ? min(r0 + 64 / NW, N)
+                                                : (uint32_t)(((uint64_t)(gw + 1) * N) / total_waves);
     const uint32_t nseg = (nb + SB - 1) / SB;
     const uint32_t nitems = (r1 - r0 + kUnitRows - 1) / kUnitRows * nseg;
     const uint32_t rb = nb * 34;
@@ -550,6 +558,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     };
     double* red = reinterpret_cast<double*>(xlds + stream_x_bytes(MODE, nb, T));
     float* rres = reinterpret_cast<float*>(red + NW) + wave * 64;
+    float* hq = reinterpret_cast<float*>(red + NW) + NW * 64;  // the group's 64 outputs (kFuseSiluQuant)
     stream_prologue<MODE, NW, FUSE, S * G::kDma, XB>(xst, fz, N, r0, r1, red, rres, ring_start);
 
     float p[TT];
@@ -576,13 +585,34 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
             for (int t = 0; t < TT; t++) {
                 float v = faddv16(p[t]);
                 if (FUSE & kFuseResidual) v = v + rres[kUnitRows * u + grp];
-                if (l == 0 && row < r1 && (TT == 1 || t < (int)T)) y[(uint64_t)t * N + row] = v;
+                if (FUSE & kFuseSiluQuant) {
+                    if (l == 0 && row < r1) hq[row - blockIdx.x * 64] = v;
+                } else if (l == 0 && row < r1 && (TT == 1 || t < (int)T)) {
+                    y[(uint64_t)t * N + row] = v;
+                }
             }
         }
         wait_lgkmcnt0();  // this stage's LDS reads are done before it is refilled
         issue(i + S);
     }
     wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+    if (FUSE & kFuseSiluQuant) {
+        __syncthreads();
+        if (wave == 0 && lane < 32) {  // 32 values of h, the 0x19 arithmetic over the block
+            const float h = silu_mul1(hq[lane], hq[32 + lane]);
+            uint32_t m = abs_key(h);
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) {
+                const uint32_t q = __shfl_xor(m, o, kWave);
+                m = m > q ? m : q;
+            }
+            float bs, inv;
+            quant_params(__uint_as_float(m), bs, inv);
+            uint8_t* out = reinterpret_cast<uint8_t*>(y);
+            out[blockIdx.x * 32 + lane] = (uint8_t)quant1(h, inv);
+            if (lane == 0) reinterpret_cast<float*>(out + N / 2)[blockIdx.x] = bs;
+        }
+    }
 }
 
 constexpr uint32_t kLdsLimit = 160 * 1024;
@@ -595,7 +625,7 @@ bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void
 
 template <int MODE, int NW, int SB, int S>
 uint64_t stream_lds(uint32_t nb, uint32_t T) {
-    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW + 256 * NW;
+    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW + 256 * NW + 256;
 }
 
 int cu_count(int dev) {
@@ -692,6 +722,36 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     if (r < 0) r = try_stream<MODE, ANE_Q8_LARGE_CFG, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
     if (r < 0) r = try_stream<MODE, 4, 32, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
     return r;
+}
+
+// The gate|up product of the decode step with SiLU*up quantized in its
+// epilogue: one workgroup per 64-row group; 8 waves of 2 units each with
+// 2-stage rings measured fastest (4 waves x 4 stages, 16 waves and 3-stage
+// rings were slower).
+int gate_up_silu_quant(uint32_t N, uint32_t nb, uint32_t K, const float* x, const void* W, void* xq,
+                       hipStream_t s, StreamFuse fz) {
+#ifndef ANE_GU_CFG
+#define ANE_GU_CFG 8, 32, 2
+#endif
+    constexpr int kCfg[3] = {ANE_GU_CFG};
+    constexpr int kNw = kCfg[0], kSb = kCfg[1], kS = kCfg[2];
+    constexpr int kFuse = kFuseNorm | kFuseSiluQuant;
+    const uint64_t lds64 = stream_lds<kModeG, kNw, kSb, kS>(nb, 1);
+    if (lds64 > kLdsLimit || (nb + kNw * 8 - 1) / (kNw * 8) > kXBatch) return -1;
+    auto fn = k_q8_0_stream<kModeG, kNw, kSb, kS, 1, kFuse>;
+    static uint32_t attr_lds[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    if (attr_lds[dev] < lds64) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds64) != hipSuccess)
+            return ANE_ERR_HIP;
+        attr_lds[dev] = (uint32_t)lds64;
+    }
+    hipLaunchKernelGGL(fn, dim3(N / 64), dim3(kNw * 64), (uint32_t)lds64, s, N, nb, K, 1u, x, (const uint8_t*)W,
+                       static_cast<float*>(xq), 0u, fz);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
 }
 
 // ====================================================== MFMA mul_mat (T > 4)
@@ -1006,6 +1066,15 @@ extern "C" int ane_hip_q8_0_matvec_q8(uint32_t N, uint32_t K, const void* xq, co
     const StreamFuse fz{nullptr, 0.0f, residual};
     const int r = residual ? stream_auto<kModeG, 1, kFusePreQuant | kFuseResidual>(N, nb, K, 1, xf, W, y, s, fz)
                            : stream_auto<kModeG, 1, kFusePreQuant>(N, nb, K, 1, xf, W, y, s, fz);
+    return r < 0 ? ANE_ERR_INVALID_ARG : r;
+}
+extern "C" int ane_hip_q8_0_gate_up_silu_quant(uint32_t F, uint32_t K, const float* x, const float* norm_w,
+                                               float eps, const void* W, void* xq, void* stream) {
+    if (F == 0) return ANE_OK;
+    const uint32_t nb = K >> 5, N = 2 * F;
+    if (!x || !norm_w || !W || !xq || (K & 31)) return ANE_ERR_BAD_POINTER;
+    if ((F & 31) || (((uintptr_t)xq) & 15) || !stream_eligible(N, nb, K, 1, W)) return ANE_ERR_INVALID_ARG;
+    const int r = gate_up_silu_quant(N, nb, K, x, W, xq, (hipStream_t)stream, StreamFuse{norm_w, eps, nullptr});
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 extern "C" int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu, const void* W,

@@ -408,7 +408,7 @@ def bench_decode(args) -> dict:
     (hidden 4096, FFN 14336, 32 q / 8 kv heads of 128, fp16 KV at context
     4096, Q8_0 weights) through ane_decode_token; every matrix product runs
     on the Q8_0 streaming kernel.  The token is captured once as a HIP graph
-    (7 launches per layer) and replayed; mul_mat share = the same graph's
+    (6 launches per layer) and replayed; mul_mat share = the same graph's
     matrix products alone / the whole token."""
     import ctypes
 
@@ -455,6 +455,7 @@ def bench_decode(args) -> dict:
     # arrive in the Q8 activation form in the token)
     xq_o = torch.zeros(ane_amd.q8_act_bytes(NH * HD), dtype=torch.uint8, device="cuda")
     xq_d = torch.zeros(ane_amd.q8_act_bytes(F), dtype=torch.uint8, device="cuda")
+    xq_g = torch.zeros(ane_amd.q8_act_bytes(F), dtype=torch.uint8, device="cuda")  # the gate|up output
     ane_amd.silu_mul_quant(NH * HD, torch.randn(2 * NH * HD, generator=gen, device="cuda"), xq_o)
     ane_amd.silu_mul_quant(F, torch.randn(2 * F, generator=gen, device="cuda"), xq_d)
 
@@ -462,8 +463,7 @@ def bench_decode(args) -> dict:
         for t in keep:
             ane_amd.q8_0_matvec_fused(nqkv, H, xin, t["w_qkv"], scratch, norm_w=t["attn_norm"], eps=1e-5, stream=st)
             ane_amd.q8_0_matvec_q8(H, NH * HD, xq_o, t["w_o"], resid, residual=resid, stream=st)
-            ane_amd.q8_0_matvec_fused(2 * F, H, xin, t["w_gate_up"], scratch, norm_w=t["ffn_norm"], eps=1e-5,
-                                      stream=st)
+            ane_amd.q8_0_gate_up_silu_quant(F, H, xin, t["ffn_norm"], t["w_gate_up"], xq_g, eps=1e-5, stream=st)
             ane_amd.q8_0_matvec_q8(H, F, xq_d, t["w_down"], resid, residual=resid, stream=st)
 
     tok_ms = graph_time(token, 3)

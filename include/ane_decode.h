@@ -15,8 +15,9 @@
  *          k, v of pos appended to the fp16 cache      one fused kernel + combine,
  *                                                    which also emits q8(attn)
  *   x    = x + W_o . q8(attn)                        fused residual epilogue
- *   gu   = W_gate_up . q8(rmsnorm(x) * ffn_norm)     fused norm prologue
- *   h    = q8(silu(gate) * up)                       one small kernel
+ *   h    = q8(silu(gate) * up), gate|up = W_gate_up . q8(rmsnorm(x) * ffn_norm)
+ *                                                    fused norm prologue and
+ *                                                    SiLU/quantize epilogue
  *   x    = x + W_down . h                            fused residual epilogue
  *
  * q8(v) is the Q8 activation form of the G mode: per 32-block, amax/127 as
@@ -25,7 +26,9 @@
  *
  * Layouts: weights are Q8_0 rows (ggml block layout) with the output
  * features as rows: W_qkv rows [q heads | k heads | v heads], W_gate_up rows
- * [gate | up].  KV cache: fp16 [n_kv_heads][ctx][head_dim].  RoPE table:
+ * gate and up interleaved in groups of 32 (gate 0..31, up 0..31, gate
+ * 32..63, up 32..63, ...), so that one workgroup owns both halves of every
+ * 32-value block of SiLU(gate) * up.  KV cache: fp16 [n_kv_heads][ctx][head_dim].  RoPE table:
  * fp32 [ctx][head_dim/2][2] = (cos, sin) of pos * base^(-2i/head_dim),
  * applied to adjacent pairs (x[2i], x[2i+1]).  All pointers are device
  * memory; the layer array itself is host memory.
@@ -54,7 +57,7 @@ struct ane_decode_config {
 struct ane_decode_layer {
     const void* w_qkv;      /* Q8_0 [(n_heads + 2 n_kv_heads) head_dim][hidden] */
     const void* w_o;        /* Q8_0 [hidden][n_heads head_dim]                  */
-    const void* w_gate_up;  /* Q8_0 [2 ffn][hidden]                             */
+    const void* w_gate_up;  /* Q8_0 [2 ffn][hidden], gate/up in 32-row groups    */
     const void* w_down;     /* Q8_0 [hidden][ffn]                               */
     const float* attn_norm; /* [hidden]                                         */
     const float* ffn_norm;  /* [hidden]                                         */
@@ -88,6 +91,16 @@ int ane_hip_q8_0_matvec_fused(uint32_t N, uint32_t K, const float* x, const floa
  * the fp32 vector xq was quantized from. */
 int ane_hip_q8_0_matvec_q8(uint32_t N, uint32_t K, const void* xq, const void* W, const float* residual,
                            float* y, void* stream);
+
+/* The gate|up product with SiLU*up fused into its epilogue: W has 2F rows,
+ * gate and up interleaved in 32-row groups (rows 64k..64k+31 = gate rows
+ * 32k.., rows 64k+32..64k+63 = up rows 32k..); with g|u = W . q8(rmsnorm(x)
+ * * norm_w) (as ane_hip_q8_0_matvec_fused), xq = q8(silu(g) * u) in the Q8
+ * activation form (F/32 * 36 bytes, 16-byte aligned, F % 32 == 0):
+ * bit-identical to ane_hip_q8_0_matvec_fused + ane_hip_silu_mul_quant on
+ * the de-interleaved output. */
+int ane_hip_q8_0_gate_up_silu_quant(uint32_t F, uint32_t K, const float* x, const float* norm_w, float eps,
+                                    const void* W, void* xq, void* stream);
 
 /* y = W . q8(silu(gu[0..K)) * gu[K..2K)) (+ residual), silu(g) = g / (1 + e^-g):
  * the down projection with SiLU * up fused into its activation prologue;

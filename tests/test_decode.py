@@ -218,7 +218,8 @@ def np_decode_token(oracle, cfg, m, caches, table, pos, x):
         attn = np_attention(q, kc, vc, pos + 1, nh, nkv).astype(F32).reshape(-1)
         x = (x + oracle.q8_0_mul_mat_g(H, nq, 1, attn, L["w_o"])[0]).astype(F32)
         xn = np_rmsnorm(x, L["ffn_norm"], cfg.eps)
-        gu = oracle.q8_0_mul_mat_g(2 * F, H, 1, xn, L["w_gate_up"])[0]
+        gu = oracle.q8_0_mul_mat_g(2 * F, H, 1, xn, L["w_gate_up"])[0]  # gate/up in 32-row groups
+        gu = gu.reshape(F // 32, 2, 32).transpose(1, 0, 2).reshape(-1)
         h = np_silu_mul(gu, F).astype(F32)
         x = (x + oracle.q8_0_mul_mat_g(H, F, 1, h, L["w_down"])[0]).astype(F32)
     return x
@@ -352,3 +353,26 @@ def test_matvec_q8_exact(ane, oracle, N, K, resid):
     y = dev(r) if resid else torch.zeros(N, dtype=torch.float32, device="cuda")
     ane.q8_0_matvec_q8(N, K, xq, dev(W), y, residual=y if resid else None)
     assert host(y).tobytes() == ref.tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F,K", [(14336, 4096), (1024, 512), (96, 256)])
+def test_gate_up_silu_quant_matches_separate(ane, F, K):
+    """The fused gate|up product == the norm-fused product, de-interleaved, then
+    silu_mul_quant, bit for bit (and the interleaving helper round-trips)."""
+    import torch
+
+    Wg, Wu = data.q8_0_weights(F, K, seed=F + 1), data.q8_0_weights(F, K, seed=F + 2)
+    W = ane.interleave_gate_up(Wg, Wu)
+    assert (W[32:64] == Wu[:32]).all() and (W[64:96] == Wg[32:64]).all()
+    x = data.activations(1, K, seed=5)[0] * F32(2.0)
+    w = (1.0 + 0.1 * data.activations(1, K, seed=6)[0]).astype(F32)
+    xd, wd, Wd = dev(x), dev(w), dev(W)
+    gu = torch.zeros(2 * F, dtype=torch.float32, device="cuda")
+    ane.q8_0_matvec_fused(2 * F, K, xd, Wd, gu, norm_w=wd, eps=1e-5)
+    gu2 = gu.view(F // 32, 2, 32).transpose(0, 1).reshape(-1).contiguous()
+    ref = torch.full((ane.q8_act_bytes(F),), 0x55, dtype=torch.uint8, device="cuda")
+    ane.silu_mul_quant(F, gu2, ref)
+    got = torch.full((ane.q8_act_bytes(F),), 0x33, dtype=torch.uint8, device="cuda")
+    ane.q8_0_gate_up_silu_quant(F, K, xd, wd, Wd, got, eps=1e-5)
+    assert host(got).tobytes() == host(ref).tobytes()
