@@ -1,4 +1,5 @@
-"""Build recipe for ane_amd/libane_amd.so (gfx950) and the CPU oracle.
+"""Build recipe for ane_amd/libane_amd.so (gfx950), the benchmark's
+libane_peaks.so and the CPU oracle.
 
 Run ``python -m ane_amd.build`` (or ``__graft_entry__.build()``).  The
 library is built in-tree so it travels with the repository snapshot; object
@@ -18,6 +19,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libane_amd.so"
+PEAKS_SRC = PKG / "probes" / "peaks.hip"
+PEAKS_LIB = PKG / "libane_peaks.so"
 
 ARCH = "gfx950"
 
@@ -72,6 +75,16 @@ def build_library(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_peaks(verbose: bool = False) -> Path:
+    """libane_peaks.so: the MFMA-loop and HBM-stream ceilings bench.py reports."""
+    tmp = PEAKS_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *HIP_FLAGS, "-shared", str(PEAKS_SRC), "-o", str(tmp)])
+    os.replace(tmp, PEAKS_LIB)
+    if verbose:
+        print(f"built {PEAKS_LIB}")
+    return PEAKS_LIB
+
+
 def build_oracle(verbose: bool = False) -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     out = ROOT / "oracle" / "libane_oracle.so"
@@ -83,6 +96,7 @@ def build_oracle(verbose: bool = False) -> Path:
 def build_all(verbose: bool = False) -> None:
     build_oracle(verbose)
     build_library(verbose)
+    build_peaks(verbose)
 
 
 if __name__ == "__main__":

@@ -211,6 +211,10 @@ k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
         }
     }
 
+    // the epilogue multiplier, read before the K loop so its latency is hidden
+    float s = p.s;
+    if (p.sdev) s = __fmul_rn(__fmul_rn(p.sdev[0], p.sdev[1]), p.smul);
+
     const uint32_t wr0 = (wave / WN) * (FM * 32);
     const uint32_t wc0 = (wave % WN) * (FN * 32);
     const uint32_t rA = wr0 + (lane & 31);
@@ -258,8 +262,6 @@ k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
     wait_vmcnt<0>();
     __syncthreads();  // all fragment reads done: the ring becomes epilogue staging
 
-    float s = p.s;
-    if (p.sdev) s = __fmul_rn(__fmul_rn(p.sdev[0], p.sdev[1]), p.smul);
     float bj[FN];
 #pragma unroll
     for (int ni = 0; ni < FN; ni++) {

@@ -14,6 +14,10 @@ Also reported (same JSON line):
   on the fly) and the reference-arithmetic opcode 0x57 ("R mode"), GB/s
   against 8 TB/s, rotating >256 MB of weight copies so the Infinity Cache
   cannot serve them.
+* ``measured_ceilings`` -- what this GPU sustains (ane_amd/libane_peaks.so):
+  an int8 MFMA loop without memory traffic on random operands, with the
+  clock it holds, and plain HBM read/write streams; each roofline also
+  carries ``frac_measured`` against the matching ceiling.
 * ``cpu_baseline`` -- the scalar CPU restatement (oracle/) on a bounded
   sample of the same workload, with the host thread count used.
 
@@ -56,7 +60,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
-    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats"], default=None,
+    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings"],
+                    default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
 
@@ -167,6 +172,9 @@ def main() -> int:
         return 0
     if args.only in ("q8g", "q8r"):
         return profile_q8(args, stream)
+    if args.only == "ceilings":
+        print(json.dumps(measured_ceilings(args)), flush=True)
+        return 0
     if args.only == "qformats":
         bench_qformats(args)
         return 0
@@ -218,11 +226,22 @@ def main() -> int:
         "traffic": read_pmc_traffic("gemm_i8_4096_pmc.txt"),
     }
 
+    ceilings = measured_ceilings(args)
+    mfma_meas = ceilings["mfma_i8_loop_random"]["TOPS"]
+    roofline["measured_peak"] = mfma_meas
+    roofline["frac_measured"] = round(gemm_tops / mfma_meas, 4)
+    roofline["measured_peak_how"] = ("int8 MFMA loop with no memory traffic on random operands "
+                                     f"(clock {ceilings['mfma_i8_loop_random']['clock_GHz']} GHz)")
+
     # ------------------------------------------------------------ Q8_0 matvec
     q8 = None
     mul_mat = None
     if not args.no_q8:
         q8 = bench_q8(args, stream)
+        rd = ceilings["hbm_read_62MB"]["GB_s"]
+        q8["roofline"]["measured_peak"] = rd
+        q8["roofline"]["frac_measured"] = round(q8["roofline"]["achieved"] / rd, 4)
+        q8["roofline"]["measured_peak_how"] = "plain read of the same 62 MB, rotating buffers"
         mul_mat = bench_mul_mat(args)
     qformats = bench_qformats(args) if not args.no_q8 else None
     m_sweep = bench_m_sweep(args, N, K) if not args.no_sweep else None
@@ -250,6 +269,7 @@ def main() -> int:
                    "M": M, "N": N, "K": K},
         "roofline": roofline,
         "phases_us": {"quantize": round(quant_ms * 1e3, 2), "contraction": round(gemm_ms * 1e3, 2)},
+        "measured_ceilings": ceilings,
         "q8_0_matvec": q8,
         "q8_0_mul_mat_config4": mul_mat,
         "other_formats_gemv": qformats,
@@ -292,6 +312,85 @@ def profile_q8(args, stream) -> int:
     alg = Nr * (Kc // 32) * 34 + 4 * Kc + 4 * Nr
     log(f"{args.only} {Nr}x{Kc}: {ms * 1e3:.2f} us/launch, {alg / ms / 1e6:.0f} GB/s")
     return 0
+
+
+def measured_ceilings(args) -> dict:
+    """Ceilings measured on this GPU with ane_amd/libane_peaks.so, reported
+    beside the datasheet peaks: an int8 MFMA loop with no memory traffic on
+    random operands (the clock the chip holds under it, from s_memtime over
+    s_memrealtime) and on constant operands, and plain HBM read / write
+    streams at the sizes the roofline kernels move."""
+    import ctypes
+
+    import torch
+
+    peaks = ctypes.CDLL(str(ROOT / "ane_amd" / "libane_peaks.so"))
+    u32, u64, vp, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+    peaks.ane_peak_mfma_i8.argtypes = [u32, u32, u32, vp, vp, vp, vp]
+    peaks.ane_peak_read.argtypes = [vp, u64, u32, i32, vp, vp]
+    peaks.ane_peak_write.argtypes = [vp, u64, u32, vp]
+    dev = torch.device("cuda:0")
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    st = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(st.cuda_stream)
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError("libane_peaks launch failed")
+
+    out = {"cus": ncu}
+    wgs, threads, iters = ncu, 512, 16000
+    sums = torch.empty(wgs * threads, dtype=torch.int32, device=dev)
+    clocks = torch.zeros(4, dtype=torch.int64, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    operands = {"random": torch.randint(-128, 128, (16384,), generator=g, dtype=torch.int8, device=dev),
+                "constant": torch.ones(16384, dtype=torch.int8, device=dev)}
+    ops = wgs * (threads // 64) * iters * 8 * 65536
+    for kind, data in operands.items():
+        fn = lambda: check(peaks.ane_peak_mfma_i8(wgs, threads, iters, data.data_ptr(), sums.data_ptr(),
+                                                  clocks.data_ptr(), sp))
+        fn()
+        ms = events_time(fn, 10, st)
+        c = clocks.cpu().tolist()
+        ghz = (c[1] - c[0]) / ((c[3] - c[2]) / 100e6) / 1e9
+        tops = ops / (ms * 1e-3) / 1e12
+        out[f"mfma_i8_loop_{kind}"] = {"TOPS": round(tops, 1), "clock_GHz": round(ghz, 3),
+                                       "frac_datasheet": round(tops / PEAK_INT8_TOPS, 4)}
+        log(f"MFMA loop, {kind} operands: {tops:.0f} TOPS ({tops / PEAK_INT8_TOPS:.1%}) at {ghz:.2f} GHz")
+    out["mfma_i8_loop_how"] = (f"{wgs} workgroups x 8 waves, 8 independent v_mfma_i32_32x32x32_i8 chains "
+                               "per wave, operands cycled through 8 A and 8 B fragments, no memory traffic")
+    del sums
+
+    hit = torch.zeros(1, dtype=torch.int32, device=dev)
+    nb = 62_390_272  # the 14336x4096 Q8_0 matrix
+    bufs = [torch.ones(nb, dtype=torch.uint8, device=dev) for _ in range(6)]
+    k = [0]
+
+    def rd(s):
+        check(peaks.ane_peak_read(bufs[k[0] % 6].data_ptr(), nb, 16 * ncu, 12345, hit.data_ptr(),
+                                  ctypes.c_void_p(s.cuda_stream)))
+        k[0] += 1
+
+    ms = graph_time(rd, 24)
+    out["hbm_read_62MB"] = {"GB_s": round(nb / ms / 1e6, 1), "us": round(ms * 1e3, 3),
+                            "how": "16-byte loads, 6 rotating 62,390,272-byte buffers (> Infinity Cache)"}
+    log(f"HBM read 62 MB: {ms * 1e3:.2f} us = {nb / ms / 1e6:.0f} GB/s")
+    del bufs
+    wb = 64 << 20
+    wbufs = [torch.empty(wb, dtype=torch.uint8, device=dev) for _ in range(5)]
+
+    def wr(s):
+        check(peaks.ane_peak_write(wbufs[k[0] % 5].data_ptr(), wb, 16 * ncu, ctypes.c_void_p(s.cuda_stream)))
+        k[0] += 1
+
+    ms = graph_time(wr, 20)
+    out["hbm_write_64MiB"] = {"GB_s": round(wb / ms / 1e6, 1), "us": round(ms * 1e3, 3),
+                              "how": "16-byte non-temporal stores, 5 rotating 64 MiB buffers"}
+    log(f"HBM write 64 MiB: {ms * 1e3:.2f} us = {wb / ms / 1e6:.0f} GB/s")
+    del wbufs
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_q8(args, stream) -> dict:
