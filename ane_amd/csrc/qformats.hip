@@ -18,7 +18,7 @@
 // the window never leaves the pointer's 16-byte granule at the front and
 // reads zeros past the matrix's last dword), two stages in flight in registers, each stage
 // written to the group's own LDS window and decoded from there with byte
-// reads.  x is staged in LDS in chunks of 8192 values shared by the 16 rows.
+// reads.  x is staged in LDS in chunks of 4096 values shared by the 16 rows.
 #include "../../include/ane_hip.h"
 #include "common.hpp"
 
@@ -49,8 +49,15 @@ struct Q40 {
     __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
         const float d = lh(s);
         const uint32_t b = lu8(s + 2 + l);
-        a = __builtin_fmaf(__fmul_rn((float)((int)(b & 15u) - 8), d), xs[l], a);
-        a = __builtin_fmaf(__fmul_rn((float)((int)(b >> 4) - 8), d), xs[16 + l], a);
+        // q - 8 without an int conversion: the float with bits 2^23 + q,
+        // minus 2^23 + 8, is q - 8 exactly.  The high nibble stays in place
+        // (16 (q - 8)) and meets d / 16, an exact scaling, so both products
+        // equal the handler's fmul((float)(q - 8), d) bit for bit (they are
+        // exact: 4- by 11-bit significands), infinities and NaNs included.
+        const float lo = __fsub_rn(__uint_as_float((b & 15u) | 0x4B000000u), 8388616.0f);
+        const float hi = __fsub_rn(__uint_as_float((b & 0xF0u) | 0x4B000000u), 8388736.0f);
+        a = __builtin_fmaf(__fmul_rn(lo, d), xs[l], a);
+        a = __builtin_fmaf(__fmul_rn(hi, __fmul_rn(d, 0.0625f)), xs[16 + l], a);
     }
 };
 
@@ -143,7 +150,7 @@ struct Q6K {
 };
 
 constexpr uint32_t kRowsPerWg = 16;
-constexpr uint32_t kXChunk = 8192;  // x values staged per pass
+constexpr uint32_t kXChunk = 4096;  // x values staged per pass (16 KB of LDS: five workgroups per CU)
 
 template <class F>
 struct Stage {
@@ -157,7 +164,9 @@ __global__ void __launch_bounds__(256)
 k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const uint8_t* Wa, uint32_t off,
         uint32_t wbytes, float* __restrict__ y) {
     using St = Stage<F>;
-    __shared__ __attribute__((aligned(16))) uint8_t win_all[kRowsPerWg][St::kWindow];
+    // windows 64 bytes apart beyond their length: the four rows of a wave
+    // read their bytes from four different bank groups
+    __shared__ __attribute__((aligned(16))) uint8_t win_all[kRowsPerWg][St::kWindow + 64];
     __shared__ float xs[kXChunk];
     const uint32_t g = threadIdx.x >> 4, l = threadIdx.x & 15;
     const uint32_t r = blockIdx.x * kRowsPerWg + g;

@@ -47,7 +47,7 @@ def weights_at(W, offset):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K", [(300, 4096), (17, 256), (33, 512), (4096, 4096), (5, 16640), (3, 8448)])
 def test_q_gemv_exact(ane, oracle, fmt, M, K):
-    """K = 16640 / 8448: inputs in several 8192-value chunks and a partial last stage."""
+    """K = 16640 / 8448: inputs in several 4096-value chunks and a partial last stage."""
     import torch
 
     W = data.q_weights(fmt, M, K, seed=M + K)
@@ -74,6 +74,27 @@ def test_q_gemv_unaligned_weights(ane, oracle, fmt, offset):
     y = torch.zeros(M, dtype=torch.float32, device="cuda")
     ane.q_gemv(fmt, M, K, dev(x), Wd, y)
     assert_same(host(y), oracle.q_gemv(fmt, M, K, x, W))
+
+
+def test_q4_0_special_scales(ane, oracle):
+    """Block scales of every fp16 class (infinities, NaN, subnormals, signed
+    zeros, the largest finite) against every nibble value."""
+    import torch
+
+    M, K = 40, 1024
+    W = data.q_weights("q4_0", M, K, seed=21).reshape(M, K // 32, 18).copy()
+    specials = np.array([0x7C00, 0xFC00, 0x7E00, 0x0001, 0x83FF, 0x8000, 0x0000, 0x7BFF, 0xBC00, 0x3C00],
+                        dtype=np.uint16)
+    rng = np.random.default_rng(22)
+    d = rng.choice(specials, size=(M, K // 32))
+    d[rng.random((M, K // 32)) < 0.5] = 0x2E66  # leave about half of the blocks ordinary
+    W[:, :, 0:2] = d.view(np.uint8).reshape(M, K // 32, 2)
+    W[:, :, 2:] = rng.integers(0, 256, size=(M, K // 32, 16), dtype=np.uint8)
+    W = W.reshape(M, -1)
+    x = data.activations(1, K, seed=23)[0]
+    y = torch.zeros(M, dtype=torch.float32, device="cuda")
+    ane.q_gemv("q4_0", M, K, dev(x), dev(W), y)
+    assert_same(host(y), oracle.q_gemv("q4_0", M, K, x, W))
 
 
 @pytest.mark.parametrize("first", ["zero", "denormal", "special"])
