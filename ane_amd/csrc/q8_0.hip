@@ -69,6 +69,30 @@ k_q8_0_quantize_x(uint64_t nblocks, uint32_t nb, uint32_t K, const float* __rest
     for (int w = 0; w < 8; w++) q[w] = pack4(s[4 * w], s[4 * w + 1], s[4 * w + 2], s[4 * w + 3], inv);
 }
 
+// Activation quantizer into the Q8 activation form (qx [T*nb][32] int8,
+// then dx [T*nb] fp32 at byte T*nb*32): 8 lanes per 32-block, one float4
+// each (coalesced), the 0x19 arithmetic of XStage::store, so a streaming
+// kernel that copies this form (kFusePreQuant) computes exactly what its own
+// prologue would.  Token t's row starts at x + t*K.
+__global__ void __launch_bounds__(256)
+k_q8_act_quantize(uint32_t nblocks, uint32_t nb, uint32_t K, const float* __restrict__ x,
+                  uint8_t* __restrict__ xq) {
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x, blk = t >> 3, part = t & 7;
+    const uint32_t tok = blk / nb, b = blk - tok * nb;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(x, (nblocks / nb) * K * 4);
+    const uint32_t o = blk < nblocks ? (tok * K + b * 32 + part * 4) * 4 : 0x80000000u;  // whole 8-lane groups
+    float f[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) f[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4 * e, 0, 0));
+    const uint32_t m = max8_u32(max(max(abs_key(f[0]), abs_key(f[1])), max(abs_key(f[2]), abs_key(f[3]))));
+    float scale, inv;
+    quant_params(__uint_as_float(m), scale, inv);
+    if (blk < nblocks) {
+        reinterpret_cast<uint32_t*>(xq)[blk * 8 + part] = pack4(f[0], f[1], f[2], f[3], inv);
+        if (part == 0) reinterpret_cast<float*>(xq + (uint64_t)nblocks * 32)[blk] = scale;
+    }
+}
+
 constexpr int kTokChunk = 4;
 
 __global__ void __launch_bounds__(256)
@@ -436,13 +460,14 @@ __device__ __forceinline__ void stream_prologue(const XStage<MODE, NW * 64>& xst
         copy4_to_lds(rr, rres, r0 + lane < r1 ? (r0 + lane) * 4 : 0x80000000u);
     }
     if (FUSE & kFusePreQuant) {
-        // 16-byte chunks: 2nb of qx (the halves of block b swapped on odd b/8,
-        // as XStage::store writes them), then nb/4 of dx
+        // 16-byte chunks: 2n of qx (n = T*nb blocks; the halves of token
+        // block b swapped on odd b/8, as XStage::store writes them), then n/4
+        // of dx
         const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        const uint32_t nq = 2 * xst.nb, nchunks = nq + xst.nb / 4;
+        const uint32_t nq = 2 * xst.n, nchunks = nq + xst.n / 4;
         for (uint32_t c0 = wave * 64; c0 < nchunks; c0 += NW * 64) {
-            const uint32_t c = c0 + lane, b = c >> 1;
-            const uint32_t src = c < nq ? (2 * b + ((c & 1) ^ ((b >> 3) & 1))) * 16 : c * 16;
+            const uint32_t c = c0 + lane, blk = c >> 1, b = blk % xst.nb;
+            const uint32_t src = c < nq ? (2 * blk + ((c & 1) ^ ((b >> 3) & 1))) * 16 : c * 16;
             if (c < nchunks) copy16_to_lds(xst.xr, xst.lds + c0 * 16, src);
         }
         ring_start();
@@ -516,7 +541,8 @@ __global__ void __launch_bounds__(NW * 64)
 k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __restrict__ x,
               const uint8_t* __restrict__ W, float* y, uint32_t total_waves, StreamFuse fz) {
     using G = Seg<SB>;
-    static_assert(FUSE == 0 || (MODE == kModeG && TT == 1), "fusions are for the G-mode decode step");
+    static_assert(FUSE == 0 || (MODE == kModeG && (TT == 1 || FUSE == kFusePreQuant)),
+                  "fusions are for the G-mode decode step; a pre-quantized input takes any token count");
     static_assert(S * G::kDma < 64, "copies in flight exceed the vmcnt range");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -551,7 +577,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     const int8_t* qxs = xlds;
     float* dxs = reinterpret_cast<float*>(xlds + ceil_to((uint64_t)T * nb * 32, 16));
     const float* xs = reinterpret_cast<const float*>(xlds);
-    const uint32_t xbytes = (FUSE & kFusePreQuant) ? nb * 36 : ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4;
+    const uint32_t xbytes = (FUSE & kFusePreQuant) ? T * nb * 36 : ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4;
     const XStage<MODE, NW * 64> xst{make_rsrc(x, xbytes), K, nb, T, MODE == kModeG ? nb * T : nb * 8, xlds, dxs};
     const auto ring_start = [&] {
 #pragma unroll
@@ -1092,6 +1118,13 @@ extern "C" int ane_hip_q8_0_matvec_silu(uint32_t N, uint32_t K, const float* gu,
     return r < 0 ? ANE_ERR_INVALID_ARG : r;
 }
 
+// Single-token products quantize x inside the streaming kernel up to this
+// many blocks (K = 8192); longer rows take the separate quantizer.
+#ifndef ANE_Q8_INLINE_QUANT_BLOCKS
+#define ANE_Q8_INLINE_QUANT_BLOCKS 256
+#endif
+constexpr uint32_t kQ8InlineQuantBlocks = ANE_Q8_INLINE_QUANT_BLOCKS;
+
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {
     const uint64_t nb = K >> 5;
     return (size_t)(ceil_to((uint64_t)T * nb * 32, 256) + ceil_to((uint64_t)T * nb * 4, 256) + 256);
@@ -1109,8 +1142,21 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
         return ANE_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
     if (T <= kMaxStreamTokens && stream_eligible(N, nb, K, T, W)) {
-        const int r = T == 1 ? stream_auto<kModeG, 1>(N, nb, K, T, x, W, y, s)
-                             : stream_auto<kModeG, kMaxStreamTokens>(N, nb, K, T, x, W, y, s);
+        int r;
+        if (T == 1 && nb <= kQ8InlineQuantBlocks) {
+            r = stream_auto<kModeG, 1>(N, nb, K, T, x, W, y, s);
+        } else {
+            // every workgroup would quantize all T*nb activation blocks: do it
+            // once into the workspace (dx follows qx: nb % 8 == 0 here) and
+            // copy the result into LDS
+            const uint32_t nblocks = T * nb;
+            hipLaunchKernelGGL(k_q8_act_quantize, dim3((nblocks * 8 + 255) / 256), dim3(256), 0, s, nblocks, nb,
+                               K, x, static_cast<uint8_t*>(workspace));
+            ANE_HIP_CHECK_LAUNCH();
+            const float* xq = static_cast<const float*>(workspace);
+            r = T == 1 ? stream_auto<kModeG, 1, kFusePreQuant>(N, nb, K, T, xq, W, y, s)
+                       : stream_auto<kModeG, kMaxStreamTokens, kFusePreQuant>(N, nb, K, T, xq, W, y, s);
+        }
         if (r >= 0) return r;
     }
     if (T > kMaxStreamTokens && nb % kMmaSb == 0 && stream_eligible(N, nb, K, T, W)) {

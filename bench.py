@@ -60,7 +60,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
-    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings"],
+    ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings",
+                             "mulmat"],
                     default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
@@ -172,6 +173,9 @@ def main() -> int:
         return 0
     if args.only in ("q8g", "q8r"):
         return profile_q8(args, stream)
+    if args.only == "mulmat":
+        print(json.dumps(bench_mul_mat(args)), flush=True)
+        return 0
     if args.only == "ceilings":
         print(json.dumps(measured_ceilings(args)), flush=True)
         return 0

@@ -330,6 +330,9 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # streaming kernel: partial segment, ragged rows, unaligned x rows, T 2..4
                                    (1001, 2304, 1), (37, 261, 3), (4097, 512, 2), (28672, 4096, 4),
                                    (3, 256, 1),
+                                   # activations quantized once into the workspace: one token
+                                   # past 256 blocks, 2..4 tokens at any K
+                                   (333, 8448, 1), (1001, 8192, 1), (4096, 14336, 3), (50, 8192, 2),
                                    # MFMA kernel (T > 4, K % 512 == 0): ragged row and token tiles,
                                    # several stages, T past 64
                                    (300, 512, 5), (17, 4096, 17), (4096, 14336, 16), (2000, 8192, 33),
@@ -351,19 +354,20 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     assert_f32_identical(host(y).reshape(T, N), ref)
 
 
-@pytest.mark.parametrize("T", [2, 20])
-def test_q8_0_mul_mat_g_special_values(ane, oracle, T):
+@pytest.mark.parametrize("T,K", [(2, 1024), (20, 1024), (1, 9216), (3, 9216)])
+def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K):
     """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules
-    per block), on the streaming (T = 2) and MFMA (T = 20) kernels."""
+    per block), on the streaming (T = 2, and the separately quantized T = 1
+    and 3 at K = 9216) and MFMA (T = 20) kernels."""
     import torch
 
-    N, K = 300, 1024
+    N = 300
     W = data.q8_0_weights(N, K, seed=11)
     x = data.activations(T, K, seed=12)
     x[0, 0:32] = 0.0
     x[0, 64] = np.nan
-    x[1, 100] = np.inf
-    x[1, 200] = -1e-40  # denormal
+    x[T - 1, 100] = np.inf
+    x[T - 1, 200] = -1e-40  # denormal
     ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
     y = zeros(T * N, torch.float32)
     ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
