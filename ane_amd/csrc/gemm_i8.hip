@@ -13,7 +13,8 @@
 // [row][128 bytes] with the 16-byte chunk index XOR-swizzled by
 // (row ^ row>>3) & 7 so the ds_read_b128 of 16 consecutive rows (one LDS
 // cycle: 64 banks x 4 bytes) hits 16 distinct bank groups.  Large shapes use the 256 x 256 kernel of
-// gemm_i8_tile256.hip instead.
+// gemm_i8_tile256.hip instead, and up to 128 rows the few-row kernel of
+// gemm_i8_skinny.hip.
 #include "gemm_i8.hpp"
 
 namespace ane {
@@ -158,10 +159,32 @@ k_gemm_i8(GemmParams p) {
     }
 }
 
+// The CU count of the current device (256-tiles are preferred from one per CU).
+static uint64_t tile256_min_tiles() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        cached[dev] = n;
+    }
+    return (uint64_t)cached[dev];
+}
+
 template <int BL, bool AU8>
 static int launch_gemm(const GemmParams& p, hipStream_t s) {
     if (p.Mout == 0 || p.Nout == 0) return ANE_OK;
-    if (BL == kBTransposed && !AU8 && tile256_eligible(p)) return launch_gemm_tile256(p, s);
+    if (BL == kBTransposed && !AU8) {
+        // 256-tiles while they fill every CU, few rows on the skinny kernel,
+        // otherwise 128-tiles (four times the workgroups)
+        const uint64_t tiles256 = (uint64_t)((p.Mout + 255) / 256) * ((p.Nout + 255) / 256);
+        const bool e256 = tile256_eligible(p);
+        if (e256 && tiles256 >= tile256_min_tiles()) return launch_gemm_tile256(p, s);
+        if (skinny_eligible(p)) return launch_gemm_skinny(p, s);
+        if (tile128_eligible(p)) return launch_gemm_tile128(p, s);
+        if (e256) return launch_gemm_tile256(p, s);
+    }
     dim3 grid((p.Nout + kBN - 1) / kBN, (p.Mout + kBM - 1) / kBM);
     if (grid.y > 65535) return ANE_ERR_INVALID_ARG;
     hipLaunchKernelGGL((k_gemm_i8<BL, AU8>), grid, dim3(kGThreads), 0, s, p);

@@ -37,4 +37,13 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
 bool tile256_eligible(const GemmParams& p);
 int launch_gemm_tile256(const GemmParams& p, hipStream_t s);
 
+// The same loop at 128 x 128 tiles (gemm_i8_tile128.hip).
+bool tile128_eligible(const GemmParams& p);
+int launch_gemm_tile128(const GemmParams& p, hipStream_t s);
+
+// Few-row kernel (gemm_i8_skinny.hip): Bt layout, signed A, M <= 128, one
+// workgroup per 16 columns.
+bool skinny_eligible(const GemmParams& p);
+int launch_gemm_skinny(const GemmParams& p, hipStream_t s);
+
 }  // namespace ane

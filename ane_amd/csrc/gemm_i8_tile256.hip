@@ -39,14 +39,36 @@
 namespace ane {
 namespace {
 
-#ifndef ANE_TILE256_WAVES
-#define ANE_TILE256_WAVES 8
+// ANE_TILE selects the output tile: 256 (this file) or 128
+// (gemm_i8_tile128.hip includes this file with ANE_TILE 128: the same loop
+// at 128 x 128 with 4 waves, two workgroups per CU, for shapes with fewer
+// 256-tiles than CUs).
+#ifndef ANE_TILE
+#define ANE_TILE 256
+#endif
+#if ANE_TILE == 256
+#define ANE_TILE_KERNEL k_gemm_i8_tile256
+#define ANE_TILE_ELIGIBLE tile256_eligible
+#define ANE_TILE_LAUNCH launch_gemm_tile256
+#ifndef ANE_TILE_WAVES
+#define ANE_TILE_WAVES 8
+#endif
+#elif ANE_TILE == 128
+#define ANE_TILE_KERNEL k_gemm_i8_tile128
+#define ANE_TILE_ELIGIBLE tile128_eligible
+#define ANE_TILE_LAUNCH launch_gemm_tile128
+#ifndef ANE_TILE_WAVES
+#define ANE_TILE_WAVES 4
+#endif
+#else
+#error "ANE_TILE is 256 or 128"
 #endif
 
-constexpr int TM = 256, TN = 256;
+constexpr int TM = ANE_TILE, TN = ANE_TILE;
 constexpr int TK = 64;                        // bytes of K per slice
 constexpr int STAGES = 4;                     // LDS ring depth
-constexpr int NW = ANE_TILE256_WAVES;         // waves per workgroup
+constexpr int NW = ANE_TILE_WAVES;            // waves per workgroup
+constexpr int kWavesPerEu = TM == 128 ? 2 : NW / 4;  // 128-tiles: two workgroups per CU
 constexpr int kThreads = NW * 64;
 constexpr int WN = NW == 16 ? 4 : 2;          // waves along N
 constexpr int WM = NW / WN;                   // waves along M
@@ -174,8 +196,8 @@ __device__ __forceinline__ void ksteps(v16i (&acc)[FM][FN], Frags& f0, Frags& f1
     }
 }
 
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
-k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu)))
+ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kLdsBytes];
 
     const uint32_t tid = threadIdx.x;
@@ -324,7 +346,7 @@ k_gemm_i8_tile256(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 
 }  // namespace
 
-bool tile256_eligible(const GemmParams& p) {
+bool ANE_TILE_ELIGIBLE(const GemmParams& p) {
     if (p.Mout < TM || p.Nout < TN) return false;
     if (p.Kp == 0 || (p.Kp % TK) != 0) return false;
     if ((p.lda & 15) || (p.ldb & 15)) return false;
@@ -337,12 +359,12 @@ bool tile256_eligible(const GemmParams& p) {
     return true;
 }
 
-int launch_gemm_tile256(const GemmParams& p, hipStream_t s) {
+int ANE_TILE_LAUNCH(const GemmParams& p, hipStream_t s) {
     const uint32_t tiles_m = (p.Mout + TM - 1) / TM;
     const uint32_t tiles_n = (p.Nout + TN - 1) / TN;
     const uint64_t total = (uint64_t)tiles_m * tiles_n;
     if (total > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(k_gemm_i8_tile256, dim3((uint32_t)total), dim3(kThreads), 0, s, p, tiles_m,
+    hipLaunchKernelGGL(ANE_TILE_KERNEL, dim3((uint32_t)total), dim3(kThreads), 0, s, p, tiles_m,
                        tiles_n);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;

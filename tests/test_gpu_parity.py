@@ -51,7 +51,12 @@ def assert_f32_identical(got, want):
                                    (300, 200, 1008), (257, 129, 4096), (64, 512, 48),
                                    # 256 x 256 tile kernel: full, partial and odd tile grids
                                    (256, 256, 128), (1000, 600, 896), (513, 257, 4096),
-                                   (2048, 1536, 256), (768, 2304, 1152)])
+                                   (2048, 1536, 256), (768, 2304, 1152),
+                                   # few-row kernel: partial 64-byte steps, ragged columns, 1..8 row blocks
+                                   (5, 17, 80), (100, 1000, 2064), (128, 1024, 4096), (17, 33, 16),
+                                   (48, 300, 592),
+                                   # 256-tiles again once they fill every CU: full and ragged grids
+                                   (4096, 4096, 128), (4352, 4096, 64)])
 def test_gemm_s8_i32_exact(ane, M, N, K):
     import torch
 
@@ -266,7 +271,8 @@ def test_dense_fused_mnist_mlp(ane, oracle):
 @pytest.mark.parametrize("M,N,K,relu,scale", [(3, 5, 7, True, 1.0), (64, 64, 1, False, 2.5),
                                               (1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0),
                                               (129, 257, 1000, False, 0.75), (7, 9, 0, True, 1.0),
-                                              (300, 700, 333, True, 1.0), (1024, 512, 4096, False, 1.0)])
+                                              (300, 700, 333, True, 1.0), (1024, 512, 4096, False, 1.0),
+                                              (128, 4096, 4096, True, 1.0), (33, 1000, 4000, True, 1.0)])
 def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
     A, B = data.gemm_inputs(M, N, K, seed=M + N + K)
     ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
