@@ -1023,8 +1023,10 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t cus = cu_count(dev);
     const uint64_t nblocks = (uint64_t)T * nb;
-    hipLaunchKernelGGL(k_q8_0_quantize_x, dim3((uint32_t)((nblocks + 255) / 256)), dim3(256), 0, s, nblocks, nb, K,
-                       x, qx, dx);
+    // nb % 16 == 0 here, so dx_off == T*nb*32: the Q8 activation form
+    (void)dx;
+    hipLaunchKernelGGL(k_q8_act_quantize, dim3((uint32_t)((nblocks * 8 + 255) / 256)), dim3(256), 0, s,
+                       (uint32_t)nblocks, nb, K, x, reinterpret_cast<uint8_t*>(qx));
     ANE_HIP_CHECK_LAUNCH();
     const uint64_t tiles = (uint64_t)((N + 15) / 16) * ((T + 15) / 16);
     const uint32_t ttiles = (T + 15) / 16;

@@ -61,7 +61,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
     ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings",
-                             "mulmat"],
+                             "mulmat", "msweep"],
                     default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
@@ -173,6 +173,9 @@ def main() -> int:
         return 0
     if args.only in ("q8g", "q8r"):
         return profile_q8(args, stream)
+    if args.only == "msweep":
+        print(json.dumps(bench_m_sweep(args, N, K)), flush=True)
+        return 0
     if args.only == "mulmat":
         print(json.dumps(bench_mul_mat(args)), flush=True)
         return 0
