@@ -166,7 +166,12 @@ k_q8_0_mul_mat_g(uint32_t N, uint32_t nb, uint32_t T, const int8_t* __restrict__
 constexpr int kUnitRows = 4;       // rows per wave pass (one per 16-lane group)
 constexpr uint32_t kXBatch = 8;    // activation float4 loads in flight per thread
 
-enum { kModeR = 0, kModeG = 1 };
+// kModeR4: the R arithmetic of q4_0_gemv (0x58) over Q4_0 blocks (18 bytes).
+enum { kModeR = 0, kModeG = 1, kModeR4 = 2 };
+
+// Bytes per block of the weight format a mode streams.
+template <int MODE>
+constexpr uint32_t kBlockBytes = MODE == kModeR4 ? 18 : 34;
 
 // LDS bytes of the activation region (G: qx then fp32 scales; R: fp32 x),
 // rounded to 16; the fp64 reduction slots of the norm fusion follow it.
@@ -176,10 +181,10 @@ __host__ __device__ __forceinline__ uint32_t stream_x_bytes(int mode, uint32_t n
     return (uint32_t)ceil_to(xb, 16);
 }
 
-template <int SB>
+template <int SB, uint32_t BB = 34>
 struct Seg {
     static_assert(SB % 16 == 0, "segment length must be a multiple of 16 blocks");
-    static constexpr uint32_t kCpr = SB * 17 / 8;              // 16-byte chunks per row segment
+    static constexpr uint32_t kCpr = SB * BB / 16;             // 16-byte chunks per row segment
     static constexpr uint32_t kPad = SB == 32 ? 0 : 4;         // staged stride = 16 or 48 dwords mod 64
     static constexpr uint32_t kRowChunks = kCpr + kPad;
     static constexpr uint32_t kStageChunks = kUnitRows * kRowChunks;
@@ -191,10 +196,11 @@ struct Seg {
 // One copy wave-instruction j of an item: the last one runs only its first
 // kLastLanes lanes, so a stage holds exactly kStageChunks chunks.  Weights
 // are streamed once per launch: non-temporal copies.
-template <int SB>
+template <int SB, uint32_t BB>
 __device__ __forceinline__ void copy_chunk(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t j,
                                            uint32_t lane, uint32_t voffset) {
-    if (Seg<SB>::kLastLanes == 64 || j + 1 < Seg<SB>::kDma || lane < Seg<SB>::kLastLanes)
+    using G = Seg<SB, BB>;
+    if (G::kLastLanes == 64 || j + 1 < G::kDma || lane < G::kLastLanes)
         copy16_to_lds_nt(w, stage + j * 1024, voffset);
 }
 
@@ -203,43 +209,44 @@ __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > 
 // Per-lane byte offsets (relative to the item's first row) of the chunks a
 // full-segment item copies; 0x80000000 marks pad chunks.  Chunk c = lane +
 // 64 j is staged row c / kRowChunks, chunk c % kRowChunks.
-template <int SB>
-__device__ __forceinline__ void full_offsets(uint32_t lane, uint32_t rb, uint32_t (&off)[Seg<SB>::kDma]) {
+template <int SB, uint32_t BB>
+__device__ __forceinline__ void full_offsets(uint32_t lane, uint32_t rb, uint32_t (&off)[Seg<SB, BB>::kDma]) {
+    using G = Seg<SB, BB>;
 #pragma unroll
-    for (uint32_t j = 0; j < Seg<SB>::kDma; j++) {
+    for (uint32_t j = 0; j < G::kDma; j++) {
         const uint32_t c = j * 64 + lane;
-        const uint32_t g = c / Seg<SB>::kRowChunks, cc = c - g * Seg<SB>::kRowChunks;
-        off[j] = (g < kUnitRows && cc < Seg<SB>::kCpr) ? g * rb + cc * 16 : 0x80000000u;
+        const uint32_t g = c / G::kRowChunks, cc = c - g * G::kRowChunks;
+        off[j] = (g < kUnitRows && cc < G::kCpr) ? g * rb + cc * 16 : 0x80000000u;
     }
 }
 
 // Copies one full-segment item: rows_live rows from byte `base` of W.  A
 // chunk is live iff its row is below rows_live, i.e. off < rows_live * rb
 // (pad offsets exceed every such bound).
-template <int SB>
+template <int SB, uint32_t BB>
 __device__ __forceinline__ void issue_full(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t lane, uint32_t base,
                                            uint32_t rows_live, uint32_t rb,
-                                           const uint32_t (&off)[Seg<SB>::kDma]) {
+                                           const uint32_t (&off)[Seg<SB, BB>::kDma]) {
     const uint32_t lim = rows_live * rb;
 #pragma unroll
-    for (uint32_t j = 0; j < Seg<SB>::kDma; j++)
-        copy_chunk<SB>(w, stage, j, lane, off[j] < lim ? base + off[j] : 0x80000000u);
+    for (uint32_t j = 0; j < Seg<SB, BB>::kDma; j++)
+        copy_chunk<SB, BB>(w, stage, j, lane, off[j] < lim ? base + off[j] : 0x80000000u);
 }
 
-// The last, shorter segment of a row (nb % SB blocks): staged stride
-// sbk*17/8 + pad chunks, offsets computed per call.
-template <int SB>
+// The last, shorter segment of a row (nb % SB blocks, a multiple of 8):
+// staged stride sbk*BB/16 + pad chunks, offsets computed per call.
+template <int SB, uint32_t BB>
 __device__ __forceinline__ void issue_partial(__amdgpu_buffer_rsrc_t w, int8_t* stage, uint32_t lane,
                                               uint32_t base, uint32_t rows_live, uint32_t rb,
                                               uint32_t sbk) {
-    const uint32_t cpr = sbk * 17 / 8;
-    const uint32_t rc = cpr + Seg<SB>::kPad;
+    const uint32_t cpr = sbk * BB / 16;
+    const uint32_t rc = cpr + Seg<SB, BB>::kPad;
 #pragma unroll
-    for (uint32_t j = 0; j < Seg<SB>::kDma; j++) {
+    for (uint32_t j = 0; j < Seg<SB, BB>::kDma; j++) {
         const uint32_t c = j * 64 + lane;
         const uint32_t g = c / rc, cc = c - g * rc;
         const bool live = g < rows_live && cc < cpr;
-        copy_chunk<SB>(w, stage, j, lane, live ? base + g * rb + cc * 16 : 0x80000000u);
+        copy_chunk<SB, BB>(w, stage, j, lane, live ? base + g * rb + cc * 16 : 0x80000000u);
     }
 }
 
@@ -399,6 +406,28 @@ __device__ __forceinline__ float compute_r(const int8_t* rowp, uint32_t l, uint3
     return acc;
 }
 
+// R mode over Q4_0 blocks (q4_0_gemv, bytecode_interpreter.s:7071-7126):
+// lane l takes the low and the high nibble of byte 2+l of every block in
+// order, w = (q - 8) * d then fma with x.  q - 8 is formed without an int
+// conversion (the float with bits 2^23 + q, minus 2^23 + 8); the high
+// nibble stays in place (16 (q - 8)) and meets d / 16, an exact scaling, so
+// both products equal fmul((float)(q - 8), d) bit for bit.
+__device__ __forceinline__ float compute_r4(const int8_t* rowp, uint32_t l, uint32_t sbk, uint32_t gb0,
+                                            const float* xs, float acc) {
+#pragma unroll 8
+    for (uint32_t b = 0; b < sbk; b++) {
+        const uint8_t* blk = reinterpret_cast<const uint8_t*>(rowp) + 18 * b;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+        const uint32_t q = blk[2 + l];
+        const float lo = __fsub_rn(__uint_as_float((q & 15u) | 0x4B000000u), 8388616.0f);
+        const float hi = __fsub_rn(__uint_as_float((q & 0xF0u) | 0x4B000000u), 8388736.0f);
+        const float* xb = xs + (gb0 + b) * 32;
+        acc = __builtin_fmaf(__fmul_rn(lo, d), xb[l], acc);
+        acc = __builtin_fmaf(__fmul_rn(hi, __fmul_rn(d, 0.0625f)), xb[16 + l], acc);
+    }
+    return acc;
+}
+
 // Optional fusions of the G-mode single-token kernel (the decode step):
 //  kFuseNorm: x' = fl(fl(x * inv) * w) with inv = 1 / sqrt(fl(fl(ss / K) + eps)),
 //    ss = sum of x^2 accumulated in fp64 (every x^2 is exact in fp64, so the
@@ -540,7 +569,8 @@ template <int MODE, int NW, int SB, int S, int TT, int FUSE = 0, int XB = kXBatc
 __global__ void __launch_bounds__(NW * 64)
 k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __restrict__ x,
               const uint8_t* __restrict__ W, float* y, uint32_t total_waves, StreamFuse fz) {
-    using G = Seg<SB>;
+    constexpr uint32_t BB = kBlockBytes<MODE>;
+    using G = Seg<SB, BB>;
     static_assert(FUSE == 0 || (MODE == kModeG && (TT == 1 || FUSE == kFusePreQuant)),
                   "fusions are for the G-mode decode step; a pre-quantized input takes any token count");
     static_assert(S * G::kDma < 64, "copies in flight exceed the vmcnt range");
@@ -558,10 +588,10 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
                                                 : (uint32_t)(((uint64_t)(gw + 1) * N) / total_waves);
     const uint32_t nseg = (nb + SB - 1) / SB;
     const uint32_t nitems = (r1 - r0 + kUnitRows - 1) / kUnitRows * nseg;
-    const uint32_t rb = nb * 34;
+    const uint32_t rb = nb * BB;
     const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(W, N * rb);
     uint32_t off[G::kDma];
-    full_offsets<SB>(lane, rb, off);
+    full_offsets<SB, BB>(lane, rb, off);
 
     auto issue = [&](uint32_t i) {
         const uint32_t u = i / nseg, s = i - u * nseg;
@@ -569,9 +599,9 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
         const uint32_t rows_live = i < nitems ? min((uint32_t)kUnitRows, r1 - row0) : 0u;
         const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
         int8_t* stage = ring + (i % S) * G::kStageBytes;
-        const uint32_t base = row0 * rb + s * (SB * 34);
-        if (sbk == (uint32_t)SB) issue_full<SB>(rsrc, stage, lane, base, rows_live, rb, off);
-        else issue_partial<SB>(rsrc, stage, lane, base, rows_live, rb, sbk);
+        const uint32_t base = row0 * rb + s * (SB * BB);
+        if (sbk == (uint32_t)SB) issue_full<SB, BB>(rsrc, stage, lane, base, rows_live, rb, off);
+        else issue_partial<SB, BB>(rsrc, stage, lane, base, rows_live, rb, sbk);
     };
 
     const int8_t* qxs = xlds;
@@ -595,7 +625,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
         wait_vmcnt<(S - 1) * G::kDma>();  // item i has landed (items i+1 .. i+S-1 may be in flight)
         const uint32_t u = i / nseg, s = i - u * nseg;
         const uint32_t sbk = min((uint32_t)SB, nb - s * SB);
-        const int8_t* rowp = ring + (i % S) * G::kStageBytes + grp * (sbk * 17 / 8 + G::kPad) * 16;
+        const int8_t* rowp = ring + (i % S) * G::kStageBytes + grp * (sbk * BB / 16 + G::kPad) * 16;
         if (s == 0) {
 #pragma unroll
             for (int t = 0; t < TT; t++) p[t] = 0.0f;
@@ -603,6 +633,8 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
         if (MODE == kModeG) {
             if (sbk == (uint32_t)SB) compute_g<SB, TT, true>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
             else compute_g<SB, TT, false>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
+        } else if (MODE == kModeR4) {
+            p[0] = compute_r4(rowp, l, sbk, s * SB, xs, p[0]);
         } else {
             p[0] = compute_r(rowp, l, sbk, s * SB, xs, p[0]);
         }
@@ -645,14 +677,15 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
 constexpr uint32_t kLdsLimit = 160 * 1024;
 constexpr int kMaxStreamTokens = 4;
 
-bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void* W) {
+bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void* W, uint32_t block_bytes = 34) {
     return nb > 0 && nb % 8 == 0 && (((uintptr_t)W) & 15) == 0 &&
-           (uint64_t)N * nb * 34 < 0x80000000ull && (uint64_t)T * K * 4 < 0x80000000ull;
+           (uint64_t)N * nb * block_bytes < 0x80000000ull && (uint64_t)T * K * 4 < 0x80000000ull;
 }
 
 template <int MODE, int NW, int SB, int S>
 uint64_t stream_lds(uint32_t nb, uint32_t T) {
-    return (uint64_t)NW * S * Seg<SB>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW + 256 * NW + 256;
+    return (uint64_t)NW * S * Seg<SB, kBlockBytes<MODE>>::kStageBytes + stream_x_bytes(MODE, nb, T) + 8 * NW +
+           256 * NW + 256;
 }
 
 int cu_count(int dev) {
@@ -1045,6 +1078,16 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
 }
 
 }  // namespace
+
+// q4_0_gemv on the streaming kernel (kModeR4) when the rows are 16-byte
+// aligned (K/32 a multiple of 8, W 16-byte aligned); -1 when they are not
+// or no configuration fits, so the caller takes the general kernel.
+int q4_0_stream_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
+    const uint32_t nb = K >> 5;
+    if (!stream_eligible(M, nb, K, 1, W, 18)) return -1;
+    return stream_auto<kModeR4, 1>(M, nb, K, 1, x, W, y, s);
+}
+
 }  // namespace ane
 
 using namespace ane;

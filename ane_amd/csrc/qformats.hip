@@ -295,9 +295,20 @@ int get_rows_launch(uint32_t n_rows, uint32_t dim, const void* table, uint64_t t
 }  // namespace
 }  // namespace ane
 
+namespace ane {
+int q4_0_stream_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s);  // q8_0.hip
+}
+
 using namespace ane;
 
+// 16-byte aligned rows stream through the Q8_0 kernel's per-wave DMA rings
+// (q8_0.hip, kModeR4); any other alignment takes k_qgemv<Q40>.  Both follow
+// the handler's arithmetic bit for bit.
 extern "C" int ane_hip_q4_0_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
+    if (M != 0 && (K >> 5) != 0 && x && W && y) {
+        const int r = q4_0_stream_gemv(M, K, x, W, y, (hipStream_t)stream);
+        if (r >= 0) return r;
+    }
     return qgemv_launch<Q40>(M, K, x, W, y, stream);
 }
 extern "C" int ane_hip_q4_k_gemv(uint32_t M, uint32_t K, const float* x, const void* W, float* y, void* stream) {
