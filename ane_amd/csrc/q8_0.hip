@@ -19,6 +19,7 @@
 //    for everything else.
 #include "../../include/ane_decode.h"
 #include "common.hpp"
+#include "qformats.hpp"
 
 namespace ane {
 namespace {
@@ -167,25 +168,57 @@ constexpr int kUnitRows = 4;       // rows per wave pass (one per 16-lane group)
 constexpr uint32_t kXBatch = 8;    // activation float4 loads in flight per thread
 
 // kModeR4: the R arithmetic of q4_0_gemv (0x58) over Q4_0 blocks (18 bytes).
-enum { kModeR = 0, kModeG = 1, kModeR4 = 2 };
+// kModeQ4K .. kModeQ5K: the K-quant GEMVs (0x75-0x78) over their 256-value
+// super-blocks, each lane decoding with the format's qf:: decoder.
+enum { kModeR = 0, kModeG = 1, kModeR4 = 2, kModeQ4K = 3, kModeQ2K = 4, kModeQ3K = 5, kModeQ5K = 6 };
 
-// Bytes per block of the weight format a mode streams.
 template <int MODE>
-constexpr uint32_t kBlockBytes = MODE == kModeR4 ? 18 : 34;
+struct ModeFmt {
+    using F = void;
+};
+template <> struct ModeFmt<kModeQ4K> { using F = qf::Q4K; };
+template <> struct ModeFmt<kModeQ2K> { using F = qf::Q2K; };
+template <> struct ModeFmt<kModeQ3K> { using F = qf::Q3K; };
+template <> struct ModeFmt<kModeQ5K> { using F = qf::Q5K; };
+
+template <int MODE>
+constexpr bool kIsQK = MODE >= kModeQ4K;
+
+// Bytes and values per block of the weight format a mode streams (a K-quant
+// super-block counts as one block).
+template <int MODE>
+constexpr uint32_t block_bytes() {
+    if constexpr (kIsQK<MODE>) return ModeFmt<MODE>::F::kBytes;
+    else return MODE == kModeR4 ? 18 : 34;
+}
+template <int MODE>
+constexpr uint32_t kBlockBytes = block_bytes<MODE>();
+template <int MODE>
+constexpr uint32_t kBlockValues = kIsQK<MODE> ? 256 : 32;
+__host__ __device__ constexpr uint32_t mode_block_values(int mode) { return mode >= kModeQ4K ? 256 : 32; }
 
 // LDS bytes of the activation region (G: qx then fp32 scales; R: fp32 x),
 // rounded to 16; the fp64 reduction slots of the norm fusion follow it.
 __host__ __device__ __forceinline__ uint32_t stream_x_bytes(int mode, uint32_t nb, uint32_t T) {
     const uint64_t xb = mode == kModeG ? ceil_to((uint64_t)T * nb * 32, 16) + (uint64_t)T * nb * 4
-                                       : (uint64_t)nb * 32 * 4;
+                                       : (uint64_t)nb * mode_block_values(mode) * 4;
     return (uint32_t)ceil_to(xb, 16);
+}
+
+// Pad chunks that put a staged row 16 or 48 dwords (mod 64) after the
+// previous one, so the four rows of a unit sit in four bank groups.
+__host__ __device__ constexpr uint32_t row_pad(uint32_t cpr) {
+    uint32_t p = 0;
+    while ((cpr + p) % 16 != 4 && (cpr + p) % 16 != 12) p++;
+    return p;
 }
 
 template <int SB, uint32_t BB = 34>
 struct Seg {
-    static_assert(SB % 16 == 0, "segment length must be a multiple of 16 blocks");
+    static_assert(BB != 34 || SB % 16 == 0, "G mode: segment length a multiple of 16 blocks");
+    static_assert((SB * BB) % 16 == 0, "a row segment is whole 16-byte chunks");
     static constexpr uint32_t kCpr = SB * BB / 16;             // 16-byte chunks per row segment
-    static constexpr uint32_t kPad = SB == 32 ? 0 : 4;         // staged stride = 16 or 48 dwords mod 64
+    static constexpr uint32_t kPad = BB == 34 ? (SB == 32 ? 0 : 4) : row_pad(kCpr);
     static constexpr uint32_t kRowChunks = kCpr + kPad;
     static constexpr uint32_t kStageChunks = kUnitRows * kRowChunks;
     static constexpr uint32_t kDma = (kStageChunks + 63) / 64;          // copy wave-instructions per item
@@ -428,6 +461,16 @@ __device__ __forceinline__ float compute_r4(const int8_t* rowp, uint32_t l, uint
     return acc;
 }
 
+// K-quant GEMVs: lane l's fmas over each staged super-block in order, with
+// the format's decoder (the same code as k_qgemv, so the same bits).
+template <class F>
+__device__ __forceinline__ float compute_qf(const int8_t* rowp, uint32_t l, uint32_t sbk, uint32_t gsb0,
+                                            const float* xs, float acc) {
+    for (uint32_t p = 0; p < sbk; p++)
+        F::acc(reinterpret_cast<const uint8_t*>(rowp) + p * F::kBytes, xs + (gsb0 + p) * 256, l, acc);
+    return acc;
+}
+
 // Optional fusions of the G-mode single-token kernel (the decode step):
 //  kFuseNorm: x' = fl(fl(x * inv) * w) with inv = 1 / sqrt(fl(fl(ss / K) + eps)),
 //    ss = sum of x^2 accumulated in fp64 (every x^2 is exact in fp64, so the
@@ -608,7 +651,8 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
     float* dxs = reinterpret_cast<float*>(xlds + ceil_to((uint64_t)T * nb * 32, 16));
     const float* xs = reinterpret_cast<const float*>(xlds);
     const uint32_t xbytes = (FUSE & kFusePreQuant) ? T * nb * 36 : ((FUSE & kFuseSiluMul) ? 2 : 1) * T * K * 4;
-    const XStage<MODE, NW * 64> xst{make_rsrc(x, xbytes), K, nb, T, MODE == kModeG ? nb * T : nb * 8, xlds, dxs};
+    const XStage<MODE, NW * 64> xst{make_rsrc(x, xbytes), K, nb, T,
+                                    MODE == kModeG ? nb * T : nb * (kBlockValues<MODE> / 4), xlds, dxs};
     const auto ring_start = [&] {
 #pragma unroll
         for (int i = 0; i < S; i++) issue(i);
@@ -630,9 +674,11 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
 #pragma unroll
             for (int t = 0; t < TT; t++) p[t] = 0.0f;
         }
-        if (MODE == kModeG) {
+        if constexpr (MODE == kModeG) {
             if (sbk == (uint32_t)SB) compute_g<SB, TT, true>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
             else compute_g<SB, TT, false>(rowp, l, sbk, s * SB, qxs, dxs, nb, T, p);
+        } else if constexpr (kIsQK<MODE>) {
+            p[0] = compute_qf<typename ModeFmt<MODE>::F>(rowp, l, sbk, s * SB, xs, p[0]);
         } else if (MODE == kModeR4) {
             p[0] = compute_r4(rowp, l, sbk, s * SB, xs, p[0]);
         } else {
@@ -675,6 +721,7 @@ k_q8_0_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* __re
 }
 
 constexpr uint32_t kLdsLimit = 160 * 1024;
+
 constexpr int kMaxStreamTokens = 4;
 
 bool stream_eligible(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const void* W, uint32_t block_bytes = 34) {
@@ -773,7 +820,8 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
         // loads all of it before the ring's copies (one batch of 16)
         constexpr int kSmallNw = Q8SmallCfg::kNw;
         const uint64_t per_pass = MODE == kModeG ? kSmallNw * 64 / 8 : kSmallNw * 64;
-        const uint64_t npass = ((MODE == kModeG ? (uint64_t)nb * T : (uint64_t)nb * 8) + per_pass - 1) / per_pass;
+        const uint64_t npass =
+            ((MODE == kModeG ? (uint64_t)nb * T : (uint64_t)nb * (kBlockValues<MODE> / 4)) + per_pass - 1) / per_pass;
         if (FUSE == 0 && TT == 1 && npass > kXBatch && npass <= 2 * kXBatch)
             r = try_stream<MODE, ANE_Q8_SMALL_CFG, TT, FUSE, 2 * kXBatch>(N, nb, K, T, x, W, y, s, fz);
         else
@@ -1077,7 +1125,41 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     return r;
 }
 
+// A K-quant GEMV on the streaming kernel: NW waves per workgroup, SB
+// super-blocks per item.  -1 when the rows are not 16-byte aligned or a
+// partial segment is not whole 16-byte chunks, so the caller takes k_qgemv.
+template <int MODE, int NW, int SB>
+int qk_stream(uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
+    constexpr uint64_t BB = kBlockBytes<MODE>;
+    const uint32_t nsb = K >> 8;
+    if (nsb == 0 || (((uintptr_t)W) & 15)) return -1;
+    if ((nsb * BB) % 16 || ((nsb % SB) * BB) % 16) return -1;
+    if ((uint64_t)M * nsb * BB >= 0x80000000ull || (uint64_t)K * 4 >= 0x80000000ull) return -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
+    const uint64_t units = ((uint64_t)M + kUnitRows - 1) / kUnitRows;
+    int r = -1;
+    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) r = try_stream<MODE, 4, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    if (r < 0) r = try_stream<MODE, NW, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    if (r < 0) r = try_stream<MODE, 4, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    return r;
+}
+
 }  // namespace
+
+// The K-quant GEMVs on the streaming kernel: fmt 1..4 = Q4_K, Q2_K, Q3_K,
+// Q5_K.  -1 when the shape does not fit it.  Waves per workgroup as
+// measured at 14336x4096; Q6_K (210-byte super-blocks, so 8 per item and
+// 6.9 KB stages) measured slower here than on k_qgemv and stays there.
+int qk_stream_gemv(int fmt, uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
+    switch (fmt) {
+        case 1: return qk_stream<kModeQ4K, 4, 4>(M, K, x, W, y, s);
+        case 2: return qk_stream<kModeQ2K, 4, 4>(M, K, x, W, y, s);
+        case 3: return qk_stream<kModeQ3K, 8, 8>(M, K, x, W, y, s);
+        case 4: return qk_stream<kModeQ5K, 4, 4>(M, K, x, W, y, s);
+    }
+    return -1;
+}
 
 // q4_0_gemv on the streaming kernel (kModeR4) when the rows are 16-byte
 // aligned (K/32 a multiple of 8, W 16-byte aligned); -1 when they are not
