@@ -17,6 +17,8 @@
 // gemm_i8_skinny.hip.
 #include "gemm_i8.hpp"
 
+#include <atomic>
+
 namespace ane {
 
 constexpr int kBM = 128, kBN = 128, kBK = 128;
@@ -161,15 +163,15 @@ k_gemm_i8(GemmParams p) {
 
 // The CU count of the current device (256-tiles are preferred from one per CU).
 static uint64_t tile256_min_tiles() {
-    static int cached[64];
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return (uint64_t)cached[dev];
+    return (uint64_t)n;
 }
 
 template <int BL, bool AU8>

@@ -21,6 +21,10 @@
 #include "common.hpp"
 #include "qformats.hpp"
 
+#include <atomic>
+#include <map>
+#include <mutex>
+
 namespace ane {
 namespace {
 
@@ -736,14 +740,42 @@ uint64_t stream_lds(uint32_t nb, uint32_t T) {
 }
 
 int cu_count(int dev) {
-    static int cached[64];
+    static std::atomic<int> cached[64];
     if (dev < 0 || dev >= 64) return 0;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
+}
+
+// Host state of one streaming-kernel instantiation: its dynamic-LDS limit is
+// raised to kLdsLimit once per device (so launches of any size up to that
+// stay valid whichever thread set it), and its occupancy is cached per
+// (device, LDS size).  A mutex makes both safe for concurrent host threads.
+struct StreamLaunchCache {
+    std::mutex mu;
+    bool attr[64] = {};
+    std::map<uint64_t, int> occ;
+};
+
+// The occupancy of fn at `lds` bytes of dynamic LDS, or a negative status.
+int stream_occupancy(StreamLaunchCache& c, const void* fn, int dev, int threads, uint32_t lds) {
+    std::lock_guard<std::mutex> lock(c.mu);
+    if (!c.attr[dev]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit) != hipSuccess)
+            return ANE_ERR_HIP;
+        c.attr[dev] = true;
+    }
+    const uint64_t key = ((uint64_t)dev << 32) | lds;
+    const auto it = c.occ.find(key);
+    if (it != c.occ.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds) != hipSuccess || occ < 1)
+        return ANE_ERR_HIP;
+    c.occ[key] = occ;
+    return occ;
 }
 
 // Launches one configuration if its LDS fits; returns -1 if it does not.
@@ -755,24 +787,15 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     if (lds64 > kLdsLimit) return -1;
     const uint32_t lds = (uint32_t)lds64;
     auto fn = k_q8_0_stream<MODE, NW, SB, S, TT, FUSE, XB>;
-    static int occ_cache[64];
-    static uint32_t occ_lds[64];
+    static StreamLaunchCache cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
-    if (occ_lds[dev] != lds) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return ANE_ERR_HIP;
-        int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, NW * 64, lds) != hipSuccess || occ < 1)
-            return ANE_ERR_HIP;
-        occ_cache[dev] = occ;
-        occ_lds[dev] = lds;
-    }
+    const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, NW * 64, lds);
+    if (occ < 0) return occ;
     const int cus = cu_count(dev);
     if (cus <= 0) return ANE_ERR_HIP;
     const uint64_t units = ((uint64_t)N + kUnitRows - 1) / kUnitRows;
-    uint64_t grid = (uint64_t)cus * occ_cache[dev];
+    uint64_t grid = (uint64_t)cus * occ;
     const uint64_t need = (units + NW - 1) / NW;
     if (grid > need) grid = need;
     if (grid < 1) grid = 1;
@@ -847,15 +870,11 @@ int gate_up_silu_quant(uint32_t N, uint32_t nb, uint32_t K, const float* x, cons
     const uint64_t lds64 = stream_lds<kModeG, kNw, kSb, kS>(nb, 1);
     if (lds64 > kLdsLimit || (nb + kNw * 8 - 1) / (kNw * 8) > kXBatch) return -1;
     auto fn = k_q8_0_stream<kModeG, kNw, kSb, kS, 1, kFuse>;
-    static uint32_t attr_lds[64];
+    static StreamLaunchCache cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
-    if (attr_lds[dev] < lds64) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds64) != hipSuccess)
-            return ANE_ERR_HIP;
-        attr_lds[dev] = (uint32_t)lds64;
-    }
+    const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, kNw * 64, (uint32_t)lds64);
+    if (occ < 0) return occ;
     hipLaunchKernelGGL(fn, dim3(N / 64), dim3(kNw * 64), (uint32_t)lds64, s, N, nb, K, 1u, x, (const uint8_t*)W,
                        static_cast<float*>(xq), 0u, fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -1075,15 +1094,11 @@ int mma_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* w
     const uint32_t lds = (uint32_t)((ring > exch ? ring : exch) + 1024 * L::kNw);
     if (lds > kLdsLimit) return -1;
     auto fn = k_q8_0_mma<RT, TT, KS, S>;
-    static uint32_t attr_set[64];
+    static StreamLaunchCache cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
-    if (!attr_set[dev]) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess)
-            return ANE_ERR_HIP;
-        attr_set[dev] = 1;
-    }
+    const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, L::kNw * 64, lds);
+    if (occ < 0) return occ;
     const uint32_t rtiles = (N + 15) / 16, ttiles = (T + 15) / 16;
     const uint64_t grid = (uint64_t)((rtiles + RT - 1) / RT) * ((ttiles + TT - 1) / TT);
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(L::kNw * 64), lds, s, N, nb, T, (const uint8_t*)W,

@@ -380,6 +380,49 @@ def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K):
     assert_f32_identical(host(y).reshape(T, N), ref)
 
 
+def test_q8_0_mul_mat_concurrent_host_threads(ane, oracle):
+    """Host threads on their own streams call the same kernel instantiations
+    with different LDS sizes at once (the launch caches are shared): every
+    result stays bit-identical to the oracle."""
+    import threading
+
+    import torch
+
+    N = 520
+    cases = []
+    for i, K in enumerate((1024, 2048, 4096, 8192)):
+        W = data.q8_0_weights(N, K, seed=40 + i)
+        x = data.activations(1, K, seed=50 + i)
+        cases.append((K, W, x, oracle.q8_0_mul_mat_g(N, K, 1, x, W)[0], oracle.q8_0_gemv(N, K, x[0], W)))
+    errors = []
+
+    def worker(K, W, x, ref_g, ref_r):
+        try:
+            st = torch.cuda.Stream()
+            Wd, xd = dev(W), dev(x)
+            yg = torch.zeros(N, dtype=torch.float32, device="cuda")
+            yr = torch.zeros(N, dtype=torch.float32, device="cuda")
+            ws = torch.empty(ane.q8_0_mul_mat_workspace_size(K, 1), dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            for _ in range(25):
+                ane.q8_0_mul_mat(N, K, 1, xd, Wd, yg, workspace=ws, stream=st)
+                ane.q8_0_gemv(N, K, xd[0], Wd, yr, stream=st)
+            st.synchronize()
+            if not np.array_equal(yg.cpu().numpy().view(np.uint32), ref_g.view(np.uint32)):
+                errors.append(f"G K={K}")
+            if not np.array_equal(yr.cpu().numpy().view(np.uint32), ref_r.view(np.uint32)):
+                errors.append(f"R K={K}")
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(f"K={K}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=c) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
 @pytest.mark.parametrize("mode", ["R", "G"])
 def test_q8_0_misaligned_weights(ane, oracle, mode):
     """W starting 2 bytes into an allocation (rows not 16-byte aligned): general kernels."""
