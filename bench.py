@@ -231,6 +231,7 @@ def main() -> int:
         "algorithmic_per_launch": f"2*M*N*K = {int(ops)} int8 ops",
         "avg_launch_us": round(gemm_ms * 1e3, 3),
         "traffic": read_pmc_traffic("gemm_i8_4096_pmc.txt"),
+        "profiles": ["profiles/gemm_i8_tile256_4096_kernel_trace.txt", "profiles/gemm_i8_4096_pmc.txt"],
     }
 
     ceilings = measured_ceilings(args)
@@ -449,7 +450,9 @@ def bench_q8(args, stream) -> dict:
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": head["frac_hbm"],
                      "algorithmic_per_launch": "N*(K/32)*34 + 4K + 4N bytes",
-                     "traffic": read_pmc_traffic("q8_0_matvec_14336x4096_pmc.txt")},
+                     "traffic": read_pmc_traffic("q8_0_matvec_14336x4096_pmc.txt"),
+                     "profiles": ["profiles/q8_0_matvec_14336x4096_g_kernel_trace.txt",
+                                  "profiles/q8_0_matvec_14336x4096_pmc.txt"]},
         "shapes": res,
     }
 
