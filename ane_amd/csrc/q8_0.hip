@@ -14,7 +14,8 @@
 //  * streaming kernels (k_q8_0_stream), R and G mode for up to 4 tokens,
 //    used when every row starts 16-byte aligned (nb % 8 == 0, W 16-byte
 //    aligned), the matrix is under 2 GB and the activations fit in LDS;
-//  * the MFMA kernel (k_q8_0_mma), G mode for 5+ tokens when nb % 16 == 0;
+//  * the MFMA kernels (k_q8_0_mma, k_q8_0_mmt), G mode for 5+ tokens when
+//    nb % 16 == 0;
 //  * general kernels (k_q8_0_gemv_r, k_q8_0_quantize_x + k_q8_0_mul_mat_g)
 //    for everything else.
 #include "../../include/ane_decode.h"
@@ -1107,37 +1108,315 @@ int mma_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* w
     return ANE_OK;
 }
 
+// ====================================================== MFMA mul_mat, token-stationary
+// G mode for 5+ tokens.  The same per-block arithmetic as k_q8_0_mma, with
+// the MFMA operands swapped: A = 16 tokens' quantized activations, B = 16
+// weight rows, so lane (g, c16) receives tokens 4g..4g+3 of a token tile for
+// weight row c16.  A lane then converts its row's fp16 d_w once per block
+// for all the token tiles it covers, and reads the four tokens' fp32 d_x
+// with one 16-byte LDS read (the activation scales are block-major in the
+// workspace: dx[b][t], t < ceil(T, 4)).
+//
+// A workgroup covers RT row tiles x TT token tiles with RT x KS waves; wave
+// (rt, ks) computes row tile rt for every token tile of the workgroup, over
+// the residues ks*16/KS .. (ks+1)*16/KS - 1 of each 16-block stage, so the
+// weights of a stage are read from LDS once per wave and the activations
+// once per row tile.  Each wave folds its residues with the lower levels of
+// the FADDV tree (its residues are a contiguous, aligned quarter/half/...
+// of the 16 leaves); the KS subtotals meet in LDS for the top levels.
+constexpr uint32_t kMmtXRowChunks = kMmaSb * 2 + 1;  // 32 + 1 pad: token rows 4 banks apart
+
+template <int RT, int TT, int KS>
+struct MmtLayout {
+    static constexpr int kNw = RT * KS;
+    static constexpr uint32_t kTok = TT * 16;
+    static constexpr uint32_t kWChunks = RT * 16 * kMmaWRowChunks;
+    static constexpr uint32_t kXChunks = kTok * kMmtXRowChunks;
+    static constexpr uint32_t kDChunks = kMmaSb * kTok / 4;
+    static constexpr uint32_t kWInstr = (kWChunks + 63) / 64, kXInstr = (kXChunks + 63) / 64,
+                              kDInstr = (kDChunks + 63) / 64;
+    static constexpr uint32_t kWSlots = (kWInstr + kNw - 1) / kNw, kXSlots = (kXInstr + kNw - 1) / kNw,
+                              kDSlots = (kDInstr + kNw - 1) / kNw;
+    static constexpr uint32_t kSlots = kWSlots + kXSlots + kDSlots;
+    static constexpr uint32_t kXOff = kWChunks * 16, kDOff = kXOff + kXChunks * 16;
+    static constexpr uint32_t kStageBytes = kDOff + kDChunks * 16;
+};
+
+// Pairwise tree over n adjacent values, in place (a[0] is the result):
+// ((a0+a1)+(a2+a3)) + ... exactly as the FADDV tree's levels.
+template <int n>
+__device__ __forceinline__ float tree_sum(float (&a)[n]) {
+#pragma unroll
+    for (int w = 1; w < n; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < n; i += 2 * w) a[i] = a[i] + a[i + w];
+    return a[0];
+}
+
+template <int RT, int TT, int KS, int S>
+__global__ void __launch_bounds__(RT * KS * 64)
+k_q8_0_mmt(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, const uint8_t* __restrict__ qws,
+           uint32_t dx_off, uint32_t T4, uint32_t n_tgroups, float* __restrict__ y) {
+    using L = MmtLayout<RT, TT, KS>;
+    constexpr int NW = L::kNw;
+    constexpr uint32_t kSbw = kMmaSb / KS;  // residues per wave
+    static_assert(kMmaSb % KS == 0, "KS divides the 16 residues");
+    static_assert((S - 1) * L::kSlots < 64, "copies in flight exceed the vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t* trash = smem + S * L::kStageBytes;  // 1 KB, the target of padding copies
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const uint32_t ks = wave % KS, rt = wave / KS;
+
+    const uint32_t wg_t = blockIdx.x % n_tgroups, wg_r = blockIdx.x / n_tgroups;
+    const uint32_t row_base = wg_r * RT * 16, tok_base = wg_t * L::kTok;
+    const uint32_t rb = nb * 34;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W, N * rb);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(qws, dx_off + nb * T4 * 4);
+    const uint32_t nst = nb / kMmaSb;
+
+    uint32_t ow[L::kWSlots], ox[L::kXSlots], od[L::kDSlots];
+#pragma unroll
+    for (uint32_t q = 0; q < L::kWSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, r = c / kMmaWRowChunks, sub = c - r * kMmaWRowChunks;
+        const uint32_t row = row_base + r;
+        ow[q] = (c < L::kWChunks && sub < kMmaSb * 17 / 8 && row < N) ? row * rb + 16 * sub : 0x80000000u;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < L::kXSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, t = c / kMmtXRowChunks, sub = c - t * kMmtXRowChunks;
+        const uint32_t tok = tok_base + t;
+        ox[q] = (c < L::kXChunks && sub < 2 * kMmaSb && tok < T) ? tok * nb * 32 + 16 * sub : 0x80000000u;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < L::kDSlots; q++) {
+        // chunk c: block c / (kTok/4) of the stage, tokens 4*(c % (kTok/4)) ..
+        const uint32_t c = 64 * (q * NW + wave) + lane, b = c / (L::kTok / 4), t4 = c - b * (L::kTok / 4);
+        const uint32_t tok = tok_base + 4 * t4;
+        od[q] = (c < L::kDChunks && tok < T4) ? dx_off + (b * T4 + tok) * 4 : 0x80000000u;
+    }
+    auto slot = [&](__amdgpu_buffer_rsrc_t r, int8_t* region, uint32_t ninstr, uint32_t nchunks, uint32_t q,
+                    uint32_t src) {
+        const uint32_t i = q * NW + wave;
+        if (i < ninstr) {
+            if (nchunks % 64 == 0 || i + 1 < ninstr || lane < nchunks % 64) copy16_to_lds(r, region + 1024 * i, src);
+        } else {
+            copy16_to_lds(r, trash, 0x80000000u);
+        }
+    };
+    auto issue = [&](uint32_t s) {
+        int8_t* st = smem + (s % S) * L::kStageBytes;
+        const bool on = s < nst;
+#pragma unroll
+        for (uint32_t q = 0; q < L::kWSlots; q++)
+            slot(wr, st, L::kWInstr, L::kWChunks, q,
+                 on && ow[q] != 0x80000000u ? ow[q] + s * (kMmaSb * 34) : 0x80000000u);
+#pragma unroll
+        for (uint32_t q = 0; q < L::kXSlots; q++)
+            slot(xr, st + L::kXOff, L::kXInstr, L::kXChunks, q,
+                 on && ox[q] != 0x80000000u ? ox[q] + s * (kMmaSb * 32) : 0x80000000u);
+#pragma unroll
+        for (uint32_t q = 0; q < L::kDSlots; q++)
+            slot(xr, st + L::kDOff, L::kDInstr, L::kDChunks, q,
+                 on && od[q] != 0x80000000u ? od[q] + s * (kMmaSb * T4 * 4) : 0x80000000u);
+    };
+
+    float p[kSbw][TT][4];
+#pragma unroll
+    for (uint32_t j = 0; j < kSbw; j++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[j][tt][i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S - 1; s++) issue(s);
+    for (uint32_t s = 0; s < nst; s++) {
+        wait_vmcnt<(S - 2) * L::kSlots>();  // this wave's copies of stage s have landed
+        __builtin_amdgcn_s_barrier();       // everyone's have; everyone is done with stage s-1
+        issue(s + S - 1);                    // refills the slot of stage s-1
+        const int8_t* st = smem + (s % S) * L::kStageBytes;
+        const int8_t* wrow = st + (rt * 16 + c16) * (kMmaWRowChunks * 16);      // B: weight row c16
+        const int8_t* xt = st + L::kXOff + c16 * (kMmtXRowChunks * 16) + 8 * g;  // A: token c16 of a tile
+        const float* dd = reinterpret_cast<const float*>(st + L::kDOff) + 4 * g;  // d_x of tokens 4g..4g+3
+#pragma unroll
+        for (uint32_t j = 0; j < kSbw; j++) {
+            const uint32_t bb = ks * kSbw + j;  // block of the stage; b % 16 == bb
+            const uint32_t o = 34 * bb + 2 + 8 * g;
+            const uint32_t* a32 = reinterpret_cast<const uint32_t*>(wrow + (o & ~3u));
+            uint32_t w0, w1;
+            if (bb & 1) {  // 34bb + 2 is 4-byte aligned for odd bb
+                w0 = a32[0];
+                w1 = a32[1];
+            } else {
+                const uint32_t d0 = a32[0], d1 = a32[1], d2 = a32[2];
+                w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                w1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+            }
+            const uint64_t wv = (uint64_t)w0 | ((uint64_t)w1 << 32);
+            const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wrow + 34 * bb));
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+                const uint64_t xv =
+                    *reinterpret_cast<const uint64_t*>(xt + tt * 16 * (kMmtXRowChunks * 16) + 32 * bb);
+                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float4 d4 = *reinterpret_cast<const float4*>(dd + bb * L::kTok + tt * 16);
+                const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
+                    p[j][tt][i] = __builtin_fmaf((float)acc[i], __fmul_rn(dw, dx[i]), p[j][tt][i]);
+            }
+        }
+    }
+    wait_vmcnt<0>();
+    // this wave's subtree of the FADDV tree
+    float v[TT][4];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float a[kSbw];
+#pragma unroll
+            for (uint32_t j = 0; j < kSbw; j++) a[j] = p[j][tt][i];
+            v[tt][i] = tree_sum(a);
+        }
+    const uint32_t row = row_base + rt * 16 + c16;
+    if (KS == 1) {
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = tok_base + tt * 16 + 4 * g + i;
+                if (row < N && t < T) y[(uint64_t)t * N + row] = v[tt][i];
+            }
+    } else {
+        // subtotals [rt][tt][ks][lane] over the ring; the top levels of the
+        // tree for token tile tt are taken by wave (rt, tt % KS)
+        __syncthreads();
+        float4* ex = reinterpret_cast<float4*>(smem);
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+            ex[((rt * TT + tt) * KS + ks) * 64 + lane] = make_float4(v[tt][0], v[tt][1], v[tt][2], v[tt][3]);
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            if ((uint32_t)(tt % KS) != ks) continue;
+            float q[4][KS];
+#pragma unroll
+            for (int k = 0; k < KS; k++) {
+                const float4 e = ex[((rt * TT + tt) * KS + k) * 64 + lane];
+                q[0][k] = e.x;
+                q[1][k] = e.y;
+                q[2][k] = e.z;
+                q[3][k] = e.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float r = tree_sum(q[i]);
+                const uint32_t t = tok_base + tt * 16 + 4 * g + i;
+                if (row < N && t < T) y[(uint64_t)t * N + row] = r;
+            }
+        }
+    }
+}
+
+// Activation quantizer for k_q8_0_mmt: qx [T][nb][32] at xq, the scales
+// block-major dx[b * T4 + t] at xq + dx_off.  The same arithmetic as
+// k_q8_act_quantize (8 lanes per block).
+__global__ void __launch_bounds__(256)
+k_q8_act_quantize_bm(uint32_t nblocks, uint32_t nb, uint32_t K, uint32_t T4, uint32_t dx_off,
+                     const float* __restrict__ x, uint8_t* __restrict__ xq) {
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x, blk = t >> 3, part = t & 7;
+    const uint32_t tok = blk / nb, b = blk - tok * nb;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(x, (nblocks / nb) * K * 4);
+    const uint32_t o = blk < nblocks ? (tok * K + b * 32 + part * 4) * 4 : 0x80000000u;
+    float f[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) f[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4 * e, 0, 0));
+    const uint32_t m = max8_u32(max(max(abs_key(f[0]), abs_key(f[1])), max(abs_key(f[2]), abs_key(f[3]))));
+    float scale, inv;
+    quant_params(__uint_as_float(m), scale, inv);
+    if (blk < nblocks) {
+        reinterpret_cast<uint32_t*>(xq)[blk * 8 + part] = pack4(f[0], f[1], f[2], f[3], inv);
+        if (part == 0) reinterpret_cast<float*>(xq + dx_off)[b * T4 + tok] = scale;
+    }
+}
+
+template <int RT, int TT, int KS, int S>
+int mmt_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* ws, uint32_t dx_off, uint32_t T4,
+               float* y, hipStream_t s) {
+    using L = MmtLayout<RT, TT, KS>;
+    const uint64_t ring = (uint64_t)S * L::kStageBytes;
+    const uint64_t exch = KS > 1 ? (uint64_t)RT * TT * KS * 64 * 16 : 0;
+    const uint32_t lds = (uint32_t)((ring > exch ? ring : exch) + 1024);
+    if (lds > kLdsLimit) return -1;
+    auto fn = k_q8_0_mmt<RT, TT, KS, S>;
+    static StreamLaunchCache cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, L::kNw * 64, lds);
+    if (occ < 0) return occ;
+    const uint32_t rtiles = (N + 15) / 16, tgroups = (T + L::kTok - 1) / L::kTok;
+    const uint64_t grid = (uint64_t)((rtiles + RT - 1) / RT) * tgroups;
+    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(L::kNw * 64), lds, s, N, nb, T, (const uint8_t*)W,
+                       (const uint8_t*)ws, dx_off, T4, tgroups, y);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
 // The MFMA path: rows 16-byte aligned (as the streaming kernels need) and
 // whole 16-block stages.  x is quantized into the workspace first.
+//
+// Kernel choice, measured on the config-4 projections (6144/4096/28672/4096
+// rows, K 4096/14336) at T = 16, 32, 64:
+//  * k_q8_0_mmt (weights read once per 32 or 64 tokens, d_w converted once
+//    per block for all of them) where there is more than one row tile per CU
+//    and more than one token tile: gate_up 28672x4096 at T = 64 takes 64 us
+//    instead of 104, at T = 32 48 instead of 58; qkv at T = 64 25 instead
+//    of 30;
+//  * k_q8_0_mma otherwise (one token tile, or at most one row tile per CU,
+//    where its split-K over residues keeps 16+ waves per CU).
 int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
                 void* workspace, hipStream_t s) {
-    int8_t* qx = (int8_t*)workspace;
-    const uint64_t dx_off = ceil_to((uint64_t)T * nb * 32, 256);
-    float* dx = (float*)((uint8_t*)workspace + dx_off);
-    if (dx_off + (uint64_t)T * nb * 4 >= 0x80000000ull) return -1;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t cus = cu_count(dev);
-    const uint64_t nblocks = (uint64_t)T * nb;
-    // nb % 16 == 0 here, so dx_off == T*nb*32: the Q8 activation form
-    (void)dx;
-    hipLaunchKernelGGL(k_q8_act_quantize, dim3((uint32_t)((nblocks * 8 + 255) / 256)), dim3(256), 0, s,
-                       (uint32_t)nblocks, nb, K, x, reinterpret_cast<uint8_t*>(qx));
-    ANE_HIP_CHECK_LAUNCH();
-    const uint64_t tiles = (uint64_t)((N + 15) / 16) * ((T + 15) / 16);
-    const uint32_t ttiles = (T + 15) / 16;
-    const bool few = tiles < 4 * cus;  // fewer than 4 tiles per CU
+    const uint64_t dx_off = ceil_to((uint64_t)T * nb * 32, 256);
     const uint32_t dxo = (uint32_t)dx_off;
-    int r;
-    // shapes measured on the config-4 projections (6144/4096/28672/4096 rows,
-    // K 4096/14336, T 16 and 64): split-K over residues pays wherever it
-    // keeps a workgroup's LDS small enough for 16+ waves per CU
+    const uint32_t nblocks = T * nb;
+    const uint64_t rtiles = (N + 15) / 16;
+    const uint32_t ttiles = (T + 15) / 16;
+    const uint32_t T4 = (T + 3) & ~3u;
+    // more than one row tile per CU; at two token tiles, at least four
+    const bool mmt = ttiles >= 2 && rtiles > cus && (ttiles > 2 || rtiles >= 4 * cus) &&
+                     dx_off + (uint64_t)nb * T4 * 4 < 0x80000000ull;
+    if (mmt) {
+        // activation scales block-major: dx[b][t] at dx_off
+        hipLaunchKernelGGL(k_q8_act_quantize_bm, dim3((nblocks * 8 + 255) / 256), dim3(256), 0, s, nblocks, nb, K,
+                           T4, dxo, x, static_cast<uint8_t*>(workspace));
+        ANE_HIP_CHECK_LAUNCH();
+        int r;
+        if (ttiles == 2)
+            r = mmt_launch<2, 2, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+        else if (rtiles >= 4 * cus)
+            r = mmt_launch<4, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+        else
+            r = mmt_launch<2, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+        if (r != -1) return r;
+        // not launched: the token-major form below overwrites the workspace
+    }
+    if (dx_off + (uint64_t)T * nb * 4 >= 0x80000000ull) return -1;
+    // nb % 16 == 0 here, so dx_off == T*nb*32: the Q8 activation form
+    hipLaunchKernelGGL(k_q8_act_quantize, dim3((nblocks * 8 + 255) / 256), dim3(256), 0, s, nblocks, nb, K, x,
+                       static_cast<uint8_t*>(workspace));
+    ANE_HIP_CHECK_LAUNCH();
+    const uint64_t tiles = rtiles * ttiles;
+    const bool few = tiles < 4 * cus;  // fewer than 4 tiles per CU
+    // split-K over residues pays wherever it keeps a workgroup's LDS small
+    // enough for 16+ waves per CU
     if (ttiles == 1)
-        r = few ? mma_launch<1, 1, 8, 2>(N, nb, T, W, workspace, dxo, y, s)
-                : mma_launch<2, 1, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
-    else
-        r = mma_launch<1, 2, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
-    return r;
+        return few ? mma_launch<1, 1, 8, 2>(N, nb, T, W, workspace, dxo, y, s)
+                   : mma_launch<2, 1, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
+    return mma_launch<1, 2, 4, 2>(N, nb, T, W, workspace, dxo, y, s);
 }
 
 // A K-quant GEMV on the streaming kernel: NW waves per workgroup, SB
@@ -1269,7 +1548,8 @@ constexpr uint32_t kQ8InlineQuantBlocks = ANE_Q8_INLINE_QUANT_BLOCKS;
 
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {
     const uint64_t nb = K >> 5;
-    return (size_t)(ceil_to((uint64_t)T * nb * 32, 256) + ceil_to((uint64_t)T * nb * 4, 256) + 256);
+    // qx, then the scales: token-major [T][nb] or block-major [nb][ceil(T, 4)]
+    return (size_t)(ceil_to((uint64_t)T * nb * 32, 256) + ceil_to(nb * (((uint64_t)T + 3) & ~3ull) * 4, 256) + 256);
 }
 
 extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,

@@ -344,7 +344,12 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    (300, 512, 5), (17, 4096, 17), (4096, 14336, 16), (2000, 8192, 33),
                                    (64, 1024, 100), (6144, 4096, 64),
                                    # the workgroup shapes for many tiles: 4x1 + split 2, 4x2, 2x3
-                                   (28672, 512, 16), (8192, 1024, 32), (6000, 512, 40)])
+                                   (28672, 512, 16), (8192, 1024, 32), (6000, 512, 40),
+                                   # token-stationary MFMA kernel (more than one row tile per CU):
+                                   # 4 row x 4 token tiles, ragged rows and tokens, two token
+                                   # groups; 2 x 2 tiles; 2 x 4 tiles just past one row tile per CU
+                                   (28672, 512, 64), (16392, 1024, 40), (16384, 512, 100),
+                                   (19990, 512, 20), (4100, 1024, 50)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
@@ -360,14 +365,15 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     assert_f32_identical(host(y).reshape(T, N), ref)
 
 
-@pytest.mark.parametrize("T,K", [(2, 1024), (20, 1024), (1, 9216), (3, 9216)])
-def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K):
+@pytest.mark.parametrize("T,K,N", [(2, 1024, 300), (20, 1024, 300), (1, 9216, 300), (3, 9216, 300),
+                                   (40, 512, 4100)])
+def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K, N):
     """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules
     per block), on the streaming (T = 2, and the separately quantized T = 1
-    and 3 at K = 9216) and MFMA (T = 20) kernels."""
+    and 3 at K = 9216), MFMA (T = 20) and token-stationary MFMA (T = 40 over
+    4100 rows) kernels."""
     import torch
 
-    N = 300
     W = data.q8_0_weights(N, K, seed=11)
     x = data.activations(T, K, seed=12)
     x[0, 0:32] = 0.0
