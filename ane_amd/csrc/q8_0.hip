@@ -896,10 +896,13 @@ int gate_up_silu_quant(uint32_t N, uint32_t nb, uint32_t K, const float* x, cons
 // weight rows (34-byte blocks, rows 35 chunks apart), of the TT*16 tokens'
 // quantized activations (rows 34 chunks apart) and of their fp32 scales,
 // copied global -> LDS with buffer_load_dwordx4 ... lds.  The copy
-// instructions of a stage are dealt round-robin to the waves (a wave with
-// fewer real ones copies zeros into its own trash slot, so every wave
-// issues the same count and the s_waitcnt immediates stay exact); each
-// stage ends with s_waitcnt + s_barrier.
+// instructions of a stage are dealt round-robin to the waves; each stage
+// ends with s_waitcnt + s_barrier.  With more than two stages a wave with
+// fewer real copies issues zero-copies into its own trash slot, so every
+// wave has the same count in flight and the s_waitcnt immediates stay
+// exact; with two stages every wave waits for vmcnt(0) and issues none
+// (the padding was measured at 7-17 % of the config-4 time: the copy
+// instructions' issue, not their bytes, paces these kernels).
 //
 // KS > 1 splits the 16 blocks of a stage among KS waves of the same tile by
 // residue: wave ks computes blocks b with (b % 16) / (16 / KS) == ks, so each
@@ -976,7 +979,7 @@ k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
         const uint32_t i = q * NW + wave;
         if (i < ninstr) {
             if (nchunks % 64 == 0 || i + 1 < ninstr || lane < nchunks % 64) copy16_to_lds(r, region + 1024 * i, src);
-        } else {
+        } else if (S > 2) {  // padding that keeps vmcnt counts uniform
             copy16_to_lds(r, trash + 1024 * wave, 0x80000000u);
         }
     };
@@ -1200,7 +1203,7 @@ k_q8_0_mmt(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
         const uint32_t i = q * NW + wave;
         if (i < ninstr) {
             if (nchunks % 64 == 0 || i + 1 < ninstr || lane < nchunks % 64) copy16_to_lds(r, region + 1024 * i, src);
-        } else {
+        } else if (S > 2) {  // padding that keeps vmcnt counts uniform (none with two stages)
             copy16_to_lds(r, trash, 0x80000000u);
         }
     };
