@@ -61,7 +61,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
     ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings",
-                             "mulmat", "msweep"],
+                             "mulmat", "msweep", "mnist"],
                     default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
@@ -176,6 +176,9 @@ def main() -> int:
     if args.only == "msweep":
         print(json.dumps(bench_m_sweep(args, N, K)), flush=True)
         return 0
+    if args.only == "mnist":
+        print(json.dumps(bench_mnist(args)), flush=True)
+        return 0
     if args.only == "mulmat":
         print(json.dumps(bench_mul_mat(args)), flush=True)
         return 0
@@ -253,6 +256,7 @@ def main() -> int:
         mul_mat = bench_mul_mat(args)
     qformats = bench_qformats(args) if not args.no_q8 else None
     m_sweep = bench_m_sweep(args, N, K) if not args.no_sweep else None
+    mnist = bench_mnist(args) if not args.no_sweep else None
     decode = bench_decode(args) if not args.no_decode else None
 
     # ------------------------------------------------------------ CPU baseline
@@ -282,6 +286,7 @@ def main() -> int:
         "q8_0_mul_mat_config4": mul_mat,
         "other_formats_gemv": qformats,
         "dense_fused_m_sweep": m_sweep,
+        "mnist_mlp_config1": mnist,
         "decode_config5": decode,
         "cpu_baseline": cpu,
     }
@@ -496,6 +501,59 @@ def bench_mul_mat(args) -> dict:
         torch.cuda.empty_cache()
     return {"workload": "config 4: Q8_0 mul_mat G mode, Llama-3-8B projections, T tokens",
             "unit": "us per call", "shapes": res}
+
+
+def bench_mnist(args) -> dict:
+    """Config 1: the MNIST-shaped MLP forward, dense_fused_i8 50x784 -> 128
+    (ReLU, scale 1.0) then 128 -> 10 (no ReLU), on the inputs of
+    tests/data.py mnist_inputs (80 % exact zeros).  Latency-bound: reported
+    as microseconds per forward, through the C entry points in a HIP graph
+    and through stream_exec (the opcode boundary, host encoding included).
+    Bit-exactness against the oracle is the test
+    tests/test_gpu_parity.py::test_dense_fused_mnist_mlp; here the two
+    routes are checked against each other."""
+    import numpy as np
+    import torch
+
+    import ane_amd
+    from tests import data
+
+    x, w1, w2 = data.mnist_inputs(seed=1)
+    dev = torch.device("cuda:0")
+    xd, w1d, w2d = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (x, w1, w2))
+    h = torch.zeros(50 * 128, dtype=torch.float32, device=dev)
+    o = torch.zeros(50 * 10, dtype=torch.float32, device=dev)
+    ws1 = torch.empty(ane_amd.dense_fused_i8_workspace_size(50, 128, 784), dtype=torch.uint8, device=dev)
+    ws2 = torch.empty(ane_amd.dense_fused_i8_workspace_size(50, 10, 128), dtype=torch.uint8, device=dev)
+
+    def fwd(st):
+        ane_amd.dense_fused_i8(50, 128, 784, 1.0, True, xd, w1d, h, workspace=ws1, stream=st)
+        ane_amd.dense_fused_i8(50, 10, 128, 1.0, False, h, w2d, o, workspace=ws2, stream=st)
+
+    graph_us = graph_time(fwd, 50) * 1e3
+    o_graph = o.clone()
+    h2 = torch.zeros_like(h)
+    o2 = torch.zeros_like(o)
+    recs = [ane_amd.rec_dense_fused_i8(50, 128, 784, 1.0, True, xd, w1d, h2),
+            ane_amd.rec_dense_fused_i8(50, 10, 128, 1.0, False, h2, w2d, o2)]
+    for _ in range(10):
+        ane_amd.stream_exec(recs)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(200):
+        t0 = time.perf_counter()
+        ane_amd.stream_exec(recs)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    exec_us = ts[len(ts) // 2] * 1e6
+    same = bool(torch.equal(o_graph.view(torch.int32), o2.view(torch.int32)))
+    ops = 2 * 50 * 784 * 128 + 2 * 50 * 128 * 10
+    log(f"config 1 MLP forward: {graph_us:.2f} us (graph), {exec_us:.1f} us (stream_exec, synchronous)")
+    return {"workload": "config 1: dense_fused_i8 50x784->128 ReLU, 128->10, scale 1.0",
+            "us_graph": round(graph_us, 2), "us_stream_exec_sync": round(exec_us, 1),
+            "ops": ops, "graph_equals_stream_exec": same,
+            "parity": "tests/test_gpu_parity.py::test_dense_fused_mnist_mlp (bit-exact against the oracle)"}
 
 
 def q8_0_random_device(N: int, K: int, gen) -> "torch.Tensor":
