@@ -11,14 +11,17 @@
 //   0x7C get_rows_q8_0  :12363-12408
 //   0x7D get_rows_q4_0  :12419-12469
 //
-// GEMV layout on the GPU: a workgroup of 256 threads takes 16 rows, one per
+// GEMV layout on the GPU: a workgroup of RW*16 threads takes RW rows (16,
+// 8 or 4, so that there are at least two workgroups per CU), one per
 // 16-lane group, lane l of a row carrying the handler's lane l.  A group
 // streams its row in stages of P super-blocks: 16-byte range-checked buffer
-// loads (non-temporal: every weight byte is read once) of the 16-byte-aligned window around the stage (any row alignment,
-// the window never leaves the pointer's 16-byte granule at the front and
-// reads zeros past the matrix's last dword), two stages in flight in registers, each stage
-// written to the group's own LDS window and decoded from there with byte
-// reads.  x is staged in LDS in chunks of 4096 values shared by the 16 rows.
+// loads (non-temporal: every weight byte is read once) of the
+// 16-byte-aligned window around the stage (any row alignment: the window
+// never leaves the pointer's 16-byte granule at the front and reads zeros
+// past the matrix's last dword), two stages in flight in registers, each
+// stage written to the group's own LDS window and decoded from there with
+// byte reads.  x is staged in LDS in chunks of 4096 values shared by the
+// workgroup's rows.
 #include "../../include/ane_hip.h"
 #include "common.hpp"
 #include "qformats.hpp"
@@ -28,7 +31,6 @@ namespace {
 
 using namespace qf;
 
-constexpr uint32_t kRowsPerWg = 16;
 constexpr uint32_t kXChunk = 4096;  // x values staged per pass (16 KB of LDS: five workgroups per CU)
 
 template <class F>
@@ -38,17 +40,18 @@ struct Stage {
     static constexpr uint32_t kWindow = kLoads * 256;
 };
 
-template <class F>
-__global__ void __launch_bounds__(256)
+// RW rows per workgroup (16, 8 or 4: RW 16-lane groups, RW * 16 threads).
+template <class F, int RW>
+__global__ void __launch_bounds__(RW * 16)
 k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const uint8_t* Wa, uint32_t off,
         uint32_t wbytes, float* __restrict__ y) {
     using St = Stage<F>;
     // windows 64 bytes apart beyond their length: the four rows of a wave
     // read their bytes from four different bank groups
-    __shared__ __attribute__((aligned(16))) uint8_t win_all[kRowsPerWg][St::kWindow + 64];
-    __shared__ float xs[kXChunk];
+    __shared__ __attribute__((aligned(16))) uint8_t win_all[RW][St::kWindow + 64];
+    __shared__ __attribute__((aligned(16))) float xs[kXChunk];
     const uint32_t g = threadIdx.x >> 4, l = threadIdx.x & 15;
-    const uint32_t r = blockIdx.x * kRowsPerWg + g;
+    const uint32_t r = blockIdx.x * RW + g;
     const bool live = r < M;
     uint8_t* win = win_all[g];
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(Wa, wbytes);
@@ -82,6 +85,7 @@ k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const
         __builtin_amdgcn_wave_barrier();
     };
 
+    const bool xvec = (K & 3) == 0 && (((uintptr_t)x) & 15) == 0;
     float acc = 0.0f;
     uint4 va[St::kLoads], vb[St::kLoads];
     load(va, 0);
@@ -90,7 +94,13 @@ k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const
         if ((st * F::kStage) % kChunkSb == 0) {  // next x chunk (every group is at the same stage)
             __syncthreads();
             const uint32_t k0 = st * F::kStage * F::kValues;
-            for (uint32_t i = threadIdx.x; i < kXChunk; i += 256) xs[i] = k0 + i < K ? x[k0 + i] : 0.0f;
+            if (xvec) {  // 16-byte loads (x 16-byte aligned, K % 4 == 0)
+                for (uint32_t i = 4 * threadIdx.x; i < kXChunk; i += 4 * RW * 16)
+                    *reinterpret_cast<float4*>(xs + i) = k0 + i < K ? *reinterpret_cast<const float4*>(x + k0 + i)
+                                                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            } else {
+                for (uint32_t i = threadIdx.x; i < kXChunk; i += RW * 16) xs[i] = k0 + i < K ? x[k0 + i] : 0.0f;
+            }
             __syncthreads();
         }
         run(va, st, acc);
@@ -150,8 +160,23 @@ int qgemv_launch(uint32_t M, uint32_t K, const float* x, const void* W, float* y
     // that crosses its end, and the bytes up to the boundary share the last
     // byte's 4-byte granule (so its page)
     const uint32_t range = (uint32_t)((off + (uint64_t)M * nsb * F::kBytes + 3) & ~(uint64_t)3);
-    hipLaunchKernelGGL(k_qgemv<F>, dim3((M + kRowsPerWg - 1) / kRowsPerWg), dim3(256), 0, (hipStream_t)stream, M,
-                       nsb, K, x, reinterpret_cast<const uint8_t*>(wp - off), off, range, y);
+    // 16 rows per workgroup from one workgroup per CU up (4096 rows on 256
+    // CUs: 8 rows per workgroup measured slower there, the x staging then
+    // serving half as many rows), 8 or 4 below that so short matrices still
+    // spread over the CUs
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return ANE_ERR_HIP;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(wp - off);
+    hipStream_t s = (hipStream_t)stream;
+    if (M >= 16u * (uint32_t)cus)
+        hipLaunchKernelGGL((k_qgemv<F, 16>), dim3((M + 15) / 16), dim3(256), 0, s, M, nsb, K, x, base, off, range, y);
+    else if (M >= 8u * (uint32_t)cus)
+        hipLaunchKernelGGL((k_qgemv<F, 8>), dim3((M + 7) / 8), dim3(128), 0, s, M, nsb, K, x, base, off, range, y);
+    else
+        hipLaunchKernelGGL((k_qgemv<F, 4>), dim3((M + 3) / 4), dim3(64), 0, s, M, nsb, K, x, base, off, range, y);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }

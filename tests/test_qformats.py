@@ -45,9 +45,12 @@ def weights_at(W, offset):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M,K", [(300, 4096), (17, 256), (33, 512), (4096, 4096), (5, 16640), (3, 8448)])
+@pytest.mark.parametrize("M,K", [(300, 4096), (17, 256), (33, 512), (4096, 4096), (5, 16640), (3, 8448),
+                                 (2100, 768)])
 def test_q_gemv_exact(ane, oracle, fmt, M, K):
-    """K = 16640 / 8448: inputs in several 4096-value chunks and a partial last stage."""
+    """K = 16640 / 8448: inputs in several 4096-value chunks and a partial last
+    stage.  The general kernel takes 4, 8 or 16 rows per workgroup by the row
+    count (on 256 CUs: 300, 2100 and 4096 rows)."""
     import torch
 
     W = data.q_weights(fmt, M, K, seed=M + K)
