@@ -238,11 +238,12 @@ def main() -> int:
     }
 
     ceilings = measured_ceilings(args)
-    mfma_meas = ceilings["mfma_i8_loop_random"]["TOPS"]
+    mfma_meas = ceilings["mfma_i8_loop_workload"]["TOPS"]
     roofline["measured_peak"] = mfma_meas
     roofline["frac_measured"] = round(gemm_tops / mfma_meas, 4)
-    roofline["measured_peak_how"] = ("int8 MFMA loop with no memory traffic on random operands "
-                                     f"(clock {ceilings['mfma_i8_loop_random']['clock_GHz']} GHz)")
+    roofline["measured_peak_how"] = ("int8 MFMA loop with no memory traffic on operands drawn like the workload's "
+                                     "(N(0,1) quantized by absmax; clock "
+                                     f"{ceilings['mfma_i8_loop_workload']['clock_GHz']} GHz)")
 
     # ------------------------------------------------------------ Q8_0 matvec
     q8 = None
@@ -357,7 +358,10 @@ def measured_ceilings(args) -> dict:
     clocks = torch.zeros(4, dtype=torch.int64, device=dev)
     g = torch.Generator(device=dev)
     g.manual_seed(11)
+    gauss = torch.randn(16384, generator=g, device=dev)
+    gauss = torch.round(gauss * (127.0 / gauss.abs().max())).to(torch.int8)  # the workload's operand distribution
     operands = {"random": torch.randint(-128, 128, (16384,), generator=g, dtype=torch.int8, device=dev),
+                "workload": gauss,
                 "constant": torch.ones(16384, dtype=torch.int8, device=dev)}
     ops = wgs * (threads // 64) * iters * 8 * 65536
     for kind, data in operands.items():
