@@ -839,6 +839,16 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t units = ((uint64_t)N + kUnitRows - 1) / kUnitRows;
     int r = -1;
+    if constexpr (MODE == kModeR && FUSE == 0 && TT == 1) {
+        // R mode keeps x as fp32 in LDS (16 KB at K = 4096), so its workgroup
+        // shapes differ (measured, 14336/4096 rows x 4096/14336): 16 waves of
+        // 16-block stages for many rows (20.4 -> 18.9 us), 2 waves of 32-block
+        // stages for few (10.2 -> 9.6 us, 27.1 -> 26.3 us)
+        const bool few = units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU;
+        r = few ? try_stream<MODE, 2, 32, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz)
+                : try_stream<MODE, 16, 16, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+        if (r >= 0) return r;
+    }
     if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) {
         // a plain single-token product whose activation needs 9-16 passes
         // loads all of it before the ring's copies (one batch of 16)
