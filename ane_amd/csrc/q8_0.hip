@@ -1381,13 +1381,14 @@ int mmt_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* w
 //
 // Kernel choice, measured on the config-4 projections (6144/4096/28672/4096
 // rows, K 4096/14336) at T = 16, 32, 64:
-//  * k_q8_0_mmt (weights read once per 32 or 64 tokens, d_w converted once
-//    per block for all of them) where there is more than one row tile per CU
-//    and more than one token tile: gate_up 28672x4096 at T = 64 takes 64 us
-//    instead of 104, at T = 32 48 instead of 58; qkv at T = 64 25 instead
-//    of 30;
-//  * k_q8_0_mma otherwise (one token tile, or at most one row tile per CU,
-//    where its split-K over residues keeps 16+ waves per CU).
+//  * k_q8_0_mmt (d_w converted once per block for all of a wave's token
+//    tiles) from four row tiles per CU up at any token count (gate_up
+//    28672x4096: T = 64 104 -> 64 us on 4x4 tiles, T = 32 58 -> 48 us and
+//    T = 16 35.9 -> 34.1 us on 2-row-tile workgroups), and from more than one
+//    row tile per CU at 3+ token tiles (qkv T = 64: 30 -> 21.7 us, two token
+//    groups of 2x2 tiles);
+//  * k_q8_0_mma otherwise (at most one row tile per CU, where its split-K
+//    over residues keeps 16+ waves per CU).
 int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
                 void* workspace, hipStream_t s) {
     int dev = 0;
@@ -1399,21 +1400,20 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     const uint64_t rtiles = (N + 15) / 16;
     const uint32_t ttiles = (T + 15) / 16;
     const uint32_t T4 = (T + 3) & ~3u;
-    // more than one row tile per CU; at two token tiles, at least four
-    const bool mmt = ttiles >= 2 && rtiles > cus && (ttiles > 2 || rtiles >= 4 * cus) &&
-                     dx_off + (uint64_t)nb * T4 * 4 < 0x80000000ull;
+    const bool many = rtiles >= 4 * cus;
+    const bool mmt = (many || (ttiles > 2 && rtiles > cus)) && dx_off + (uint64_t)nb * T4 * 4 < 0x80000000ull;
     if (mmt) {
         // activation scales block-major: dx[b][t] at dx_off
         hipLaunchKernelGGL(k_q8_act_quantize_bm, dim3((nblocks * 8 + 255) / 256), dim3(256), 0, s, nblocks, nb, K,
                            T4, dxo, x, static_cast<uint8_t*>(workspace));
         ANE_HIP_CHECK_LAUNCH();
         int r;
-        if (ttiles == 2)
+        if (ttiles == 1)
+            r = mmt_launch<2, 1, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+        else if (ttiles == 2 || !many)
             r = mmt_launch<2, 2, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
-        else if (rtiles >= 4 * cus)
-            r = mmt_launch<4, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
         else
-            r = mmt_launch<2, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+            r = mmt_launch<4, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
         if (r != -1) return r;
         // not launched: the token-major form below overwrites the workspace
     }

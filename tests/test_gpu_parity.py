@@ -343,11 +343,12 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # several stages, T past 64
                                    (300, 512, 5), (17, 4096, 17), (4096, 14336, 16), (2000, 8192, 33),
                                    (64, 1024, 100), (6144, 4096, 64),
-                                   # the workgroup shapes for many tiles: 4x1 + split 2, 4x2, 2x3
+                                   # the workgroup shapes for many tiles: 2 row tiles of one token
+                                   # tile on the token-stationary kernel, 1x2 + split 4, 1x2
                                    (28672, 512, 16), (8192, 1024, 32), (6000, 512, 40),
-                                   # token-stationary MFMA kernel (more than one row tile per CU):
-                                   # 4 row x 4 token tiles, ragged rows and tokens, two token
-                                   # groups; 2 x 2 tiles; 2 x 4 tiles just past one row tile per CU
+                                   # token-stationary MFMA kernel: 4 row x 4 token tiles (ragged
+                                   # rows and tokens, two token groups); 2 x 2 tiles at two token
+                                   # tiles, and at three or four just past one row tile per CU
                                    (28672, 512, 64), (16392, 1024, 40), (16384, 512, 100),
                                    (19990, 512, 20), (4100, 1024, 50)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
