@@ -849,6 +849,16 @@ int stream_auto(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
                 : try_stream<MODE, 16, 16, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
         if (r >= 0) return r;
     }
+    if constexpr (MODE == kModeG && TT == kMaxStreamTokens && FUSE == kFusePreQuant) {
+        // 2-4 pre-quantized tokens over many rows: 16-block stages leave
+        // room for two workgroups per CU beside the activations (gate_up
+        // 28672x4096 at T = 4: 31.3 -> 29.6 us; fewer rows measured best on
+        // the shapes below)
+        if (units >= (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) {
+            r = try_stream<MODE, 8, 16, 2, TT, FUSE>(N, nb, K, T, x, W, y, s, fz);
+            if (r >= 0) return r;
+        }
+    }
     if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) {
         // a plain single-token product whose activation needs 9-16 passes
         // loads all of it before the ring's copies (one batch of 16)
