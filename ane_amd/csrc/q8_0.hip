@@ -1443,37 +1443,42 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
 }
 
 // A K-quant GEMV on the streaming kernel: NW waves per workgroup, SB
-// super-blocks per item.  -1 when the rows are not 16-byte aligned or a
-// partial segment is not whole 16-byte chunks, so the caller takes k_qgemv.
-template <int MODE, int NW, int SB>
+// super-blocks per item, SBF per item for matrices with few rows (4-wave
+// workgroups).  -1 when the rows are not 16-byte aligned or a partial
+// segment is not whole 16-byte chunks, so the caller takes k_qgemv.
+template <int MODE, int NW, int SB, int SBF = SB>
 int qk_stream(uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
     constexpr uint64_t BB = kBlockBytes<MODE>;
     const uint32_t nsb = K >> 8;
     if (nsb == 0 || (((uintptr_t)W) & 15)) return -1;
-    if ((nsb * BB) % 16 || ((nsb % SB) * BB) % 16) return -1;
+    if ((nsb * BB) % 16) return -1;
     if ((uint64_t)M * nsb * BB >= 0x80000000ull || (uint64_t)K * 4 >= 0x80000000ull) return -1;
+    const bool seg_ok = ((nsb % SB) * BB) % 16 == 0, segf_ok = ((nsb % SBF) * BB) % 16 == 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t units = ((uint64_t)M + kUnitRows - 1) / kUnitRows;
     int r = -1;
-    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU) r = try_stream<MODE, 4, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
-    if (r < 0) r = try_stream<MODE, NW, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
-    if (r < 0) r = try_stream<MODE, 4, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    if (units < (uint64_t)cu_count(dev) * ANE_Q8_SMALL_UNITS_PER_CU && segf_ok)
+        r = try_stream<MODE, 4, SBF, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    if (r < 0 && seg_ok) r = try_stream<MODE, NW, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
+    if (r < 0 && seg_ok) r = try_stream<MODE, 4, SB, 2, 1>(M, nsb, K, 1, x, W, y, s);
     return r;
 }
 
 }  // namespace
 
 // The K-quant GEMVs on the streaming kernel: fmt 1..4 = Q4_K, Q2_K, Q3_K,
-// Q5_K.  -1 when the shape does not fit it.  Waves per workgroup as
-// measured at 14336x4096; Q6_K (210-byte super-blocks, so 8 per item and
+// Q5_K.  -1 when the shape does not fit it.  Shapes as measured at
+// 14336x4096 and 4096x14336 (8 super-blocks per item for 4096 rows: Q4_K
+// 41.2 -> 38.9 us, Q5_K 46.0 -> 41.7; and for Q2_K at any size: 18.2 ->
+// 16.6, 27.7 -> 23.9); Q6_K (210-byte super-blocks, so 8 per item and
 // 6.9 KB stages) measured slower here than on k_qgemv and stays there.
 int qk_stream_gemv(int fmt, uint32_t M, uint32_t K, const float* x, const void* W, float* y, hipStream_t s) {
     switch (fmt) {
-        case 1: return qk_stream<kModeQ4K, 4, 4>(M, K, x, W, y, s);
-        case 2: return qk_stream<kModeQ2K, 4, 4>(M, K, x, W, y, s);
+        case 1: return qk_stream<kModeQ4K, 4, 4, 8>(M, K, x, W, y, s);
+        case 2: return qk_stream<kModeQ2K, 8, 8, 8>(M, K, x, W, y, s);
         case 3: return qk_stream<kModeQ3K, 8, 8>(M, K, x, W, y, s);
-        case 4: return qk_stream<kModeQ5K, 4, 4>(M, K, x, W, y, s);
+        case 4: return qk_stream<kModeQ5K, 4, 4, 8>(M, K, x, W, y, s);
     }
     return -1;
 }
