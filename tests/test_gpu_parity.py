@@ -387,6 +387,43 @@ def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K, N):
     assert_f32_identical(host(y).reshape(T, N), ref)
 
 
+@pytest.mark.parametrize("mode,N,K,T", [("R", 300, 1024, 1), ("G", 300, 1024, 1), ("G", 300, 1024, 2),
+                                        ("G", 300, 9216, 3), ("G", 300, 1024, 20), ("G", 4100, 1024, 40),
+                                        ("G", 16384, 512, 16)])
+def test_q8_0_special_weight_scales(ane, oracle, mode, N, K, T):
+    """Weight block scales of every fp16 class (infinities, NaN, subnormals,
+    signed zeros, the largest finite), with all-zero blocks among them so
+    0 * inf reaches the fma, on the R matvec, the G streaming kernel (T = 1,
+    2, and 3 on separately quantized activations), the MFMA kernel (T = 20)
+    and the token-stationary MFMA kernel (2 x 2 and 2 x 1 tile shapes)."""
+    import torch
+
+    nb = K // 32
+    W = data.q8_0_weights(N, K, seed=31).reshape(N, nb, 34).copy()
+    specials = np.array([0x7C00, 0xFC00, 0x7E00, 0x0001, 0x83FF, 0x8000, 0x0000, 0x7BFF, 0xBC00],
+                        dtype=np.uint16)
+    rng = np.random.default_rng(32)
+    d = rng.choice(specials, size=(N, nb))
+    d[rng.random((N, nb)) < 0.97] = 0x2E66  # leave most blocks ordinary
+    W[:, :, 0:2] = d.view(np.uint8).reshape(N, nb, 2)
+    W[rng.random((N, nb)) < 0.05, 2:] = 0  # isum 0 against an infinite scale gives NaN
+    W = W.reshape(N, -1)
+    x = data.activations(T, K, seed=33)
+    if mode == "R":
+        ref = oracle.q8_0_gemv(N, K, x[0], W)
+        y = zeros(N, torch.float32)
+        ane.q8_0_gemv(N, K, dev(x[0]), dev(W), y)
+        assert_f32_identical(host(y), ref)
+    else:
+        ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
+        y = zeros(T * N, torch.float32)
+        ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
+        assert_f32_identical(host(y).reshape(T, N), ref)
+    # the cases reach NaN, finite and (G: one isum per block) infinite outputs;
+    # an R-mode infinite block mixes both signs across its lanes, giving NaN
+    assert np.isnan(ref).any() and np.isfinite(ref).any() and (mode == "R" or np.isinf(ref).any())
+
+
 def test_q8_0_mul_mat_concurrent_host_threads(ane, oracle):
     """Host threads on their own streams call the same kernel instantiations
     with different LDS sizes at once (the launch caches are shared): every
