@@ -100,6 +100,35 @@ def test_q4_0_special_scales(ane, oracle):
     assert_same(host(y), oracle.q_gemv("q4_0", M, K, x, W))
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q2_k", "q3_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("offset", [0, 2])
+def test_k_quant_special_scales(ane, oracle, fmt, offset):
+    """Super-block d and dmin of every fp16 class (infinities, NaN,
+    subnormals, signed zeros, the largest finite), on the streaming kernel
+    (aligned rows) and on k_qgemv (rows 2 bytes off)."""
+    import torch
+
+    M, K = 64, 4096
+    sbb, _, fp16_at = data.Q_BLOCK[fmt]
+    W = data.q_weights(fmt, M, K, seed=41).reshape(M, K // 256, sbb).copy()
+    specials = np.array([0x7C00, 0xFC00, 0x7E00, 0x0001, 0x83FF, 0x8000, 0x0000, 0x7BFF, 0xBC00],
+                        dtype=np.uint16)
+    rng = np.random.default_rng(42)
+    for pos in fp16_at:
+        d = W[:, :, pos:pos + 2].copy().view(np.uint16)[..., 0]
+        pick = rng.random(d.shape) < 0.1
+        d[pick] = rng.choice(specials, size=int(pick.sum()))
+        W[:, :, pos:pos + 2] = d.view(np.uint8).reshape(M, K // 256, 2)
+    W = W.reshape(M, -1)
+    x = data.activations(1, K, seed=43)[0]
+    buf, Wd = weights_at(W, offset)
+    y = torch.zeros(M, dtype=torch.float32, device="cuda")
+    ane.q_gemv(fmt, M, K, dev(x), Wd, y)
+    ref = oracle.q_gemv(fmt, M, K, x, W)
+    assert_same(host(y), ref)
+    assert np.isnan(ref).any() and np.isfinite(ref).any()
+
+
 @pytest.mark.parametrize("first", ["zero", "denormal", "special"])
 def test_q3_k_first_half_inputs(ane, oracle, first):
     """The second halves' decode depends on the first halves' input bits."""
