@@ -283,6 +283,37 @@ def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
+@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny"])
+@pytest.mark.parametrize("M,N,K", [(129, 257, 1000), (256, 512, 2048)])
+def test_dense_fused_special_operands(ane, oracle, case, M, N, K):
+    """The fused max|x| and quantize passes on operands the quantizer
+    special-cases: a NaN or an infinity (NaN or infinite per-tensor scale),
+    an all-zero tensor (the zero guard) and a tensor of denormals and signed
+    zeros only."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M + K)
+    if case == "a_nan":
+        A[M // 2, K // 3] = np.nan
+    elif case == "b_inf":
+        B[K - 1, N // 2] = np.inf
+    elif case == "a_neg_inf":
+        A[0, 0] = -np.inf
+    elif case == "a_zero":
+        A[:] = 0.0
+    else:
+        B[:] = np.where(np.arange(K * N).reshape(K, N) % 3 == 0, -0.0, F32(1e-40))
+        B[1, 2] = F32(-3e-39)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    finally:
+        oracle.set_threads(1)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
 def test_dense_fused_4096_cubed_sampled(ane, oracle):
     """Config 2 at full size: both per-tensor scales exact, and a sample of
     rows of C identical to the oracle's contraction of the oracle-quantized
