@@ -455,6 +455,29 @@ def test_q8_0_special_weight_scales(ane, oracle, mode, N, K, T):
     assert np.isnan(ref).any() and np.isfinite(ref).any() and (mode == "R" or np.isinf(ref).any())
 
 
+def test_q8_0_degenerate_shapes(ane, oracle):
+    """No rows or no tokens leave y untouched; K < 32 (nb = K >> 5 = 0 blocks)
+    writes the empty sum, as the oracle does."""
+    import torch
+
+    x = data.activations(3, 64, seed=51)
+    W = data.q8_0_weights(7, 64, seed=52)
+    y = torch.full((21,), 7.0, dtype=torch.float32, device="cuda")
+    ane.q8_0_gemv(0, 64, dev(x[0]), dev(W), y)
+    ane.q8_0_mul_mat(0, 64, 3, dev(x), dev(W), y)
+    ane.q8_0_mul_mat(7, 64, 0, dev(x), dev(W), y)
+    assert (host(y) == 7.0).all()
+    for K in (0, 20):
+        xs = data.activations(3, K, seed=53)
+        Wk = np.zeros((7, 0), np.uint8)
+        ane.q8_0_gemv(7, K, dev(xs[0]), dev(Wk), y)
+        assert_f32_identical(host(y)[:7], oracle.q8_0_gemv(7, K, xs[0], Wk))
+        y.fill_(7.0)
+        ane.q8_0_mul_mat(7, K, 3, dev(xs), dev(Wk), y)
+        assert_f32_identical(host(y).reshape(3, 7), oracle.q8_0_mul_mat_g(7, K, 3, xs, Wk))
+        y.fill_(7.0)
+
+
 def test_q8_0_mul_mat_concurrent_host_threads(ane, oracle):
     """Host threads on their own streams call the same kernel instantiations
     with different LDS sizes at once (the launch caches are shared): every
