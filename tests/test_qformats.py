@@ -129,6 +129,24 @@ def test_k_quant_special_scales(ane, oracle, fmt, offset):
     assert np.isnan(ref).any() and np.isfinite(ref).any()
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_q_gemv_degenerate_shapes(ane, oracle, fmt):
+    """No rows leave y untouched; K below one block (the handlers' K >> 5 or
+    K >> 8 is 0) writes the empty sum, as the oracle does."""
+    import torch
+
+    y = torch.full((9,), 7.0, dtype=torch.float32, device="cuda")
+    x = data.activations(1, 512, seed=61)[0]
+    ane.q_gemv(fmt, 0, 512, dev(x), dev(data.q_weights(fmt, 2, 512, seed=62)), y)
+    assert (host(y) == 7.0).all()
+    for K in (0, 20):
+        xk = data.activations(1, K, seed=63)[0]
+        Wk = np.zeros((9, 0), np.uint8)
+        ane.q_gemv(fmt, 9, K, dev(xk), dev(Wk), y)
+        assert_same(host(y), oracle.q_gemv(fmt, 9, K, xk, Wk))
+        y.fill_(7.0)
+
+
 @pytest.mark.parametrize("first", ["zero", "denormal", "special"])
 def test_q3_k_first_half_inputs(ane, oracle, first):
     """The second halves' decode depends on the first halves' input bits."""
