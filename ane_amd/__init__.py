@@ -275,45 +275,103 @@ def encode(op: int, *args: _Arg) -> Record:
     return rec
 
 
+def _ceil(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def _need(t: Any, nbytes: int, what: str) -> None:
+    """Raise AneError(ANE_ERR_BUFFER_TOO_SMALL) if tensor ``t`` holds fewer
+    than ``nbytes`` bytes from its first element to the end of its storage.
+
+    stream_exec checks every operand against its HIP allocation, but torch's
+    caching allocator carves tensors out of larger allocations, so a short
+    tensor would pass that check and the kernel would touch its neighbours.
+    Raw integer addresses are left to stream_exec's check."""
+    if nbytes <= 0 or not hasattr(t, "untyped_storage"):
+        return
+    have = t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
+    if have < nbytes:
+        raise AneError(3, f"{what} needs {nbytes} bytes, the tensor holds {have}")
+
+
 # Typed records with the reference's argument order (Appendix of the opcode
 # table: bytecode_interpreter.s parse sites cited in ane_amd/csrc/stream_exec.cpp).
+# Tensor operands are checked against the extents the opcode reads and writes.
 def rec_dense_i8(M, N, K, sa, sb, relu, A, Bp, bias, C, unsigned_a=False) -> bytes:
     op = Op.dense_u8s8 if unsigned_a else Op.dense_i8
+    if N:
+        Mp, Kp = max(16, _ceil(M, 16)), _ceil(K, 64)
+        _need(A, Mp * Kp, "dense A")
+        _need(Bp, _ceil(N, 16) // 16 * (Kp // 4) * 64, "dense B_packed")
+        _need(bias, 4 * N, "dense bias")
+        _need(C, 4 * Mp * N, "dense C")
     return encode(op, u32(M), u32(N), u32(K), f32(sa), f32(sb), boolean(relu), ptr(A), ptr(Bp),
                   ptr(bias), ptr(C))
 
 
 def rec_quantize(count, src, dst, scale_out) -> bytes:
+    n = max(16, _ceil(count, 16))
+    _need(src, 4 * n, "quantize_fp32_i8 src")
+    _need(dst, n, "quantize_fp32_i8 dst")
+    _need(scale_out, 4, "quantize_fp32_i8 scale_out")
     return encode(Op.quantize_fp32_i8, u32(count), ptr(src), ptr(dst), ptr(scale_out))
 
 
 def rec_dequantize(count, scale, src, dst) -> bytes:
+    n = _ceil(count, 16)
+    _need(src, n, "dequantize_i8_fp32 src")
+    _need(dst, 4 * n, "dequantize_i8_fp32 dst")
     return encode(Op.dequantize_i8_fp32, u32(count), f32(scale), ptr(src), ptr(dst))
 
 
 def rec_pack_b(K, N, src, dst) -> bytes:
+    _need(src, K * N, "pack_b_i8 src")
+    _need(dst, _ceil(N, 16) // 16 * (_ceil(K, 4) // 4) * 64, "pack_b_i8 dst")
     return encode(Op.pack_b_i8, u32(K), u32(N), ptr(src), ptr(dst))
 
 
 def rec_channelwise(rows, cols, src, dst, scales) -> bytes:
+    if rows:
+        cpad = max(16, _ceil(cols, 16))
+        _need(src, 4 * rows * cpad, "channelwise src")
+        _need(dst, rows * cpad, "channelwise dst")
+        _need(scales, 4 * rows, "channelwise scales")
     return encode(Op.quantize_fp32_i8_channelwise, u32(rows), u32(cols), ptr(src), ptr(dst), ptr(scales))
 
 
 def rec_q8_0_gemv(M, K, x, W, y) -> bytes:
+    if M:
+        nb = K >> 5
+        _need(x, 4 * 32 * nb, "q8_0_gemv x")
+        _need(W, M * nb * 34, "q8_0_gemv W")
+        _need(y, 4 * M, "q8_0_gemv y")
     return encode(Op.q8_0_gemv, u32(M), u32(K), ptr(x), ptr(W), ptr(y))
 
 
 def rec_q_gemv(fmt, M, K, x, W, y) -> bytes:
     """Record of one of the QFORMATS GEMVs (same layout as q8_0_gemv)."""
+    if M:
+        bb, vals = QFORMATS[fmt]
+        nsb = K // vals
+        _need(x, 4 * vals * nsb, f"{fmt}_gemv x")
+        _need(W, M * nsb * bb, f"{fmt}_gemv W")
+        _need(y, 4 * M, f"{fmt}_gemv y")
     return encode(Op[f"{fmt}_gemv"], u32(M), u32(K), ptr(x), ptr(W), ptr(y))
 
 
 def rec_get_rows(fmt, n_rows, dim, table, indices, out) -> bytes:
     """get_rows_q8_0 / get_rows_q4_0 record: [n_rows:u32][dim:u32][table][indices][out]."""
+    if n_rows and dim >= 32:
+        _need(indices, 4 * n_rows, f"get_rows_{fmt} indices")
+        _need(out, 4 * n_rows * (dim >> 5) * 32, f"get_rows_{fmt} out")
     return encode(Op[f"get_rows_{fmt}"], u32(n_rows), u32(dim), ptr(table), ptr(indices), ptr(out))
 
 
 def rec_dense_fused_i8(M, N, K, scale, relu, A, B, C) -> bytes:
+    if M > 0 and N > 0:
+        _need(A, 4 * M * K, "dense_fused_i8 A")
+        _need(B, 4 * K * N, "dense_fused_i8 B")
+        _need(C, 4 * M * N, "dense_fused_i8 C")
     return encode(Op.dense_fused_i8, i32(M), i32(N), i32(K), f32(scale), boolean(relu), ptr(A), ptr(B),
                   ptr(C))
 
@@ -360,24 +418,39 @@ def _p(t: Any) -> int:
     return int(t.data_ptr()) if hasattr(t, "data_ptr") else int(t)
 
 
-# Kernel-level wrappers (device tensors, current torch stream unless given).
-def quantize_fp32_i8(src, dst, scale_out, count=None, pad16=True, workspace=None, stream=None):
+def _scratch(nbytes: int, device, stream: Any = None, zero: bool = False):
+    """A temporary device workspace for a call launched on ``stream``.
+
+    It is allocated on that stream (torch's caching allocator keys blocks by
+    the stream they were allocated on), so when the tensor is dropped right
+    after the asynchronous call the block is only reused by work ordered
+    after the kernels on that same stream."""
     import torch
 
+    if stream is None:
+        s = torch.cuda.current_stream(device)
+    elif isinstance(stream, torch.cuda.Stream):
+        s = stream
+    else:
+        s = torch.cuda.ExternalStream(_stream_handle(stream), device=device)
+    with torch.cuda.stream(s):
+        return (torch.zeros if zero else torch.empty)(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# Kernel-level wrappers (device tensors, current torch stream unless given).
+def quantize_fp32_i8(src, dst, scale_out, count=None, pad16=True, workspace=None, stream=None):
     n = src.numel() if count is None else count
     L = lib()
     wsb = L.ane_hip_quantize_workspace_size(n)
-    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=src.device)
+    ws = workspace if workspace is not None else _scratch(wsb, src.device, stream)
     check(L.ane_hip_quantize_fp32_i8(n, 1 if pad16 else 0, _p(src), _p(dst), _p(scale_out), _p(ws), wsb,
                                      _stream_handle(stream)), "quantize_fp32_i8")
 
 
 def dense_fused_i8(M, N, K, scale, relu, A, B, C, scales_out=None, workspace=None, stream=None):
-    import torch
-
     L = lib()
     wsb = L.ane_hip_dense_fused_i8_workspace_size(M, N, K)
-    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=A.device)
+    ws = workspace if workspace is not None else _scratch(wsb, A.device, stream)
     check(L.ane_hip_dense_fused_i8(M, N, K, scale, 1 if relu else 0, _p(A), _p(B), _p(C), _p(scales_out),
                                    _p(ws), wsb, _stream_handle(stream)), "dense_fused_i8")
 
@@ -428,11 +501,9 @@ def q8_0_mul_mat_workspace_size(K, T) -> int:
 
 
 def q8_0_mul_mat(N, K, T, x, W, y, workspace=None, stream=None):
-    import torch
-
     L = lib()
     wsb = L.ane_hip_q8_0_mul_mat_workspace_size(K, T)
-    ws = workspace if workspace is not None else torch.empty(wsb, dtype=torch.uint8, device=W.device)
+    ws = workspace if workspace is not None else _scratch(wsb, W.device, stream)
     check(L.ane_hip_q8_0_mul_mat(N, K, T, _p(x), _p(W), _p(y), _p(ws), wsb, _stream_handle(stream)),
           "q8_0_mul_mat")
 
@@ -578,11 +649,9 @@ def rope_kv_append(cfg, qkv, table, pos, k_cache, v_cache, stream=None):
 
 
 def attention_decode(cfg, q, k_cache, v_cache, length, out, workspace=None, stream=None):
-    import torch
-
     L = lib()
     wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
-    ws = workspace if workspace is not None else torch.zeros(wsb, dtype=torch.uint8, device=q.device)
+    ws = workspace if workspace is not None else _scratch(wsb, q.device, stream, zero=True)
     check(L.ane_hip_attention_decode(ctypes.byref(cfg), _p(q), _p(k_cache), _p(v_cache), length, _p(out), _p(ws),
                                      wsb, _stream_handle(stream)), "attention_decode")
 
@@ -593,11 +662,9 @@ def q8_0_matvec_silu(N, K, gu, W, y, residual=None, stream=None):
 
 
 def attention_decode_rope(cfg, qkv, table, pos, k_cache, v_cache, out, workspace=None, stream=None, out_q8=None):
-    import torch
-
     L = lib()
     wsb = L.ane_hip_attention_workspace_size(ctypes.byref(cfg))
-    ws = workspace if workspace is not None else torch.zeros(wsb, dtype=torch.uint8, device=qkv.device)
+    ws = workspace if workspace is not None else _scratch(wsb, qkv.device, stream, zero=True)
     check(L.ane_hip_attention_decode_rope(ctypes.byref(cfg), _p(qkv), _p(table), pos, _p(k_cache), _p(v_cache),
                                           _p(out), _p(out_q8), _p(ws), wsb, _stream_handle(stream)),
           "attention_decode_rope")

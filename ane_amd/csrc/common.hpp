@@ -190,6 +190,13 @@ __device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcn
 
 }  // namespace ane
 
+namespace ane {
+// Set (on the calling host thread) while ane_decode_token checks that every
+// step of a layer can launch: the launch helpers then make all their checks
+// and return ANE_OK just before launching anything.
+extern thread_local bool t_plan_only;
+}  // namespace ane
+
 #define ANE_HIP_CHECK_LAUNCH()                                   \
     do {                                                         \
         hipError_t e__ = hipGetLastError();                      \

@@ -360,8 +360,8 @@ k_silu_mul_quant(uint32_t nb, const float* __restrict__ gu, uint8_t* __restrict_
 
 bool cfg_ok(const ane_decode_config* c) {
     return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
-           c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->ctx <= (1u << 20) && c->hidden % 32 == 0 &&
-           c->ffn % 32 == 0 &&
+           c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->ctx <= (1u << 20) && c->hidden % 256 == 0 &&
+           c->ffn % 256 == 0 &&
            (uint64_t)c->n_heads * kHD % 32 == 0;
 }
 
@@ -391,6 +391,7 @@ int attention_launch(const ane_decode_config* cfg, bool rope, const float* q, co
     if (out_q8 && (((uintptr_t)out_q8) & 15)) return ANE_ERR_INVALID_ARG;
     if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < attn_layout(cfg, nullptr, nullptr))
         return ANE_ERR_WORKSPACE;
+    if (t_plan_only) return ANE_OK;
     AttnWs w;
     attn_layout(cfg, workspace, &w);
     const uint32_t nch = n_chunks(len);
@@ -513,8 +514,7 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
     const uint32_t H = cfg->hidden, F = cfg->ffn;
     const uint32_t nq = cfg->n_heads * kHD;
     const uint32_t nqkv = (cfg->n_heads + 2 * cfg->n_kv_heads) * kHD;
-    for (uint32_t l = 0; l < cfg->n_layers; l++) {
-        const ane_decode_layer& L = layers[l];
+    auto run_layer = [&](const ane_decode_layer& L) -> int {
         int st;
         if ((st = ane_hip_q8_0_matvec_fused(nqkv, H, x, L.attn_norm, cfg->eps, L.w_qkv, nullptr, w.qkv, stream)))
             return st;
@@ -524,7 +524,30 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
         if ((st = ane_hip_q8_0_matvec_q8(H, nq, w.attn_q8, L.w_o, x, x, stream))) return st;
         if ((st = ane_hip_q8_0_gate_up_silu_quant(F, H, x, L.ffn_norm, cfg->eps, L.w_gate_up, w.h_q8, stream)))
             return st;
-        if ((st = ane_hip_q8_0_matvec_q8(H, F, w.h_q8, L.w_down, x, x, stream))) return st;
+        return ane_hip_q8_0_matvec_q8(H, F, w.h_q8, L.w_down, x, x, stream);
+    };
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
+        const ane_decode_layer& L = layers[l];
+        if (!L.w_qkv || !L.w_o || !L.w_gate_up || !L.w_down || !L.attn_norm || !L.ffn_norm || !L.k_cache ||
+            !L.v_cache)
+            return ANE_ERR_BAD_POINTER;
+        // the streaming products take 16-byte aligned weights
+        if (((uintptr_t)L.w_qkv | (uintptr_t)L.w_o | (uintptr_t)L.w_gate_up | (uintptr_t)L.w_down) & 15)
+            return ANE_ERR_INVALID_ARG;
+    }
+    // Every step's preconditions (shapes, alignment, LDS fit, rows per wave)
+    // are checked on layer 0 before anything is launched (the layers share
+    // their shapes), so a configuration that cannot run fails with x and
+    // the KV caches untouched.
+    if (cfg->n_layers > 0) {
+        t_plan_only = true;
+        const int st = run_layer(layers[0]);
+        t_plan_only = false;
+        if (st) return st;
+    }
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
+        const int st = run_layer(layers[l]);
+        if (st) return st;
     }
     return ANE_OK;
 }

@@ -27,6 +27,9 @@
 #include <mutex>
 
 namespace ane {
+
+thread_local bool t_plan_only = false;
+
 namespace {
 
 // ====================================================== general kernels
@@ -804,6 +807,7 @@ int try_stream(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, 
     if ((FUSE & kFuseResidual) && ((uint64_t)N + grid * NW - 1) / (grid * NW) > 64) return -1;
     // the norm fusion holds all of x in registers until the sum of squares is known
     if ((FUSE & kFuseNorm) && (nb + NW * 8 - 1) / (NW * 8) > XB) return -1;
+    if (t_plan_only) return ANE_OK;
     hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(NW * 64), lds, s, N, nb, K, T, x,
                        (const uint8_t*)W, y, (uint32_t)(grid * NW), fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -896,6 +900,7 @@ int gate_up_silu_quant(uint32_t N, uint32_t nb, uint32_t K, const float* x, cons
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
     const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, kNw * 64, (uint32_t)lds64);
     if (occ < 0) return occ;
+    if (t_plan_only) return ANE_OK;
     hipLaunchKernelGGL(fn, dim3(N / 64), dim3(kNw * 64), (uint32_t)lds64, s, N, nb, K, 1u, x, (const uint8_t*)W,
                        static_cast<float*>(xq), 0u, fz);
     ANE_HIP_CHECK_LAUNCH();
@@ -1626,3 +1631,4 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
+

@@ -45,6 +45,7 @@ template <class F, int RW>
 __global__ void __launch_bounds__(RW * 16)
 k_qgemv(uint32_t M, uint32_t nsb, uint32_t K, const float* __restrict__ x, const uint8_t* Wa, uint32_t off,
         uint32_t wbytes, float* __restrict__ y) {
+    // K here is nsb * values: the x staging below never reads past it
     using St = Stage<F>;
     // windows 64 bytes apart beyond their length: the four rows of a wave
     // read their bytes from four different bank groups
@@ -171,12 +172,15 @@ int qgemv_launch(uint32_t M, uint32_t K, const float* x, const void* W, float* y
         return ANE_ERR_HIP;
     const uint8_t* base = reinterpret_cast<const uint8_t*>(wp - off);
     hipStream_t s = (hipStream_t)stream;
+    // x is staged only up to the values the super-blocks consume: a
+    // remainder of K past them is never read (the caller's x may end there)
+    const uint32_t kx = nsb * F::kValues;
     if (M >= 16u * (uint32_t)cus)
-        hipLaunchKernelGGL((k_qgemv<F, 16>), dim3((M + 15) / 16), dim3(256), 0, s, M, nsb, K, x, base, off, range, y);
+        hipLaunchKernelGGL((k_qgemv<F, 16>), dim3((M + 15) / 16), dim3(256), 0, s, M, nsb, kx, x, base, off, range, y);
     else if (M >= 8u * (uint32_t)cus)
-        hipLaunchKernelGGL((k_qgemv<F, 8>), dim3((M + 7) / 8), dim3(128), 0, s, M, nsb, K, x, base, off, range, y);
+        hipLaunchKernelGGL((k_qgemv<F, 8>), dim3((M + 7) / 8), dim3(128), 0, s, M, nsb, kx, x, base, off, range, y);
     else
-        hipLaunchKernelGGL((k_qgemv<F, 4>), dim3((M + 3) / 4), dim3(64), 0, s, M, nsb, K, x, base, off, range, y);
+        hipLaunchKernelGGL((k_qgemv<F, 4>), dim3((M + 3) / 4), dim3(64), 0, s, M, nsb, kx, x, base, off, range, y);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }

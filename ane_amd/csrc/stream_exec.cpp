@@ -47,37 +47,51 @@ int fail(int status, const char* fmt, ...) {
 
 // ---------------------------------------------------------------- workspace
 // One grow-only device buffer per (device, stream).  Work on one stream is
-// ordered, so reusing its buffer between records is safe; growing it waits
-// for the stream first.  Freed at process exit.
+// ordered, so reusing its buffer between records is safe.  A record holds
+// the buffer's lock (a Lease) from the moment it takes the pointer until its
+// kernels are enqueued: another host thread on the same stream that needs a
+// bigger buffer waits for that, then synchronises the stream (so the
+// enqueued kernels have finished) before it frees the old buffer.  Freed at
+// process exit.
 struct Workspace {
+    std::mutex mu;
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace>* g_ws = nullptr;
 
-int get_workspace(hipStream_t s, size_t bytes, void** out) {
+struct Lease {
+    std::unique_lock<std::mutex> lock;
+    void* ptr = nullptr;
+};
+
+int get_workspace(hipStream_t s, size_t bytes, Lease& lease) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(ANE_ERR_HIP, "hipGetDevice failed");
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    if (!g_ws) g_ws = new std::map<std::pair<int, hipStream_t>, Workspace>();
-    Workspace& w = (*g_ws)[{dev, s}];
-    if (w.bytes < bytes) {
-        if (w.ptr) {
+    Workspace* w = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        if (!g_ws) g_ws = new std::map<std::pair<int, hipStream_t>, Workspace>();
+        w = &(*g_ws)[{dev, s}];  // map nodes never move
+    }
+    lease.lock = std::unique_lock<std::mutex>(w->mu);
+    if (w->bytes < bytes) {
+        if (w->ptr) {
             if (hipStreamSynchronize(s) != hipSuccess) return fail(ANE_ERR_HIP, "stream sync failed");
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
+            (void)hipFree(w->ptr);
+            w->ptr = nullptr;
+            w->bytes = 0;
         }
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-        if (hipMalloc(&w.ptr, want) != hipSuccess) {
+        if (hipMalloc(&w->ptr, want) != hipSuccess) {
             (void)hipGetLastError();
-            w.ptr = nullptr;
+            w->ptr = nullptr;
             return fail(ANE_ERR_HIP, "workspace hipMalloc(%zu) failed", want);
         }
-        w.bytes = want;
+        w->bytes = want;
     }
-    *out = w.ptr;
+    lease.ptr = w->ptr;
     return ANE_OK;
 }
 
@@ -181,8 +195,9 @@ int op_quantize(Reader& r, hipStream_t s) {
     CHECK(check_range(dst, n, "quantize_fp32_i8 dst", false, nullptr));
     CHECK(check_range(scale_out, 4, "quantize_fp32_i8 scale_out", true, &w));
     const size_t wsb = ane_hip_quantize_workspace_size(n) + 256;
-    void* ws = nullptr;
-    CHECK(get_workspace(s, wsb, &ws));
+    Lease lease;
+    CHECK(get_workspace(s, wsb, lease));
+    void* ws = lease.ptr;
     float* dev_scale = w == Where::kHost ? (float*)ws : scale_out;
     void* part = (uint8_t*)ws + 256;
     CHECK(hip_status(ane_hip_quantize_fp32_i8(count, 1, src, dst, dev_scale, part, wsb - 256, s),
@@ -232,10 +247,10 @@ int op_channelwise(Reader& r, hipStream_t s) {
     CHECK(check_range(dst, (uint64_t)rows * cpad, "channelwise dst", false, nullptr));
     CHECK(check_range(scales, (uint64_t)rows * 4, "channelwise scales", true, &w));
     float* dev_scales = scales;
+    Lease lease;
     if (w == Where::kHost) {
-        void* ws = nullptr;
-        CHECK(get_workspace(s, (size_t)rows * 4, &ws));
-        dev_scales = (float*)ws;
+        CHECK(get_workspace(s, (size_t)rows * 4, lease));
+        dev_scales = (float*)lease.ptr;
     }
     CHECK(hip_status(ane_hip_quantize_channelwise(rows, cols, src, dst, dev_scales, s),
                      "quantize_fp32_i8_channelwise"));
@@ -307,9 +322,9 @@ int op_dense_fused(Reader& r, hipStream_t s) {
     CHECK(check_range(B, (uint64_t)K * N * 4, "dense_fused_i8 B", false, nullptr));
     CHECK(check_range(C, (uint64_t)M * N * 4, "dense_fused_i8 C", false, nullptr));
     const size_t wsb = ane_hip_dense_fused_i8_workspace_size(M, N, K);
-    void* ws = nullptr;
-    CHECK(get_workspace(s, wsb, &ws));
-    return hip_status(ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, ws, wsb, s),
+    Lease lease;
+    CHECK(get_workspace(s, wsb, lease));
+    return hip_status(ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, lease.ptr, wsb, s),
                       "dense_fused_i8");
 }
 

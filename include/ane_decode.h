@@ -45,8 +45,8 @@ extern "C" {
 
 struct ane_decode_config {
     uint32_t n_layers;
-    uint32_t hidden;      /* model width (4096)                 */
-    uint32_t ffn;         /* feed-forward width (14336)         */
+    uint32_t hidden;      /* model width (4096; a multiple of 256)         */
+    uint32_t ffn;         /* feed-forward width (14336; a multiple of 256) */
     uint32_t n_heads;     /* query heads (32)                   */
     uint32_t n_kv_heads;  /* key/value heads (8)                */
     uint32_t head_dim;    /* 128 (the only supported value)     */
@@ -71,6 +71,9 @@ size_t ane_decode_workspace_size(const struct ane_decode_config* cfg);
 /* One token at position pos (< ctx) through every layer: x (fp32 [hidden],
  * the residual stream) is updated in place, and k/v of pos are written into
  * each layer's cache; positions 0..pos of the caches are attended to.
+ * Every step's preconditions are checked before the first launch (weights
+ * 16-byte aligned, the products' LDS and rows-per-wave limits), so an error
+ * return leaves x and the caches untouched.
  * Asynchronous on stream; returns an ane_status. */
 int ane_decode_token(const struct ane_decode_config* cfg, const struct ane_decode_layer* layers,
                      const float* rope_table, uint32_t pos, float* x, void* workspace,

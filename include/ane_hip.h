@@ -11,6 +11,11 @@
  *     (hipMalloc / hipMallocManaged / hipHostMalloc); the call is synchronous
  *     like the reference's, and failures are reported through
  *     ane_last_error() because the reference signature returns void.
+ *     Each operand's extent is checked against the HIP allocation that holds
+ *     it.  That is per allocation, not per tensor: a caching allocator (such
+ *     as torch's) carves many tensors out of one allocation, and a short
+ *     tensor inside it passes the check (the Python records check tensor
+ *     extents themselves before encoding).
  *
  *  2. The kernel-level ABI (ane_hip_*): device pointers, an explicit HIP
  *     stream (hipStream_t passed as void*, 0 = the null stream), an int

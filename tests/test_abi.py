@@ -130,3 +130,23 @@ def test_decoder_null_operand():
 def test_empty_stream_is_ok():
     st, _ = _run_async(b"")
     assert st == 0
+
+
+def test_records_refuse_short_tensors():
+    """A tensor shorter than the extent its opcode touches is refused while
+    encoding (the caching allocator's segments would hide it from the
+    per-allocation check inside stream_exec)."""
+    import torch
+
+    src = torch.zeros(100, dtype=torch.float32)
+    with pytest.raises(ane_amd.AneError) as e:
+        ane_amd.rec_quantize(100, src, torch.zeros(112, dtype=torch.int8), torch.zeros(1))  # pads to 112
+    assert e.value.status == 3
+    big = torch.zeros(4096, dtype=torch.float32)
+    view = big[4000:]  # 96 floats from its first element to the storage end
+    with pytest.raises(ane_amd.AneError):
+        ane_amd.rec_dense_fused_i8(4, 4, 32, 1.0, True, view, big, big[:16])  # A needs 128 floats
+    rec = ane_amd.rec_dense_fused_i8(4, 4, 8, 1.0, True, big[:32], big, big[:16])
+    assert len(rec) == 42
+    with pytest.raises(ane_amd.AneError):
+        ane_amd.rec_q8_0_gemv(3, 64, big, torch.zeros(3 * 2 * 34 - 1, dtype=torch.uint8), big)

@@ -341,6 +341,83 @@ def test_dense_fused_4096_cubed_sampled(ane, oracle):
     assert (Ch >= 0).all()
 
 
+def test_dense_fused_4096_cubed_all_rows(ane, oracle):
+    """Config 2's headline shape, every row of C: the GPU's 4096 x 4096
+    output is bit-identical to the oracle's quantize + contraction +
+    epilogue (the oracle runs multi-threaded over rows)."""
+    import torch
+
+    M = N = K = 4096
+    A, B = data.gemm_inputs(M, N, K, seed=2)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    Ch = host(C).reshape(M, N)
+    oracle.set_threads(0)
+    try:
+        qA, sa = oracle.quantize_exact(A.ravel())
+        qB, sb = oracle.quantize_exact(B.ravel())
+        st = F32(F32(sa * sb) * F32(1.0))
+        for r0 in range(0, M, 512):
+            rows = oracle.dense_fused_rows(r0, r0 + 512, N, K, st, True, qA, qB)
+            assert_f32_identical(Ch[r0: r0 + 512], rows)
+    finally:
+        oracle.set_threads(1)
+
+
+@pytest.mark.parametrize("M", [1, 16, 128, 1024])
+def test_dense_fused_config2_m_sweep_shapes(ane, oracle, M):
+    """Config 2's M sweep at its exact shapes (N = K = 4096), every output."""
+    import torch
+
+    N = K = 4096
+    A, B = data.gemm_inputs(M, N, K, seed=2 + M)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    finally:
+        oracle.set_threads(1)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
+def test_stream_exec_workspace_two_threads_one_stream(ane, oracle):
+    """Two host threads share the null stream (and so stream_exec's workspace
+    for it) and alternate small and large dense_fused_i8 records, so the
+    workspace grows while the other thread's records use it."""
+    import threading
+
+    import torch
+
+    shapes = [(64, 64, 256), (384, 512, 1024), (32, 100, 64), (512, 256, 2048)]
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        A, B = data.gemm_inputs(M, N, K, seed=70 + i)
+        cases.append((M, N, K, dev(A), dev(B), oracle.dense_fused_i8(M, N, K, F32(1.0), i % 2 == 0, A, B)))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(order):
+        try:
+            for it in range(6):
+                for i in order:
+                    M, N, K, A, B, ref = cases[i]
+                    C = torch.full((M * N,), 9.0, dtype=torch.float32, device="cuda")
+                    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, i % 2 == 0, A, B, C), stream=0)
+                    got = C.cpu().numpy().reshape(M, N)
+                    if not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
+                        errors.append(f"case {i} iteration {it}")
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(o,)) for o in ([0, 1, 2, 3], [3, 2, 1, 0])]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
 # ---------------------------------------------------------------- Q8_0
 @pytest.mark.parametrize("M,K", [(1, 32), (3, 40), (4096, 4096), (14336, 4096), (4096, 14336), (77, 96),
                                  # streaming kernel: partial last segment, ragged row split, K % 32 != 0
@@ -387,6 +464,30 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
 
     W = data.q8_0_weights(N, K - K % 32, seed=N + K)
     x = data.activations(T, K, seed=T + 100)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
+    finally:
+        oracle.set_threads(1)
+    y = zeros(T * N, torch.float32)
+    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
+    assert_f32_identical(host(y).reshape(T, N), ref)
+
+
+# config 4: the four Llama-3-8B projections (rows x K) at every token count
+CONFIG4 = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64])
+@pytest.mark.parametrize("proj", list(CONFIG4))
+def test_q8_0_mul_mat_config4_shapes(ane, oracle, proj, T):
+    """Config 4 at its exact shapes: every (projection, tokens) pair, every
+    output bit-identical to the oracle's G-mode definition."""
+    import torch
+
+    N, K = CONFIG4[proj]
+    W = data.q8_0_weights(N, K, seed=N + K + 1)
+    x = data.activations(T, K, seed=T + 200)
     oracle.set_threads(0)
     try:
         ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)

@@ -255,3 +255,30 @@ def test_get_rows_out_of_table(ane, oracle, fmt):
         assert e.value.status == 1
     finally:
         hip.hipFree(p)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,K", [(37, 300), (300, 33), (4096, 520), (5, 4200)])
+def test_q_gemv_k_remainder_exact_x(ane, oracle, fmt, M, K):
+    """K with a remainder the handlers ignore (K >> 5, K >> 8): x lives in an
+    allocation of exactly the values the blocks consume, and the record
+    passes stream_exec's extent check, so no kernel may stage x past it."""
+    import torch
+
+    vals = ane.QFORMATS[fmt][1]
+    nsb = K // vals
+    if nsb == 0:
+        pytest.skip("no whole block")
+    W = data.q_weights(fmt, M, K, seed=M + 7 * K)
+    x = data.activations(1, K, seed=K + 1)[0]
+    hip = _hip()
+    p = ctypes.c_void_p()
+    nbytes = nsb * vals * 4
+    assert hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nbytes)) == 0
+    try:
+        assert hip.hipMemcpy(p, x.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(nbytes), 1) == 0
+        y = torch.full((M,), 3.0, dtype=torch.float32, device="cuda")
+        ane.stream_exec(ane.rec_q_gemv(fmt, M, K, p.value, dev(W), y))
+        assert_same(host(y), oracle.q_gemv(fmt, M, K, x, W))
+    finally:
+        hip.hipFree(p)
