@@ -103,6 +103,8 @@ EXPORTS = (
     "ane_hip_get_rows_q4_0",
     "ane_hip_q8_0_mul_mat_workspace_size",
     "ane_hip_q8_0_mul_mat",
+    "ane_hip_q8_0_mul_mat_noalloc_max_bytes",
+    "ane_hip_q8_0_mul_mat_noalloc",
     "ane_hip_device_check",
     "ane_hip_version",
     # include/ggml-ane-hip.h
@@ -172,6 +174,8 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         _c.c_int,
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _c.c_size_t, _P],
     ),
+    "ane_hip_q8_0_mul_mat_noalloc_max_bytes": (_c.c_size_t, []),
+    "ane_hip_q8_0_mul_mat_noalloc": (_c.c_int, [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _P, _P, _P]),
     "ane_hip_device_check": (_c.c_int, []),
     "ane_hip_version": (_c.c_char_p, []),
     "ane_ggml_backend_name": (_c.c_char_p, []),
@@ -506,6 +510,13 @@ def q8_0_mul_mat(N, K, T, x, W, y, workspace=None, stream=None):
     ws = workspace if workspace is not None else _scratch(wsb, W.device, stream)
     check(L.ane_hip_q8_0_mul_mat(N, K, T, _p(x), _p(W), _p(y), _p(ws), wsb, _stream_handle(stream)),
           "q8_0_mul_mat")
+
+
+def q8_0_mul_mat_noalloc(N, K, T, x, W, y, stream=None):
+    """q8_0_mul_mat with its workspace in the library's static device array
+    (no allocation; calls overlapping on one device race)."""
+    check(lib().ane_hip_q8_0_mul_mat_noalloc(N, K, T, _p(x), _p(W), _p(y), _stream_handle(stream)),
+          "q8_0_mul_mat_noalloc")
 
 
 def pack_b_i8(K, N, src, dst, stream=None):

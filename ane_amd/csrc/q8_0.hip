@@ -1632,3 +1632,49 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
     return ANE_OK;
 }
 
+// ------------------------------------------- the no-allocation mul_mat
+// ane_hip_q8_0_mul_mat_noalloc: the same product with its workspace (the
+// quantized activations) in a file-scope device array instead of a caller
+// buffer.  Each device holds its own copy of the array until the process
+// ends; its address is looked up once per device (with that device
+// current) and only that address is ever handed to kernels.  Every call on
+// a device shares the array, so calls that overlap on one device race.  No
+// byte of it needs to start at zero: every call writes the activations it
+// reads (the padding entries past T feed only token columns that are never
+// stored).
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+int scratch_ptr(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return ANE_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return ANE_OK;
+}
+}  // namespace
+
+extern "C" size_t ane_hip_q8_0_mul_mat_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int ane_hip_q8_0_mul_mat_noalloc(uint32_t N, uint32_t K, uint32_t T, const float* x, const void* W,
+                                            float* y, void* stream) {
+    if (N == 0 || T == 0) return ANE_OK;
+    const size_t need = ane_hip_q8_0_mul_mat_workspace_size(K, T);
+    if (need > kNoAllocScratchBytes) return ANE_ERR_WORKSPACE;
+    void* ws = nullptr;
+    const int st = scratch_ptr(&ws);
+    if (st != ANE_OK) return st;
+    return ane_hip_q8_0_mul_mat(N, K, T, x, W, y, ws, kNoAllocScratchBytes, stream);
+}

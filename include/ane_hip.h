@@ -173,6 +173,20 @@ int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,
                          const void* W, float* y, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ane_hip_q8_0_mul_mat without a workspace argument and without allocating:
+ * the quantized activations live in a static device array of
+ * ane_hip_q8_0_mul_mat_noalloc_max_bytes() bytes (4 MiB; one per device,
+ * held until the process ends).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Shapes whose
+ * ane_hip_q8_0_mul_mat_workspace_size(K, T) exceeds that size return
+ * ANE_ERR_WORKSPACE.  All calls on one device share the array: calls that
+ * overlap on one device (two streams, two threads) race.  Results are
+ * bit-identical to ane_hip_q8_0_mul_mat. */
+size_t ane_hip_q8_0_mul_mat_noalloc_max_bytes(void);
+int ane_hip_q8_0_mul_mat_noalloc(uint32_t N, uint32_t K, uint32_t T, const float* x,
+                                 const void* W, float* y, void* stream);
+
 /* The other weight formats, "R mode" like 0x57: fp32 x, y[m] = FADDV16 of
  * the handler's 16 fma lanes, bit-identical to the reference's arithmetic.
  * W: M rows of K/values blocks, any alignment; a remainder of K is ignored
