@@ -37,6 +37,9 @@ class Op(enum.IntEnum):
     dense_u8s8 = 0x1E
     q8_0_gemv = 0x57
     q4_0_gemv = 0x58
+    cblas_igemm = 0x61
+    cblas_ugemm = 0x62
+    cblas_usgemm = 0x63
     q4_k_gemv = 0x75
     q2_k_gemv = 0x76
     q3_k_gemv = 0x77
@@ -93,6 +96,8 @@ EXPORTS = (
     "ane_hip_dense_fused_i8_gemm",
     "ane_hip_gemm_s8_i32",
     "ane_hip_q8_0_gemv",
+    "ane_hip_cblas_igemm_workspace_size",
+    "ane_hip_cblas_igemm",
     "ane_hip_q4_0_gemv",
     "ane_hip_q4_k_gemv",
     "ane_hip_q2_k_gemv",
@@ -166,6 +171,12 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _c.c_uint32, _P, _c.c_uint32, _P, _P],
     ),
     "ane_hip_q8_0_gemv": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]),
+    "ane_hip_cblas_igemm_workspace_size": (_c.c_size_t, [_c.c_uint32, _c.c_uint32, _c.c_uint32]),
+    "ane_hip_cblas_igemm": (
+        _c.c_int,
+        [_c.c_int, _c.c_int, _c.c_uint8, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32,
+         _c.c_uint32, _c.c_float, _c.c_float, _P, _P, _P, _P, _c.c_size_t, _P],
+    ),
     **{f"ane_hip_{f}_gemv": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P]) for f in QFORMATS},
     "ane_hip_get_rows_q8_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
     "ane_hip_get_rows_q4_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
@@ -371,6 +382,39 @@ def rec_get_rows(fmt, n_rows, dim, table, indices, out) -> bytes:
     return encode(Op[f"get_rows_{fmt}"], u32(n_rows), u32(dim), ptr(table), ptr(indices), ptr(out))
 
 
+IGEMM_VARIANTS = {"igemm": 0, "ugemm": 1, "usgemm": 2}
+
+
+def _igemm_extents(flags, M, N, K, lda, ldb, ldc):
+    """Bytes of A, B and C the integer GEMM handler's arithmetic touches."""
+    Ke = K // 64 * 64
+    a = b = 0
+    if Ke and M and N:
+        if flags & 1:
+            g = (M - 1) - (M - 1) % 16
+            mx = ((M - 1) % 16) * lda + g
+            if M > 16:
+                mx = max(mx, 15 * lda + g - 16)
+            a = mx + Ke
+        else:
+            a = (M - 1) * lda + Ke
+        b = (N - 1) * ldb + Ke if flags & 2 else (Ke - 1) * ldb + N
+    c = 4 * ((M - 1) * ldc + N) if M and N else 0
+    return a, b, c
+
+
+def rec_cblas_igemm(kind, flags, M, N, K, lda, ldb, ldc, alpha, beta, A, B, C) -> bytes:
+    """cblas_igemm / cblas_ugemm / cblas_usgemm (kind "igemm", "ugemm",
+    "usgemm"): [op][flags:u8][M N K lda ldb ldc:u32][alpha beta:f32][A][B][C]
+    (bytecode_interpreter.s:8355-8369)."""
+    a, b, c = _igemm_extents(flags, M, N, K, lda, ldb, ldc)
+    _need(A, a, f"cblas_{kind} A")
+    _need(B, b, f"cblas_{kind} B")
+    _need(C, c, f"cblas_{kind} C")
+    return encode(Op.cblas_igemm + IGEMM_VARIANTS[kind], u8(flags), u32(M), u32(N), u32(K), u32(lda), u32(ldb),
+                  u32(ldc), f32(alpha), f32(beta), ptr(A), ptr(B), ptr(C))
+
+
 def rec_dense_fused_i8(M, N, K, scale, relu, A, B, C) -> bytes:
     if M > 0 and N > 0:
         _need(A, 4 * M * K, "dense_fused_i8 A")
@@ -478,6 +522,17 @@ def dense_fused_i8_workspace_size(M, N, K) -> int:
 def gemm_s8_i32(A, Bt, acc, M, N, K, lda=None, ldb=None, stream=None):
     check(lib().ane_hip_gemm_s8_i32(M, N, K, _p(A), lda or K, _p(Bt), ldb or K, _p(acc),
                                     _stream_handle(stream)), "gemm_s8_i32")
+
+
+def cblas_igemm(kind, flags, M, N, K, lda, ldb, ldc, alpha, beta, A, B, C, blas=False, workspace=None,
+                stream=None):
+    """The integer GEMMs on the kernel-level ABI; blas=False reproduces the
+    handler (what stream_exec runs), blas=True the BLAS form."""
+    L = lib()
+    wsb = L.ane_hip_cblas_igemm_workspace_size(M, N, K)
+    ws = workspace if workspace is not None else _scratch(wsb, C.device, stream)
+    check(L.ane_hip_cblas_igemm(IGEMM_VARIANTS[kind], 1 if blas else 0, flags, M, N, K, lda, ldb, ldc, alpha, beta,
+                                _p(A), _p(B), _p(C), _p(ws), wsb, _stream_handle(stream)), f"cblas_{kind}")
 
 
 def q8_0_gemv(M, K, x, W, y, stream=None):

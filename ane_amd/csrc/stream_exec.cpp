@@ -20,6 +20,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <vector>
 #include <map>
@@ -328,6 +329,54 @@ int op_dense_fused(Reader& r, hipStream_t s) {
                       "dense_fused_i8");
 }
 
+// 0x61 / 0x62 / 0x63 [flags:u8][M][N][K][lda][ldb][ldc:u32][alpha:f32][beta:f32][A][B][C]
+// (bytecode_interpreter.s:8355-8369).  The extents checked are exactly the
+// bytes the handler's arithmetic uses: A and B only over the K/64 whole
+// blocks, C over rows < M and columns < N (read too when beta's bits are
+// nonzero).
+int op_cblas_igemm(Reader& r, hipStream_t s, int variant) {
+    static const char* const kName[3] = {"cblas_igemm", "cblas_ugemm", "cblas_usgemm"};
+    const char* nm = kName[variant];
+    const uint8_t flags = r.get<uint8_t>();
+    const uint32_t M = r.get<uint32_t>();
+    const uint32_t N = r.get<uint32_t>();
+    const uint32_t K = r.get<uint32_t>();
+    const uint32_t lda = r.get<uint32_t>();
+    const uint32_t ldb = r.get<uint32_t>();
+    const uint32_t ldc = r.get<uint32_t>();
+    const float alpha = r.get<float>();
+    const float beta = r.get<float>();
+    const void* A = r.ptr<const void>();
+    const void* B = r.ptr<const void>();
+    float* C = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "%s record truncated", nm);
+    if (M == 0 || N == 0) return ANE_OK;
+    if (ldc < N) return fail(ANE_ERR_INVALID_ARG, "%s: ldc %u < N %u (overlapping output rows)", nm, ldc, N);
+    if ((uintptr_t)C & 3) return fail(ANE_ERR_INVALID_ARG, "%s: C must be 4-byte aligned", nm);
+    const uint64_t Ke = (uint64_t)(K / 64) * 64;
+    if (Ke) {
+        uint64_t a_ext;
+        if (!(flags & 1)) {
+            a_ext = (uint64_t)(M - 1) * lda + Ke;
+        } else {  // row i reads from (i%16)*lda + (i - i%16)
+            const uint64_t g = (uint64_t)(M - 1) - (M - 1) % 16;
+            uint64_t mx = (uint64_t)((M - 1) % 16) * lda + g;
+            if (M > 16) mx = std::max(mx, (uint64_t)15 * lda + g - 16);
+            a_ext = mx + Ke;
+        }
+        const uint64_t b_ext = (flags & 2) ? (uint64_t)(N - 1) * ldb + Ke : (Ke - 1) * ldb + N;
+        CHECK(check_range(A, a_ext, nm, false, nullptr));
+        CHECK(check_range(B, b_ext, nm, false, nullptr));
+    }
+    CHECK(check_range(C, ((uint64_t)(M - 1) * ldc + N) * 4, nm, false, nullptr));
+    const size_t wsb = ane_hip_cblas_igemm_workspace_size(M, N, K);
+    Lease lease;
+    CHECK(get_workspace(s, wsb, lease));
+    return hip_status(ane_hip_cblas_igemm(variant, ANE_IGEMM_REFERENCE, flags, M, N, K, lda, ldb, ldc, alpha, beta,
+                                          A, B, C, lease.ptr, wsb, s),
+                      nm);
+}
+
 // 0x58, 0x75-0x79 [M:u32][K:u32][x][W][y]: the other weight formats' GEMVs
 // (bytecode_interpreter.s:7071-7079, 11024-11032 and the same prologue in
 // each K-quant handler).
@@ -415,6 +464,9 @@ int run(const uint8_t* data, size_t size, hipStream_t s) {
             case ANE_OP_DENSE_FUSED_I8: st = op_dense_fused(r, s); break;
             case ANE_OP_GET_ROWS_Q8_0: st = op_get_rows(r, s, false); break;
             case ANE_OP_GET_ROWS_Q4_0: st = op_get_rows(r, s, true); break;
+            case ANE_OP_CBLAS_IGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_SIGNED); break;
+            case ANE_OP_CBLAS_UGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_UNSIGNED); break;
+            case ANE_OP_CBLAS_USGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_MIXED); break;
             default: {
                 const QGemv* f = nullptr;
                 for (const QGemv& q : kQGemv)

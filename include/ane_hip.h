@@ -60,6 +60,9 @@ enum ane_status {
 #define ANE_OP_DENSE_U8S8 0x1E
 #define ANE_OP_Q8_0_GEMV 0x57
 #define ANE_OP_Q4_0_GEMV 0x58
+#define ANE_OP_CBLAS_IGEMM 0x61
+#define ANE_OP_CBLAS_UGEMM 0x62
+#define ANE_OP_CBLAS_USGEMM 0x63
 #define ANE_OP_Q4_K_GEMV 0x75
 #define ANE_OP_Q2_K_GEMV 0x76
 #define ANE_OP_Q3_K_GEMV 0x77
@@ -157,6 +160,30 @@ int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, float scale,
 int ane_hip_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int8_t* A,
                         uint32_t lda, const int8_t* Bt, uint32_t ldb,
                         int32_t* acc, void* stream);
+
+/* 0x61 cblas_igemm / 0x62 cblas_ugemm / 0x63 cblas_usgemm
+ * (bytecode_interpreter.s:8328-9139, the CBLAS_INTEGER_GEMM macro):
+ * A and B int8 (variant SIGNED), uint8 (UNSIGNED) or uint8 A x int8 B
+ * (MIXED); C fp32, rows < M and columns < N written with stride ldc >= N;
+ * flags bit 0 transA, bit 1 transB; only K/64 whole blocks of K are used.
+ * semantics ANE_IGEMM_REFERENCE reproduces the handler: C = fl(fl32(acc) *
+ * alpha), where acc starts from the bit pattern of fl(beta * C) when beta's
+ * bits are nonzero (:8402-8488), and with transA output row i reads
+ * A[(i%16)*lda + (i - i%16) + k] (:8513-8514) -- this is what stream_exec
+ * runs for the opcodes.  ANE_IGEMM_BLAS computes the documented form instead:
+ * op(A) = A^T (A is K x M, stride lda) with transA, and
+ * C = fl(fl(fl32(acc) * alpha) + fl(beta * C)), C not read when beta == 0.
+ * Accumulation wraps modulo 2^32 in both. */
+#define ANE_IGEMM_SIGNED 0
+#define ANE_IGEMM_UNSIGNED 1
+#define ANE_IGEMM_MIXED 2
+#define ANE_IGEMM_REFERENCE 0
+#define ANE_IGEMM_BLAS 1
+size_t ane_hip_cblas_igemm_workspace_size(uint32_t M, uint32_t N, uint32_t K);
+int ane_hip_cblas_igemm(int variant, int semantics, uint8_t flags, uint32_t M, uint32_t N,
+                        uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
+                        float beta, const void* A, const void* B, float* C, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* 0x57 q8_0_gemv "R mode" (bytecode_interpreter.s:7010-7063): fp32 x,
  * y[m] = FADDV16 of 16 fma lanes, bit-identical to the reference's

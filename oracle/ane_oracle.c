@@ -610,3 +610,75 @@ void oracle_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, c
         }
     }
 }
+
+/* 0x61 cblas_igemm / 0x62 cblas_ugemm / 0x63 cblas_usgemm: the
+ * CBLAS_INTEGER_GEMM macro, bytecode_interpreter.s:8328-9135, instantiated
+ * at :9137-9139 with smopa / umopa / usmopa.  variant 0: s8 x s8, 1: u8 x u8,
+ * 2: u8 x s8.  Only rows < M and columns < N of C are written (the store
+ * predicates, :8946-8960 and the w15 row count).
+ *   k blocks      : K / 64 (:8375), a remainder of K is never read;
+ *   A, transA = 0 : row i at A + i*lda (:8504-8509, :8521-8560);
+ *   A, transA = 1 : the handler adds the k offset to A + ti and steps rows by
+ *                   lda (:8513-8514, :8562-8575), so output row i reads
+ *                   A[(i % 16)*lda + (i - i % 16) + k] -- not A^T;
+ *   B, transB = 0 : B[k*ldb + j], one byte per ld1b lane (:8604-8680);
+ *   B, transB = 1 : B[j*ldb + k], rows of B transposed through za3
+ *                   (:8768-8872);
+ *   accumulator   : zero when the bits of beta are zero, otherwise seeded
+ *                   with the BIT PATTERN of fl(beta * C[i][j]) (:8402-8488:
+ *                   fmul, then mova into the int32 za tiles), then the
+ *                   products are added as wrapping int32 (smopa);
+ *   store         : C = fl(fl32(acc) * alpha) (scvtf, fmul: :8962-8980).
+ * semantics 1 instead computes what the header comment (:8330) describes:
+ * op(A) = A^T for transA, and C = fl(fl(fl32(acc) * alpha) + fl(beta * C))
+ * with C not read when beta == 0. */
+static inline int32_t igemm_elem(const uint8_t* p, int is_unsigned) {
+    return is_unsigned ? (int32_t)*p : (int32_t)(int8_t)*p;
+}
+
+void oracle_cblas_igemm(int variant, int semantics, uint8_t flags, uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha, float beta, const void* A,
+                        const void* B, float* C) {
+    const uint8_t* a8 = (const uint8_t*)A;
+    const uint8_t* b8 = (const uint8_t*)B;
+    const int au = variant == 1 || variant == 2, bu = variant == 1;
+    const int ta = flags & 1, tb = (flags >> 1) & 1;
+    const size_t Ke = (size_t)(K / 64) * 64;
+    uint32_t beta_bits;
+    memcpy(&beta_bits, &beta, 4);
+    int nt = g_threads;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long ii = 0; ii < (long)M; ii++) {
+        const size_t i = (size_t)ii;
+        size_t arow, astep;
+        if (!ta) {
+            arow = i * lda;
+            astep = 1;
+        } else if (semantics == 0) {
+            arow = (i % 16) * (size_t)lda + (i - i % 16);
+            astep = 1;
+        } else {
+            arow = i;
+            astep = lda;
+        }
+        for (size_t j = 0; j < N; j++) {
+            float* c = C + i * ldc + j;
+            uint32_t acc = 0;
+            if (semantics == 0 && beta_bits != 0) {
+                float seed = beta * *c; /* fmul (:8449-8450) */
+                memcpy(&acc, &seed, 4);
+            }
+            for (size_t k = 0; k < Ke; k++) {
+                const int32_t a = igemm_elem(a8 + arow + k * astep, au);
+                const int32_t b = igemm_elem(b8 + (tb ? j * (size_t)ldb + k : k * (size_t)ldb + j), bu);
+                acc += (uint32_t)(a * b);
+            }
+            float v = (float)(int32_t)acc * alpha;
+            if (semantics == 1 && beta != 0.0f) {
+                float cb = beta * *c;
+                v = v + cb;
+            }
+            *c = v;
+        }
+    }
+}

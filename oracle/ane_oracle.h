@@ -29,6 +29,15 @@
  *       (get_rows_q8_0); FADDV tree and fma pinned by closed-form cases
  *       (one-hot x, power-of-two data that makes every sum exact, and a
  *       tree-order case whose sequential sum differs).
+ *   cblas_igemm / ugemm / usgemm : the reference KAT
+ *       test_remaining_ops.cpp:131-184 (16x32x64, alpha 1 and 0.5, beta 0),
+ *       exact int64 numpy products of s8/u8 operands for every variant and
+ *       transB (transB = 1 equals transB = 0 on the transposed matrix).
+ *       The handler-only behaviours (transA's row addressing, the beta
+ *       bit-pattern seed) have no reference test: they are restated from the
+ *       cited lines and checked against their closed forms (K < 64 leaves
+ *       only the seed; beta = -0.0 seeds; transA on a matrix whose row i
+ *       equals the addressed bytes).
  *   q8_0 G mode    : the build's own definition (the reference has no
  *       quantized-activation matvec); isum_b pinned exactly by integer
  *       numpy, combination order pinned by an independent numpy loop with
@@ -139,6 +148,19 @@ void oracle_get_rows_q8_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, c
                           float* out);
 void oracle_get_rows_q4_0(uint32_t n_rows, uint32_t dim, const uint8_t* table, const uint32_t* indices,
                           float* out);
+
+/* 0x61 / 0x62 / 0x63 cblas_igemm / cblas_ugemm / cblas_usgemm
+ * (bytecode_interpreter.s:8328-9139): variant 0 = s8 x s8, 1 = u8 x u8,
+ * 2 = u8 x s8; flags bit 0 transA, bit 1 transB; C fp32 rows < M, columns
+ * < N, stride ldc, updated in place.  semantics 0 = the handler's
+ * arithmetic (K/64 blocks; transA reads A[(i%16)*lda + i - i%16 + k]; a
+ * nonzero beta seeds the int32 accumulator with the bits of fl(beta*C);
+ * C = fl(fl32(acc) * alpha)); semantics 1 = the BLAS form its header
+ * describes (op(A) = A^T; C = fl(fl(fl32(acc)*alpha) + fl(beta*C)), C not
+ * read when beta == 0). */
+void oracle_cblas_igemm(int variant, int semantics, uint8_t flags, uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha, float beta, const void* A,
+                        const void* B, float* C);
 
 /* IEEE half -> float (exact), as fcvt s, h. */
 float oracle_f16_to_f32(uint16_t h);

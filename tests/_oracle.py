@@ -51,6 +51,8 @@ class Oracle:
             "oracle_f16_to_f32": (c.c_float, [c.c_uint16]),
             "oracle_get_rows_q8_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
             "oracle_get_rows_q4_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_cblas_igemm": (None, [c.c_int, c.c_int, c.c_uint8, c.c_uint32, c.c_uint32, c.c_uint32,
+                                          c.c_uint32, c.c_uint32, c.c_uint32, c.c_float, c.c_float, P, P, P]),
         }
         for fmt in QFORMATS:
             sig[f"oracle_{fmt}_gemv"] = (None, [c.c_uint32, c.c_uint32, P, P, P])
@@ -174,6 +176,16 @@ class Oracle:
         out = np.zeros((max(n_rows, 1), max(dim // 32 * 32, 1)), np.float32)
         getattr(self.lib, f"oracle_get_rows_{fmt}")(n_rows, dim, _p(table), _p(idx), _p(out))
         return out[:n_rows, : dim // 32 * 32]
+
+    def cblas_igemm(self, variant, flags, M, N, K, lda, ldb, ldc, alpha, beta, A, B, C, semantics=0):
+        """0x61-0x63 on host buffers: returns a copy of C updated in place
+        (variant 0 igemm, 1 ugemm, 2 usgemm; semantics 0 handler, 1 BLAS)."""
+        A = np.ascontiguousarray(A).view(np.uint8)
+        B = np.ascontiguousarray(B).view(np.uint8)
+        C = np.array(C, dtype=np.float32, copy=True)
+        self.lib.oracle_cblas_igemm(variant, semantics, flags, M, N, K, lda, ldb, ldc, np.float32(alpha),
+                                    np.float32(beta), _p(A), _p(B), _p(C))
+        return C
 
     def f16_to_f32(self, h: int) -> float:
         return self.lib.oracle_f16_to_f32(h)

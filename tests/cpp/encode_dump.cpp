@@ -31,5 +31,12 @@ int main() {
                   reinterpret_cast<uintptr_t>(B), reinterpret_cast<uintptr_t>(C));
     // README.md:87-97
     ane::dispatch(ane::Op::dense_fused_i8, 50, 128, 784, 1.0f, true, xf, xf, C);
+    // test_remaining_ops.cpp:150-156: uint8_t flags, six uint32_t, two floats, uintptr_t A, B, C
+    ane::dispatch(ane::Op::cblas_igemm, uint8_t(0), uint32_t(16), uint32_t(32), uint32_t(64), uint32_t(64),
+                  uint32_t(32), uint32_t(32), 0.5f, 0.0f, reinterpret_cast<uintptr_t>(A),
+                  reinterpret_cast<uintptr_t>(B), reinterpret_cast<uintptr_t>(C));
+    ane::dispatch(ane::Op::cblas_usgemm, uint8_t(3), uint32_t(5), uint32_t(7), uint32_t(130), uint32_t(9),
+                  uint32_t(140), uint32_t(11), -1.0f, 2.0f, reinterpret_cast<uintptr_t>(A),
+                  reinterpret_cast<uintptr_t>(B), reinterpret_cast<uintptr_t>(C));
     return 0;
 }

@@ -145,5 +145,46 @@ def main() -> None:
          W=W, x=xs, y_r=yr, y_g=yg)
 
 
+def cblas_fixtures() -> None:
+    """The integer GEMM opcodes (0x61-0x63) through the oracle's restatement
+    of their handler, each checked against an exact int64 product."""
+    o = _oracle.load()
+    # reference KAT tests/test_remaining_ops.cpp:131-184: flags 0, lda=K,
+    # ldb=ldc=N, beta 0, alpha 1 then 0.5; expected = (float)sum * alpha
+    M, N, K = 16, 32, 64
+    A = ((np.arange(M * K) % 11) - 5).astype(np.int8)
+    B = ((np.arange(K * N) % 13) - 6).astype(np.int8)
+    ref = A.reshape(M, K).astype(np.int64) @ B.reshape(K, N).astype(np.int64)  # the test's triple loop
+    C0 = np.zeros((M, N), F32)
+    c1 = o.cblas_igemm(0, 0, M, N, K, K, N, N, 1.0, 0.0, A, B, C0)
+    c05 = o.cblas_igemm(0, 0, M, N, K, K, N, N, 0.5, 0.0, A, B, C0)
+    assert same_bits(c1, (ref.astype(F32) * F32(1.0)).astype(F32))
+    assert same_bits(c05, (ref.astype(F32) * F32(0.5)).astype(F32))
+    assert same_bits(c05, (c1 * F32(0.5)).astype(F32))  # the test's own alpha-scaling check, exactly
+    # u8 x u8 and u8 x s8 with transB, strides and a K remainder
+    g = np.random.default_rng(21)
+    M2, N2, K2, lda, ldb, ldc = 21, 37, 200, 203, 205, 40
+    Au = g.integers(0, 256, size=M2 * lda).astype(np.uint8)
+    Bu = g.integers(0, 256, size=N2 * ldb).astype(np.uint8)
+    Bs = g.integers(-128, 128, size=N2 * ldb).astype(np.int8)
+    C2 = g.standard_normal((M2, ldc)).astype(F32)
+    am = Au.reshape(M2, lda)[:, :192].astype(np.int64)
+    outs = {}
+    for name, variant, Bx in (("ugemm", 1, Bu), ("usgemm", 2, Bs)):
+        acc = am @ Bx.reshape(N2, ldb)[:, :192].T.astype(np.int64)
+        c = o.cblas_igemm(variant, 2, M2, N2, K2, lda, ldb, ldc, -1.25, 0.0, Au, Bx, C2)
+        assert same_bits(c[:, :N2], (acc.astype(F32) * F32(-1.25)).astype(F32))
+        assert same_bits(c[:, N2:], C2[:, N2:])
+        outs[f"C_{name}"] = c
+    save("cblas_igemm_kat", "reference tests/test_remaining_ops.cpp:131-184 (cblas_igemm 16x32x64, A=(i%11)-5, "
+         "B=(i%13)-6, alpha 1 and 0.5, beta 0), plus ugemm / usgemm 21x37, K=200 (192 used), transB, "
+         "lda 203, ldb 205, ldc 40, alpha -1.25 over C2",
+         A=A, B=B, C_alpha1=c1, C_alpha05=c05, Au=Au, Bu=Bu, Bs=Bs, C2=C2, **outs)
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["cblas"]:
+        cblas_fixtures()
+    else:
+        main()
+        cblas_fixtures()

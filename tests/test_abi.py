@@ -65,6 +65,7 @@ def test_record_sizes():
     assert len(ane_amd.rec_channelwise(1, 16, 0, 0, 0)) == 33
     assert len(ane_amd.rec_q8_0_gemv(1, 32, 0, 0, 0)) == 33
     assert len(ane_amd.rec_dense_fused_i8(1, 1, 1, 1.0, True, 0, 0, 0)) == 42
+    assert len(ane_amd.rec_cblas_igemm("ugemm", 0, 1, 1, 64, 64, 1, 1, 1.0, 0.0, 0, 0, 0)) == 58  # :8355-8369
 
 
 def test_python_encoding_matches_cpp_header(tmp_path):
@@ -86,6 +87,8 @@ def test_python_encoding_matches_cpp_header(tmp_path):
         ane_amd.rec_channelwise(7, 48, xf, A, scale),
         ane_amd.rec_q8_0_gemv(4096, 14336, xf, B, C),
         ane_amd.rec_dense_fused_i8(50, 128, 784, 1.0, True, xf, xf, C),
+        ane_amd.rec_cblas_igemm("igemm", 0, 16, 32, 64, 64, 32, 32, 0.5, 0.0, A, B, C),
+        ane_amd.rec_cblas_igemm("usgemm", 3, 5, 7, 130, 9, 140, 11, -1.0, 2.0, A, B, C),
     ]
     assert lines == [e.hex() for e in expect]
 

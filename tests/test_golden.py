@@ -29,7 +29,8 @@ def same_bits(a, b):
 def test_fixture_set_complete():
     names = sorted(p.stem for p in GOLDEN.glob("*.npz"))
     assert names == sorted(["quantize_kat", "igemm_kat", "q8_0_get_rows_kat_32", "q8_0_get_rows_kat_64",
-                            "dense_fused_mnist", "dense_u8s8_small", "channelwise_small", "q8_0_small"])
+                            "dense_fused_mnist", "dense_u8s8_small", "channelwise_small", "q8_0_small",
+                            "cblas_igemm_kat"])
     for n in names:
         assert str(fx(n)["source"])  # every fixture names its origin
 
@@ -52,6 +53,22 @@ def test_oracle_igemm_kat(oracle):
     same_bits(oracle.pack_b(f["B"], 64, 32), f["Bp"])
     C = oracle.dense_i8(16, 32, 64, F32(1), F32(1), 0, f["A"], f["Bp"], np.zeros(32, F32))
     same_bits(C, f["C"])
+
+
+def test_oracle_cblas_igemm_kat(oracle):
+    """Opcode 0x61 on the reference KAT: the stored C equals the test's own
+    expectation (float)sum * alpha, and alpha 0.5 halves alpha 1 exactly."""
+    f = fx("cblas_igemm_kat")
+    A, B = f["A"], f["B"]
+    ref = (A.reshape(16, 64).astype(np.int64) @ B.reshape(64, 32).astype(np.int64)).astype(F32)
+    same_bits(f["C_alpha1"], ref)
+    same_bits(f["C_alpha05"], (ref * F32(0.5)).astype(F32))
+    z = np.zeros((16, 32), F32)
+    same_bits(oracle.cblas_igemm(0, 0, 16, 32, 64, 64, 32, 32, 1.0, 0.0, A, B, z), f["C_alpha1"])
+    same_bits(oracle.cblas_igemm(0, 0, 16, 32, 64, 64, 32, 32, 0.5, 0.0, A, B, z), f["C_alpha05"])
+    for name, variant, Bx in (("ugemm", 1, f["Bu"]), ("usgemm", 2, f["Bs"])):
+        same_bits(oracle.cblas_igemm(variant, 2, 21, 37, 200, 203, 205, 40, -1.25, 0.0, f["Au"], Bx, f["C2"]),
+                  f[f"C_{name}"])
 
 
 @pytest.mark.parametrize("dim", [32, 64])
@@ -118,6 +135,26 @@ def test_gpu_quantize_kat(ane):
     ane.stream_exec(ane.rec_quantize(256, dev(f["x"]), q, s))
     same_bits(host(q), f["q"])
     same_bits(host(s), f["scale"])
+
+
+@pytest.mark.gpu
+def test_gpu_cblas_igemm_kat(ane):
+    """The reference KAT through stream_exec records 0x61 (alpha 1 and 0.5),
+    and the ugemm / usgemm fixture through 0x62 / 0x63."""
+    import torch
+
+    f = fx("cblas_igemm_kat")
+    A, B = dev(f["A"]), dev(f["B"])
+    C1 = torch.full((16, 32), 7.0, dtype=torch.float32, device="cuda")
+    C05 = torch.full((16, 32), 7.0, dtype=torch.float32, device="cuda")
+    ane.stream_exec([ane.rec_cblas_igemm("igemm", 0, 16, 32, 64, 64, 32, 32, 1.0, 0.0, A, B, C1),
+                     ane.rec_cblas_igemm("igemm", 0, 16, 32, 64, 64, 32, 32, 0.5, 0.0, A, B, C05)])
+    same_bits(host(C1), f["C_alpha1"])
+    same_bits(host(C05), f["C_alpha05"])
+    for kind, Bx in (("ugemm", f["Bu"]), ("usgemm", f["Bs"])):
+        C = dev(f["C2"])
+        ane.stream_exec(ane.rec_cblas_igemm(kind, 2, 21, 37, 200, 203, 205, 40, -1.25, 0.0, dev(f["Au"]), dev(Bx), C))
+        same_bits(host(C), f[f"C_{kind}"])
 
 
 @pytest.mark.gpu

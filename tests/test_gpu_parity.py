@@ -418,6 +418,98 @@ def test_stream_exec_workspace_two_threads_one_stream(ane, oracle):
     assert not errors, errors
 
 
+# ---------------------------------------------------------------- cblas integer GEMMs
+def _igemm_case(kind, flags, M, N, K, lda, ldb, ldc, seed):
+    a_ext, b_ext, _ = ane_amd_extents(flags, M, N, K, lda, ldb, ldc)
+    g = np.random.default_rng(seed)
+    au, bu = kind in ("ugemm", "usgemm"), kind == "ugemm"
+    A = g.integers(0 if au else -128, 256 if au else 128, size=max(a_ext, 1)).astype(np.uint8 if au else np.int8)
+    B = g.integers(0 if bu else -128, 256 if bu else 128, size=max(b_ext, 1)).astype(np.uint8 if bu else np.int8)
+    C = g.standard_normal((M, ldc)).astype(F32)
+    return A, B, C
+
+
+def ane_amd_extents(*args):
+    import ane_amd
+
+    return ane_amd._igemm_extents(*args)
+
+
+IGEMM_VARIANT = {"igemm": 0, "ugemm": 1, "usgemm": 2}
+
+
+@pytest.mark.parametrize("kind", ["igemm", "ugemm", "usgemm"])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,N,K,beta", [(16, 32, 64, 0.0), (5, 7, 130, 0.5), (37, 300, 256, -0.0),
+                                        (300, 200, 512, 0.0), (20, 70, 40, 1.0), (1, 4096, 4096, 0.0)])
+def test_cblas_igemm_opcodes_parity(ane, oracle, kind, flags, M, N, K, beta):
+    """0x61-0x63 through stream_exec: every variant, transA/transB, strides
+    past the logical sizes, K remainders and K < 64, and beta seeding the
+    accumulator bits, bit-identical to the handler's arithmetic."""
+    lda = (K + 3) if not flags & 1 else (M + 5)
+    ldb = (N + 2) if not flags & 2 else (K + 7)
+    ldc = N + 3
+    A, B, C = _igemm_case(kind, flags, M, N, K, lda, ldb, ldc, seed=M + N + K + flags)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.cblas_igemm(IGEMM_VARIANT[kind], flags, M, N, K, lda, ldb, ldc, -0.75, beta, A, B, C)
+    finally:
+        oracle.set_threads(1)
+    Cd = dev(C)
+    ane.stream_exec(ane.rec_cblas_igemm(kind, flags, M, N, K, lda, ldb, ldc, -0.75, beta, dev(A), dev(B), Cd))
+    assert_f32_identical(host(Cd), ref)
+
+
+@pytest.mark.parametrize("kind", ["igemm", "ugemm", "usgemm"])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,N,K,beta", [(33, 40, 256, 0.5), (1024, 1024, 1024, 0.0), (260, 520, 192, -2.0)])
+def test_cblas_igemm_blas_semantics(ane, oracle, kind, flags, M, N, K, beta):
+    """The kernel-level BLAS form: op(A) = A^T with transA (A is K x M), and
+    C = alpha*acc + beta*C with two roundings; 1024^3 takes the 256-tile
+    contraction."""
+    lda = (K + 16) if not flags & 1 else (M + 16)
+    ldb = (N + 16) if not flags & 2 else (K + 16)
+    ldc = N
+    g = np.random.default_rng(M + N + flags)
+    au, bu = kind in ("ugemm", "usgemm"), kind == "ugemm"
+    na = (K * lda) if flags & 1 else (M * lda)
+    nb = (N * ldb) if flags & 2 else (K * ldb)
+    A = g.integers(0 if au else -128, 256 if au else 128, size=na).astype(np.uint8 if au else np.int8)
+    B = g.integers(0 if bu else -128, 256 if bu else 128, size=nb).astype(np.uint8 if bu else np.int8)
+    C = g.standard_normal((M, ldc)).astype(F32)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.cblas_igemm(IGEMM_VARIANT[kind], flags, M, N, K, lda, ldb, ldc, 0.5, beta, A, B, C, semantics=1)
+    finally:
+        oracle.set_threads(1)
+    Cd = dev(C)
+    ane.cblas_igemm(kind, flags, M, N, K, lda, ldb, ldc, 0.5, beta, dev(A), dev(B), Cd, blas=True)
+    assert_f32_identical(host(Cd), ref)
+
+
+def test_cblas_igemm_short_a_rejected(ane):
+    """transA's handler addressing reaches 15*lda + 16*floor((M-1)/16) - 16
+    + Ke bytes: one byte less in A's allocation is refused before anything
+    runs."""
+    import torch
+
+    M, N, K, lda = 40, 8, 64, 100
+    a_ext, b_ext, _ = ane_amd_extents(1, M, N, K, lda, N, N)
+    assert a_ext == 15 * lda + 32 - 16 + 64
+    hip = _hip()
+    p = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(a_ext - 1)) == 0
+    try:
+        C = torch.full((M * N,), 2.0, dtype=torch.float32, device="cuda")
+        B = zeros(b_ext, torch.int8)
+        with pytest.raises(ane.AneError) as e:
+            ane.stream_exec(ane.rec_cblas_igemm("igemm", 1, M, N, K, lda, N, N, 1.0, 0.0, p.value, B, C))
+        assert e.value.status == 3
+        assert (host(C) == 2.0).all()
+    finally:
+        hip.hipFree(p)
+
+
 # ---------------------------------------------------------------- Q8_0
 @pytest.mark.parametrize("M,K", [(1, 32), (3, 40), (4096, 4096), (14336, 4096), (4096, 14336), (77, 96),
                                  # streaming kernel: partial last segment, ragged row split, K % 32 != 0

@@ -338,3 +338,100 @@ def test_q8_0_g_close_to_r(oracle):
     _, dx = oracle.q8_0_quantize_x(K, x)
     bound = (d * np.abs(qs.astype(F32)).sum(-1) * (dx[None, :] / 2)).sum(-1)
     assert np.all(np.abs(yg - yr) <= bound * 1.001 + 1e-5)
+
+
+# ---------------------------------------------------------------- cblas integer GEMMs (0x61-0x63)
+def _igemm_operands(variant, M, N, K, lda, ldb, tb, seed):
+    g = np.random.default_rng(seed)
+    au, bu = variant in (1, 2), variant == 1
+    A = g.integers(0 if au else -128, 256 if au else 128, size=M * lda).astype(np.uint8 if au else np.int8)
+    nb = (N * ldb) if tb else (K * ldb)
+    B = g.integers(0 if bu else -128, 256 if bu else 128, size=nb).astype(np.uint8 if bu else np.int8)
+    return A, B
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(16, 32, 64), (5, 7, 130), (33, 40, 256)])
+def test_cblas_igemm_matches_int64_numpy(oracle, variant, tb, M, N, K):
+    """Every variant and transB against an exact int64 numpy product over the
+    K/64 whole blocks, then the two float32 roundings (scvtf, fmul alpha)."""
+    lda, ldb, ldc = K + 3, (K + 5) if tb else (N + 2), N + 1
+    A, B = _igemm_operands(variant, M, N, K, lda, ldb, tb, seed=M + N + K + variant)
+    Ke = K // 64 * 64
+    Am = A.reshape(M, lda)[:, :Ke].astype(np.int64)
+    Bm = (B.reshape(N, ldb)[:, :Ke].T if tb else B.reshape(K, ldb)[:Ke, :N]).astype(np.int64)
+    acc = (Am @ Bm).astype(np.int64)
+    assert np.abs(acc).max() < 2 ** 31
+    want = (acc.astype(np.float32) * F32(-0.75)).astype(F32)
+    C0 = np.full((M, ldc), 3.0, F32)
+    got = oracle.cblas_igemm(variant, tb << 1, M, N, K, lda, ldb, ldc, -0.75, 0.0, A, B, C0)
+    np.testing.assert_array_equal(got[:, :N].view(np.uint32), want.view(np.uint32))
+    assert (got[:, N:] == 3.0).all()  # columns past N are never written
+
+
+def test_cblas_igemm_transb_equals_transposed_copy(oracle):
+    M, N, K = 9, 20, 192
+    A, B = _igemm_operands(0, M, N, K, K, N, 0, seed=1)
+    Bt = np.ascontiguousarray(B.reshape(K, N).T)
+    C0 = np.zeros((M, N), F32)
+    c0 = oracle.cblas_igemm(0, 0, M, N, K, K, N, N, 1.0, 0.0, A, B, C0)
+    c1 = oracle.cblas_igemm(0, 2, M, N, K, K, K, N, 1.0, 0.0, A, Bt, C0)
+    assert np.array_equal(c0, c1)
+
+
+def test_cblas_igemm_beta_seeds_accumulator_bits(oracle):
+    """K < 64 leaves no products: the handler stores fl(fl32(seed) * alpha),
+    seed = the bits of fl(beta * C) whenever beta's bits are nonzero
+    (bytecode_interpreter.s:8402-8488), so beta = -0.0 seeds too."""
+    A = np.zeros(64, np.int8)
+    C0 = np.array([[1.0, 2.0, -1.5]], F32)
+    out = oracle.cblas_igemm(0, 0, 1, 3, 32, 32, 3, 3, 1.0, 1.0, A, A, C0)
+    assert out[0, 0] == F32(0x3F800000)           # bits of 1.0 as an integer
+    assert out[0, 1] == F32(0x40000000)
+    assert out[0, 2] == F32(np.int32(np.uint32(0xBFC00000)))  # negative as int32
+    out = oracle.cblas_igemm(0, 0, 1, 3, 32, 32, 3, 3, 1.0, -0.0, A, A, C0)
+    assert out[0, 0] == F32(-2.0 ** 31) and out[0, 2] == 0.0  # -0.0 -> INT32_MIN, +0.0 -> 0
+    out = oracle.cblas_igemm(0, 0, 1, 3, 32, 32, 3, 3, 2.0, 0.0, A, A, C0)
+    assert (out == 0.0).all()
+    # the BLAS form on the same inputs: alpha*0 + beta*C
+    out = oracle.cblas_igemm(0, 0, 1, 3, 32, 32, 3, 3, 1.0, 1.0, A, A, C0, semantics=1)
+    assert np.array_equal(out, C0)
+
+
+def test_cblas_igemm_beta_seed_adds_to_products(oracle):
+    """With products the seed and the sum wrap together: seed + acc as int32."""
+    M, N, K = 4, 8, 64
+    A, B = _igemm_operands(0, M, N, K, K, N, 0, seed=5)
+    C0 = np.random.default_rng(6).standard_normal((M, N)).astype(F32)
+    acc = A.reshape(M, K).astype(np.int64) @ B.reshape(K, N).astype(np.int64)
+    seed = (C0 * F32(0.5)).astype(F32).view(np.int32).astype(np.int64)
+    tot = ((acc + seed + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int64)
+    want = (tot.astype(np.float32) * F32(1.0)).astype(F32)
+    got = oracle.cblas_igemm(0, 0, M, N, K, K, N, N, 1.0, 0.5, A, B, C0)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    blas = oracle.cblas_igemm(0, 0, M, N, K, K, N, N, 1.0, 0.5, A, B, C0, semantics=1)
+    np.testing.assert_array_equal(blas, (acc.astype(F32) + (C0 * F32(0.5)).astype(F32)).astype(F32))
+
+
+def test_cblas_igemm_transa_handler_addressing(oracle):
+    """transA: the handler adds the k offset to A + ti and steps rows by lda,
+    so the first 16 rows read exactly what transA = 0 reads, and row 16 + r
+    starts at byte 16 + r * lda (not A^T)."""
+    M, N, K, lda = 20, 8, 64, 80
+    size = 15 * lda + 16 + K
+    g = np.random.default_rng(9)
+    A = g.integers(-128, 128, size=size).astype(np.int8)
+    B = g.integers(-128, 128, size=K * N).astype(np.int8)
+    C0 = np.zeros((M, N), F32)
+    t1 = oracle.cblas_igemm(0, 1, M, N, K, lda, N, N, 1.0, 0.0, A, B, C0)
+    rows = np.stack([A[(i % 16) * lda + (i - i % 16):][:K] for i in range(M)]).astype(np.int64)
+    want = (rows @ B.reshape(K, N).astype(np.int64)).astype(F32)
+    assert np.array_equal(t1, want)
+    t0 = oracle.cblas_igemm(0, 0, 16, N, K, lda, N, N, 1.0, 0.0, A, B, C0[:16])
+    assert np.array_equal(t1[:16], t0)
+    # the BLAS form: A is K x M with stride lda
+    At = g.integers(-128, 128, size=K * lda).astype(np.int8)
+    tb = oracle.cblas_igemm(0, 1, M, N, K, lda, N, N, 1.0, 0.0, At, B, C0, semantics=1)
+    want = (At.reshape(K, lda)[:, :M].T.astype(np.int64) @ B.reshape(K, N).astype(np.int64)).astype(F32)
+    assert np.array_equal(tb, want)
