@@ -1,5 +1,6 @@
 """Build recipe for ane_amd/libane_amd.so (gfx950), the benchmark's
-libane_peaks.so and the CPU oracle.
+bench_peaks.so (beside bench.py, not part of the package) and the CPU
+oracle.
 
 Run ``python -m ane_amd.build`` (or ``__graft_entry__.build()``).  The
 library is built in-tree so it travels with the repository snapshot; object
@@ -19,8 +20,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libane_amd.so"
-PEAKS_SRC = PKG / "probes" / "peaks.hip"
-PEAKS_LIB = PKG / "libane_peaks.so"
+PEAKS_SRC = ROOT / "bench_peaks.hip"
+PEAKS_LIB = ROOT / "bench_peaks.so"
 
 ARCH = "gfx950"
 
@@ -76,7 +77,7 @@ def build_library(verbose: bool = False) -> Path:
 
 
 def build_peaks(verbose: bool = False) -> Path:
-    """libane_peaks.so: the MFMA-loop and HBM-stream ceilings bench.py reports."""
+    """bench_peaks.so: the MFMA-loop and HBM-stream ceilings bench.py reports."""
     tmp = PEAKS_LIB.with_suffix(".so.tmp")
     _run([hipcc(), *HIP_FLAGS, "-shared", str(PEAKS_SRC), "-o", str(tmp)])
     os.replace(tmp, PEAKS_LIB)

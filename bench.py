@@ -14,7 +14,8 @@ Also reported (same JSON line):
   on the fly) and the reference-arithmetic opcode 0x57 ("R mode"), GB/s
   against 8 TB/s, rotating >256 MB of weight copies so the Infinity Cache
   cannot serve them.
-* ``measured_ceilings`` -- what this GPU sustains (ane_amd/libane_peaks.so):
+* ``measured_ceilings`` -- what this GPU sustains (bench_peaks.so, built from
+  bench_peaks.hip beside this file):
   an int8 MFMA loop without memory traffic on random operands, with the
   clock it holds, and plain HBM read/write streams; each roofline also
   carries ``frac_measured`` against the matching ceiling.
@@ -60,8 +61,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--layers", type=int, default=32, help="decoder layers of the config-5 model")
     ap.add_argument("--kernel-reps", type=int, default=200, help="launches per kernel timing")
+    ap.add_argument("--eager", action="store_true", help="--only gemm/fused: eager launches, no HIP graph")
     ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings",
-                             "mulmat", "msweep", "mnist"],
+                             "mulmat", "msweep", "mnist", "mfma_loop", "vendor_int8"],
                     default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
@@ -119,6 +121,15 @@ def read_pmc_traffic(name: str):
     if not p.exists():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def read_profile_value(name: str, key: str):
+    """A 'key: <number>' line of a committed profile summary (profiles/<name>)."""
+    p = PROFILES / name
+    if not p.exists():
+        return None
+    m = re.search(rf"^{re.escape(key)}:\s*([0-9.eE+]+)", p.read_text(), flags=re.M)
     return float(m.group(1)) if m else None
 
 
@@ -192,13 +203,42 @@ def main() -> int:
         bench_decode(args)
         return 0
 
+    if args.only == "vendor_int8":
+        # a vendor comparison point, not part of the product: torch._int_mm
+        # (hipBLASLt on ROCm) on int8 operands of the same shape, int32 out,
+        # HIP-graph replayed like the contraction
+        a8 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+        b8 = torch.randint(-127, 128, (K, N), dtype=torch.int8, device=dev)
+        out = torch.empty((M, N), dtype=torch.int32, device=dev)
+
+        def vend(st):
+            torch._int_mm(a8, b8, out=out)
+
+        ms = graph_time(vend, args.steps)
+        log(f"torch._int_mm int8 {M}x{N}x{K}: {ms * 1e3:.2f} us/launch, {ops / ms / 1e9:.1f} TOPS")
+        print(json.dumps({"only": "vendor_int8", "us_per_launch": round(ms * 1e3, 3),
+                          "TOPS": round(ops / ms / 1e9, 2)}), flush=True)
+        return 0
+    if args.only == "mfma_loop":
+        # the int8 MFMA loop of bench_peaks.so alone (counter calibration)
+        print(json.dumps(mfma_loop_only(args)), flush=True)
+        return 0
     if args.only in ("gemm", "fused"):
+        # the same HIP-graph replay the headline roofline measures, so a
+        # kernel trace of this command reproduces the line's avg_launch_us
         fn = gemm_phase if args.only == "gemm" else fused
         quant_phase()
-        for _ in range(args.warmup):
-            fn()
-        ms = events_time(fn, args.steps, stream)
-        log(f"{args.only}: {ms * 1e3:.2f} us/launch, {ops / ms / 1e9:.1f} TOPS")
+        torch.cuda.synchronize()
+        if args.eager:
+            for _ in range(args.warmup):
+                fn()
+            ms = events_time(fn, args.steps, stream)
+        else:
+            ms = graph_time(fn, args.steps)
+        log(f"{args.only}: {ms * 1e3:.2f} us/launch, {ops / ms / 1e9:.1f} TOPS "
+            f"({'eager launches' if args.eager else 'HIP-graph replay, median of 5 rounds'})")
+        print(json.dumps({"only": args.only, "us_per_launch": round(ms * 1e3, 3),
+                          "TOPS": round(ops / ms / 1e9, 2)}), flush=True)
         return 0
 
     # ------------------------------------------------------------ headline
@@ -234,8 +274,18 @@ def main() -> int:
         "algorithmic_per_launch": f"2*M*N*K = {int(ops)} int8 ops",
         "avg_launch_us": round(gemm_ms * 1e3, 3),
         "traffic": read_pmc_traffic("gemm_i8_4096_pmc.txt"),
-        "profiles": ["profiles/gemm_i8_tile256_4096_kernel_trace.txt", "profiles/gemm_i8_4096_pmc.txt"],
+        "mfma_util": read_profile_value("gemm_i8_4096_mfma_pmc.txt", "mfma_util"),
+        "held_clock_GHz": read_profile_value("gemm_i8_4096_mfma_pmc.txt", "held_clock_GHz"),
+        "mfma_util_how": ("SQ_VALU_MFMA_BUSY_CYCLES per SIMD / SQ_BUSY_CYCLES per SE over the contraction's "
+                          "dispatch (rocprofv3 --pmc, profiles/gemm_i8_4096_mfma_pmc.txt); the clock it held "
+                          "is SQ_BUSY_CYCLES per SE / dispatch time"),
+        "profiles": ["profiles/gemm_i8_tile256_4096_kernel_trace.txt", "profiles/gemm_i8_4096_pmc.txt",
+                     "profiles/gemm_i8_4096_mfma_pmc.txt"],
     }
+    if roofline["held_clock_GHz"]:
+        # the same kernel against the peak at the clock it holds (8192 int8 ops/clk/CU)
+        held_peak = 8192 * torch.cuda.get_device_properties(0).multi_processor_count * roofline["held_clock_GHz"] / 1e3
+        roofline["frac_at_held_clock"] = round(gemm_tops / held_peak, 4)
 
     ceilings = measured_ceilings(args)
     mfma_meas = ceilings["mfma_i8_loop_workload"]["TOPS"]
@@ -328,8 +378,51 @@ def profile_q8(args, stream) -> int:
     return 0
 
 
+def _peaks():
+    import ctypes
+
+    peaks = ctypes.CDLL(str(ROOT / "bench_peaks.so"))
+    u32, u64, vp, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+    peaks.ane_peak_mfma_i8.argtypes = [u32, u32, u32, vp, vp, vp, vp]
+    peaks.ane_peak_read.argtypes = [vp, u64, u32, i32, vp, vp]
+    peaks.ane_peak_write.argtypes = [vp, u64, u32, vp]
+    return peaks
+
+
+def mfma_loop_only(args) -> dict:
+    """The int8 MFMA loop on workload-distributed operands, --steps launches:
+    the reference kernel for reading MFMA counters (its ops, time and
+    in-kernel clock are known)."""
+    import ctypes
+
+    import torch
+
+    peaks = _peaks()
+    dev = torch.device("cuda:0")
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    st = torch.cuda.current_stream()
+    wgs, threads, iters = ncu, 512, 16000
+    sums = torch.empty(wgs * threads, dtype=torch.int32, device=dev)
+    clocks = torch.zeros(4, dtype=torch.int64, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    gauss = torch.randn(16384, generator=g, device=dev)
+    data = torch.round(gauss * (127.0 / gauss.abs().max())).to(torch.int8)
+    ops = wgs * (threads // 64) * iters * 8 * 65536
+    fn = lambda: peaks.ane_peak_mfma_i8(wgs, threads, iters, data.data_ptr(), sums.data_ptr(), clocks.data_ptr(),
+                                        ctypes.c_void_p(st.cuda_stream))
+    fn()
+    ms = events_time(fn, args.steps, st)
+    c = clocks.cpu().tolist()
+    ghz = (c[1] - c[0]) / ((c[3] - c[2]) / 100e6) / 1e9
+    tops = ops / (ms * 1e-3) / 1e12
+    log(f"MFMA loop (workload operands): {ms * 1e3:.2f} us/launch, {tops:.0f} TOPS at {ghz:.3f} GHz")
+    return {"only": "mfma_loop", "us_per_launch": round(ms * 1e3, 3), "TOPS": round(tops, 1),
+            "clock_GHz": round(ghz, 3), "ops_per_launch": ops}
+
+
 def measured_ceilings(args) -> dict:
-    """Ceilings measured on this GPU with ane_amd/libane_peaks.so, reported
+    """Ceilings measured on this GPU with bench_peaks.so, reported
     beside the datasheet peaks: an int8 MFMA loop with no memory traffic on
     random operands (the clock the chip holds under it, from s_memtime over
     s_memrealtime) and on constant operands, and plain HBM read / write
@@ -338,11 +431,7 @@ def measured_ceilings(args) -> dict:
 
     import torch
 
-    peaks = ctypes.CDLL(str(ROOT / "ane_amd" / "libane_peaks.so"))
-    u32, u64, vp, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
-    peaks.ane_peak_mfma_i8.argtypes = [u32, u32, u32, vp, vp, vp, vp]
-    peaks.ane_peak_read.argtypes = [vp, u64, u32, i32, vp, vp]
-    peaks.ane_peak_write.argtypes = [vp, u64, u32, vp]
+    peaks = _peaks()
     dev = torch.device("cuda:0")
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     st = torch.cuda.current_stream()
@@ -350,7 +439,7 @@ def measured_ceilings(args) -> dict:
 
     def check(rc):
         if rc != 0:
-            raise RuntimeError("libane_peaks launch failed")
+            raise RuntimeError("bench_peaks launch failed")
 
     out = {"cus": ncu}
     wgs, threads, iters = ncu, 512, 16000
@@ -743,48 +832,141 @@ def bench_m_sweep(args, N, K) -> dict:
     return {"workload": "config 2 M sweep: dense_fused_i8 M x 4096 x 4096, whole op", "shapes": out}
 
 
+def _host_threads() -> int:
+    """Host threads for the all-core rows: the CPUs this process may run on,
+    capped by OMP_NUM_THREADS (the GPU box sets it to its per-GPU CPU share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, min_s: float = 1.0, reps: int = 3):
+    """Median seconds per call over >= reps calls and >= min_s in total."""
+    ts = []
+    t_all = time.perf_counter()
+    while len(ts) < reps or time.perf_counter() - t_all < min_s:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if len(ts) >= 50:
+            break
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_baseline(A, B, C, M, N, K) -> dict:
-    """Scalar oracle on the host: full per-tensor quantization of A and B,
-    then rows of the contraction until ~10 s of work; extrapolated to the
-    whole op.  Also checks the sampled rows against the GPU's C."""
+    """The scalar CPU restatement (oracle/, -O2 -ffp-contract=off, OpenMP over
+    output rows) on the host cores, for configs 1-4 at 1 thread and at every
+    thread this process may use.  Config 2's 4096^3 rows are a bounded sample
+    (about 4 s per thread count), extrapolated to the whole op; the sampled
+    rows are compared bit for bit with the GPU's C.  `value` is config 2 at
+    all threads."""
     import numpy as np
 
-    from tests import _oracle
+    from tests import _oracle, data
 
     oracle = _oracle.load()
-    threads = min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
+    nth = _host_threads()
+    rows_out = []
+    Cg = C.cpu().numpy()
     An = A.cpu().numpy()
     Bn = B.cpu().numpy()
-    t0 = time.perf_counter()
-    qA, sa = oracle.quantize_exact(An.ravel())
-    qB, sb = oracle.quantize_exact(Bn.ravel())
-    t_quant = time.perf_counter() - t0
-    s = np.float32(np.float32(sa * sb) * np.float32(1.0))
-    rows = 0
-    t_rows = 0.0
-    chunk = 64
-    sample_rows = []
-    while rows < M and t_rows < 10.0:
-        r1 = min(M, rows + chunk)
-        t1 = time.perf_counter()
-        out = oracle.dense_fused_rows(rows, r1, N, K, s, True, qA, qB)
-        t_rows += time.perf_counter() - t1
-        sample_rows.append((rows, out))
-        rows = r1
+    match = True
+    cfg2 = {}
+    for threads in (1, nth):
+        oracle.set_threads(threads)
+        t0 = time.perf_counter()
+        qA, sa = oracle.quantize_exact(An.ravel())
+        qB, sb = oracle.quantize_exact(Bn.ravel())
+        t_quant = time.perf_counter() - t0
+        s = np.float32(np.float32(sa * sb) * np.float32(1.0))
+        done, t_rows, chunk = 0, 0.0, max(8, 8 * threads)
+        while done < M and t_rows < 4.0:
+            r1 = min(M, done + chunk)
+            t1 = time.perf_counter()
+            out = oracle.dense_fused_rows(done, r1, N, K, s, True, qA, qB)
+            t_rows += time.perf_counter() - t1
+            match = match and np.array_equal(Cg[done:r1].view(np.uint32), out.view(np.uint32))
+            done = r1
+        t_full = t_quant + t_rows * (M / done)
+        tops = 2.0 * M * N * K / t_full / 1e12
+        cfg2[threads] = tops
+        rows_out.append({"config": f"2: dense_fused_i8 {M}x{N}x{K}", "threads": threads, "value": round(tops, 5),
+                         "unit": "TOPS", "sample": f"quantize all of A and B ({t_quant:.2f} s) + {done} of {M} rows "
+                         f"({t_rows:.2f} s), extrapolated to the whole op"})
+        log(f"cpu config 2, {threads} thread(s): {tops:.4f} TOPS ({done} of {M} rows sampled)")
+
+    # config 1: the MNIST-shaped MLP forward through dense_fused_i8
+    x, w1, w2 = data.mnist_inputs(seed=1)
+    ops1 = 2.0 * 50 * (784 * 128 + 128 * 10)
+    for threads in (1, nth):
+        oracle.set_threads(threads)
+
+        def mlp():
+            h = oracle.dense_fused_i8(50, 128, 784, np.float32(1.0), True, x, w1)
+            oracle.dense_fused_i8(50, 10, 128, np.float32(1.0), False, h, w2)
+
+        sec = _timed(mlp)
+        rows_out.append({"config": "1: MNIST MLP 50x784->128 ReLU ->10", "threads": threads,
+                         "value": round(sec * 1e6, 1), "unit": "us per forward", "TOPS": round(ops1 / sec / 1e12, 6),
+                         "sample": "whole forward, median of >= 3 runs and >= 1 s"})
+
+    # config 3: Q8_0 matvec 14336x4096, R mode (opcode 0x57) and G mode
+    Nq, Kq = 14336, 4096
+    Wq = data.q8_0_weights(Nq, Kq, seed=3)
+    xq = data.activations(1, Kq, seed=4)
+    wbytes = Nq * (Kq // 32) * 34 + 4 * (Nq + Kq)
+    for threads in (1, nth):
+        oracle.set_threads(threads)
+        for mode, fn in (("R", lambda: oracle.q8_0_gemv(Nq, Kq, xq[0], Wq)),
+                         ("G", lambda: oracle.q8_0_mul_mat_g(Nq, Kq, 1, xq, Wq))):
+            sec = _timed(fn)
+            rows_out.append({"config": f"3: Q8_0 matvec {Nq}x{Kq} {mode} mode", "threads": threads,
+                             "value": round(wbytes / sec / 1e9, 2), "unit": "GB/s",
+                             "us": round(sec * 1e6, 1), "sample": "whole matvec, median of >= 3 runs and >= 1 s"})
+
+    # config 4: Q8_0 mul_mat at the four projections, T tokens (bounded: one call each)
+    proj = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
+    for threads in (1, nth):
+        oracle.set_threads(threads)
+        for T in (1, 4, 16, 64):
+            tot_s, tot_ops = 0.0, 0.0
+            for name, (Np, Kp) in proj.items():
+                if threads == 1 and T > 4:
+                    continue  # the 1-thread rows stop at 4 tokens to stay bounded
+                W = data.q8_0_weights(Np, Kp, seed=Np + Kp + 1)
+                xs = data.activations(T, Kp, seed=T + 200)
+                t0 = time.perf_counter()
+                oracle.q8_0_mul_mat_g(Np, Kp, T, xs, W)
+                tot_s += time.perf_counter() - t0
+                tot_ops += 2.0 * Np * Kp * T
+            if tot_s:
+                rows_out.append({"config": f"4: Q8_0 mul_mat T={T}, qkv+o+gate_up+down", "threads": threads,
+                                 "value": round(tot_ops / tot_s / 1e12, 5), "unit": "TOPS",
+                                 "us": round(tot_s * 1e6, 1), "sample": "one call per projection"})
     oracle.set_threads(1)
-    t_full = t_quant + t_rows * (M / rows)
-    tops = 2.0 * M * N * K / t_full / 1e12
-    Cg = C.cpu().numpy()
-    match = all(np.array_equal(Cg[r0:r0 + o.shape[0]].view(np.uint32), o.view(np.uint32))
-                for r0, o in sample_rows)
-    log(f"cpu baseline: {threads} threads, quantize {t_quant:.2f}s, {rows} rows in {t_rows:.2f}s "
-        f"-> {tops:.4f} TOPS (sampled rows bit-identical to GPU: {match})")
-    return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"oracle/ane_oracle.c (-O2, OpenMP over rows): quantize all of A and B "
-                      f"({t_quant:.2f} s) + {rows} of {M} rows of the int32 contraction and "
-                      f"epilogue ({t_rows:.2f} s), extrapolated to the full {M}x{N}x{K} op",
-            "gpu_rows_bit_identical": bool(match)}
+    model = _cpu_model()
+    log(f"cpu baseline: {model}, {nth} threads; config 2 {cfg2[nth]:.4f} TOPS ({cfg2[1]:.4f} at 1 thread); "
+        f"sampled rows bit-identical to the GPU: {match}")
+    return {"value": round(cfg2[nth], 5), "unit": "TOPS", "cores": nth, "kind": "port",
+            "cpu_model": model,
+            "sample": f"oracle/ane_oracle.c (-O2 -ffp-contract=off, OpenMP over output rows) on config 2 "
+                      f"({M}x{N}x{K}): quantize all of A and B + a bounded sample of the contraction's rows "
+                      f"(about 4 s), extrapolated to the whole op; every config's rows in 'rows'",
+            "gpu_rows_bit_identical": bool(match),
+            "rows": rows_out}
 
 
 if __name__ == "__main__":

@@ -1,8 +1,8 @@
-// peaks.hip -- measured ceilings that bench.py reports beside the datasheet
-// peaks: an int8 MFMA loop with no memory traffic (and the shader clock it
-// runs at), and plain HBM read and write streams.  Built into
-// libane_peaks.so, which only the benchmark loads; it is not part of ane's
-// interface.
+// bench_peaks.hip -- measured ceilings that bench.py reports beside the
+// datasheet peaks: an int8 MFMA loop with no memory traffic (and the shader
+// clock it runs at), and plain HBM read and write streams.  Built into
+// bench_peaks.so beside bench.py, which only the benchmark loads; it is not
+// part of ane_amd or of ane's interface.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
