@@ -35,6 +35,10 @@ class Op(enum.IntEnum):
     pack_b_i8 = 0x1B
     quantize_fp32_i8_channelwise = 0x1C
     dense_u8s8 = 0x1E
+    rms_norm_fp32 = 0x51
+    silu_fp32 = 0x54
+    rope_fp32 = 0x55
+    softmax_fp32 = 0x56
     q8_0_gemv = 0x57
     q4_0_gemv = 0x58
     cblas_igemm = 0x61
@@ -134,6 +138,16 @@ EXPORTS = (
     "ane_hip_q8_0_matvec_q8",
     "ane_hip_q8_0_gate_up_silu_quant",
     "ane_hip_silu_mul_quant",
+    "ane_hip_rms_norm",
+    "ane_hip_add_fp32",
+    "ane_hip_rms_norm_fp32",
+    "ane_hip_silu_fp32",
+    "ane_hip_rope_fp32",
+    "ane_hip_softmax_fp32",
+    "ane_decode_ggml_workspace_size",
+    "ane_decode_token_ggml",
+    "ane_ggml_backend_get_stream",
+    "ane_ggml_backend_set_stream",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -209,6 +223,16 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_hip_q8_0_matvec_q8": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _P]),
     "ane_hip_q8_0_gate_up_silu_quant": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _c.c_float, _P, _P, _P]),
     "ane_hip_silu_mul_quant": (_c.c_int, [_c.c_uint32, _P, _P, _P]),
+    "ane_hip_rms_norm": (_c.c_int, [_c.c_uint32, _P, _P, _c.c_float, _P, _P]),
+    "ane_hip_add_fp32": (_c.c_int, [_c.c_uint32, _P, _P, _P, _P]),
+    "ane_hip_rms_norm_fp32": (_c.c_int, [_c.c_uint32, _c.c_uint32, _c.c_float, _P, _P, _P, _P]),
+    "ane_hip_silu_fp32": (_c.c_int, [_c.c_uint64, _P, _P, _P]),
+    "ane_hip_rope_fp32": (_c.c_int, [_c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_float, _P, _P, _P]),
+    "ane_hip_softmax_fp32": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _P, _P]),
+    "ane_decode_ggml_workspace_size": (_c.c_size_t, [_P]),
+    "ane_decode_token_ggml": (_c.c_int, [_P, _P, _P, _c.c_float, _c.c_uint32, _P, _P, _c.c_size_t, _P, _c.c_int]),
+    "ane_ggml_backend_get_stream": (_P, [_P]),
+    "ane_ggml_backend_set_stream": (None, [_P, _P]),
 }
 
 
@@ -413,6 +437,34 @@ def rec_cblas_igemm(kind, flags, M, N, K, lda, ldb, ldc, alpha, beta, A, B, C) -
     _need(C, c, f"cblas_{kind} C")
     return encode(Op.cblas_igemm + IGEMM_VARIANTS[kind], u8(flags), u32(M), u32(N), u32(K), u32(lda), u32(ldb),
                   u32(ldc), f32(alpha), f32(beta), ptr(A), ptr(B), ptr(C))
+
+
+def rec_rms_norm(dim, eps, x, w, out) -> bytes:
+    """rms_norm_fp32 (0x51): [dim:u32][eps:f32][in][weight][out] (bytecode_interpreter.s:6509-6514)."""
+    for t, nm in ((x, "in"), (w, "weight"), (out, "out")):
+        _need(t, 4 * dim, f"rms_norm_fp32 {nm}")
+    return encode(Op.rms_norm_fp32, u32(dim), f32(eps), ptr(x), ptr(w), ptr(out))
+
+
+def rec_silu(count, x, out) -> bytes:
+    """silu_fp32 (0x54): [count:u32][in][out] (:6618-6621)."""
+    _need(x, 4 * count, "silu_fp32 in")
+    _need(out, 4 * count, "silu_fp32 out")
+    return encode(Op.silu_fp32, u32(count), ptr(x), ptr(out))
+
+
+def rec_rope(dim, pos, theta, x, out) -> bytes:
+    """rope_fp32 (0x55): [dim:u32][pos:u32][theta:f32][in][out] (:6715-6720)."""
+    _need(x, 4 * (dim // 2 * 2), "rope_fp32 in")
+    _need(out, 4 * (dim // 2 * 2), "rope_fp32 out")
+    return encode(Op.rope_fp32, u32(dim), u32(pos), f32(theta), ptr(x), ptr(out))
+
+
+def rec_softmax(dim, x, out) -> bytes:
+    """softmax_fp32 (0x56): [dim:u32][in][out] (:6914-6917)."""
+    _need(x, 4 * dim, "softmax_fp32 in")
+    _need(out, 4 * dim, "softmax_fp32 out")
+    return encode(Op.softmax_fp32, u32(dim), ptr(x), ptr(out))
 
 
 def rec_dense_fused_i8(M, N, K, scale, relu, A, B, C) -> bytes:
@@ -656,6 +708,13 @@ class GgmlBackend:
             raise AneError(6, "ane_ggml_backend_init failed")
         self.L.ane_ggml_backend_set_q8_mode(self.h, q8_mode)
 
+    @property
+    def stream(self) -> int:
+        return int(self.L.ane_ggml_backend_get_stream(self.h) or 0)
+
+    def set_stream(self, stream) -> None:
+        self.L.ane_ggml_backend_set_stream(self.h, _stream_handle(stream))
+
     def supports(self, node: GgmlTensor) -> bool:
         return bool(self.L.ane_ggml_supports_op(ctypes.byref(node)))
 
@@ -774,6 +833,46 @@ def decode_workspace(cfg, device="cuda"):
     import torch
 
     return torch.zeros(lib().ane_decode_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device=device)
+
+
+ARITH_BUILD = 0
+ARITH_REFERENCE = 1
+
+
+def rms_norm(K, x, w, eps, out, stream=None):
+    """The build's RMSNorm (the fused products' arithmetic), one row."""
+    check(lib().ane_hip_rms_norm(K, _p(x), _p(w), float(eps), _p(out), _stream_handle(stream)), "rms_norm")
+
+
+def rms_norm_fp32(rows, dim, eps, x, w, out, stream=None):
+    check(lib().ane_hip_rms_norm_fp32(rows, dim, float(eps), _p(x), _p(w), _p(out), _stream_handle(stream)),
+          "rms_norm_fp32")
+
+
+def silu_fp32(count, x, out, stream=None):
+    check(lib().ane_hip_silu_fp32(count, _p(x), _p(out), _stream_handle(stream)), "silu_fp32")
+
+
+def rope_fp32(rows, dim, pos, theta, x, out, stream=None):
+    check(lib().ane_hip_rope_fp32(rows, dim, pos, float(theta), _p(x), _p(out), _stream_handle(stream)),
+          "rope_fp32")
+
+
+def softmax_fp32(rows, dim, x, out, stream=None):
+    check(lib().ane_hip_softmax_fp32(rows, dim, _p(x), _p(out), _stream_handle(stream)), "softmax_fp32")
+
+
+def decode_ggml_workspace(cfg, device="cuda"):
+    import torch
+
+    return torch.zeros(lib().ane_decode_ggml_workspace_size(ctypes.byref(cfg)), dtype=torch.uint8, device=device)
+
+
+def decode_token_ggml(cfg, layers, table, pos, x, workspace, backend, arith=ARITH_BUILD, theta=500000.0):
+    """One token through the ggml backend (GgmlBackend): MUL_MAT nodes for the
+    products, the steps around them in the build's or the reference's arithmetic."""
+    check(lib().ane_decode_token_ggml(ctypes.byref(cfg), layers, _p(table), float(theta), pos, _p(x),
+                                      _p(workspace), workspace.numel(), backend.h, arith), "decode_token_ggml")
 
 
 def decode_token(cfg, layers, table, pos, x, workspace, stream=None):

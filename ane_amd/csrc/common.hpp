@@ -134,6 +134,42 @@ __device__ __forceinline__ uint32_t max8_u32(uint32_t m) {
 // with an exp approximation; fp32 expf here).
 __device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
+// The canonical sum of squares of RMSNorm over K = 32 * nb values, the same
+// bits whatever the workgroup shape that computes it:
+//   q(b, p) = (x0^2 + x1^2) + (x2^2 + x3^2) for part p (values 4p..4p+3) of
+//             32-block b, in fp64 (every square is exact);
+//   s(b)    = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
+//   c(l)    = s(l) + s(l + 64) + s(l + 128) + ... in increasing b, l < 64;
+//   ss      = the pairwise tree over c(0..63), adjacent pairs first.
+// Lanes 8k..8k+7 of a wave hold the eight parts of one block.
+__device__ __forceinline__ double sumsq4_f64(float4 f) {
+    return ((double)f.x * f.x + (double)f.y * f.y) + ((double)f.z * f.z + (double)f.w * f.w);
+}
+__device__ __forceinline__ double sum8_f64(double v) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    return v;
+}
+__device__ __forceinline__ double tree64_f64(double v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+// c(l) then the tree, by one whole wave over the block sums s[0..nb).
+__device__ __forceinline__ double canon_total_f64(const double* s, uint32_t nb) {
+    const uint32_t lane = threadIdx.x & 63;
+    double c = 0.0;
+    for (uint32_t b = lane; b < nb; b += 64) c += s[b];
+    return tree64_f64(c);
+}
+
+// RMSNorm's scale from the canonical sum of squares: 1 / sqrt(fl(fl(ss/K) + eps)).
+__device__ __forceinline__ float rms_inv(double ss, uint32_t K, float eps) {
+    const float ms = (float)(ss / (double)K);
+    return 1.0f / sqrtf(ms + eps);
+}
+
 // Four quantized values packed little-endian into one dword.
 __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
     return (uint32_t)(quant1(a, inv) & 0xff) | ((uint32_t)(quant1(b, inv) & 0xff) << 8) |

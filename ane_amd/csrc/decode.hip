@@ -21,6 +21,7 @@
 #include <math.h>
 
 #include "../../include/ane_decode.h"
+#include "../../include/ggml-ane-hip.h"
 #include "common.hpp"
 
 namespace ane {
@@ -358,6 +359,48 @@ k_silu_mul_quant(uint32_t nb, const float* __restrict__ gu, uint8_t* __restrict_
     }
 }
 
+// The build's RMSNorm on its own (one workgroup of 256 threads per row):
+// the canonical sum of squares of common.hpp, so the result is bit-identical
+// to the norm the fused products apply in their prologue.  Dynamic LDS:
+// K/32 doubles of block sums.
+__global__ void __launch_bounds__(256)
+k_rms_norm_build(uint32_t K, float eps, const float* __restrict__ x, const float* __restrict__ w,
+                 float* __restrict__ out) {
+    extern __shared__ double sums[];
+    __shared__ double tot;
+    const uint32_t nb = K / 32, part = threadIdx.x & 7;
+    for (uint32_t b0 = 0; b0 < nb; b0 += 32) {  // uniform trip count: whole 8-lane groups
+        const uint32_t b = b0 + (threadIdx.x >> 3);
+        float4 f = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (b < nb) f = *reinterpret_cast<const float4*>(x + b * 32 + part * 4);
+        const double sb = sum8_f64(sumsq4_f64(f));
+        if (part == 0 && b < nb) sums[b] = sb;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const double t = canon_total_f64(sums, nb);
+        if (threadIdx.x == 0) tot = t;
+    }
+    __syncthreads();
+    const float inv = rms_inv(tot, K, eps);
+    for (uint32_t i = threadIdx.x; i < K; i += 256) out[i] = __fmul_rn(__fmul_rn(x[i], inv), w[i]);
+}
+
+__global__ void __launch_bounds__(256)
+k_add(uint32_t n, const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = __fadd_rn(a[i], b[i]);
+}
+
+// h[i] = silu(g_i) * u_i (silu_mul1) on gate|up interleaved in 32-row groups.
+__global__ void __launch_bounds__(256)
+k_silu_mul_il(uint32_t F, const float* __restrict__ gu, float* __restrict__ h) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= F) return;
+    const uint32_t b = 64 * (i / 32) + (i % 32);
+    h[i] = silu_mul1(gu[b], gu[b + 32]);
+}
+
 bool cfg_ok(const ane_decode_config* c) {
     return c && c->head_dim == kHD && c->n_kv_heads > 0 && c->n_heads == kGroup * c->n_kv_heads &&
            c->hidden > 0 && c->ffn > 0 && c->ctx > 0 && c->ctx <= (1u << 20) && c->hidden % 256 == 0 &&
@@ -434,7 +477,72 @@ size_t layout(const ane_decode_config* c, uint8_t* base, DecodeWs* w) {
     return off;
 }
 
+// The ggml route's workspace: the norm output, qkv, the attention output,
+// a product output, gate|up, h, then the attention scratch (the build's
+// chunk partials or the reference mode's scores and probabilities).
+struct GgmlWs {
+    float *xn, *qkv, *attn, *y, *gu, *h;
+    void* att;
+    size_t attb;
+};
+
+size_t ggml_layout(const ane_decode_config* c, uint8_t* base, GgmlWs* w) {
+    const uint64_t nqkv = (uint64_t)(c->n_heads + 2 * c->n_kv_heads) * kHD, nq = (uint64_t)c->n_heads * kHD;
+    size_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const size_t o = off;
+        off += ceil_to(bytes, 256);
+        return base ? base + o : nullptr;
+    };
+    float* xn = reinterpret_cast<float*>(take((uint64_t)c->hidden * 4));
+    float* qkv = reinterpret_cast<float*>(take(nqkv * 4));
+    float* attn = reinterpret_cast<float*>(take(nq * 4));
+    float* y = reinterpret_cast<float*>(take((uint64_t)c->hidden * 4));
+    float* gu = reinterpret_cast<float*>(take((uint64_t)c->ffn * 8));
+    float* h = reinterpret_cast<float*>(take((uint64_t)c->ffn * 4));
+    size_t attb = ane_hip_attention_workspace_size(c);
+    const size_t refb = (size_t)c->n_heads * c->ctx * 8;
+    if (refb > attb) attb = refb;
+    void* att = take(attb);
+    if (w) *w = GgmlWs{xn, qkv, attn, y, gu, h, att, attb};
+    return off;
+}
+
+// One GGML_OP_MUL_MAT node: Q8_0 weights W (N rows of K values) times one
+// fp32 column x, into y -- ggml's shapes: src0 ne = {K, N}, src1 ne = {K, 1},
+// dst ne = {N, 1}, contiguous strides.
+struct MulMatNode {
+    ane_ggml_tensor w, a, d;
+    MulMatNode(const void* W, uint32_t N, uint32_t K, const float* x, float* y) : w(), a(), d() {
+        const size_t rb = (size_t)(K / 32) * 34;
+        w.type = ANE_GGML_TYPE_Q8_0;
+        w.ne[0] = K, w.ne[1] = N, w.ne[2] = w.ne[3] = 1;
+        w.nb[0] = 34, w.nb[1] = rb, w.nb[2] = w.nb[3] = rb * N;
+        w.data = const_cast<void*>(W);
+        a.type = ANE_GGML_TYPE_F32;
+        a.ne[0] = K, a.ne[1] = a.ne[2] = a.ne[3] = 1;
+        a.nb[0] = 4, a.nb[1] = a.nb[2] = a.nb[3] = (size_t)K * 4;
+        a.data = const_cast<float*>(x);
+        d.type = ANE_GGML_TYPE_F32;
+        d.op = ANE_GGML_OP_MUL_MAT;
+        d.ne[0] = N, d.ne[1] = d.ne[2] = d.ne[3] = 1;
+        d.nb[0] = 4, d.nb[1] = d.nb[2] = d.nb[3] = (size_t)N * 4;
+        d.src[0] = &w;
+        d.src[1] = &a;
+        d.data = y;
+    }
+};
+
 }  // namespace
+
+int rms_norm_ref_launch(uint32_t rows, uint32_t dim, float eps, const float* in, const float* w, float* out,
+                        uint64_t stride, hipStream_t s);
+int rope_ref_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos, uint32_t ctx, float theta,
+                       uint16_t* kc, uint16_t* vc, hipStream_t s);
+int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
+                         const uint16_t* kc, const uint16_t* vc, float* out, float* ws, hipStream_t s);
+int silu_mul_ref_il_launch(uint32_t F, const float* gu, float* h, hipStream_t s);
+
 }  // namespace ane
 
 using namespace ane;
@@ -549,5 +657,108 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
         const int st = run_layer(layers[l]);
         if (st) return st;
     }
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_rms_norm(uint32_t K, const float* x, const float* w, float eps, float* out, void* stream) {
+    if (K == 0) return ANE_OK;
+    if (!x || !w || !out) return ANE_ERR_BAD_POINTER;
+    if ((K & 31) || (((uintptr_t)x) & 15) || K > (1u << 20)) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_rms_norm_build, dim3(1), dim3(256), (K / 32) * 8, (hipStream_t)stream, K, eps, x, w, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_add_fp32(uint32_t n, const float* a, const float* b, float* out, void* stream) {
+    if (n == 0) return ANE_OK;
+    if (!a || !b || !out) return ANE_ERR_BAD_POINTER;
+    hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, n, a, b, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" size_t ane_decode_ggml_workspace_size(const ane_decode_config* cfg) {
+    if (!cfg_ok(cfg)) return 0;
+    return ggml_layout(cfg, nullptr, nullptr);
+}
+
+extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_decode_layer* layers,
+                                     const float* rope_table, float rope_theta, uint32_t pos, float* x,
+                                     void* workspace, size_t workspace_bytes, ane_ggml_backend_t backend,
+                                     int arith) {
+    if (!cfg_ok(cfg) || (arith != ANE_DECODE_ARITH_BUILD && arith != ANE_DECODE_ARITH_REFERENCE))
+        return ANE_ERR_INVALID_ARG;
+    if (!layers || !x || !backend || (arith == ANE_DECODE_ARITH_BUILD && !rope_table)) return ANE_ERR_BAD_POINTER;
+    if (pos >= cfg->ctx || (((uintptr_t)x) & 15)) return ANE_ERR_INVALID_ARG;
+    if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ggml_layout(cfg, nullptr, nullptr))
+        return ANE_ERR_WORKSPACE;
+    GgmlWs w;
+    ggml_layout(cfg, static_cast<uint8_t*>(workspace), &w);
+    const uint32_t H = cfg->hidden, F = cfg->ffn;
+    const uint32_t nq = cfg->n_heads * kHD, nqkv = (cfg->n_heads + 2 * cfg->n_kv_heads) * kHD;
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
+        const ane_decode_layer& L = layers[l];
+        if (!L.w_qkv || !L.w_o || !L.w_gate_up || !L.w_down || !L.attn_norm || !L.ffn_norm || !L.k_cache ||
+            !L.v_cache)
+            return ANE_ERR_BAD_POINTER;
+    }
+    // every product must be a node the hook computes before anything runs
+    if (cfg->n_layers > 0) {
+        const ane_decode_layer& L = layers[0];
+        const MulMatNode n1(L.w_qkv, nqkv, H, w.xn, w.qkv), n2(L.w_o, H, nq, w.attn, w.y),
+            n3(L.w_gate_up, 2 * F, H, w.xn, w.gu), n4(L.w_down, H, F, w.h, w.y);
+        if (!ane_ggml_supports_op(&n1.d) || !ane_ggml_supports_op(&n2.d) || !ane_ggml_supports_op(&n3.d) ||
+            !ane_ggml_supports_op(&n4.d))
+            return ANE_ERR_INVALID_ARG;
+    }
+    hipStream_t s = (hipStream_t)ane_ggml_backend_get_stream(backend);
+    const bool ref = arith == ANE_DECODE_ARITH_REFERENCE;
+    // the products' arithmetic goes with the mode: G (int8 dots) for the
+    // build's, R (opcode 0x57, what the reference's hook runs) for the reference's
+    ane_ggml_backend_set_q8_mode(backend, ref ? ANE_GGML_Q8_R : ANE_GGML_Q8_G);
+    const uint32_t gA = (H + 255) / 256;
+    int st;
+#define ANE_TRY(e)             \
+    do {                       \
+        if ((st = (e))) return st; \
+    } while (0)
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
+        const ane_decode_layer& L = layers[l];
+        if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.attn_norm, w.xn, H, s));
+        else ANE_TRY(ane_hip_rms_norm(H, x, L.attn_norm, cfg->eps, w.xn, s));
+        {
+            const MulMatNode n(L.w_qkv, nqkv, H, w.xn, w.qkv);
+            ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
+        }
+        if (ref) {
+            ANE_TRY(rope_ref_kv_launch(w.qkv, cfg->n_heads, cfg->n_kv_heads, pos, cfg->ctx, rope_theta, L.k_cache,
+                                       L.v_cache, s));
+            ANE_TRY(attention_ref_launch(cfg->n_heads, cfg->n_kv_heads, pos + 1, cfg->ctx, w.qkv, L.k_cache,
+                                         L.v_cache, w.attn, static_cast<float*>(w.att), s));
+        } else {
+            ANE_TRY(ane_hip_attention_decode_rope(cfg, w.qkv, rope_table, pos, L.k_cache, L.v_cache, w.attn, nullptr,
+                                                  w.att, w.attb, s));
+        }
+        {
+            const MulMatNode n(L.w_o, H, nq, w.attn, w.y);
+            ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
+        }
+        hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+        if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.ffn_norm, w.xn, H, s));
+        else ANE_TRY(ane_hip_rms_norm(H, x, L.ffn_norm, cfg->eps, w.xn, s));
+        {
+            const MulMatNode n(L.w_gate_up, 2 * F, H, w.xn, w.gu);
+            ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
+        }
+        if (ref) ANE_TRY(silu_mul_ref_il_launch(F, w.gu, w.h, s));
+        else hipLaunchKernelGGL(k_silu_mul_il, dim3((F + 255) / 256), dim3(256), 0, s, F, w.gu, w.h);
+        {
+            const MulMatNode n(L.w_down, H, F, w.h, w.y);
+            ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
+        }
+        hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+        ANE_HIP_CHECK_LAUNCH();
+    }
+#undef ANE_TRY
     return ANE_OK;
 }

@@ -1,0 +1,500 @@
+// decode_ref.hip -- the reference's decode-step handlers on gfx950, in their
+// exact fp32 operation sequence, and the steps of the reference-arithmetic
+// decode mode built from them.
+//
+// Handlers (src/bytecode_interpreter.s):
+//   0x51 rms_norm_fp32  :6508-6565   16 fmla lanes over x^2, FADDV, fdiv by
+//        (float)dim, fadd eps, frsqrte + two frsqrts steps, fl(fl(x*r)*w)
+//   0x54 silu_fp32      :6617-6713   exp(-x) by a floor range reduction, a
+//        degree-4 Horner polynomial and exponent-bit injection; 1/(1+e) by
+//        frecpe + two frecps steps; fl(x * r)
+//   0x55 rope_fp32      :6714-6912   ratio = theta^(2/dim) from a log/exp
+//        polynomial chain; per pair pos / power, range reduction by rint of
+//        x/pi, sin/cos Horner polynomials (fmad), rotation by fmul + fmls/fmla
+//   0x56 softmax_fp32   :6913-7009   fmax, the same exp polynomial, 16 fadd
+//        lanes, FADDV, fdiv 1/sum, fmul
+// The estimate instructions follow the Arm ARM pseudocode (FPRSqrtEstimate /
+// RecipSqrtEstimate, FPRecipEstimate / RecipEstimate, FPCR.AH = 0); FRSQRTS
+// and FRECPS are fused: (3 - a*b)/2 and 2 - a*b.  Every fmla / fmls / fmad is
+// an fmaf here, every other operation one correctly rounded fp32 operation
+// (the file is compiled with -ffp-contract=off and denormals kept).
+//
+// A "lane" of the handlers is a 16-wide SVE vector lane: sums and dot
+// products run in 16 sequential chains (element i in chain i mod 16) that
+// meet in the FADDV tree, and the kernels below keep exactly those chains.
+#include "../../include/ane_decode.h"
+#include "common.hpp"
+
+namespace ane {
+namespace {
+
+constexpr uint32_t kLog2e = 0x3FB8AA3Bu, kC4 = 0x3C1D955Au, kC3 = 0x3D635847u, kC2 = 0x3E75FDF0u,
+                   kLn2 = 0x3F317218u;
+
+__device__ __forceinline__ float f_of(uint32_t u) { return __uint_as_float(u); }
+
+// RecipSqrtEstimate(a), a in [128, 512) (the Arm ARM's loop).
+__device__ uint32_t recip_sqrt_estimate(uint32_t a) {
+    if (a < 256) a = a * 2 + 1;
+    else a = (((a >> 1) << 1) + 1) * 2;
+    uint64_t b = 512;
+    while ((uint64_t)a * (b + 1) * (b + 1) < (1ull << 28)) b++;
+    return (uint32_t)((b + 1) / 2);
+}
+
+__device__ float frsqrte_a(float x) {
+    const uint32_t u = __float_as_uint(x), sign = u >> 31, ex = (u >> 23) & 0xff, fr = u & 0x7fffff;
+    if (ex == 0xff && fr) return f_of(u | 0x00400000u);
+    if (ex == 0 && fr == 0) return f_of((sign << 31) | 0x7f800000u);
+    if (sign) return f_of(0x7fc00000u);
+    if (ex == 0xff) return 0.0f;
+    uint64_t f52 = (uint64_t)fr << 29;
+    int e = (int)ex;
+    if (e == 0) {
+        while (!(f52 & (1ull << 51))) {
+            f52 <<= 1;
+            e--;
+        }
+        f52 = (f52 << 1) & ((1ull << 52) - 1);
+    }
+    const uint32_t scaled = (e & 1) == 0 ? 256u + (uint32_t)(f52 >> 44) : 128u + (uint32_t)(f52 >> 45);
+    const int rexp = (380 - e) / 2;
+    const uint32_t est = recip_sqrt_estimate(scaled);
+    return f_of(((uint32_t)(rexp & 0xff) << 23) | ((est & 0xff) << 15));
+}
+
+__device__ __forceinline__ float frecpe_a(float x) {
+    const uint32_t u = __float_as_uint(x), sign = u >> 31, ex = (u >> 23) & 0xff, fr = u & 0x7fffff;
+    if (ex == 0xff && fr) return f_of(u | 0x00400000u);
+    if (ex == 0xff) return f_of(sign << 31);
+    if (ex == 0 && fr < (1u << 21)) return f_of((sign << 31) | 0x7f800000u);  // zero or |x| < 2^-128
+    uint64_t f52 = (uint64_t)fr << 29;
+    int e = (int)ex;
+    if (e == 0) {
+        if (!(f52 & (1ull << 51))) {
+            e = -1;
+            f52 = (f52 << 2) & ((1ull << 52) - 1);
+        } else {
+            f52 = (f52 << 1) & ((1ull << 52) - 1);
+        }
+    }
+    const uint32_t scaled = 256u + (uint32_t)(f52 >> 44);
+    int rexp = 253 - e;
+    const uint32_t est = ((1u << 19) / (scaled * 2 + 1) + 1) / 2;
+    uint64_t frac = (uint64_t)(est & 0xff) << 44;
+    if (rexp == 0) {
+        frac = (1ull << 51) | (frac >> 1);
+    } else if (rexp == -1) {
+        frac = (1ull << 50) | (frac >> 2);
+        rexp = 0;
+    }
+    return f_of((sign << 31) | ((uint32_t)(rexp & 0xff) << 23) | (uint32_t)(frac >> 29));
+}
+
+__device__ __forceinline__ bool inf_times_zero(float a, float b) {
+    return (__builtin_isinf(a) && b == 0.0f) || (a == 0.0f && __builtin_isinf(b));
+}
+__device__ __forceinline__ float frsqrts_a(float a, float b) {
+    return inf_times_zero(a, b) ? 1.5f : __fmul_rn(__builtin_fmaf(-a, b, 3.0f), 0.5f);
+}
+__device__ __forceinline__ float frecps_a(float a, float b) {
+    return inf_times_zero(a, b) ? 2.0f : __builtin_fmaf(-a, b, 2.0f);
+}
+
+// fcvtzs to int32: truncation, saturating, NaN -> 0.
+__device__ __forceinline__ int32_t cvtzs_a(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return 0x7fffffff;
+    if (x <= -2147483648.0f) return (int32_t)0x80000000u;
+    return (int32_t)x;
+}
+
+// The handlers' exp approximation (:6627-6665, :6965-6989): 2^n injected as
+// exponent bits (n + 127) << 23, n clamped below at -127 when `clamp`.
+__device__ __forceinline__ float exp_poly_a(float x, bool clamp) {
+    const float t = __fmul_rn(x, f_of(kLog2e));
+    const float n = floorf(t);
+    const float f = __fsub_rn(t, n);
+    float p = __fmul_rn(f_of(kC4), f);
+    p = __fadd_rn(p, f_of(kC3));
+    p = __fmul_rn(p, f);
+    p = __fadd_rn(p, f_of(kC2));
+    p = __fmul_rn(p, f);
+    p = __fadd_rn(p, f_of(kLn2));
+    p = __fmul_rn(p, f);
+    p = __fadd_rn(p, 1.0f);
+    int32_t ni = cvtzs_a(n);
+    if (clamp && ni < -127) ni = -127;
+    return __fmul_rn(p, f_of(((uint32_t)ni + 127u) << 23));
+}
+
+__device__ __forceinline__ float silu_a(float x) {
+    const float e = exp_poly_a(-x, true);
+    const float d = __fadd_rn(e, 1.0f);
+    float r = frecpe_a(d);
+    r = __fmul_rn(r, frecps_a(d, r));
+    r = __fmul_rn(r, frecps_a(d, r));
+    return __fmul_rn(x, r);
+}
+
+// rope_fp32's theta^(2/dim) (:6725-6783).
+__device__ float rope_ratio_a(uint32_t dim, float theta) {
+    const uint32_t tb = __float_as_uint(theta);
+    const int32_t e = (int32_t)((tb >> 23) & 0xff) - 127;
+    const float fe = (float)e;
+    const float m = f_of((tb & ~(0xffu << 23)) | (127u << 23));
+    const float t = __fsub_rn(m, 1.0f);
+    float l = __fmul_rn(f_of(0x3E943014u), t);
+    l = __fadd_rn(l, f_of(0xBEFBD464u));
+    l = __fmul_rn(l, t);
+    l = __fadd_rn(l, f_of(0x3F7FF972u));
+    l = __fmul_rn(l, t);
+    float lt = __fmul_rn(fe, f_of(kLn2));
+    lt = __fadd_rn(lt, l);
+    float step = __fdiv_rn(2.0f, (float)dim);
+    step = __fmul_rn(step, lt);
+    return exp_poly_a(step, false);
+}
+
+// The rotation of pair p (:6827-6905): power = ratio^(p mod 16) by
+// sequential products, times ratio^16 once per earlier 16-pair chunk.
+__device__ __forceinline__ float2 rope_pair_a(float a, float b, uint32_t p, float ratio, float posf) {
+    float power = 1.0f, r16 = 1.0f;
+    for (uint32_t k = 0; k < 16; k++) {
+        if (k == (p & 15)) power = r16;
+        r16 = __fmul_rn(r16, ratio);
+    }
+    for (uint32_t c = 0; c < (p >> 4); c++) power = __fmul_rn(power, r16);
+    const float freq = __fdiv_rn(posf, power);
+    const float nq = __builtin_rintf(__fmul_rn(freq, f_of(0x3EA2F983u)));
+    const uint32_t odd = ((uint32_t)cvtzs_a(nq) & 1u) << 31;
+    const float r = __builtin_fmaf(-nq, f_of(0x40490FDBu), freq);
+    const float r2 = __fmul_rn(r, r);
+    float sn = f_of(0xB9500D01u);
+    sn = __builtin_fmaf(sn, r2, f_of(0x3C088889u));
+    sn = __builtin_fmaf(sn, r2, f_of(0xBE2AAAABu));
+    sn = __builtin_fmaf(sn, r2, 1.0f);
+    sn = __fmul_rn(sn, r);
+    float cs = f_of(0xBAB60B61u);
+    cs = __builtin_fmaf(cs, r2, f_of(0x3D2AAAABu));
+    cs = __builtin_fmaf(cs, r2, -0.5f);
+    cs = __builtin_fmaf(cs, r2, 1.0f);
+    sn = f_of(__float_as_uint(sn) ^ odd);
+    cs = f_of(__float_as_uint(cs) ^ odd);
+    float oe = __fmul_rn(a, cs);
+    oe = __builtin_fmaf(-b, sn, oe);
+    float oo = __fmul_rn(b, cs);
+    oo = __builtin_fmaf(a, sn, oo);
+    return make_float2(oe, oo);
+}
+
+// NaN-propagating FMAX (AArch64, not FMAXNM): max(+0, -0) = +0.
+__device__ __forceinline__ float fmax_nan(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return __float_as_uint(a) >> 31 ? b : a;
+    return a > b ? a : b;
+}
+
+constexpr uint32_t kStageFloats = 8192;  // rows up to this long are staged in LDS (32 KB)
+
+// chain l of a 16-lane accumulation over v[0..n): acc = op(v[i], acc) for
+// i = l, l + 16, ... in order; 8 values are loaded ahead of each 8 steps.
+template <bool FMA_SQ>
+__device__ __forceinline__ float chain16(const float* v, uint32_t n, uint32_t l) {
+    float acc = 0.0f;
+    uint32_t i = l;
+    for (; i + 7 * 16 < n; i += 8 * 16) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) t[k] = v[i + 16 * k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc = FMA_SQ ? __builtin_fmaf(t[k], t[k], acc) : __fadd_rn(acc, t[k]);
+    }
+    for (; i < n; i += 16) acc = FMA_SQ ? __builtin_fmaf(v[i], v[i], acc) : __fadd_rn(acc, v[i]);
+    return acc;
+}
+
+// 0x51, one workgroup (256 threads) per row; the row is staged in LDS when
+// it fits.  Every lane of wave 0 runs chain lane & 15 (four copies of the 16
+// chains), so the FADDV tree reads only active DPP rows.
+__global__ void __launch_bounds__(256)
+k_rms_norm_ref(uint32_t dim, float eps, const float* __restrict__ in, const float* __restrict__ w,
+               float* __restrict__ out, uint64_t stride) {
+    __shared__ float rs;
+    __shared__ float xs[kStageFloats];
+    const float* x = in + blockIdx.x * stride;
+    float* o = out + blockIdx.x * stride;
+    const bool staged = dim <= kStageFloats;
+    if (staged) {
+        for (uint32_t i = threadIdx.x; i < dim; i += 256) xs[i] = x[i];
+        __syncthreads();
+    }
+    if (threadIdx.x < 64) {
+        const uint32_t l = threadIdx.x & 15;
+        const float acc = chain16<true>(staged ? xs : x, dim, l);
+        const float ss = faddv16(acc);
+        const float mean = __fdiv_rn(ss, (float)dim);
+        const float t = __fadd_rn(mean, eps);
+        float r = frsqrte_a(t);
+        float s = __fmul_rn(r, r);
+        s = frsqrts_a(t, s);
+        r = __fmul_rn(r, s);
+        s = __fmul_rn(r, r);
+        s = frsqrts_a(t, s);
+        r = __fmul_rn(r, s);
+        if (threadIdx.x == 0) rs = r;
+    }
+    __syncthreads();
+    const float r = rs;
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(__fmul_rn(x[i], r), w[i]);
+}
+
+__global__ void __launch_bounds__(256) k_silu_ref(uint64_t n, const float* __restrict__ in, float* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = silu_a(in[i]);
+}
+
+// 0x55 over `rows` rows of dim floats (row stride `stride` floats), one
+// thread per pair.
+__global__ void __launch_bounds__(256)
+k_rope_ref(uint32_t rows, uint32_t dim, uint32_t pos, float theta, const float* __restrict__ in,
+           float* __restrict__ out, uint64_t stride) {
+    const uint32_t pairs = dim / 2;
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (uint64_t)rows * pairs) return;
+    const uint32_t row = (uint32_t)(t / pairs), p = (uint32_t)(t - (uint64_t)row * pairs);
+    const float ratio = rope_ratio_a(dim, theta);
+    const float* x = in + row * stride;
+    const float2 v = rope_pair_a(x[2 * p], x[2 * p + 1], p, ratio, (float)pos);
+    float* o = out + row * stride;
+    o[2 * p] = v.x;
+    o[2 * p + 1] = v.y;
+}
+
+// 0x56, one workgroup per row: the max (any order: max is exact), e stored
+// in out, the 16 fadd chains (in wave 0, four copies), FADDV, 1/sum, scale.
+// A dim that is not a multiple of 16 leaves the last chains shorter.
+__global__ void __launch_bounds__(256)
+k_softmax_ref(uint32_t dim, const float* __restrict__ in, float* __restrict__ out, uint64_t stride) {
+    __shared__ float red[4];
+    __shared__ float sinv;
+    __shared__ float es[kStageFloats];
+    const float* x = in + blockIdx.x * stride;
+    float* o = out + blockIdx.x * stride;
+    const bool staged = dim <= kStageFloats;
+    float m = -__builtin_inff();
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) m = fmax_nan(m, x[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmax_nan(m, __shfl_xor(m, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmax_nan(fmax_nan(red[0], red[1]), fmax_nan(red[2], red[3]));
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) {
+        const float e = exp_poly_a(__fsub_rn(x[i], m), true);
+        if (staged) es[i] = e;
+        else o[i] = e;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float acc = chain16<false>(staged ? es : o, dim, threadIdx.x & 15);
+        const float inv = __fdiv_rn(1.0f, faddv16(acc));
+        if (threadIdx.x == 0) sinv = inv;
+    }
+    __syncthreads();
+    const float inv = sinv;
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(staged ? es[i] : o[i], inv);
+}
+
+__device__ __forceinline__ uint16_t f16_bits(float f) {
+    const _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+// ---------------------------------------------------- decode steps (reference mode)
+// RoPE (0x55 arithmetic, dim 128) of the q and k heads of the qkv vector at
+// pos: q rotated in place, k rotated and appended to the fp16 cache, v
+// appended.  One thread per pair (q and k heads) or per v element.
+__global__ void __launch_bounds__(256)
+k_rope_ref_kv(float* __restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos, uint32_t ctx, float theta,
+              uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t nrot = (n_heads + n_kv) * 64, nv = n_kv * 128;
+    if (t < nrot) {
+        const uint32_t head = t / 64, p = t % 64;
+        float* x = qkv + head * 128;
+        const float2 v = rope_pair_a(x[2 * p], x[2 * p + 1], p, rope_ratio_a(128, theta), (float)pos);
+        if (head < n_heads) {
+            x[2 * p] = v.x;
+            x[2 * p + 1] = v.y;
+        } else {
+            uint16_t* kc = k_cache + ((uint64_t)(head - n_heads) * ctx + pos) * 128;
+            kc[2 * p] = f16_bits(v.x);
+            kc[2 * p + 1] = f16_bits(v.y);
+        }
+    } else if (t < nrot + nv) {
+        const uint32_t i = t - nrot, g = i / 128, d = i % 128;
+        v_cache[((uint64_t)g * ctx + pos) * 128 + d] = f16_bits(qkv[(n_heads + n_kv) * 128 + i]);
+    }
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h); }
+
+// s[h][j] = fl(dot16(q_h, k_j) * fl(1/sqrt(128))), one thread per (h, j):
+// 16 chains of 8 fmas, then the FADDV tree in registers.
+__global__ void __launch_bounds__(256)
+k_attn_scores_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, const float* __restrict__ q,
+                  const uint16_t* __restrict__ k_cache, float* __restrict__ s) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (uint64_t)n_heads * len) return;
+    const uint32_t h = (uint32_t)(t / len), j = (uint32_t)(t - (uint64_t)h * len);
+    const float* qh = q + h * 128;
+    const uint16_t* kj = k_cache + ((uint64_t)(h / group) * ctx + j) * 128;
+    float acc[16];
+#pragma unroll
+    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int l = 0; l < 16; l++) acc[l] = __builtin_fmaf(qh[16 * i + l], h2f(kj[16 * i + l]), acc[l]);
+    float t8[8], t4[4];
+#pragma unroll
+    for (int l = 0; l < 8; l++) t8[l] = __fadd_rn(acc[2 * l], acc[2 * l + 1]);
+#pragma unroll
+    for (int l = 0; l < 4; l++) t4[l] = __fadd_rn(t8[2 * l], t8[2 * l + 1]);
+    const float dot = __fadd_rn(__fadd_rn(t4[0], t4[1]), __fadd_rn(t4[2], t4[3]));
+    s[(uint64_t)h * len + j] = __fmul_rn(dot, f_of(0x3DB504F3u));
+}
+
+// out[h][d] = FADDV over 16 chains, chain l = fma(p_j, v_j[d], acc) for
+// j = l mod 16 in increasing j: 16 lanes per (h, d).
+__global__ void __launch_bounds__(256)
+k_attn_pv_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, const float* __restrict__ p,
+              const uint16_t* __restrict__ v_cache, float* __restrict__ out) {
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t od = t >> 4, l = t & 15;  // output element (h, d)
+    const bool live = od < n_heads * 128;
+    const uint32_t h = live ? od / 128 : 0, d = od % 128;
+    const float* ph = p + (uint64_t)h * len;
+    const uint16_t* vg = v_cache + (uint64_t)(h / group) * ctx * 128 + d;
+    float acc = 0.0f;
+    if (live) {
+        uint32_t j = l;
+        for (; j + 7 * 16 < len; j += 8 * 16) {  // 8 positions loaded ahead of their 8 steps
+            float pj[8], vj[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                pj[k] = ph[j + 16 * k];
+                vj[k] = h2f(vg[(uint64_t)(j + 16 * k) * 128]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = __builtin_fmaf(pj[k], vj[k], acc);
+        }
+        for (; j < len; j += 16) acc = __builtin_fmaf(ph[j], h2f(vg[(uint64_t)j * 128]), acc);
+    }
+    const float v = faddv16(acc);  // whole 16-lane groups, live or not
+    if (live && l == 0) out[od] = v;
+}
+
+// h[i] = fl(silu_fp32(g_i) * u_i) on gate|up interleaved in 32-row groups.
+__global__ void __launch_bounds__(256)
+k_silu_mul_ref_il(uint32_t F, const float* __restrict__ gu, float* __restrict__ h) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= F) return;
+    const uint32_t b = 64 * (i / 32) + (i % 32);
+    h[i] = __fmul_rn(silu_a(gu[b]), gu[b + 32]);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------- launchers
+int rms_norm_ref_launch(uint32_t rows, uint32_t dim, float eps, const float* in, const float* w, float* out,
+                        uint64_t stride, hipStream_t s) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (rows > 0x7fffffffu) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_rms_norm_ref, dim3(rows), dim3(256), 0, s, dim, eps, in, w, out, stride);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int softmax_ref_launch(uint32_t rows, uint32_t dim, const float* in, float* out, uint64_t stride, hipStream_t s) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (rows > 0x7fffffffu) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_softmax_ref, dim3(rows), dim3(256), 0, s, dim, in, out, stride);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int rope_ref_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos, uint32_t ctx, float theta,
+                       uint16_t* kc, uint16_t* vc, hipStream_t s) {
+    const uint32_t n = (n_heads + n_kv) * 64 + n_kv * 128;
+    hipLaunchKernelGGL(k_rope_ref_kv, dim3((n + 255) / 256), dim3(256), 0, s, qkv, n_heads, n_kv, pos, ctx, theta,
+                       kc, vc);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+// Reference-mode attention over positions 0..len-1: scores, softmax_fp32
+// per head, then P.V.  ws holds n_heads * len floats of scores and as many
+// of probabilities.
+int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
+                         const uint16_t* kc, const uint16_t* vc, float* out, float* ws, hipStream_t s) {
+    const uint32_t group = n_heads / n_kv;
+    float* sc = ws;
+    float* pr = ws + (uint64_t)n_heads * len;
+    const uint64_t ns = (uint64_t)n_heads * len;
+    hipLaunchKernelGGL(k_attn_scores_ref, dim3((uint32_t)((ns + 255) / 256)), dim3(256), 0, s, n_heads, group, len,
+                       ctx, q, kc, sc);
+    hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
+    hipLaunchKernelGGL(k_attn_pv_ref, dim3((n_heads * 128 * 16 + 255) / 256), dim3(256), 0, s, n_heads, group, len,
+                       ctx, pr, vc, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int silu_mul_ref_il_launch(uint32_t F, const float* gu, float* h, hipStream_t s) {
+    hipLaunchKernelGGL(k_silu_mul_ref_il, dim3((F + 255) / 256), dim3(256), 0, s, F, gu, h);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+}  // namespace ane
+
+using namespace ane;
+
+extern "C" int ane_hip_rms_norm_fp32(uint32_t rows, uint32_t dim, float eps, const float* in, const float* w,
+                                     float* out, void* stream) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (!in || !w || !out) return ANE_ERR_BAD_POINTER;
+    return rms_norm_ref_launch(rows, dim, eps, in, w, out, dim, (hipStream_t)stream);
+}
+
+extern "C" int ane_hip_silu_fp32(uint64_t count, const float* in, float* out, void* stream) {
+    if (count == 0) return ANE_OK;
+    if (!in || !out) return ANE_ERR_BAD_POINTER;
+    const uint64_t blocks = (count + 255) / 256;
+    if (blocks > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_silu_ref, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, count, in, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_rope_fp32(uint32_t rows, uint32_t dim, uint32_t pos, float theta, const float* in, float* out,
+                                 void* stream) {
+    const uint64_t n = (uint64_t)rows * (dim / 2);
+    if (n == 0) return ANE_OK;
+    if (!in || !out) return ANE_ERR_BAD_POINTER;
+    if ((n + 255) / 256 > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_rope_ref, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, rows, dim,
+                       pos, theta, in, out, (uint64_t)dim);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+extern "C" int ane_hip_softmax_fp32(uint32_t rows, uint32_t dim, const float* in, float* out, void* stream) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (!in || !out) return ANE_ERR_BAD_POINTER;
+    return softmax_ref_launch(rows, dim, in, out, dim, (hipStream_t)stream);
+}

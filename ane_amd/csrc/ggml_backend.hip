@@ -195,6 +195,12 @@ extern "C" void ane_ggml_backend_free(ane_ggml_backend_t be) {
     delete be;
 }
 
+extern "C" void* ane_ggml_backend_get_stream(ane_ggml_backend_t be) { return be ? (void*)be->stream : nullptr; }
+
+extern "C" void ane_ggml_backend_set_stream(ane_ggml_backend_t be, void* stream) {
+    if (be) be->stream = (hipStream_t)stream;
+}
+
 extern "C" void ane_ggml_backend_set_q8_mode(ane_ggml_backend_t be, int mode) {
     if (be) be->q8_mode = mode == ANE_GGML_Q8_R ? ANE_GGML_Q8_R : ANE_GGML_Q8_G;
 }

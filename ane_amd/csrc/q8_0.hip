@@ -481,9 +481,9 @@ __device__ __forceinline__ float compute_qf(const int8_t* rowp, uint32_t l, uint
 
 // Optional fusions of the G-mode single-token kernel (the decode step):
 //  kFuseNorm: x' = fl(fl(x * inv) * w) with inv = 1 / sqrt(fl(fl(ss / K) + eps)),
-//    ss = sum of x^2 accumulated in fp64 (every x^2 is exact in fp64, so the
-//    fp32 value of ss / K does not depend on the summation order), then x' is
-//    quantized as usual;
+//    ss = the sum of x^2 in fp64 in the canonical order of common.hpp
+//    (sumsq4_f64 .. canon_total_f64), the same bits as the standalone
+//    ane_hip_rms_norm and the oracle, then x' is quantized as usual;
 //  kFuseResidual: y[n] = fl(FADDV(p) + r[n]) (r may alias y: each row is read
 //    by the wave that owns it, into LDS, before that wave writes it).
 //  kFuseSiluMul: the input is gate|up (2K floats) and the row quantized is
@@ -502,24 +502,6 @@ struct StreamFuse {
     float eps;
     const float* residual;
 };
-
-template <int NW>
-__device__ __forceinline__ double block_sum_f64(double v, double* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    wait_lgkmcnt0();
-    lds_barrier();
-    double s = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) s += red[w];
-    return s;
-}
-
-__device__ __forceinline__ float rms_inv(double ss, uint32_t K, float eps) {
-    const float ms = (float)(ss / (double)K);
-    return 1.0f / sqrtf(ms + eps);
-}
 
 // The prologue of the streaming kernels: copies the residual of rows
 // r0 .. r1-1 (at most 64, one per lane) into this wave's LDS slot rres,
@@ -577,13 +559,27 @@ __device__ __forceinline__ void stream_prologue(const XStage<MODE, NW * 64>& xst
         }
     }
     if (FUSE & kFuseNorm) {  // the host guarantees npass <= XB for this fusion
-        double ss = 0.0;
+        // the canonical order of common.hpp: block sums into the x staging
+        // area (free until the quantized x is stored), then wave 0's tree
+        double* sums = reinterpret_cast<double*>(xst.lds);
 #pragma unroll
         for (uint32_t k = 0; k < XB; k++) {
-            const float4 f = xv[k];  // lanes past the end hold zeros
-            ss += (double)f.x * f.x + (double)f.y * f.y + (double)f.z * f.z + (double)f.w * f.w;
+            if (k < npass) {  // uniform: every lane takes the same passes
+                const double sb = sum8_f64(sumsq4_f64(xv[k]));  // lanes past the end hold zeros
+                const uint32_t blk = k * XStage<MODE, NW * 64>::kPerPass + (threadIdx.x >> 3);
+                if ((threadIdx.x & 7) == 0 && blk < xst.n) sums[blk] = sb;
+            }
         }
-        ss = block_sum_f64<NW>(ss, red);
+        wait_lgkmcnt0();
+        lds_barrier();
+        if (threadIdx.x < 64) {
+            const double tot = canon_total_f64(sums, xst.n);
+            if (threadIdx.x == 0) red[0] = tot;
+        }
+        // a second barrier: the quantized x is stored over the block sums
+        wait_lgkmcnt0();
+        lds_barrier();
+        const double ss = red[0];
         const float inv = rms_inv(ss, xst.K, fz.eps);
 #pragma unroll
         for (uint32_t k = 0; k < XB; k++) {

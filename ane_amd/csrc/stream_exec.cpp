@@ -28,6 +28,7 @@
 #include <string>
 #include <utility>
 
+#include "../../include/ane_decode.h"
 #include "../../include/ane_hip.h"
 
 namespace {
@@ -377,6 +378,66 @@ int op_cblas_igemm(Reader& r, hipStream_t s, int variant) {
                       nm);
 }
 
+// The decode-step handlers (bytecode_interpreter.s:6508-7009).  Their loops
+// step 16 lanes with no tail, so a dim or count that is not a multiple of 16
+// (which never ends there) is refused.
+// 0x51 [dim:u32][eps:f32][in][w][out]  (:6509-6514)
+int op_rms_norm(Reader& r, hipStream_t s) {
+    const uint32_t dim = r.get<uint32_t>();
+    const float eps = r.get<float>();
+    const float* in = r.ptr<const float>();
+    const float* w = r.ptr<const float>();
+    float* out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "rms_norm_fp32 record truncated");
+    if (dim == 0) return ANE_OK;
+    if (dim % 16) return fail(ANE_ERR_INVALID_ARG, "rms_norm_fp32: dim %u is not a multiple of 16", dim);
+    CHECK(check_range(in, (uint64_t)dim * 4, "rms_norm_fp32 in", false, nullptr));
+    CHECK(check_range(w, (uint64_t)dim * 4, "rms_norm_fp32 weight", false, nullptr));
+    CHECK(check_range(out, (uint64_t)dim * 4, "rms_norm_fp32 out", false, nullptr));
+    return hip_status(ane_hip_rms_norm_fp32(1, dim, eps, in, w, out, s), "rms_norm_fp32");
+}
+
+// 0x54 [count:u32][in][out]  (:6618-6621)
+int op_silu(Reader& r, hipStream_t s) {
+    const uint32_t count = r.get<uint32_t>();
+    const float* in = r.ptr<const float>();
+    float* out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "silu_fp32 record truncated");
+    if (count == 0) return ANE_OK;
+    if (count % 16) return fail(ANE_ERR_INVALID_ARG, "silu_fp32: count %u is not a multiple of 16", count);
+    CHECK(check_range(in, (uint64_t)count * 4, "silu_fp32 in", false, nullptr));
+    CHECK(check_range(out, (uint64_t)count * 4, "silu_fp32 out", false, nullptr));
+    return hip_status(ane_hip_silu_fp32(count, in, out, s), "silu_fp32");
+}
+
+// 0x55 [dim:u32][pos:u32][theta:f32][in][out]  (:6715-6720); pairs dim/2
+int op_rope(Reader& r, hipStream_t s) {
+    const uint32_t dim = r.get<uint32_t>();
+    const uint32_t pos = r.get<uint32_t>();
+    const float theta = r.get<float>();
+    const float* in = r.ptr<const float>();
+    float* out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "rope_fp32 record truncated");
+    const uint64_t n = (uint64_t)(dim / 2) * 2;
+    if (n == 0) return ANE_OK;
+    CHECK(check_range(in, n * 4, "rope_fp32 in", false, nullptr));
+    CHECK(check_range(out, n * 4, "rope_fp32 out", false, nullptr));
+    return hip_status(ane_hip_rope_fp32(1, dim, pos, theta, in, out, s), "rope_fp32");
+}
+
+// 0x56 [dim:u32][in][out]  (:6914-6917)
+int op_softmax(Reader& r, hipStream_t s) {
+    const uint32_t dim = r.get<uint32_t>();
+    const float* in = r.ptr<const float>();
+    float* out = r.ptr<float>();
+    if (!r.ok) return fail(ANE_ERR_TRUNCATED, "softmax_fp32 record truncated");
+    if (dim == 0) return ANE_OK;
+    if (dim % 16) return fail(ANE_ERR_INVALID_ARG, "softmax_fp32: dim %u is not a multiple of 16", dim);
+    CHECK(check_range(in, (uint64_t)dim * 4, "softmax_fp32 in", false, nullptr));
+    CHECK(check_range(out, (uint64_t)dim * 4, "softmax_fp32 out", false, nullptr));
+    return hip_status(ane_hip_softmax_fp32(1, dim, in, out, s), "softmax_fp32");
+}
+
 // 0x58, 0x75-0x79 [M:u32][K:u32][x][W][y]: the other weight formats' GEMVs
 // (bytecode_interpreter.s:7071-7079, 11024-11032 and the same prologue in
 // each K-quant handler).
@@ -464,6 +525,10 @@ int run(const uint8_t* data, size_t size, hipStream_t s) {
             case ANE_OP_DENSE_FUSED_I8: st = op_dense_fused(r, s); break;
             case ANE_OP_GET_ROWS_Q8_0: st = op_get_rows(r, s, false); break;
             case ANE_OP_GET_ROWS_Q4_0: st = op_get_rows(r, s, true); break;
+            case ANE_OP_RMS_NORM_FP32: st = op_rms_norm(r, s); break;
+            case ANE_OP_SILU_FP32: st = op_silu(r, s); break;
+            case ANE_OP_ROPE_FP32: st = op_rope(r, s); break;
+            case ANE_OP_SOFTMAX_FP32: st = op_softmax(r, s); break;
             case ANE_OP_CBLAS_IGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_SIGNED); break;
             case ANE_OP_CBLAS_UGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_UNSIGNED); break;
             case ANE_OP_CBLAS_USGEMM: st = op_cblas_igemm(r, s, ANE_IGEMM_MIXED); break;

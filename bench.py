@@ -757,12 +757,57 @@ def bench_decode(args) -> dict:
     log(f"decode (config 5, {nl} layers, ctx {CTX}): {tok_ms * 1e3:.1f} us/token = {tok_s:.1f} tok/s; "
         f"mul_mat {mm_ms * 1e3:.1f} us ({mm_ms / tok_ms:.1%}); weights+KV {(wbytes + kv_bytes) / tok_ms / 1e6:.0f} GB/s")
     res = {"workload": f"config 5: decode 1 token, Llama-3-8B shapes, {nl} layers, Q8_0 weights, fp16 KV ctx {CTX}",
+           "route": "fused: ane_decode_token (6 launches per layer, the steps fused into the products)",
            "tok_s": round(tok_s, 1), "us_per_token": round(tok_ms * 1e3, 1),
            "mul_mat_us": round(mm_ms * 1e3, 1), "mul_mat_share": round(mm_ms / tok_ms, 4),
            "weights_bytes": int(wbytes), "kv_bytes": int(kv_bytes),
            "GB_s_weights_plus_kv": round((wbytes + kv_bytes) / tok_ms / 1e6, 1),
            "upper_bound_tok_s_at_8TBs": round(8e12 / (wbytes + kv_bytes), 1)}
-    del keep
+
+    # The same model through the ggml hook: each layer's four products are
+    # GGML_OP_MUL_MAT nodes run by ane_ggml_compute_forward, the steps around
+    # them separate kernels.  mul_mat share = a graph of the token's MUL_MAT
+    # nodes alone (same shapes, same backend) / the whole token.
+    be = ane_amd.GgmlBackend()
+    ws_g = ane_amd.decode_ggml_workspace(cfg)
+    T, Gop = ane_amd.GgmlType, ane_amd.GgmlOp
+    col_h = torch.randn(H, generator=gen, device="cuda")
+    col_f = torch.randn(F, generator=gen, device="cuda")
+    col_q = torch.randn(NH * HD, generator=gen, device="cuda")
+    out_big = torch.empty(2 * F, device="cuda")
+    nodes = []
+    for t in keep:
+        for W, N_, K_, xcol in ((t["w_qkv"], nqkv, H, col_h), (t["w_o"], H, NH * HD, col_q),
+                                (t["w_gate_up"], 2 * F, H, col_h), (t["w_down"], H, F, col_f)):
+            wt = ane_amd.ggml_tensor(T.Q8_0, [K_, N_], W)
+            xt = ane_amd.ggml_tensor(T.F32, [K_, 1], xcol)
+            nodes.append((wt, xt, ane_amd.ggml_tensor(T.F32, [N_, 1], out_big, op=Gop.MUL_MAT, src=(wt, xt))))
+    routes = {}
+    for name, arith, mode in (("build", ane_amd.ARITH_BUILD, 0), ("reference", ane_amd.ARITH_REFERENCE, 1)):
+        def token_g(st, arith=arith):
+            be.set_stream(st)
+            ane_amd.decode_token_ggml(cfg, layers, table, pos, x, ws_g, be, arith)
+
+        def mul_mats(st, mode=mode):
+            be.set_stream(st)
+            be.L.ane_ggml_backend_set_q8_mode(be.h, mode)
+            for n in nodes:
+                be.compute(n[2])
+
+        g_ms = graph_time(token_g, 3)
+        gm_ms = graph_time(mul_mats, 3)
+        routes[name] = {"tok_s": round(1e3 / g_ms, 1), "us_per_token": round(g_ms * 1e3, 1),
+                        "mul_mat_us": round(gm_ms * 1e3, 1), "mul_mat_share": round(gm_ms / g_ms, 4),
+                        "q8_0_mode": "G (int8 dots)" if mode == 0 else "R (opcode 0x57 arithmetic)"}
+        log(f"decode via the ggml hook, {name} arithmetic: {g_ms * 1e3:.1f} us/token = {1e3 / g_ms:.1f} tok/s; "
+            f"MUL_MAT nodes {gm_ms * 1e3:.1f} us ({gm_ms / g_ms:.1%})")
+    res["ggml_route"] = {
+        "how": "ane_decode_token_ggml: per layer 4 GGML_OP_MUL_MAT nodes (qkv, o, gate|up, down) through "
+               "ane_ggml_compute_forward, plus RMSNorm, RoPE + KV append, attention, SiLU*up and residual "
+               "kernels; 'build' is bit-identical to the fused route, 'reference' runs the handlers' arithmetic",
+        **routes}
+    be.close()
+    del keep, nodes
     torch.cuda.empty_cache()
     return res
 

@@ -140,6 +140,59 @@ int ane_hip_silu_mul(uint32_t n, const float* gu, float* h, void* stream);
  * aligned, n/32 * 36 bytes). */
 int ane_hip_silu_mul_quant(uint32_t n, const float* gu, void* xq, void* stream);
 
+/* The build's RMSNorm on its own, one row: out = fl(fl(x * inv) * w),
+ * inv = 1/sqrtf((float)(ss / K) + eps) with ss the fp64 sum of squares in
+ * the fixed order the fused products use, so the output is bit-identical to
+ * the normalised activation those kernels quantize.  K % 32 == 0, x 16-byte
+ * aligned. */
+int ane_hip_rms_norm(uint32_t K, const float* x, const float* w, float eps, float* out, void* stream);
+
+/* out = fl(a + b), n elements (out may alias a or b). */
+int ane_hip_add_fp32(uint32_t n, const float* a, const float* b, float* out, void* stream);
+
+/* The reference's decode-step handlers in their exact fp32 operation
+ * sequence (bytecode_interpreter.s; the estimates per the Arm ARM
+ * pseudocode of FRSQRTE / FRECPE):
+ *   0x51 rms_norm_fp32 (:6508-6565): rows x dim, out may alias in;
+ *   0x54 silu_fp32     (:6617-6713): count elements;
+ *   0x55 rope_fp32     (:6714-6912): rows x dim (each row rotated at pos,
+ *        adjacent pairs, ratio theta^(2/dim));
+ *   0x56 softmax_fp32  (:6913-7009): rows x dim, out may alias in.
+ * The handlers loop in 16-lane vectors with no tail, so stream_exec refuses
+ * dim % 16 != 0 for 0x51, 0x54 and 0x56; these kernel entries accept any
+ * dim, a short last vector contributing nothing (identical for multiples
+ * of 16). */
+int ane_hip_rms_norm_fp32(uint32_t rows, uint32_t dim, float eps, const float* in, const float* w, float* out,
+                          void* stream);
+int ane_hip_silu_fp32(uint64_t count, const float* in, float* out, void* stream);
+int ane_hip_rope_fp32(uint32_t rows, uint32_t dim, uint32_t pos, float theta, const float* in, float* out,
+                      void* stream);
+int ane_hip_softmax_fp32(uint32_t rows, uint32_t dim, const float* in, float* out, void* stream);
+
+/* One token through the ggml backend (include/ggml-ane-hip.h): each layer's
+ * four products are GGML_OP_MUL_MAT nodes computed by
+ * ane_ggml_compute_forward on the backend's stream, with the steps around
+ * them as separate kernels.
+ *   ANE_DECODE_ARITH_BUILD: the products in G mode and the steps in the
+ *     arithmetic of ane_decode_token (canonical fp64 RMSNorm, the RoPE table,
+ *     the chunked attention, expf SiLU): x and the caches come out
+ *     bit-identical to ane_decode_token's;
+ *   ANE_DECODE_ARITH_REFERENCE: the products in R mode (opcode 0x57, what the
+ *     reference hook runs) and the steps in the handlers' arithmetic:
+ *     rms_norm_fp32, rope_fp32 at rope_theta on q and k (dim 128), an
+ *     attention of 16-lane fma dot products scaled by fl(1/sqrt(128)),
+ *     softmax_fp32 over positions 0..pos and 16-lane fma sums over the
+ *     values, silu_fp32 times up, fp32 residual adds.
+ * Sets the backend's Q8_0 mode accordingly.  x 16-byte aligned; workspace
+ * from ane_decode_ggml_workspace_size (256-byte aligned).  Asynchronous. */
+#define ANE_DECODE_ARITH_BUILD 0
+#define ANE_DECODE_ARITH_REFERENCE 1
+struct ane_ggml_backend;
+size_t ane_decode_ggml_workspace_size(const struct ane_decode_config* cfg);
+int ane_decode_token_ggml(const struct ane_decode_config* cfg, const struct ane_decode_layer* layers,
+                          const float* rope_table, float rope_theta, uint32_t pos, float* x, void* workspace,
+                          size_t workspace_bytes, struct ane_ggml_backend* backend, int arith);
+
 #ifdef __cplusplus
 }
 #endif

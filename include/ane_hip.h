@@ -58,6 +58,10 @@ enum ane_status {
 #define ANE_OP_PACK_B_I8 0x1B
 #define ANE_OP_QUANTIZE_FP32_I8_CHANNELWISE 0x1C
 #define ANE_OP_DENSE_U8S8 0x1E
+#define ANE_OP_RMS_NORM_FP32 0x51 /* declared in ane_decode.h with 0x54-0x56 */
+#define ANE_OP_SILU_FP32 0x54
+#define ANE_OP_ROPE_FP32 0x55
+#define ANE_OP_SOFTMAX_FP32 0x56
 #define ANE_OP_Q8_0_GEMV 0x57
 #define ANE_OP_Q4_0_GEMV 0x58
 #define ANE_OP_CBLAS_IGEMM 0x61

@@ -75,6 +75,12 @@ ane_ggml_backend_t ane_ggml_backend_init(void* stream);
 void ane_ggml_backend_free(ane_ggml_backend_t backend);
 void ane_ggml_backend_set_q8_mode(ane_ggml_backend_t backend, int mode);
 
+/* The HIP stream the backend computes on (set_stream: later nodes run on
+ * `stream`; the workspace stays the backend's, so the caller orders the old
+ * stream's work before the new one's). */
+void* ane_ggml_backend_get_stream(ane_ggml_backend_t backend);
+void ane_ggml_backend_set_stream(ane_ggml_backend_t backend, void* stream);
+
 /* Replaces ane_dev_supports_op (ggml-ane.cpp:363-368): 1 if this backend
  * computes the node.  MUL_MAT: src0 Q8_0 or Q4_0 (the reference's routing,
  * ggml-ane.cpp:135-146; Q4_0 in its q4_0_gemv arithmetic for every token),

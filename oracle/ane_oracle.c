@@ -682,3 +682,283 @@ void oracle_cblas_igemm(int variant, int semantics, uint8_t flags, uint32_t M, u
         }
     }
 }
+
+/* ------------------------------------------------------------------------
+ * The decode-step handlers: rms_norm_fp32 (0x51), silu_fp32 (0x54),
+ * rope_fp32 (0x55) and softmax_fp32 (0x56), bytecode_interpreter.s:6508-7009,
+ * in their exact fp32 operation sequence.  fmla/fmls/fmad are fused (fmaf),
+ * every other operation rounds once.  The estimate instructions follow the
+ * Arm ARM pseudocode (FPRSqrtEstimate / RecipSqrtEstimate, FPRecipEstimate /
+ * RecipEstimate, FPCR.AH = 0, no increased precision), and the step
+ * instructions FRSQRTS / FRECPS are the fused (3 - a*b)/2 and 2 - a*b.
+ * ---------------------------------------------------------------------- */
+static inline float f_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* RecipSqrtEstimate(a), a in [128, 512): the Arm ARM's loop, literally. */
+static uint32_t recip_sqrt_estimate(uint32_t a) {
+    if (a < 256) a = a * 2 + 1;
+    else { a = (a >> 1) << 1; a = (a + 1) * 2; }
+    uint64_t b = 512;
+    while ((uint64_t)a * (b + 1) * (b + 1) < (1ull << 28)) b++;
+    return (uint32_t)((b + 1) / 2);
+}
+
+float oracle_frsqrte(float x) {
+    const uint32_t u = fbits(x), sign = u >> 31, ex = (u >> 23) & 0xff, fr = u & 0x7fffff;
+    if (ex == 0xff && fr) return f_of(u | 0x00400000u);          /* quiet the NaN */
+    if (ex == 0 && fr == 0) return f_of((sign << 31) | 0x7f800000u); /* +-0 -> +-inf */
+    if (sign) return f_of(0x7fc00000u);                           /* default NaN */
+    if (ex == 0xff) return 0.0f;                                  /* +inf -> +0 */
+    uint64_t f52 = (uint64_t)fr << 29;
+    int e = (int)ex;
+    if (e == 0) {                                                 /* normalise a denormal */
+        while (!(f52 & (1ull << 51))) { f52 <<= 1; e--; }
+        f52 = (f52 << 1) & ((1ull << 52) - 1);
+    }
+    const uint32_t scaled = (e & 1) == 0 ? 256u + (uint32_t)(f52 >> 44) : 128u + (uint32_t)(f52 >> 45);
+    const int rexp = (380 - e) / 2;
+    const uint32_t est = recip_sqrt_estimate(scaled);
+    return f_of(((uint32_t)(rexp & 0xff) << 23) | ((est & 0xff) << 15));
+}
+
+float oracle_frecpe(float x) {
+    const uint32_t u = fbits(x), sign = u >> 31, ex = (u >> 23) & 0xff, fr = u & 0x7fffff;
+    if (ex == 0xff && fr) return f_of(u | 0x00400000u);
+    if (ex == 0xff) return f_of(sign << 31);                       /* +-inf -> +-0 */
+    if (ex == 0 && fr == 0) return f_of((sign << 31) | 0x7f800000u);
+    if (ex == 0 && fr < (1u << 21)) return f_of((sign << 31) | 0x7f800000u); /* |x| < 2^-128: overflow, RNE */
+    uint64_t f52 = (uint64_t)fr << 29;
+    int e = (int)ex;
+    if (e == 0) {
+        if (!(f52 & (1ull << 51))) { e = -1; f52 = (f52 << 2) & ((1ull << 52) - 1); }
+        else f52 = (f52 << 1) & ((1ull << 52) - 1);
+    }
+    const uint32_t scaled = 256u + (uint32_t)(f52 >> 44);
+    int rexp = 253 - e;
+    const uint32_t a = scaled * 2 + 1;
+    const uint32_t est = ((1u << 19) / a + 1) / 2;                 /* RecipEstimate */
+    uint64_t frac = (uint64_t)(est & 0xff) << 44;
+    if (rexp == 0) frac = (1ull << 51) | (frac >> 1);
+    else if (rexp == -1) { frac = (1ull << 50) | (frac >> 2); rexp = 0; }
+    return f_of((sign << 31) | ((uint32_t)(rexp & 0xff) << 23) | (uint32_t)(frac >> 29));
+}
+
+static inline float frsqrts(float a, float b) {
+    if ((isinf(a) && b == 0.0f) || (a == 0.0f && isinf(b))) return 1.5f;
+    return fmaf(-a, b, 3.0f) * 0.5f;
+}
+static inline float frecps(float a, float b) {
+    if ((isinf(a) && b == 0.0f) || (a == 0.0f && isinf(b))) return 2.0f;
+    return fmaf(-a, b, 2.0f);
+}
+#define K_LOG2E 0x3FB8AA3Bu
+#define K_C4 0x3C1D955Au
+#define K_C3 0x3D635847u
+#define K_C2 0x3E75FDF0u
+#define K_LN2 0x3F317218u
+
+/* The exp approximation of silu/softmax (:6627-6665, :6965-6989): range
+ * reduction by floor, a degree-4 Horner polynomial of 2^f, and 2^n injected
+ * as exponent bits ((n + 127) << 23, n clamped below at -127 when clamp). */
+static float exp_poly(float x, int clamp) {
+    const float t = x * f_of(K_LOG2E);
+    const float n = floorf(t);
+    const float f = t - n;
+    float p = f_of(K_C4) * f;
+    p = p + f_of(K_C3);
+    p = p * f;
+    p = p + f_of(K_C2);
+    p = p * f;
+    p = p + f_of(K_LN2);
+    p = p * f;
+    p = p + 1.0f;
+    int32_t ni = cvtzs(n);
+    if (clamp && ni < -127) ni = -127;
+    return p * f_of(((uint32_t)ni + 127u) << 23);
+}
+
+/* 0x54 silu_fp32 (:6617-6713): out = fl(x * r), r = 1/(1 + e^-x) by frecpe
+ * and two frecps steps.  count elements. */
+void oracle_silu_fp32(uint32_t count, const float* in, float* out) {
+    for (uint32_t i = 0; i < count; i++) {
+        const float x = in[i];
+        const float e = exp_poly(-x, 1);
+        const float d = e + 1.0f;
+        float r = oracle_frecpe(d);
+        r = r * frecps(d, r);
+        r = r * frecps(d, r);
+        out[i] = x * r;
+    }
+}
+
+/* 0x51 rms_norm_fp32 (:6508-6565): 16 fmla lanes over x^2, FADDV, fdiv by
+ * (float)dim, fadd eps, frsqrte + two frsqrts steps, out = fl(fl(x*r)*w).
+ * dim a multiple of 16 (the handler's loops step 16 lanes to zero). */
+void oracle_rms_norm_fp32(uint32_t dim, float eps, const float* in, const float* w, float* out) {
+    float acc[16];
+    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+    for (uint32_t i = 0; i < dim; i++) acc[i % 16] = fmaf(in[i], in[i], acc[i % 16]);
+    const float ss = faddv16(acc);
+    const float mean = ss / (float)dim;
+    const float t = mean + eps;
+    float r = oracle_frsqrte(t);
+    float s = r * r;
+    s = frsqrts(t, s);
+    r = r * s;
+    s = r * r;
+    s = frsqrts(t, s);
+    r = r * s;
+    for (uint32_t i = 0; i < dim; i++) out[i] = (in[i] * r) * w[i];
+}
+
+/* 0x56 softmax_fp32 (:6913-7009): fmax over all, then e = exp_poly(x - max)
+ * stored, 16 fadd lanes of e (lane l takes i = l mod 16, increasing i),
+ * FADDV, fdiv 1/sum, out = fl(e * inv).  The handler needs dim % 16 == 0;
+ * here a lane past dim contributes nothing, which equals it for those. */
+void oracle_softmax_fp32(uint32_t dim, const float* in, float* out) {
+    if (dim == 0) return;
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < dim; i++) mx = fmaxA(mx, in[i]);
+    float acc[16];
+    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+    for (uint32_t i = 0; i < dim; i++) {
+        const float e = exp_poly(in[i] - mx, 1);
+        out[i] = e;
+        acc[i % 16] = acc[i % 16] + e;
+    }
+    const float inv = 1.0f / faddv16(acc);
+    for (uint32_t i = 0; i < dim; i++) out[i] = out[i] * inv;
+}
+
+/* rope_fp32's ratio theta^(2/dim) (:6725-6783): ln(theta) from the exponent
+ * and a cubic in the mantissa, then the exp polynomial without the clamp. */
+static float rope_ratio(uint32_t dim, float theta) {
+    const uint32_t tb = fbits(theta);
+    const int32_t e = (int32_t)((tb >> 23) & 0xff) - 127;
+    const float fe = (float)e;
+    const float m = f_of((tb & ~(0xffu << 23)) | (127u << 23));
+    const float t = m - 1.0f;
+    float l = f_of(0x3E943014u) * t;
+    l = l + f_of(0xBEFBD464u);
+    l = l * t;
+    l = l + f_of(0x3F7FF972u);
+    l = l * t;
+    float lt = fe * f_of(K_LN2);
+    lt = lt + l;
+    float step = 2.0f / (float)dim;
+    step = step * lt;
+    return exp_poly(step, 0);
+}
+
+/* 0x55 rope_fp32 (:6714-6912): pair k of 16-pair chunk c uses power =
+ * ratio^(k mod 16) (sequential products) times ratio^16 applied c times;
+ * freq = pos / power; r = freq - rint(freq / pi) * pi (fused); sin and cos
+ * by fmad Horner polynomials, both negated for odd rint; then
+ * out_even = fmls(a*cos, b, sin), out_odd = fmla(b*cos, a, sin). */
+void oracle_rope_fp32(uint32_t dim, uint32_t pos, float theta, const float* in, float* out) {
+    const uint32_t pairs = dim / 2;
+    if (!pairs) return;
+    const float ratio = rope_ratio(dim, theta);
+    float pw[16], s2 = 1.0f;
+    for (int k = 0; k < 16; k++) { pw[k] = s2; s2 = s2 * ratio; }
+    const float r16 = s2, posf = (float)pos;
+    for (uint32_t c = 0; c * 16 < pairs; c++) {
+        for (uint32_t l = 0; l < 16 && c * 16 + l < pairs; l++) {
+            const uint32_t p = c * 16 + l;
+            float power = pw[l];
+            for (uint32_t i = 0; i < c; i++) power = power * r16;
+            const float freq = posf / power;
+            const float nq = rintf(freq * f_of(0x3EA2F983u));
+            const uint32_t odd = ((uint32_t)cvtzs(nq) & 1u) << 31;
+            const float r = fmaf(-nq, f_of(0x40490FDBu), freq);
+            const float r2 = r * r;
+            float sn = f_of(0xB9500D01u);
+            sn = fmaf(sn, r2, f_of(0x3C088889u));
+            sn = fmaf(sn, r2, f_of(0xBE2AAAABu));
+            sn = fmaf(sn, r2, 1.0f);
+            sn = sn * r;
+            float cs = f_of(0xBAB60B61u);
+            cs = fmaf(cs, r2, f_of(0x3D2AAAABu));
+            cs = fmaf(cs, r2, -0.5f);
+            cs = fmaf(cs, r2, 1.0f);
+            sn = f_of(fbits(sn) ^ odd);
+            cs = f_of(fbits(cs) ^ odd);
+            const float a = in[2 * p], b = in[2 * p + 1];
+            float oe = a * cs;
+            oe = fmaf(-b, sn, oe);
+            float oo = b * cs;
+            oo = fmaf(a, sn, oo);
+            out[2 * p] = oe;
+            out[2 * p + 1] = oo;
+        }
+    }
+}
+
+/* The build's RMSNorm (the fused decode kernels and ane_hip_rms_norm): the
+ * canonical fp64 sum of squares (per 32-block part sums, block sums, 64
+ * strided lane sums, adjacent-pairs tree), ms = (float)(ss / K), inv =
+ * 1 / sqrtf(ms + eps), out = fl(fl(x * inv) * w).  K % 32 == 0. */
+void oracle_rms_norm_build(uint32_t K, float eps, const float* x, const float* w, float* out) {
+    const uint32_t nb = K / 32;
+    double c[64];
+    for (int l = 0; l < 64; l++) c[l] = 0.0;
+    for (uint32_t b = 0; b < nb; b++) {
+        double q[8];
+        for (int p = 0; p < 8; p++) {
+            const float* v = x + 32 * b + 4 * p;
+            q[p] = ((double)v[0] * v[0] + (double)v[1] * v[1]) + ((double)v[2] * v[2] + (double)v[3] * v[3]);
+        }
+        const double sb = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+        c[b % 64] = c[b % 64] + sb;
+    }
+    for (int off = 1; off < 64; off <<= 1) {
+        double n[64];
+        for (int l = 0; l < 64; l++) n[l] = c[l] + c[l ^ off];
+        memcpy(c, n, sizeof c);
+    }
+    const float ms = (float)(c[0] / (double)K);
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = 0; i < K; i++) out[i] = (x[i] * inv) * w[i];
+}
+
+/* 16-lane dot product in the handlers' style: lane l accumulates
+ * fma(a[i], b[i], acc) for i = l mod 16 in increasing i, then FADDV. */
+static float dot16(const float* a, const float* b, uint32_t n) {
+    float acc[16];
+    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+    for (uint32_t i = 0; i < n; i++) acc[i % 16] = fmaf(a[i], b[i], acc[i % 16]);
+    return faddv16(acc);
+}
+
+/* Decode attention in the reference-arithmetic mode (the build's
+ * composition of the handlers' arithmetic: the reference has no single-query
+ * attention over a cache): for query head h and positions j < len of kv head
+ * g = h / (n_heads / n_kv):  s_j = fl(dot16(q_h, k_j) * c), c = fl(1/sqrt(128)),
+ * p = softmax_fp32(s), out_h[d] = FADDV of 16 lanes, lane l accumulating
+ * fma(p_j, v_j[d], acc) for j = l mod 16 in increasing j.  k and v are fp16
+ * [n_kv][ctx][128], widened exactly. */
+void oracle_attention_ref(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
+                          const uint16_t* kc, const uint16_t* vc, float* out) {
+    const uint32_t G = n_heads / n_kv;
+    const float c = f_of(0x3DB504F3u);
+    float* s = (float*)malloc(sizeof(float) * (len ? len : 1));
+    float* p = (float*)malloc(sizeof(float) * (len ? len : 1));
+    float kj[128];
+    for (uint32_t h = 0; h < n_heads; h++) {
+        const uint32_t g = h / G;
+        for (uint32_t j = 0; j < len; j++) {
+            for (int d = 0; d < 128; d++) kj[d] = oracle_f16_to_f32(kc[((size_t)g * ctx + j) * 128 + d]);
+            s[j] = dot16(q + (size_t)h * 128, kj, 128) * c;
+        }
+        oracle_softmax_fp32(len, s, p);
+        for (int d = 0; d < 128; d++) {
+            float acc[16];
+            for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+            for (uint32_t j = 0; j < len; j++)
+                acc[j % 16] = fmaf(p[j], oracle_f16_to_f32(vc[((size_t)g * ctx + j) * 128 + d]), acc[j % 16]);
+            out[(size_t)h * 128 + d] = faddv16(acc);
+        }
+    }
+    free(s);
+    free(p);
+}

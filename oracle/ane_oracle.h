@@ -162,6 +162,31 @@ void oracle_cblas_igemm(int variant, int semantics, uint8_t flags, uint32_t M, u
                         uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha, float beta, const void* A,
                         const void* B, float* C);
 
+/* The decode-step handlers in their exact fp32 sequence
+ * (bytecode_interpreter.s:6508-7009), with FRSQRTE / FRECPE from the Arm
+ * ARM pseudocode (FPRSqrtEstimate, FPRecipEstimate; FPCR.AH = 0):
+ *   0x51 rms_norm_fp32  :6508-6565  dim % 16 == 0
+ *   0x54 silu_fp32      :6617-6713
+ *   0x55 rope_fp32      :6714-6912  adjacent pairs, ratio theta^(2/dim)
+ *   0x56 softmax_fp32   :6913-7009  (dim % 16 != 0: absent lanes add nothing)
+ * oracle_frsqrte / oracle_frecpe expose the two estimates. */
+float oracle_frsqrte(float x);
+float oracle_frecpe(float x);
+void oracle_rms_norm_fp32(uint32_t dim, float eps, const float* in, const float* w, float* out);
+void oracle_silu_fp32(uint32_t count, const float* in, float* out);
+void oracle_rope_fp32(uint32_t dim, uint32_t pos, float theta, const float* in, float* out);
+void oracle_softmax_fp32(uint32_t dim, const float* in, float* out);
+
+/* The build's RMSNorm (fused decode kernels, ane_hip_rms_norm): fp64 sum of
+ * squares in a fixed canonical order, inv = 1/sqrtf((float)(ss/K) + eps),
+ * out = fl(fl(x*inv)*w). */
+void oracle_rms_norm_build(uint32_t K, float eps, const float* x, const float* w, float* out);
+
+/* Reference-arithmetic decode attention: scores fl(dot16(q, k_j) * fl(1/sqrt(128))),
+ * softmax_fp32, then 16-lane fma chains over positions and FADDV. */
+void oracle_attention_ref(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
+                          const uint16_t* kc, const uint16_t* vc, float* out);
+
 /* IEEE half -> float (exact), as fcvt s, h. */
 float oracle_f16_to_f32(uint16_t h);
 

@@ -51,6 +51,14 @@ class Oracle:
             "oracle_f16_to_f32": (c.c_float, [c.c_uint16]),
             "oracle_get_rows_q8_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
             "oracle_get_rows_q4_0": (None, [c.c_uint32, c.c_uint32, P, P, P]),
+            "oracle_frsqrte": (c.c_float, [c.c_float]),
+            "oracle_frecpe": (c.c_float, [c.c_float]),
+            "oracle_rms_norm_fp32": (None, [c.c_uint32, c.c_float, P, P, P]),
+            "oracle_silu_fp32": (None, [c.c_uint32, P, P]),
+            "oracle_rope_fp32": (None, [c.c_uint32, c.c_uint32, c.c_float, P, P]),
+            "oracle_softmax_fp32": (None, [c.c_uint32, P, P]),
+            "oracle_rms_norm_build": (None, [c.c_uint32, c.c_float, P, P, P]),
+            "oracle_attention_ref": (None, [c.c_uint32, c.c_uint32, c.c_uint32, c.c_uint32, P, P, P, P]),
             "oracle_cblas_igemm": (None, [c.c_int, c.c_int, c.c_uint8, c.c_uint32, c.c_uint32, c.c_uint32,
                                           c.c_uint32, c.c_uint32, c.c_uint32, c.c_float, c.c_float, P, P, P]),
         }
@@ -186,6 +194,56 @@ class Oracle:
         self.lib.oracle_cblas_igemm(variant, semantics, flags, M, N, K, lda, ldb, ldc, np.float32(alpha),
                                     np.float32(beta), _p(A), _p(B), _p(C))
         return C
+
+    # the decode-step handlers 0x51 / 0x54 / 0x55 / 0x56 and the build's RMSNorm
+    def frsqrte(self, x) -> np.float32:
+        return np.float32(self.lib.oracle_frsqrte(np.float32(x)))
+
+    def frecpe(self, x) -> np.float32:
+        return np.float32(self.lib.oracle_frecpe(np.float32(x)))
+
+    def rms_norm_fp32(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.zeros(max(x.size, 1), np.float32)
+        self.lib.oracle_rms_norm_fp32(x.size, np.float32(eps), _p(x), _p(w), _p(out))
+        return out[: x.size]
+
+    def silu_fp32(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(max(x.size, 1), np.float32)
+        self.lib.oracle_silu_fp32(x.size, _p(x), _p(out))
+        return out[: x.size]
+
+    def rope_fp32(self, x, pos, theta):
+        x = np.ascontiguousarray(x, np.float32)
+        out = x.copy()
+        self.lib.oracle_rope_fp32(x.size, pos, np.float32(theta), _p(x), _p(out))
+        return out
+
+    def softmax_fp32(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(max(x.size, 1), np.float32)
+        self.lib.oracle_softmax_fp32(x.size, _p(x), _p(out))
+        return out[: x.size]
+
+    def rms_norm_build(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.zeros(max(x.size, 1), np.float32)
+        self.lib.oracle_rms_norm_build(x.size, np.float32(eps), _p(x), _p(w), _p(out))
+        return out[: x.size]
+
+    def attention_ref(self, q, kc, vc, length):
+        """q [n_heads][128] fp32, kc/vc fp16 [n_kv][ctx][128] -> [n_heads][128]."""
+        q = np.ascontiguousarray(q, np.float32)
+        kc = np.ascontiguousarray(kc, np.float16)
+        vc = np.ascontiguousarray(vc, np.float16)
+        nh, nkv, ctx = q.shape[0], kc.shape[0], kc.shape[1]
+        out = np.zeros((nh, 128), np.float32)
+        self.lib.oracle_attention_ref(nh, nkv, length, ctx, _p(q), _p(kc.view(np.uint16)),
+                                      _p(vc.view(np.uint16)), _p(out))
+        return out
 
     def f16_to_f32(self, h: int) -> float:
         return self.lib.oracle_f16_to_f32(h)

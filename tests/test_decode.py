@@ -88,6 +88,30 @@ def test_workspace_sizes():
     assert L.ane_decode_workspace_size(ctypes.byref(bad)) == 0
 
 
+def test_decode_refuses_unsupported_configs_before_launching():
+    """Shapes the products cannot take (ffn not a multiple of 256) and
+    misaligned weights are refused up front: nothing is launched, so x and
+    the caches (here fake addresses that are never touched) stay as they
+    were.  No GPU is needed to reach these checks."""
+    L = ane_amd.lib()
+    x = (ctypes.c_float * 4096)(*([1.5] * 4096))
+    ws = ctypes.create_string_buffer(1 << 16)
+    table = ctypes.c_void_p(0x1000)
+    for cfg in (ane_amd.DecodeConfig(2, 4096, 14336 + 32, 32, 8, 128, 4096, 1e-5),
+                ane_amd.DecodeConfig(2, 4096 + 32, 14336, 32, 8, 128, 4096, 1e-5)):
+        layers = (ane_amd.DecodeLayer * 2)(*[ane_amd.DecodeLayer(*([0x10000] * 8)) for _ in range(2)])
+        assert L.ane_decode_token(ctypes.byref(cfg), layers, table, 0, x, ws, len(ws), None) == 1
+        assert L.ane_decode_workspace_size(ctypes.byref(cfg)) == 0
+    cfg = ane_amd.DecodeConfig(2, 4096, 14336, 32, 8, 128, 4096, 1e-5)
+    need = L.ane_decode_workspace_size(ctypes.byref(cfg))
+    big = ctypes.create_string_buffer(need + 256)
+    base = (ctypes.addressof(big) + 255) & ~255
+    layers = (ane_amd.DecodeLayer * 2)(ane_amd.DecodeLayer(*([0x10000] * 8)),
+                                       ane_amd.DecodeLayer(0x10008, *([0x10000] * 7)))  # layer 1's w_qkv misaligned
+    assert L.ane_decode_token(ctypes.byref(cfg), layers, table, 0, x, base, need, None) == 1
+    assert list(x)[:4] == [1.5] * 4
+
+
 # ------------------------------------------------------------------ GPU
 def dev(a):
     import torch
