@@ -38,5 +38,14 @@ int main() {
     ane::dispatch(ane::Op::cblas_usgemm, uint8_t(3), uint32_t(5), uint32_t(7), uint32_t(130), uint32_t(9),
                   uint32_t(140), uint32_t(11), -1.0f, 2.0f, reinterpret_cast<uintptr_t>(A),
                   reinterpret_cast<uintptr_t>(B), reinterpret_cast<uintptr_t>(C));
+    // test_transformer.cpp:105-107, 184-185, 269-270; test_new_ops.cpp:589-590
+    ane::dispatch(ane::Op::rms_norm_fp32, uint32_t(4096), 1e-5f, reinterpret_cast<uintptr_t>(xf),
+                  reinterpret_cast<uintptr_t>(B), reinterpret_cast<uintptr_t>(C));
+    ane::dispatch(ane::Op::softmax_fp32, uint32_t(4096), reinterpret_cast<uintptr_t>(xf),
+                  reinterpret_cast<uintptr_t>(C));
+    ane::dispatch(ane::Op::silu_fp32, uint32_t(14336), reinterpret_cast<uintptr_t>(xf),
+                  reinterpret_cast<uintptr_t>(C));
+    ane::dispatch(ane::Op::rope_fp32, uint32_t(128), uint32_t(7), 500000.0f, reinterpret_cast<uintptr_t>(xf),
+                  reinterpret_cast<uintptr_t>(C));
     return 0;
 }
