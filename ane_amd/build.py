@@ -22,6 +22,9 @@ OBJ = PKG / "_build"
 LIB = PKG / "libane_amd.so"
 PEAKS_SRC = ROOT / "bench_peaks.hip"
 PEAKS_LIB = ROOT / "bench_peaks.so"
+GGML_SRC = PKG / "ggml" / "ggml-ane.cpp"
+GGML_IFACE = ROOT / "tests" / "ggml_iface"
+GGML_TEST_LIB = GGML_IFACE / "libggml_ane_test.so"
 
 ARCH = "gfx950"
 
@@ -86,6 +89,27 @@ def build_peaks(verbose: bool = False) -> Path:
     return PEAKS_LIB
 
 
+def ggml_adapter_cmd(out: Path) -> list[str]:
+    """g++ line building the ggml registry adapter (ane_amd/ggml/ggml-ane.cpp)
+    against the restated ggml interface of tests/ggml_iface, with that
+    folder's test harness, into one shared library linking libane_amd.so.
+    In a real build the adapter is compiled inside a ggml tree instead."""
+    return ["g++", "-std=c++17", "-O1", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
+            "-I/opt/rocm/include", f"-I{ROOT / 'include'}", f"-I{PKG / 'ggml'}", f"-I{GGML_IFACE}",
+            str(GGML_SRC), str(GGML_IFACE / "ggml_test_support.cpp"), "-o", str(out),
+            f"-L{PKG}", "-lane_amd", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/../../ane_amd",
+            "-L/opt/rocm/lib", "-lamdhip64"]
+
+
+def build_ggml_adapter(verbose: bool = False) -> Path:
+    tmp = GGML_TEST_LIB.with_suffix(".so.tmp")
+    _run(ggml_adapter_cmd(tmp))
+    os.replace(tmp, GGML_TEST_LIB)
+    if verbose:
+        print(f"built {GGML_TEST_LIB}")
+    return GGML_TEST_LIB
+
+
 def build_oracle(verbose: bool = False) -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     out = ROOT / "oracle" / "libane_oracle.so"
@@ -98,6 +122,7 @@ def build_all(verbose: bool = False) -> None:
     build_oracle(verbose)
     build_library(verbose)
     build_peaks(verbose)
+    build_ggml_adapter(verbose)
 
 
 if __name__ == "__main__":
