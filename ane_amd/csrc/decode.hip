@@ -359,22 +359,48 @@ k_silu_mul_quant(uint32_t nb, const float* __restrict__ gu, uint8_t* __restrict_
     }
 }
 
-// The build's RMSNorm on its own (one workgroup of 256 threads per row):
-// the canonical sum of squares of common.hpp, so the result is bit-identical
-// to the norm the fused products apply in their prologue.  Dynamic LDS:
-// K/32 doubles of block sums.
+// The build's RMSNorm of one row, with an optional residual add first:
+// x' = y ? fl(x + y) : x, written to xsum when y is given (xsum may alias x:
+// every element is read and written by the same thread); out =
+// fl(fl(x' * inv) * w).  The sum of squares takes the canonical order of
+// common.hpp, so the result is bit-identical to the norm the fused products
+// apply in their prologue.  One workgroup of 256 threads; in pass p, thread
+// t holds 4 values of block 32p + t/8 (x and y 16-byte aligned).  A batch of
+// kNormBatch passes (K <= 16384 in one batch) is loaded before its first
+// reduction, and kept in registers for the output when one batch holds the
+// row.  Dynamic LDS: K/32 doubles of block sums.
+constexpr uint32_t kNormBatch = 16;
 __global__ void __launch_bounds__(256)
-k_rms_norm_build(uint32_t K, float eps, const float* __restrict__ x, const float* __restrict__ w,
-                 float* __restrict__ out) {
+k_rms_norm_build(uint32_t K, float eps, const float* x, const float* __restrict__ y, const float* __restrict__ w,
+                 float* xsum, float* __restrict__ out) {
     extern __shared__ double sums[];
     __shared__ double tot;
-    const uint32_t nb = K / 32, part = threadIdx.x & 7;
-    for (uint32_t b0 = 0; b0 < nb; b0 += 32) {  // uniform trip count: whole 8-lane groups
-        const uint32_t b = b0 + (threadIdx.x >> 3);
+    const uint32_t nb = K / 32, part = threadIdx.x & 7, npass = (nb + 31) / 32;
+    auto load = [&](uint32_t p) {
+        const uint32_t b = 32 * p + (threadIdx.x >> 3);
         float4 f = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (b < nb) f = *reinterpret_cast<const float4*>(x + b * 32 + part * 4);
-        const double sb = sum8_f64(sumsq4_f64(f));
-        if (part == 0 && b < nb) sums[b] = sb;
+        if (b < nb) {
+            f = *reinterpret_cast<const float4*>(x + b * 32 + part * 4);
+            if (y) {
+                const float4 r = *reinterpret_cast<const float4*>(y + b * 32 + part * 4);
+                f = make_float4(__fadd_rn(f.x, r.x), __fadd_rn(f.y, r.y), __fadd_rn(f.z, r.z), __fadd_rn(f.w, r.w));
+            }
+        }
+        return f;
+    };
+    float4 f[kNormBatch];
+    for (uint32_t p0 = 0; p0 < npass; p0 += kNormBatch) {
+#pragma unroll
+        for (uint32_t k = 0; k < kNormBatch; k++)
+            if (p0 + k < npass) f[k] = load(p0 + k);
+#pragma unroll
+        for (uint32_t k = 0; k < kNormBatch; k++) {
+            if (p0 + k < npass) {  // uniform: whole 8-lane groups take the same passes
+                const uint32_t b = 32 * (p0 + k) + (threadIdx.x >> 3);
+                const double sb = sum8_f64(sumsq4_f64(f[k]));
+                if (part == 0 && b < nb) sums[b] = sb;
+            }
+        }
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -383,7 +409,26 @@ k_rms_norm_build(uint32_t K, float eps, const float* __restrict__ x, const float
     }
     __syncthreads();
     const float inv = rms_inv(tot, K, eps);
-    for (uint32_t i = threadIdx.x; i < K; i += 256) out[i] = __fmul_rn(__fmul_rn(x[i], inv), w[i]);
+    for (uint32_t p0 = 0; p0 < npass; p0 += kNormBatch) {
+        if (npass > kNormBatch) {
+#pragma unroll
+            for (uint32_t k = 0; k < kNormBatch; k++)
+                if (p0 + k < npass) f[k] = load(p0 + k);  // the same bits again
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kNormBatch; k++) {
+            const uint32_t b = 32 * (p0 + k) + (threadIdx.x >> 3);
+            if (p0 + k < npass && b < nb) {
+                const uint32_t i = b * 32 + part * 4;
+                const float v[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (y) xsum[i + e] = v[e];
+                    out[i + e] = __fmul_rn(__fmul_rn(v[e], inv), w[i + e]);
+                }
+            }
+        }
+    }
 }
 
 __global__ void __launch_bounds__(256)
@@ -663,8 +708,10 @@ extern "C" int ane_decode_token(const ane_decode_config* cfg, const ane_decode_l
 extern "C" int ane_hip_rms_norm(uint32_t K, const float* x, const float* w, float eps, float* out, void* stream) {
     if (K == 0) return ANE_OK;
     if (!x || !w || !out) return ANE_ERR_BAD_POINTER;
-    if ((K & 31) || (((uintptr_t)x) & 15) || K > (1u << 20)) return ANE_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(k_rms_norm_build, dim3(1), dim3(256), (K / 32) * 8, (hipStream_t)stream, K, eps, x, w, out);
+    // K/32 doubles of block sums in LDS: at most 128 KB
+    if ((K & 31) || (((uintptr_t)x) & 15) || K > (1u << 19)) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_rms_norm_build, dim3(1), dim3(256), (K / 32) * 8, (hipStream_t)stream, K, eps, x,
+                       (const float*)nullptr, w, (float*)nullptr, out);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -689,7 +736,8 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
     if (!cfg_ok(cfg) || (arith != ANE_DECODE_ARITH_BUILD && arith != ANE_DECODE_ARITH_REFERENCE))
         return ANE_ERR_INVALID_ARG;
     if (!layers || !x || !backend || (arith == ANE_DECODE_ARITH_BUILD && !rope_table)) return ANE_ERR_BAD_POINTER;
-    if (pos >= cfg->ctx || (((uintptr_t)x) & 15)) return ANE_ERR_INVALID_ARG;
+    // the norms keep hidden/32 doubles of block sums in LDS
+    if (pos >= cfg->ctx || (((uintptr_t)x) & 15) || cfg->hidden > (1u << 19)) return ANE_ERR_INVALID_ARG;
     if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < ggml_layout(cfg, nullptr, nullptr))
         return ANE_ERR_WORKSPACE;
     GgmlWs w;
@@ -722,10 +770,16 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
     do {                       \
         if ((st = (e))) return st; \
     } while (0)
+    // the build's residual adds ride on the norm that follows them:
+    // x = fl(x + y), xn = norm(x) in one launch
+    auto add_norm = [&](const float* y, const float* nw) {
+        hipLaunchKernelGGL(k_rms_norm_build, dim3(1), dim3(256), (H / 32) * 8, s, H, cfg->eps, (const float*)x, y,
+                           nw, x, w.xn);
+    };
     for (uint32_t l = 0; l < cfg->n_layers; l++) {
         const ane_decode_layer& L = layers[l];
         if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.attn_norm, w.xn, H, s));
-        else ANE_TRY(ane_hip_rms_norm(H, x, L.attn_norm, cfg->eps, w.xn, s));
+        else if (l == 0) ANE_TRY(ane_hip_rms_norm(H, x, L.attn_norm, cfg->eps, w.xn, s));
         {
             const MulMatNode n(L.w_qkv, nqkv, H, w.xn, w.qkv);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
@@ -743,9 +797,12 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
             const MulMatNode n(L.w_o, H, nq, w.attn, w.y);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
         }
-        hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
-        if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.ffn_norm, w.xn, H, s));
-        else ANE_TRY(ane_hip_rms_norm(H, x, L.ffn_norm, cfg->eps, w.xn, s));
+        if (ref) {
+            hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+            ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.ffn_norm, w.xn, H, s));
+        } else {
+            add_norm(w.y, L.ffn_norm);
+        }
         {
             const MulMatNode n(L.w_gate_up, 2 * F, H, w.xn, w.gu);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
@@ -756,7 +813,8 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
             const MulMatNode n(L.w_down, H, F, w.h, w.y);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
         }
-        hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+        if (!ref && l + 1 < cfg->n_layers) add_norm(w.y, layers[l + 1].attn_norm);
+        else hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
         ANE_HIP_CHECK_LAUNCH();
     }
 #undef ANE_TRY

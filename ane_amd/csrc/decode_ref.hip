@@ -33,13 +33,21 @@ constexpr uint32_t kLog2e = 0x3FB8AA3Bu, kC4 = 0x3C1D955Au, kC3 = 0x3D635847u, k
 
 __device__ __forceinline__ float f_of(uint32_t u) { return __uint_as_float(u); }
 
-// RecipSqrtEstimate(a), a in [128, 512) (the Arm ARM's loop).
+// RecipSqrtEstimate(a), a in [128, 512).  The Arm ARM steps b up from 512
+// while a' * (b+1)^2 < 2^28 (a' = 2a+1, or the even part of a plus one,
+// doubled), then returns (b+1)/2: so b+1 is the least m >= 513 with
+// a' * m^2 >= 2^28.  Here m comes from a double-precision sqrt and one
+// integer correction each way, which gives the loop's result for all 384
+// inputs (m is within one of ceil(sqrt(2^28 / a'))), instead of up to ~500
+// serial iterations.
 __device__ uint32_t recip_sqrt_estimate(uint32_t a) {
     if (a < 256) a = a * 2 + 1;
     else a = (((a >> 1) << 1) + 1) * 2;
-    uint64_t b = 512;
-    while ((uint64_t)a * (b + 1) * (b + 1) < (1ull << 28)) b++;
-    return (uint32_t)((b + 1) / 2);
+    uint32_t m = (uint32_t)ceil(sqrt(268435456.0 / (double)a));
+    if (m < 513) m = 513;
+    if ((uint64_t)a * m * m < (1ull << 28)) m++;
+    if (m > 513 && (uint64_t)a * (m - 1) * (m - 1) >= (1ull << 28)) m--;
+    return m / 2;
 }
 
 __device__ float frsqrte_a(float x) {
@@ -50,11 +58,10 @@ __device__ float frsqrte_a(float x) {
     if (ex == 0xff) return 0.0f;
     uint64_t f52 = (uint64_t)fr << 29;
     int e = (int)ex;
-    if (e == 0) {
-        while (!(f52 & (1ull << 51))) {
-            f52 <<= 1;
-            e--;
-        }
+    if (e == 0) {  // normalise a denormal: its leading one to bit 51, then dropped
+        const int sh = __builtin_clzll(f52) - 12;
+        f52 <<= sh;
+        e -= sh;
         f52 = (f52 << 1) & ((1ull << 52) - 1);
     }
     const uint32_t scaled = (e & 1) == 0 ? 256u + (uint32_t)(f52 >> 44) : 128u + (uint32_t)(f52 >> 45);
@@ -369,33 +376,64 @@ k_attn_scores_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, 
 }
 
 // out[h][d] = FADDV over 16 chains, chain l = fma(p_j, v_j[d], acc) for
-// j = l mod 16 in increasing j: 16 lanes per (h, d).
+// j = l mod 16 in increasing j.  One workgroup per (kv head g, block of 16
+// dimensions): its kPvHeads query heads share every V row.  Thread (hq, l)
+// runs chain l of head kPvHeads*g + hq/4 for the 4 dimensions 4(hq%4)..
+// of the block.  Positions pass through LDS in chunks of kPvChunk, copied
+// global -> LDS directly (V rows as 16-byte pieces, P as dwords; positions
+// at or past len read as zeros and are never folded), double-buffered so
+// chunk c+1 is in flight while chunk c is folded.
+constexpr uint32_t kPvHeads = 4, kPvChunk = 1024;
 __global__ void __launch_bounds__(256)
-k_attn_pv_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, const float* __restrict__ p,
-              const uint16_t* __restrict__ v_cache, float* __restrict__ out) {
-    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t od = t >> 4, l = t & 15;  // output element (h, d)
-    const bool live = od < n_heads * 128;
-    const uint32_t h = live ? od / 128 : 0, d = od % 128;
-    const float* ph = p + (uint64_t)h * len;
-    const uint16_t* vg = v_cache + (uint64_t)(h / group) * ctx * 128 + d;
-    float acc = 0.0f;
-    if (live) {
-        uint32_t j = l;
-        for (; j + 7 * 16 < len; j += 8 * 16) {  // 8 positions loaded ahead of their 8 steps
-            float pj[8], vj[8];
+k_attn_pv_ref(uint32_t len, uint32_t ctx, const float* __restrict__ p, const uint16_t* __restrict__ v_cache,
+              float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPvChunk * 16];    // 2 x 32 KB
+    __shared__ __attribute__((aligned(16))) float ps[2][kPvHeads * kPvChunk];  // 2 x 16 KB
+    const uint32_t g = blockIdx.x >> 3, db = blockIdx.x & 7;
+    const uint32_t t = threadIdx.x, l = t & 15, hq = t >> 4, hl = hq >> 2, d4 = (hq & 3) * 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+    const uint16_t* vg = v_cache + (uint64_t)g * ctx * 128 + db * 16;
+    const float* pg = p + (uint64_t)g * kPvHeads * len;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vg, len * 256);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pg, kPvHeads * len * 4);
+    const uint32_t nch = (len + kPvChunk - 1) / kPvChunk;
+    auto issue = [&](uint32_t c) {
+        const uint32_t j0 = c * kPvChunk, buf = c & 1;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                pj[k] = ph[j + 16 * k];
-                vj[k] = h2f(vg[(uint64_t)(j + 16 * k) * 128]);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) acc = __builtin_fmaf(pj[k], vj[k], acc);
+        for (uint32_t i = 0; i < kPvChunk * 2 / 256; i++) {  // V: piece q = row q/2, half q%2
+            const uint32_t q = 64 * (wave + 4 * i) + lane, j = j0 + (q >> 1);
+            copy16_to_lds(rv, reinterpret_cast<int8_t*>(vs[buf]) + 1024 * (wave + 4 * i),
+                          j < len ? j * 256 + (q & 1) * 16 : 0x80000000u);
         }
-        for (; j < len; j += 16) acc = __builtin_fmaf(ph[j], h2f(vg[(uint64_t)j * 128]), acc);
+#pragma unroll
+        for (uint32_t i = 0; i < kPvHeads * kPvChunk / 256; i++) {  // P: element e = head e/kPvChunk
+            const uint32_t e = 64 * (wave + 4 * i) + lane, h = e / kPvChunk, j = j0 + e % kPvChunk;
+            copy4_to_lds(rp, ps[buf] + 64 * (wave + 4 * i), j < len ? (h * len + j) * 4 : 0x80000000u);
+        }
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    issue(0);
+    for (uint32_t c = 0; c < nch; c++) {
+        wait_vmcnt<0>();  // chunk c's copies of this wave
+        __syncthreads();  // everyone's; everyone is done with chunk c-1, whose buffer is refilled next
+        if (c + 1 < nch) issue(c + 1);
+        const uint32_t buf = c & 1, j0 = c * kPvChunk;
+        const uint32_t nj = min(kPvChunk, len - j0);
+        for (uint32_t k = l; k < nj; k += 16) {
+            const float pj = ps[buf][hl * kPvChunk + k];
+            const uint2 raw = *reinterpret_cast<const uint2*>(vs[buf] + k * 16 + d4);
+            acc[0] = __builtin_fmaf(pj, h2f(raw.x & 0xffff), acc[0]);
+            acc[1] = __builtin_fmaf(pj, h2f(raw.x >> 16), acc[1]);
+            acc[2] = __builtin_fmaf(pj, h2f(raw.y & 0xffff), acc[2]);
+            acc[3] = __builtin_fmaf(pj, h2f(raw.y >> 16), acc[3]);
+        }
     }
-    const float v = faddv16(acc);  // whole 16-lane groups, live or not
-    if (live && l == 0) out[od] = v;
+    float* o = out + (uint64_t)(g * kPvHeads + hl) * 128 + db * 16 + d4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float v = faddv16(acc[i]);
+        if (l == 0) o[i] = v;
+    }
 }
 
 // h[i] = fl(silu_fp32(g_i) * u_i) on gate|up interleaved in 32-row groups.
@@ -442,14 +480,14 @@ int rope_ref_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos
 int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
                          const uint16_t* kc, const uint16_t* vc, float* out, float* ws, hipStream_t s) {
     const uint32_t group = n_heads / n_kv;
+    if (group != kPvHeads) return ANE_ERR_INVALID_ARG;
     float* sc = ws;
     float* pr = ws + (uint64_t)n_heads * len;
     const uint64_t ns = (uint64_t)n_heads * len;
     hipLaunchKernelGGL(k_attn_scores_ref, dim3((uint32_t)((ns + 255) / 256)), dim3(256), 0, s, n_heads, group, len,
                        ctx, q, kc, sc);
     hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
-    hipLaunchKernelGGL(k_attn_pv_ref, dim3((n_heads * 128 * 16 + 255) / 256), dim3(256), 0, s, n_heads, group, len,
-                       ctx, pr, vc, out);
+    hipLaunchKernelGGL(k_attn_pv_ref, dim3(n_kv * 8), dim3(256), 0, s, len, ctx, pr, vc, out);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }

@@ -143,8 +143,8 @@ int ane_hip_silu_mul_quant(uint32_t n, const float* gu, void* xq, void* stream);
 /* The build's RMSNorm on its own, one row: out = fl(fl(x * inv) * w),
  * inv = 1/sqrtf((float)(ss / K) + eps) with ss the fp64 sum of squares in
  * the fixed order the fused products use, so the output is bit-identical to
- * the normalised activation those kernels quantize.  K % 32 == 0, x 16-byte
- * aligned. */
+ * the normalised activation those kernels quantize.  K % 32 == 0,
+ * K <= 2^19, x 16-byte aligned. */
 int ane_hip_rms_norm(uint32_t K, const float* x, const float* w, float eps, float* out, void* stream);
 
 /* out = fl(a + b), n elements (out may alias a or b). */

@@ -112,6 +112,16 @@ def test_decode_refuses_unsupported_configs_before_launching():
     assert list(x)[:4] == [1.5] * 4
 
 
+def test_rms_norm_refuses_sizes_before_launching():
+    """The standalone norm keeps K/32 fp64 block sums in LDS: K past 2^19,
+    or not a multiple of 32, is refused before any launch (the fake
+    addresses are never touched, so no GPU is needed)."""
+    L = ane_amd.lib()
+    p = ctypes.c_void_p(0x10000)
+    for K in ((1 << 19) + 32, 1 << 20, 100):
+        assert L.ane_hip_rms_norm(K, p, p, ctypes.c_float(1e-5), p, None) == 1
+
+
 # ------------------------------------------------------------------ GPU
 def dev(a):
     import torch

@@ -67,6 +67,40 @@ def test_rms_norm_fp32_many_rows(ane, oracle):
         same(got[r], oracle.rms_norm_fp32(x[r], w, 1e-6))
 
 
+def rsqrte_bucket(t):
+    """FRSQRTE's table input for a positive normal float32 t: 256 + the top
+    8 fraction bits for an even biased exponent, 128 + the top 7 for odd."""
+    u = np.asarray(t, F32).view(np.uint32)
+    e, fr = (u >> 23) & 0xFF, u & 0x7FFFFF
+    return np.where(e % 2 == 0, 256 + (fr >> 15), 128 + (fr >> 16)) + 1000 * (e % 2)
+
+
+def test_rms_norm_fp32_frsqrte_table_and_denormals(ane, oracle):
+    """Every one of the 384 FRSQRTE table inputs (both exponent parities),
+    checked by the rows' mean squares, plus rows whose mean square is a
+    denormal (eps = 0), which FRSQRTE normalises first."""
+    import torch
+
+    g = np.random.default_rng(5)
+    rows, dim = 6000, 16
+    x = (g.standard_normal((rows, dim)) * np.exp(g.uniform(-30, 30, (rows, 1)))).astype(F32)
+    w = (1 + 0.1 * g.standard_normal(dim)).astype(F32)
+    t = (np.mean(x.astype(np.float64) ** 2, axis=1) + 1e-6).astype(F32)
+    assert len(np.unique(rsqrte_bucket(t))) >= 380  # (float64 means: edge rows may shift a bucket)
+    out = torch.zeros((rows, dim), dtype=torch.float32, device="cuda")
+    ane.rms_norm_fp32(rows, dim, 1e-6, dev(x), dev(w), out)
+    got = host(out)
+    for r in range(rows):
+        same(got[r], oracle.rms_norm_fp32(x[r], w, 1e-6))
+    tiny = (g.standard_normal((64, dim)) * np.exp(g.uniform(-52, -44, (64, 1)))).astype(F32)
+    assert (np.mean(tiny.astype(np.float64) ** 2, axis=1) < 1.2e-38).all()  # denormal mean squares
+    out = torch.zeros((64, dim), dtype=torch.float32, device="cuda")
+    ane.rms_norm_fp32(64, dim, 0.0, dev(tiny), dev(w), out)
+    got = host(out)
+    for r in range(64):
+        same(got[r], oracle.rms_norm_fp32(tiny[r], w, 0.0))
+
+
 @pytest.mark.parametrize("n", [32, 4096, 1 << 20])
 def test_silu_fp32_opcode(ane, oracle, n):
     import torch
@@ -164,8 +198,10 @@ def test_opcodes_refuse_partial_vectors(ane):
         assert e.value.status == 1
 
 
-@pytest.mark.parametrize("K", [32, 512, 4096, 14336])
+@pytest.mark.parametrize("K", [32, 512, 4096, 4128, 14336, 16384, 40960])
 def test_rms_norm_build_matches_oracle(ane, oracle, K):
+    """K = 4128: a last pass with one block; above 16384 the kernel holds
+    x in batches and reloads it for the output."""
     import torch
 
     x = (data.activations(1, K, seed=K)[0] * 3).astype(F32)
