@@ -176,6 +176,31 @@ __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, fl
            ((uint32_t)(quant1(c, inv) & 0xff) << 16) | ((uint32_t)(quant1(d, inv) & 0xff) << 24);
 }
 
+// pack4 for a tensor whose quantization steps stay finite: inv finite and
+// every |x| <= amax finite, so t = x*inv is a finite fp32 (no NaN: no NaN
+// operand exists and inv is finite; no inf: |t| <= ~127).  Then
+//   fmed3(t, -127, 127)  = the clamp of quant1,
+//   c + 1.5 * 2^23       = a float in [2^23, 2^24) whose ulp is 1, so the
+//                          addition rounds c half-to-even to an integer
+//                          (frintn) and the low byte of its bits is that
+//                          integer's two's-complement int8,
+// and two v_perm_b32 gather the four low bytes.  Bit-identical to pack4
+// under that condition; callers check it once per tensor (fast_quant_ok).
+__device__ __forceinline__ uint32_t quant_byte_bits(float x, float inv) {
+    const float c = __builtin_amdgcn_fmed3f(__fmul_rn(x, inv), -127.0f, 127.0f);
+    return __float_as_uint(__fadd_rn(c, 12582912.0f));
+}
+__device__ __forceinline__ uint32_t pack4_fast(float a, float b, float c, float d, float inv) {
+    const uint32_t ab = __builtin_amdgcn_perm(quant_byte_bits(b, inv), quant_byte_bits(a, inv), 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(quant_byte_bits(d, inv), quant_byte_bits(c, inv), 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+// The condition of pack4_fast: amax (the NaN-propagating max of |x|) and
+// inv = 127 / amax (or 127 when amax == 0) both finite.
+__device__ __forceinline__ bool fast_quant_ok(float amax, float inv) {
+    return __builtin_isfinite(amax) && __builtin_isfinite(inv);
+}
+
 // ----------------------------------------------------------- LDS copy helpers
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 

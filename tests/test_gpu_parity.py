@@ -284,12 +284,14 @@ def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
 
 
 @pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny"])
-@pytest.mark.parametrize("M,N,K", [(129, 257, 1000), (256, 512, 2048)])
+@pytest.mark.parametrize("M,N,K", [(129, 257, 1000), (256, 512, 2048), (256, 2048, 2048)])
 def test_dense_fused_special_operands(ane, oracle, case, M, N, K):
     """The fused max|x| and quantize passes on operands the quantizer
     special-cases: a NaN or an infinity (NaN or infinite per-tensor scale),
     an all-zero tensor (the zero guard) and a tensor of denormals and signed
-    zeros only."""
+    zeros only (127 / amax overflows to +inf, so 0 * inf reaches the
+    quantizer).  256 x 2048 x 2048 (18 MiB of operands) takes the one-launch
+    resident quantizer, the others the two-pass one."""
     import torch
 
     A, B = data.gemm_inputs(M, N, K, seed=M + K)
@@ -311,6 +313,26 @@ def test_dense_fused_special_operands(ane, oracle, case, M, N, K):
         oracle.set_threads(1)
     C = zeros(M * N, torch.float32)
     ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 2048, 2048), (5000, 64, 4096), (777, 2048, 4096), (64, 2048, 2048)])
+def test_dense_fused_resident_quantizer_shapes(ane, oracle, M, N, K):
+    """Shapes on the one-launch resident quantizer (K % 128 == 0, N % 64 == 0,
+    at least 12 MiB of operands): a workgroup's share of A all in LDS
+    (256, 777 and 64 rows; 777 rows give every workgroup a ragged share), and
+    past LDS into registers and the batched re-read (5000 x 4096: 20,000
+    float4 per workgroup, the last batch ragged)."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M + 3 * N + K)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), False, A, B)
+    finally:
+        oracle.set_threads(1)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, False, dev(A), dev(B), C))
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
