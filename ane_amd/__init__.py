@@ -98,6 +98,8 @@ EXPORTS = (
     "ane_hip_dense_fused_i8",
     "ane_hip_dense_fused_i8_quantize",
     "ane_hip_dense_fused_i8_gemm",
+    "ane_hip_grid_wait_status",
+    "ane_hip_set_grid_wait_limit",
     "ane_hip_gemm_s8_i32",
     "ane_hip_q8_0_gemv",
     "ane_hip_cblas_igemm_workspace_size",
@@ -180,6 +182,8 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _P, _P, _P, _P, _c.c_size_t, _P]),
     "ane_hip_dense_fused_i8_gemm": (
         _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _c.c_float, _c.c_int, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_grid_wait_status": (_c.c_int, [_P]),
+    "ane_hip_set_grid_wait_limit": (None, [_c.c_uint64]),
     "ane_hip_gemm_s8_i32": (
         _c.c_int,
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _c.c_uint32, _P, _c.c_uint32, _P, _P],

@@ -14,6 +14,7 @@
 //    tensors (per-block partial maxima), then one quantize pass in which
 //    every block first folds its tensor's partials.  It takes the shapes
 //    the resident route does not.
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -438,6 +439,7 @@ std::mutex g_res_mu;
 ResidentDevice g_res_dev[64];
 std::map<std::pair<int, hipStream_t>, int> g_res_slot;
 int g_res_next[64] = {};
+std::atomic<uint64_t> g_wait_limit{kSyncTimeoutTicks};
 
 // The device's sync array and grid, and the slot of (device, stream); false
 // when the resident route is unavailable (then the two-pass route runs).
@@ -499,9 +501,20 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     const uint64_t nA4 = (uint64_t)M * K / 4;
     const uint64_t perA4 = (nA4 + G - 1) / G;
     hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, A, B, N, K, nA4, perA4,
-                       (uint32_t)nTiles, perT, partials, qA, qBt, scales, slot, kSyncTimeoutTicks);
+                       (uint32_t)nTiles, perT, partials, qA, qBt, scales, slot,
+                       g_wait_limit.load(std::memory_order_relaxed));
     if (hipGetLastError() != hipSuccess) *status = ANE_ERR_HIP;
     return true;
+}
+
+// The slot of (current device, s) if one was ever assigned.
+uint32_t* resident_slot_of(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_res_mu);
+    auto it = g_res_slot.find({dev, s});
+    if (it == g_res_slot.end() || !g_res_dev[dev].sync) return nullptr;
+    return g_res_dev[dev].sync + (size_t)it->second * kSyncSlotDw;
 }
 
 uint32_t blocks_for(uint64_t n) {
@@ -533,3 +546,26 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
 }
 
 }  // namespace ane
+
+extern "C" void ane_hip_set_grid_wait_limit(uint64_t ticks) {
+    ane::g_wait_limit.store(ticks ? ticks : ane::kSyncTimeoutTicks, std::memory_order_relaxed);
+}
+
+extern "C" int ane_hip_grid_wait_status(void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* slot = ane::resident_slot_of(s);
+    if (!slot) return ANE_OK;
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    uint32_t err = 0;
+    if (hipMemcpy(&err, slot + 1, 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    if (!err) return ANE_OK;
+    const uint32_t zero = 0;
+    if (hipMemcpy(slot + 1, &zero, 4, hipMemcpyHostToDevice) != hipSuccess) (void)hipGetLastError();
+    return ANE_ERR_HIP;
+}

@@ -36,6 +36,7 @@ namespace {
 thread_local int t_status = ANE_OK;
 thread_local std::string t_message;
 thread_local hipStream_t t_stream = nullptr;
+thread_local bool t_ran_fused = false;  // a dense_fused_i8 record ran in this stream_exec call
 
 int fail(int status, const char* fmt, ...) {
     char buf[512];
@@ -326,6 +327,7 @@ int op_dense_fused(Reader& r, hipStream_t s) {
     const size_t wsb = ane_hip_dense_fused_i8_workspace_size(M, N, K);
     Lease lease;
     CHECK(get_workspace(s, wsb, lease));
+    t_ran_fused = true;
     return hip_status(ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, lease.ptr, wsb, s),
                       "dense_fused_i8");
 }
@@ -558,11 +560,14 @@ int run(const uint8_t* data, size_t size, hipStream_t s) {
 
 extern "C" void stream_exec(const uint8_t* data, size_t size) {
     hipStream_t s = t_stream;
+    t_ran_fused = false;
     int st = run(data, size, s);
     if (hipStreamSynchronize(s) != hipSuccess) {
         (void)hipGetLastError();
         if (st == ANE_OK) st = fail(ANE_ERR_HIP, "hipStreamSynchronize failed");
     }
+    if (t_ran_fused && ane_hip_grid_wait_status(s) != ANE_OK && st == ANE_OK)
+        st = fail(ANE_ERR_HIP, "dense_fused_i8: the quantizer's grid-wide wait gave up; C is not valid");
     t_status = st;
 }
 

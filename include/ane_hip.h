@@ -145,6 +145,19 @@ int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
                            float* scales_out, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* The operand quantizer of dense_fused_i8 runs, for large shapes (K % 128
+ * == 0, N % 64 == 0, at least 12 MiB of operands), as one launch whose
+ * workgroups (one per CU) exchange their maxima through a grid-wide wait.
+ * Every workgroup is resident at once, so the wait ends; it is bounded all
+ * the same, and a workgroup that gives up leaves C invalid and records it.
+ * ane_hip_grid_wait_status(stream) synchronizes the stream and returns
+ * ANE_ERR_HIP (and clears the record) if a launch on it gave up since the
+ * last call, else ANE_OK; stream_exec checks it itself.
+ * ane_hip_set_grid_wait_limit sets the bound, in ticks of the 100 MHz
+ * realtime counter, for launches made after it (0: the default, 2 s). */
+int ane_hip_grid_wait_status(void* stream);
+void ane_hip_set_grid_wait_limit(uint64_t ticks);
+
 /* The two phases of ane_hip_dense_fused_i8, for callers that quantize an
  * operand pair once and run the contraction repeatedly (the reference's own
  * quantize-once / reuse pattern, tests/test_mnist_i8.cpp:198-207, 415):

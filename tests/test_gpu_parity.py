@@ -336,6 +336,40 @@ def test_dense_fused_resident_quantizer_shapes(ane, oracle, M, N, K):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
+def test_dense_fused_grid_wait_limit(ane, oracle):
+    """The resident quantizer's bounded grid-wide wait, forced from the host
+    to a one-tick limit: every workgroup still finishes, and a launch whose
+    workgroups gave up is reported by stream_exec (C is then not valid);
+    one that did not is exact.  Restored to the default, the same record is
+    exact and reports nothing."""
+    import torch
+
+    M, N, K = 256, 2048, 2048
+    A, B = data.gemm_inputs(M, N, K, seed=11)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    finally:
+        oracle.set_threads(1)
+    dA, dB = dev(A), dev(B)
+    lib = ane.lib()
+    C = zeros(M * N, torch.float32)
+    try:
+        lib.ane_hip_set_grid_wait_limit(1)
+        try:
+            ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dA, dB, C))
+        except ane.AneError as e:
+            assert e.status == 6 and "grid-wide wait" in str(e)  # ANE_ERR_HIP
+        else:
+            assert_f32_identical(host(C).reshape(M, N), ref)
+    finally:
+        lib.ane_hip_set_grid_wait_limit(0)
+    C.zero_()
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dA, dB, C))
+    assert lib.ane_hip_grid_wait_status(ane._stream_handle(None)) == 0
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
 def test_dense_fused_4096_cubed_sampled(ane, oracle):
     """Config 2 at full size: both per-tensor scales exact, and a sample of
     rows of C identical to the oracle's contraction of the oracle-quantized
