@@ -180,7 +180,7 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
 //      so the float4 j of A is the dword j of qA); the first kRLdsA4 of
 //      them are copied into LDS, the rest are read for the maximum and read
 //      again to quantize.
-// Sync slot: one per stream, zero at module load (layout and protocol at
+// Sync slot: one per device, zero at module load (layout and protocol at
 // grid_arrive_wait).
 constexpr int kRT = 512;
 constexpr int kRNT = 8;
@@ -424,30 +424,34 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     }
 }
 
-// Sync slots in device memory: zero when the code object loads, left zero
-// by every launch.  One slot per (device, stream), so launches on
-// different streams never share one; launches on one stream are ordered.
-constexpr int kSyncSlots = 32;
-__device__ __align__(256) uint32_t resident_sync[kSyncSlots * kSyncSlotDw];
+// The wait's slot in device memory: zero when the code object loads, left
+// with its counters at rest by every launch.  Resident launches on a device
+// are ordered (launch_resident), so one slot per device serves them all.
+__device__ __align__(256) uint32_t resident_sync[kSyncSlotDw];
 
 struct ResidentDevice {
     uint32_t* sync = nullptr;  // device address of resident_sync
     uint32_t grid = 0;         // CUs x resident workgroups per CU (0: route unusable)
     bool probed = false;
+    // The last resident launch made by a host call: two grids that each need
+    // every CU must not run at once (their workgroups would split the CUs
+    // and neither grid could pass its wait), so a launch on another stream
+    // first waits for this event.
+    hipEvent_t last = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool last_valid = false;
 };
 std::mutex g_res_mu;
 ResidentDevice g_res_dev[64];
-std::map<std::pair<int, hipStream_t>, int> g_res_slot;
-int g_res_next[64] = {};
 std::atomic<uint64_t> g_wait_limit{kSyncTimeoutTicks};
 
-// The device's sync array and grid, and the slot of (device, stream); false
-// when the resident route is unavailable (then the two-pass route runs).
-bool resident_setup(hipStream_t s, uint32_t** slot, uint32_t* grid) {
-    if (s == hipStreamPerThread) return false;
+// The device's slot and grid (probed once per device, with it current);
+// null when the resident route is unavailable (then the two-pass route
+// runs).  Called with g_res_mu held.
+ResidentDevice* resident_device(hipStream_t s, int* dev_out) {
+    if (s == hipStreamPerThread) return nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    std::lock_guard<std::mutex> lock(g_res_mu);
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     ResidentDevice& d = g_res_dev[dev];
     if (!d.probed) {
         d.probed = true;
@@ -457,26 +461,16 @@ bool resident_setup(hipStream_t s, uint32_t** slot, uint32_t* grid) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_quantize_resident, kRT, 0) != hipSuccess) {
             (void)hipGetLastError();
-            return false;
+            return nullptr;
         }
         if (cus > 0 && occ > 0 && (uint64_t)cus * occ <= kFusedPartials) {
             d.sync = (uint32_t*)p;
             d.grid = (uint32_t)(cus * occ);
         }
     }
-    if (!d.grid) return false;
-    auto it = g_res_slot.find({dev, s});
-    int idx;
-    if (it != g_res_slot.end()) {
-        idx = it->second;
-    } else {
-        if (g_res_next[dev] >= kSyncSlots) return false;
-        idx = g_res_next[dev]++;
-        g_res_slot[{dev, s}] = idx;
-    }
-    *slot = d.sync + (size_t)idx * kSyncSlotDw;
-    *grid = d.grid;
-    return true;
+    if (!d.grid) return nullptr;
+    *dev_out = dev;
+    return &d;
 }
 
 // The resident route, when the shape allows it: whole 128 x 64 B tiles
@@ -492,29 +486,66 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     // 64 x 2048 x 2048 10.0 against 9.4 us)
     if (((uint64_t)M * K + (uint64_t)K * N) * 4 < kResidentMinBytes) return false;
     if ((((uintptr_t)A) | ((uintptr_t)B)) & 15) return false;
-    uint32_t* slot = nullptr;
-    uint32_t G = 0;
-    if (!resident_setup(s, &slot, &G)) return false;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(g_res_mu);
+    int dev = 0;
+    ResidentDevice* dp = resident_device(s, &dev);
+    if (!dp) return false;
+    ResidentDevice& d = *dp;
+    const uint32_t G = d.grid;
     const uint64_t nTiles = (uint64_t)(K / kBTK) * (N / kBTN);
     if (nTiles > (uint64_t)kRNT * G) return false;
     const uint32_t perT = (uint32_t)((nTiles + G - 1) / G);
     const uint64_t nA4 = (uint64_t)M * K / 4;
     const uint64_t perA4 = (nA4 + G - 1) / G;
+    // Resident launches on one device are ordered: a launch on another
+    // stream than the previous one waits for it.  A captured launch cannot
+    // wait for work outside its graph, so under capture the route is taken
+    // only on the stream of the previous launch (graph replays are ordered
+    // by their caller).
+    const bool other = d.last_valid && d.last_stream != s;
+    if (capturing && other) return false;
+    if (!capturing) {
+        if (!d.last && hipEventCreateWithFlags(&d.last, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            d.last = nullptr;
+            return false;
+        }
+        if (other && hipStreamWaitEvent(s, d.last, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+    }
     hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, A, B, N, K, nA4, perA4,
-                       (uint32_t)nTiles, perT, partials, qA, qBt, scales, slot,
+                       (uint32_t)nTiles, perT, partials, qA, qBt, scales, d.sync,
                        g_wait_limit.load(std::memory_order_relaxed));
-    if (hipGetLastError() != hipSuccess) *status = ANE_ERR_HIP;
+    if (hipGetLastError() != hipSuccess) {
+        *status = ANE_ERR_HIP;
+        return true;
+    }
+    if (!capturing) {
+        if (hipEventRecord(d.last, s) != hipSuccess) {
+            (void)hipGetLastError();
+            *status = ANE_ERR_HIP;
+            return true;
+        }
+        d.last_stream = s;
+        d.last_valid = true;
+    }
     return true;
 }
 
-// The slot of (current device, s) if one was ever assigned.
-uint32_t* resident_slot_of(hipStream_t s) {
+// The current device's slot, if the resident route was ever set up on it.
+uint32_t* resident_slot_of() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     std::lock_guard<std::mutex> lock(g_res_mu);
-    auto it = g_res_slot.find({dev, s});
-    if (it == g_res_slot.end() || !g_res_dev[dev].sync) return nullptr;
-    return g_res_dev[dev].sync + (size_t)it->second * kSyncSlotDw;
+    return g_res_dev[dev].sync;
 }
 
 uint32_t blocks_for(uint64_t n) {
@@ -553,7 +584,7 @@ extern "C" void ane_hip_set_grid_wait_limit(uint64_t ticks) {
 
 extern "C" int ane_hip_grid_wait_status(void* stream) {
     hipStream_t s = (hipStream_t)stream;
-    uint32_t* slot = ane::resident_slot_of(s);
+    uint32_t* slot = ane::resident_slot_of();
     if (!slot) return ANE_OK;
     if (hipStreamSynchronize(s) != hipSuccess) {
         (void)hipGetLastError();

@@ -150,9 +150,16 @@ int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
  * workgroups (one per CU) exchange their maxima through a grid-wide wait.
  * Every workgroup is resident at once, so the wait ends; it is bounded all
  * the same, and a workgroup that gives up leaves C invalid and records it.
+ * Two such launches must not run at once on one device (each needs every
+ * CU): calls on different streams are ordered by the library (a call waits
+ * for the previous call's launch), and under stream capture the route is
+ * taken only on the stream of the previous call.  Replays of captured
+ * graphs are not ordered by the library: a caller replaying graphs that
+ * hold this op on several streams at once orders them itself.
  * ane_hip_grid_wait_status(stream) synchronizes the stream and returns
- * ANE_ERR_HIP (and clears the record) if a launch on it gave up since the
- * last call, else ANE_OK; stream_exec checks it itself.
+ * ANE_ERR_HIP (and clears the record) if such a launch on the current
+ * device gave up since the last call, else ANE_OK; stream_exec checks it
+ * itself.
  * ane_hip_set_grid_wait_limit sets the bound, in ticks of the 100 MHz
  * realtime counter, for launches made after it (0: the default, 2 s). */
 int ane_hip_grid_wait_status(void* stream);

@@ -370,6 +370,36 @@ def test_dense_fused_grid_wait_limit(ane, oracle):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
+def test_dense_fused_resident_two_streams(ane, oracle):
+    """Two resident-route dense_fused_i8 calls issued back to back on two
+    streams with nothing between them: each grid needs every CU, so the
+    library orders the second launch after the first (a stream-event wait);
+    both results are exact and no grid-wide wait gives up."""
+    import torch
+
+    M, N, K = 256, 2048, 2048
+    ins = [data.gemm_inputs(M, N, K, seed=s) for s in (21, 22)]
+    oracle.set_threads(0)
+    try:
+        refs = [oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B) for A, B in ins]
+    finally:
+        oracle.set_threads(1)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wsb = ane.dense_fused_i8_workspace_size(M, N, K)
+    bufs = [(dev(A), dev(B), zeros(M * N, torch.float32), torch.empty(wsb, dtype=torch.uint8, device="cuda"))
+            for A, B in ins]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (dA, dB, C, ws), st in zip(bufs, streams):
+            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws, stream=st)
+        for st in streams:
+            st.synchronize()
+            assert ane.lib().ane_hip_grid_wait_status(ane._stream_handle(st)) == 0
+        for (dA, dB, C, ws), ref in zip(bufs, refs):
+            assert_f32_identical(host(C).reshape(M, N), ref)
+            C.zero_()
+
+
 def test_dense_fused_4096_cubed_sampled(ane, oracle):
     """Config 2 at full size: both per-tensor scales exact, and a sample of
     rows of C identical to the oracle's contraction of the oracle-quantized
