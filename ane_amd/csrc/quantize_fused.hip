@@ -167,7 +167,7 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
 }
 
 // ------------------------------------------------------------ resident route
-// Grid: one 512-thread workgroup per CU (its 148 KB of LDS allows no
+// Grid: one 512-thread workgroup per CU (its 158 KB of LDS allows no
 // second), every workgroup resident at once, so the grid-wide barrier
 // below always completes; its wait is bounded anyway (kSyncTimeoutTicks of
 // the 100 MHz realtime counter), and a workgroup that gives up records it
@@ -178,16 +178,22 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
 //      float4 VGPRs per tile.
 //   A: workgroup w holds float4s [w*perA4, (w+1)*perA4) of A (K % 128 == 0,
 //      so the float4 j of A is the dword j of qA); the first kRLdsA4 of
-//      them are copied into LDS, the rest are read for the maximum and read
-//      again to quantize.
+//      them are copied into LDS, the next kRVA per thread are loaded into
+//      VGPRs, and any rest is read for the maximum and read again to
+//      quantize.  In phase 2 the B transposes are staged in A's LDS once
+//      A's LDS part has been written out.
 // Sync slot: one per device, zero at module load (layout and protocol at
 // grid_arrive_wait).
 constexpr int kRT = 512;
 constexpr int kRNT = 8;
-constexpr uint32_t kRLdsA4 = 8192;  // 128 KB of A in LDS
-constexpr int kRBatch = 8;          // float4 loads in flight per thread on the A stream
-constexpr int kRSA = 8;             // float4s per thread of A's streamed part loaded at once after the barrier
+constexpr uint32_t kRLdsA4 = 10112;  // float4s of A in LDS (158 KB, a multiple of 64); B's transposes reuse it
+constexpr uint32_t kRLdsSteps = (kRLdsA4 + kRT - 1) / kRT;
+constexpr int kRVA = 10;             // float4s of A per thread in VGPRs (249 VGPRs in all, no spill)
+constexpr uint64_t kROnChip4 = kRLdsA4 + (uint64_t)kRVA * kRT;  // 15,232 float4s (238 KB) of A on chip
+constexpr int kRBatch = 8;           // float4 loads in flight per thread on the rest of A
 constexpr uint32_t kTileDw = 64 * kTileRowDw;
+static_assert(kRLdsA4 % kWave == 0, "the LDS part of A is copied in whole 64-slot runs");
+static_assert(2 * kTileDw * 4 <= kRLdsA4 * 16, "the B transposes fit in A's LDS");
 constexpr uint64_t kSyncTimeoutTicks = 200000000ull;  // 2 s at 100 MHz
 constexpr uint64_t kResidentMinBytes = (uint64_t)12 << 20;
 
@@ -257,8 +263,8 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
                     uint32_t* __restrict__ partials, int8_t* __restrict__ qA, int8_t* __restrict__ qBt,
                     float* __restrict__ scales, uint32_t* __restrict__ sync, uint64_t timeout_ticks) {
     __shared__ float4 As[kRLdsA4];
-    __shared__ uint32_t tileT[2 * kTileDw];
     __shared__ uint32_t red[2 * (kRT / kWave)];
+    uint32_t* tileT = reinterpret_cast<uint32_t*>(As);  // phase 2, once A's LDS part is written out
     const uint32_t t = threadIdx.x, wv = t >> 6, lane = t & 63;
     const uint32_t G = gridDim.x, w = blockIdx.x;
     const uint32_t ntn = N / kBTN;
@@ -283,21 +289,29 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     }
 
     // ---- A: the first kRLdsA4 float4s of this workgroup's range into LDS
+    // (a wave copies only whole 64-slot runs below nres, so no copy writes
+    // past As), the next kRVA per thread into VGPRs
     const uint64_t a0 = (uint64_t)w * perA4;
     const uint64_t a1 = a0 + perA4 < nA4 ? a0 + perA4 : nA4;
     const uint32_t nres = a1 > a0 ? (uint32_t)(a1 - a0 < kRLdsA4 ? a1 - a0 : kRLdsA4) : 0;
     {
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(A + 4 * a0, nres * 16u);
 #pragma unroll
-        for (uint32_t s = 0; s < kRLdsA4 / kRT; s++)
-            if (s * kRT < nres) copy16_to_lds(rs, &As[s * kRT + wv * kWave], (s * kRT + t) * 16u);
+        for (uint32_t s = 0; s < kRLdsSteps; s++)
+            if (s * kRT + wv * kWave < nres) copy16_to_lds(rs, &As[s * kRT + wv * kWave], (s * kRT + t) * 16u);
     }
-    // ---- A past the LDS part: read for the maximum only, kRBatch loads in
-    // flight per thread
     const float4* A4 = reinterpret_cast<const float4*>(A);
+    const uint64_t jv = a0 + kRLdsA4 + t;
+    float4 av[kRVA];
+#pragma unroll
+    for (int u = 0; u < kRVA; u++)
+        av[u] = jv + u * kRT < a1 ? A4[jv + u * kRT] : make_float4(0.f, 0.f, 0.f, 0.f);
+    // ---- A past the on-chip part (at 4096 x 4096, 1,152 of a workgroup's
+    // 16,384 float4s): read for the maximum only, kRBatch loads in flight
+    // per thread
     uint32_t mA = 0, mB = 0;
     {
-        uint64_t j = a0 + kRLdsA4 + t;
+        uint64_t j = a0 + kROnChip4 + t;
         for (; j + (kRBatch - 1) * kRT < a1; j += kRBatch * kRT) {
             float4 v[kRBatch];
 #pragma unroll
@@ -311,13 +325,15 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     for (int i = 0; i < kRNT; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) mB = umax(mB, absmax4(bv[i][r]));
+#pragma unroll
+    for (int u = 0; u < kRVA; u++) mA = umax(mA, absmax4(av[u]));
     wait_vmcnt<0>();
     lds_barrier();
 #pragma unroll
-    for (uint32_t s = 0; s < kRLdsA4 / kRT; s++)
+    for (uint32_t s = 0; s < kRLdsSteps; s++)
         if (s * kRT + t < nres) mA = umax(mA, absmax4(As[s * kRT + t]));
 
-    // ---- workgroup maxima, then the grid-wide barrier
+    // ---- workgroup maxima, then the grid-wide wait
     mA = wave_max_u32(mA);
     mB = wave_max_u32(mB);
     if (lane == 0) {
@@ -366,22 +382,19 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         return fastA ? pack4_fast(v.x, v.y, v.z, v.w, invA) : pack4(v.x, v.y, v.z, v.w, invA);
     };
 
-    // ---- A past the LDS part: its first kRSA float4s per thread are loaded
-    // before this phase stores anything (loads and stores share one in-order
-    // vmcnt, so a load issued after a store could only be waited for once
-    // that store had completed)
+    // ---- A from LDS, then from VGPRs (K % 128 == 0: float4 j of A is dword j of qA)
     uint32_t* qA32 = reinterpret_cast<uint32_t*>(qA);
-    const uint64_t js = a0 + kRLdsA4 + t;
-    float4 rv[kRSA];
 #pragma unroll
-    for (int u = 0; u < kRSA; u++)
-        if (js + u * kRT < a1) rv[u] = A4[js + u * kRT];
-    // ---- A from LDS
-#pragma unroll
-    for (uint32_t s = 0; s < kRLdsA4 / kRT; s++) {
+    for (uint32_t s = 0; s < kRLdsSteps; s++) {
         const uint32_t idx = s * kRT + t;
         if (idx < nres) qA32[a0 + idx] = qa(As[idx]);
     }
+#pragma unroll
+    for (int u = 0; u < kRVA; u++)
+        if (jv + u * kRT < a1) qA32[jv + u * kRT] = qa(av[u]);
+    wait_lgkmcnt0();  // every read of As is done: the B transposes reuse it
+    lds_barrier();
+
     // ---- B tiles from VGPRs: transposed through LDS into 128-byte qBt row segments
 #pragma unroll
     for (int i = 0; i < kRNT; i++) {
@@ -408,12 +421,8 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
             *reinterpret_cast<v4i*>(qBt + (uint64_t)(n0 + n) * K + k0 + part * 16) = v;
         }
     }
-    // ---- A past the LDS part: the registers, then (past kRSA float4s per
-    // thread, for large M) the rest in batches
-#pragma unroll
-    for (int u = 0; u < kRSA; u++)
-        if (js + u * kRT < a1) qA32[js + u * kRT] = qa(rv[u]);
-    for (uint64_t jr = js + kRSA * kRT; jr < a1; jr += kRBatch * kRT) {
+    // ---- A past the on-chip part: read again and quantize
+    for (uint64_t jr = a0 + kROnChip4 + t; jr < a1; jr += kRBatch * kRT) {
         float4 v[kRBatch];
 #pragma unroll
         for (int u = 0; u < kRBatch; u++)
