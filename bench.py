@@ -285,8 +285,26 @@ def main() -> int:
     log(f"whole op: {ms_per_step * 1e3:.2f} us/step = {value:.1f} TOPS")
 
     # ------------------------------------------------------------ kernel roofline
+    # The contraction's launch duration: kernel_reps launches captured into
+    # one HIP graph and replayed between HIP events (graph_time).  Its
+    # rocprofv3 traces: bench.py --only gemm (the same replay) and --only
+    # fused (inside the op).  A second reading brackets each contraction
+    # inside eager dense_fused_i8 calls with HIP events; those event packets
+    # add their own dispatch latency, so it reads a few us above the kernel.
     quant_phase()
     torch.cuda.synchronize()
+    reps = max(20, args.kernel_reps // 4)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in [(None, None)] * 3 + marks:
+        quant_phase()
+        if e0 is not None:
+            e0.record(stream)
+        gemm_phase()
+        if e1 is not None:
+            e1.record(stream)
+    torch.cuda.synchronize()
+    in_op = sorted(e0.elapsed_time(e1) for e0, e1 in marks)
+    in_op_ms = sum(in_op) / len(in_op)
     gemm_ms = graph_time(gemm_phase, args.kernel_reps)
     gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
     quant_ms = graph_time(quant_phase, max(20, args.kernel_reps // 4))
@@ -302,14 +320,22 @@ def main() -> int:
         "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
         "algorithmic_per_launch": f"2*M*N*K = {int(ops)} int8 ops",
         "avg_launch_us": round(gemm_ms * 1e3, 3),
+        "avg_launch_how": (f"{args.kernel_reps} contraction launches as one HIP graph, replayed between HIP "
+                           "events (median of 5 replays); rocprofv3 traces: bench.py --only gemm "
+                           "(profiles/gemm_i8_tile256_4096_kernel_trace.txt) and, inside the op, --only fused "
+                           "(profiles/dense_fused_i8_4096_kernel_trace.txt)"),
+        "in_op_events_us": round(in_op_ms * 1e3, 3),
+        "in_op_events_how": (f"HIP events around the contraction inside {reps} eager dense_fused_i8 calls on one "
+                             "stream (mean); includes the event packets' dispatch latency"),
         "traffic": read_pmc_traffic("gemm_i8_4096_pmc.txt"),
         "mfma_util": read_profile_value("gemm_i8_4096_mfma_pmc.txt", "mfma_util"),
         "held_clock_GHz": read_profile_value("gemm_i8_4096_mfma_pmc.txt", "held_clock_GHz"),
         "mfma_util_how": ("SQ_VALU_MFMA_BUSY_CYCLES per SIMD / SQ_BUSY_CYCLES per SE over the contraction's "
                           "dispatch (rocprofv3 --pmc, profiles/gemm_i8_4096_mfma_pmc.txt); the clock it held "
                           "is SQ_BUSY_CYCLES per SE / dispatch time"),
-        "profiles": ["profiles/gemm_i8_tile256_4096_kernel_trace.txt", "profiles/gemm_i8_4096_pmc.txt",
-                     "profiles/gemm_i8_4096_mfma_pmc.txt"],
+        "profiles": ["profiles/gemm_i8_tile256_4096_kernel_trace.txt",
+                     "profiles/dense_fused_i8_4096_kernel_trace.txt", "profiles/gemm_i8_4096_pmc.txt",
+                     "profiles/gemm_i8_4096_mfma_pmc.txt", "profiles/gemm_i8_4096_lds_pmc.txt"],
     }
     if roofline["held_clock_GHz"]:
         # the same kernel against the peak at the clock it holds (8192 int8 ops/clk/CU)
