@@ -193,7 +193,7 @@ constexpr uint64_t kROnChip4 = kRLdsA4 + (uint64_t)kRVA * kRT;  // 15,232 float4
 constexpr int kRBatch = 8;           // float4 loads in flight per thread on the rest of A
 constexpr uint32_t kTileDw = 64 * kTileRowDw;
 static_assert(kRLdsA4 % kWave == 0, "the LDS part of A is copied in whole 64-slot runs");
-static_assert(2 * kTileDw * 4 <= kRLdsA4 * 16, "the B transposes fit in A's LDS");
+static_assert(kRNT * kTileDw * 4 <= kRLdsA4 * 16, "the B transposes fit in A's LDS");
 constexpr uint64_t kSyncTimeoutTicks = 200000000ull;  // 2 s at 100 MHz
 constexpr uint64_t kResidentMinBytes = (uint64_t)12 << 20;
 
@@ -395,11 +395,13 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     wait_lgkmcnt0();  // every read of As is done: the B transposes reuse it
     lds_barrier();
 
-    // ---- B tiles from VGPRs: transposed through LDS into 128-byte qBt row segments
+    // ---- B tiles from VGPRs: every tile packed and staged in LDS (tile i in
+    // A's freed LDS at i * kTileDw), one barrier, then read back as 128-byte
+    // qBt row segments and stored
 #pragma unroll
     for (int i = 0; i < kRNT; i++) {
         if ((uint32_t)i < nt) {
-            uint32_t* buf = tileT + (i & 1) * kTileDw;
+            uint32_t* buf = tileT + i * kTileDw;
             if (fastB) {
                 buf[(4 * nq + 0) * kTileRowDw + kq] = pack4_fast(bv[i][0].x, bv[i][1].x, bv[i][2].x, bv[i][3].x, invB);
                 buf[(4 * nq + 1) * kTileRowDw + kq] = pack4_fast(bv[i][0].y, bv[i][1].y, bv[i][2].y, bv[i][3].y, invB);
@@ -411,14 +413,21 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
                 buf[(4 * nq + 2) * kTileRowDw + kq] = pack4(bv[i][0].z, bv[i][1].z, bv[i][2].z, bv[i][3].z, invB);
                 buf[(4 * nq + 3) * kTileRowDw + kq] = pack4(bv[i][0].w, bv[i][1].w, bv[i][2].w, bv[i][3].w, invB);
             }
-            wait_lgkmcnt0();
-            lds_barrier();
-            const uint32_t tile = tb0 + i;
-            const uint32_t k0 = (tile / ntn) * kBTK, n0 = (tile % ntn) * kBTN;
-            const uint32_t n = t >> 3, part = t & 7;
-            const uint32_t* row = buf + n * kTileRowDw + part * 4;
-            const v4i v = {(int)row[0], (int)row[1], (int)row[2], (int)row[3]};
-            *reinterpret_cast<v4i*>(qBt + (uint64_t)(n0 + n) * K + k0 + part * 16) = v;
+        }
+    }
+    wait_lgkmcnt0();
+    lds_barrier();
+    {
+        const uint32_t n = t >> 3, part = t & 7;
+#pragma unroll
+        for (int i = 0; i < kRNT; i++) {
+            if ((uint32_t)i < nt) {
+                const uint32_t* row = tileT + i * kTileDw + n * kTileRowDw + part * 4;
+                const v4i v = {(int)row[0], (int)row[1], (int)row[2], (int)row[3]};
+                const uint32_t tile = tb0 + i;
+                const uint32_t k0 = (tile / ntn) * kBTK, n0 = (tile % ntn) * kBTN;
+                *reinterpret_cast<v4i*>(qBt + (uint64_t)(n0 + n) * K + k0 + part * 16) = v;
+            }
         }
     }
     // ---- A past the on-chip part: read again and quantize
