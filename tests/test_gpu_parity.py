@@ -336,6 +336,40 @@ def test_dense_fused_resident_quantizer_shapes(ane, oracle, M, N, K):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 2048, 2048), (1, 4096, 4096), (5000, 64, 4096), (300, 700, 333)])
+def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
+    """The quantize phase alone (ane_hip_dense_fused_i8_quantize), byte for
+    byte: the workspace's qA (M x Kp) and qBt (N x Kp, B transposed), zeros
+    for k >= K, and the two scales, against the oracle's per-tensor
+    quantization of A and of B.  The first three shapes take the one-launch
+    resident quantizer (1 row; 5000 rows, whose workgroup shares run past
+    LDS and registers), the last the two-pass one (K % 128 != 0).
+    Workspace layout (gemm_i8.hip, fused_layout): scales at 0, the partial
+    maxima at 256 (2 x 1024 uint32), qA at 8448, qBt after qA rounded up to
+    256 bytes; Kp = ceil(K / 128) * 128."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M + N + 5)
+    qa_ref, sa = oracle.quantize_exact(A.ravel())
+    qb_ref, sb = oracle.quantize_exact(B.ravel())
+    Kp = -(-K // 128) * 128
+    want_a = np.zeros((M, Kp), np.int8)
+    want_a[:, :K] = qa_ref[: M * K].reshape(M, K)
+    want_b = np.zeros((N, Kp), np.int8)
+    want_b[:, :K] = qb_ref[: K * N].reshape(K, N).T
+    ws = torch.full((ane.dense_fused_i8_workspace_size(M, N, K),), 0x5A, dtype=torch.uint8, device="cuda")
+    sc = zeros(2, torch.float32)
+    ane.dense_fused_i8_quantize(M, N, K, dev(A), dev(B), ws, scales_out=sc)
+    w = host(ws)
+    off_a = 8448
+    off_b = off_a + -(-(M * Kp) // 256) * 256
+    got_a = w[off_a: off_a + M * Kp].view(np.int8).reshape(M, Kp)
+    got_b = w[off_b: off_b + N * Kp].view(np.int8).reshape(N, Kp)
+    np.testing.assert_array_equal(got_a, want_a)
+    np.testing.assert_array_equal(got_b, want_b)
+    assert host(sc).tobytes() == np.array([sa, sb], F32).tobytes()
+
+
 def test_dense_fused_grid_wait_limit(ane, oracle):
     """The resident quantizer's bounded grid-wide wait, forced from the host
     to a one-tick limit: every workgroup still finishes, and a launch whose
