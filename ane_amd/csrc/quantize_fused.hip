@@ -191,6 +191,7 @@ constexpr uint32_t kRLdsSteps = (kRLdsA4 + kRT - 1) / kRT;
 constexpr int kRVA = 10;             // float4s of A per thread in VGPRs (249 VGPRs in all, no spill)
 constexpr uint64_t kROnChip4 = kRLdsA4 + (uint64_t)kRVA * kRT;  // 15,232 float4s (238 KB) of A on chip
 constexpr int kRBatch = 8;           // float4 loads in flight per thread on the rest of A
+static_assert(kRNT * 4 + kRVA + kRBatch < 64, "the loads issued after A's copies fit the vmcnt field");
 constexpr uint32_t kTileDw = 64 * kTileRowDw;
 static_assert(kRLdsA4 % kWave == 0, "the LDS part of A is copied in whole 64-slot runs");
 static_assert(kRNT * kTileDw * 4 <= kRLdsA4 * 16, "the B transposes fit in A's LDS");
@@ -208,8 +209,9 @@ constexpr uint64_t kResidentMinBytes = (uint64_t)12 << 20;
 // generation word, which the waiting workgroups poll (gen0 read before
 // arriving, so the advance cannot be missed).  Group counters return to
 // zero and the top counter to a multiple of the group count, so the slot
-// needs no reset between launches.  The wait gives up after timeout_ticks
-// of the 100 MHz realtime counter and records that in the error word.
+// needs no reset between launches (a launch's resets complete before the
+// kernel does).  The wait gives up after timeout_ticks of the 100 MHz
+// realtime counter and records that in the error word.
 constexpr uint32_t kSyncGroups = 16;
 constexpr uint32_t kSyncLineDw = 32;                       // 128-byte lines
 constexpr uint32_t kSyncSlotDw = (1 + 2 * kSyncGroups) * kSyncLineDw;
@@ -230,6 +232,18 @@ __device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// max over the 64 lanes, every lane gets it: DPP within each 16-lane row,
+// then the four row maxima through readlane (no LDS round trips)
+__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t m) {
+    m = umax(m, dpp_u32<kDppQuadXor1>(m));
+    m = umax(m, dpp_u32<kDppQuadXor2>(m));
+    m = umax(m, dpp_u32<kDppHalfMirror>(m));
+    m = umax(m, dpp_u32<kDppRowMirror>(m));
+    const uint32_t r0 = __builtin_amdgcn_readlane(m, 0), r1 = __builtin_amdgcn_readlane(m, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(m, 32), r3 = __builtin_amdgcn_readlane(m, 48);
+    return umax(umax(r0, r1), umax(r2, r3));
+}
+
 __device__ __forceinline__ void grid_arrive_wait(uint32_t* sync, uint32_t* partials, uint32_t ma, uint32_t mb,
                                                  uint32_t w, uint32_t G, uint64_t timeout_ticks) {
     const uint32_t ng = G < kSyncGroups ? G : kSyncGroups;
@@ -240,15 +254,17 @@ __device__ __forceinline__ void grid_arrive_wait(uint32_t* sync, uint32_t* parti
     st_agent(&partials[G + w], mb);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (add_agent(sync_sub(sync, g), 1u) == members - 1) {
-        st_agent(sync_sub(sync, g), 0u);
-        if (add_agent(sync_top(sync), 1u) % ng == ng - 1) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // the group's counter is reset after the top counter's add, so that
+        // add does not queue behind the store
+        const bool last = add_agent(sync_top(sync), 1u) % ng == ng - 1;
+        if (last)
             for (uint32_t i = 0; i < ng; i++) st_agent(sync_gen(sync, i), gen0 + 1);
-        }
+        st_agent(sync_sub(sync, g), 0u);
+        if (last) return;
     }
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (ld_agent(gen) == gen0) {
-        __builtin_amdgcn_s_sleep(16);
+        __builtin_amdgcn_s_sleep(4);
         if (__builtin_amdgcn_s_memrealtime() - t0 > timeout_ticks) {
             __hip_atomic_fetch_or(sync_err(sync), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
@@ -256,6 +272,29 @@ __device__ __forceinline__ void grid_arrive_wait(uint32_t* sync, uint32_t* parti
     }
     asm volatile("" ::: "memory");
 }
+
+// Range-checked buffer access (make_rsrc): a load past the resource's
+// range returns zeros and a store past it is dropped, so the resident
+// kernel's per-lane edge cases need no branches, and the compiler's
+// s_waitcnt counts stay exact (a branch around a load makes it drain
+// every load in flight at the join).  kOff is past every range.
+constexpr uint32_t kOff = 0x80000000u;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t r, uint32_t off, v4i v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 0);
+}
+template <bool B_>
+struct BoolTag {
+    static constexpr bool value = B_;
+};
 
 __global__ void __launch_bounds__(kRT)
 k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, uint32_t N, uint32_t K,
@@ -269,57 +308,53 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     const uint32_t G = gridDim.x, w = blockIdx.x;
     const uint32_t ntn = N / kBTN;
 
-    // ---- B tiles into VGPRs
+    // ---- phase 1: every operand byte read once.  Vector-memory loads
+    // complete in issue order, so the copies of A's LDS part go first: they
+    // are waited for (by count) and reduced while the B tiles, A's VGPR part
+    // and the first batch of A's rest are still in flight.
+    //   A: this workgroup's nw float4s from a0.  The first kRLdsA4 are copied
+    //      into LDS (a wave copies only whole 64-slot runs that start below
+    //      nres, so no copy writes past As), the next kRVA per thread are
+    //      loaded into VGPRs, and the rest is read for the maximum here and
+    //      read again in phase 2.
+    //   B: perT tiles into VGPRs (tiles past this workgroup's read as zeros).
+    const uint64_t a0 = (uint64_t)w * perA4;
+    const uint32_t nw = a0 < nA4 ? (uint32_t)(a0 + perA4 < nA4 ? perA4 : nA4 - a0) : 0;
+    const uint32_t nres = nw < kRLdsA4 ? nw : kRLdsA4;
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(A + 4 * a0, nw * 16u);
+#pragma unroll
+    for (uint32_t s = 0; s < kRLdsSteps; s++)
+        if (s * kRT + wv * kWave < nres) copy16_to_lds(rsA, &As[s * kRT + wv * kWave], (s * kRT + t) * 16u);
+    asm volatile("" ::: "memory");  // keeps the loads below after the copies
+
     const uint32_t tb0 = w * perT;
     const uint32_t nt = nTiles > tb0 ? (nTiles - tb0 < perT ? nTiles - tb0 : perT) : 0;
     const uint32_t kq = t >> 4, nq = t & 15;
+    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(B, K * N * 4u);
     float4 bv[kRNT][4];
 #pragma unroll
     for (int i = 0; i < kRNT; i++) {
-        if ((uint32_t)i < nt) {
-            const uint32_t tile = tb0 + i;
-            const uint32_t k0 = (tile / ntn) * kBTK, n0 = (tile % ntn) * kBTN;
-            const float* src = B + (uint64_t)(k0 + 4 * kq) * N + n0 + 4 * nq;
+        const uint32_t tile = tb0 + i;
+        const uint32_t k0 = (tile / ntn) * kBTK, n0 = (tile % ntn) * kBTN;
+        const uint32_t off = ((k0 + 4 * kq) * N + n0 + 4 * nq) * 4u;
 #pragma unroll
-            for (int r = 0; r < 4; r++) bv[i][r] = *reinterpret_cast<const float4*>(src + (uint64_t)r * N);
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; r++) bv[i][r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int r = 0; r < 4; r++) bv[i][r] = load4(rsB, (uint32_t)i < nt ? off + r * N * 4u : kOff);
     }
-
-    // ---- A: the first kRLdsA4 float4s of this workgroup's range into LDS
-    // (a wave copies only whole 64-slot runs below nres, so no copy writes
-    // past As), the next kRVA per thread into VGPRs
-    const uint64_t a0 = (uint64_t)w * perA4;
-    const uint64_t a1 = a0 + perA4 < nA4 ? a0 + perA4 : nA4;
-    const uint32_t nres = a1 > a0 ? (uint32_t)(a1 - a0 < kRLdsA4 ? a1 - a0 : kRLdsA4) : 0;
-    {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(A + 4 * a0, nres * 16u);
-#pragma unroll
-        for (uint32_t s = 0; s < kRLdsSteps; s++)
-            if (s * kRT + wv * kWave < nres) copy16_to_lds(rs, &As[s * kRT + wv * kWave], (s * kRT + t) * 16u);
-    }
-    const float4* A4 = reinterpret_cast<const float4*>(A);
-    const uint64_t jv = a0 + kRLdsA4 + t;
     float4 av[kRVA];
 #pragma unroll
-    for (int u = 0; u < kRVA; u++)
-        av[u] = jv + u * kRT < a1 ? A4[jv + u * kRT] : make_float4(0.f, 0.f, 0.f, 0.f);
-    // ---- A past the on-chip part (at 4096 x 4096, 1,152 of a workgroup's
-    // 16,384 float4s): read for the maximum only, kRBatch loads in flight
-    // per thread
+    for (int u = 0; u < kRVA; u++) av[u] = load4(rsA, (kRLdsA4 + u * kRT + t) * 16u);
+    float4 rv[kRBatch];
+#pragma unroll
+    for (int u = 0; u < kRBatch; u++) rv[u] = load4(rsA, (kROnChip4 + u * kRT + t) * 16u);
+
+    wait_vmcnt<kRNT * 4 + kRVA + kRBatch>();  // this wave's copies have landed
+    lds_barrier();
     uint32_t mA = 0, mB = 0;
-    {
-        uint64_t j = a0 + kROnChip4 + t;
-        for (; j + (kRBatch - 1) * kRT < a1; j += kRBatch * kRT) {
-            float4 v[kRBatch];
 #pragma unroll
-            for (int u = 0; u < kRBatch; u++) v[u] = A4[j + u * kRT];
-#pragma unroll
-            for (int u = 0; u < kRBatch; u++) mA = umax(mA, absmax4(v[u]));
-        }
-        for (; j < a1; j += kRT) mA = umax(mA, absmax4(A4[j]));
+    for (uint32_t s = 0; s < kRLdsSteps; s++) {
+        const uint32_t idx = s * kRT + t;
+        const uint32_t m = absmax4(As[idx < kRLdsA4 ? idx : kRLdsA4 - 1]);
+        mA = umax(mA, idx < nres ? m : 0u);
     }
 #pragma unroll
     for (int i = 0; i < kRNT; i++)
@@ -327,15 +362,18 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         for (int r = 0; r < 4; r++) mB = umax(mB, absmax4(bv[i][r]));
 #pragma unroll
     for (int u = 0; u < kRVA; u++) mA = umax(mA, absmax4(av[u]));
-    wait_vmcnt<0>();
-    lds_barrier();
 #pragma unroll
-    for (uint32_t s = 0; s < kRLdsSteps; s++)
-        if (s * kRT + t < nres) mA = umax(mA, absmax4(As[s * kRT + t]));
+    for (int u = 0; u < kRBatch; u++) mA = umax(mA, absmax4(rv[u]));
+    for (uint32_t base = kROnChip4 + kRBatch * kRT; base < nw; base += kRBatch * kRT) {
+#pragma unroll
+        for (int u = 0; u < kRBatch; u++) rv[u] = load4(rsA, (base + u * kRT + t) * 16u);
+#pragma unroll
+        for (int u = 0; u < kRBatch; u++) mA = umax(mA, absmax4(rv[u]));
+    }
 
     // ---- workgroup maxima, then the grid-wide wait
-    mA = wave_max_u32(mA);
-    mB = wave_max_u32(mB);
+    mA = wave_max_dpp(mA);
+    mB = wave_max_dpp(mB);
     if (lane == 0) {
         red[wv] = mA;
         red[kRT / kWave + wv] = mB;
@@ -355,8 +393,8 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         pa = umax(pa, ld_agent(&partials[i]));
         pb = umax(pb, ld_agent(&partials[G + i]));
     }
-    pa = wave_max_u32(pa);
-    pb = wave_max_u32(pb);
+    pa = wave_max_dpp(pa);
+    pb = wave_max_dpp(pb);
     if (lane == 0) {
         red[wv] = pa;
         red[kRT / kWave + wv] = pb;
@@ -376,70 +414,87 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         scales[0] = scaleA;
         scales[1] = scaleB;
     }
-    const bool fastA = fast_quant_ok(__uint_as_float(pa), invA);
-    const bool fastB = fast_quant_ok(__uint_as_float(pb), invB);
-    auto qa = [&](float4 v) {
-        return fastA ? pack4_fast(v.x, v.y, v.z, v.w, invA) : pack4(v.x, v.y, v.z, v.w, invA);
-    };
 
-    // ---- A from LDS, then from VGPRs (K % 128 == 0: float4 j of A is dword j of qA)
-    uint32_t* qA32 = reinterpret_cast<uint32_t*>(qA);
+    // ---- phase 2, straight-line for one quantizer (pack4_fast when both
+    // tensors allow it, else the exact pack4 for both).  Order: A from VGPRs
+    // (freeing them for the first batch of A's rest, whose loads then fly
+    // under the stores that follow), A from LDS, then the B tiles (packed
+    // and staged in A's freed LDS at i * kTileDw, one barrier, read back as
+    // 128-byte qBt row segments), then A's rest.  K % 128 == 0, so float4 j
+    // of A is dword j of qA.
+    const __amdgpu_buffer_rsrc_t rsQ = make_rsrc(reinterpret_cast<uint32_t*>(qA) + a0, nw * 4u);
+    const __amdgpu_buffer_rsrc_t rsQB = make_rsrc(qBt, K * N);
+    auto phase2 = [&](auto tag, auto full_tag) {
+        constexpr bool F = decltype(tag)::value;
+        // U: A's LDS and VGPR parts are full here, so their stores need no
+        // guard; otherwise workgroup-uniform guards skip the arithmetic on
+        // zeros (workgroups holding little or no A)
+        constexpr bool U = decltype(full_tag)::value;
+        auto q4 = [&](float a, float b, float c, float d, float inv) {
+            return F ? pack4_fast(a, b, c, d, inv) : pack4(a, b, c, d, inv);
+        };
 #pragma unroll
-    for (uint32_t s = 0; s < kRLdsSteps; s++) {
-        const uint32_t idx = s * kRT + t;
-        if (idx < nres) qA32[a0 + idx] = qa(As[idx]);
-    }
+        for (int u = 0; u < kRVA; u++)
+            if (U || kRLdsA4 + u * kRT < nw)
+                store1(rsQ, (kRLdsA4 + u * kRT + t) * 4u, q4(av[u].x, av[u].y, av[u].z, av[u].w, invA));
+        // the first batch of A's rest: loaded here on the fast path, after
+        // the B tiles on the exact one (whose pack4 needs more registers)
+        auto load_rest = [&] {
 #pragma unroll
-    for (int u = 0; u < kRVA; u++)
-        if (jv + u * kRT < a1) qA32[jv + u * kRT] = qa(av[u]);
-    wait_lgkmcnt0();  // every read of As is done: the B transposes reuse it
-    lds_barrier();
-
-    // ---- B tiles from VGPRs: every tile packed and staged in LDS (tile i in
-    // A's freed LDS at i * kTileDw), one barrier, then read back as 128-byte
-    // qBt row segments and stored
+            for (int u = 0; u < kRVA; u++) av[u] = load4(rsA, (kROnChip4 + u * kRT + t) * 16u);
+        };
+        if (F) load_rest();
 #pragma unroll
-    for (int i = 0; i < kRNT; i++) {
-        if ((uint32_t)i < nt) {
-            uint32_t* buf = tileT + i * kTileDw;
-            if (fastB) {
-                buf[(4 * nq + 0) * kTileRowDw + kq] = pack4_fast(bv[i][0].x, bv[i][1].x, bv[i][2].x, bv[i][3].x, invB);
-                buf[(4 * nq + 1) * kTileRowDw + kq] = pack4_fast(bv[i][0].y, bv[i][1].y, bv[i][2].y, bv[i][3].y, invB);
-                buf[(4 * nq + 2) * kTileRowDw + kq] = pack4_fast(bv[i][0].z, bv[i][1].z, bv[i][2].z, bv[i][3].z, invB);
-                buf[(4 * nq + 3) * kTileRowDw + kq] = pack4_fast(bv[i][0].w, bv[i][1].w, bv[i][2].w, bv[i][3].w, invB);
-            } else {
-                buf[(4 * nq + 0) * kTileRowDw + kq] = pack4(bv[i][0].x, bv[i][1].x, bv[i][2].x, bv[i][3].x, invB);
-                buf[(4 * nq + 1) * kTileRowDw + kq] = pack4(bv[i][0].y, bv[i][1].y, bv[i][2].y, bv[i][3].y, invB);
-                buf[(4 * nq + 2) * kTileRowDw + kq] = pack4(bv[i][0].z, bv[i][1].z, bv[i][2].z, bv[i][3].z, invB);
-                buf[(4 * nq + 3) * kTileRowDw + kq] = pack4(bv[i][0].w, bv[i][1].w, bv[i][2].w, bv[i][3].w, invB);
+        for (uint32_t s = 0; s < kRLdsSteps; s++) {
+            if (U || s * kRT < nres) {
+                const uint32_t idx = s * kRT + t;
+                const float4 v = As[idx < kRLdsA4 ? idx : kRLdsA4 - 1];
+                store1(rsQ, idx < nres ? idx * 4u : kOff, q4(v.x, v.y, v.z, v.w, invA));
             }
         }
-    }
-    wait_lgkmcnt0();
-    lds_barrier();
-    {
-        const uint32_t n = t >> 3, part = t & 7;
+        wait_lgkmcnt0();  // every read of As is done: the B transposes reuse it
+        lds_barrier();
 #pragma unroll
         for (int i = 0; i < kRNT; i++) {
-            if ((uint32_t)i < nt) {
+            uint32_t* buf = tileT + i * kTileDw;
+            buf[(4 * nq + 0) * kTileRowDw + kq] = q4(bv[i][0].x, bv[i][1].x, bv[i][2].x, bv[i][3].x, invB);
+            buf[(4 * nq + 1) * kTileRowDw + kq] = q4(bv[i][0].y, bv[i][1].y, bv[i][2].y, bv[i][3].y, invB);
+            buf[(4 * nq + 2) * kTileRowDw + kq] = q4(bv[i][0].z, bv[i][1].z, bv[i][2].z, bv[i][3].z, invB);
+            buf[(4 * nq + 3) * kTileRowDw + kq] = q4(bv[i][0].w, bv[i][1].w, bv[i][2].w, bv[i][3].w, invB);
+        }
+        wait_lgkmcnt0();
+        lds_barrier();
+        {
+            const uint32_t n = t >> 3, part = t & 7;
+#pragma unroll
+            for (int i = 0; i < kRNT; i++) {
                 const uint32_t* row = tileT + i * kTileDw + n * kTileRowDw + part * 4;
                 const v4i v = {(int)row[0], (int)row[1], (int)row[2], (int)row[3]};
                 const uint32_t tile = tb0 + i;
                 const uint32_t k0 = (tile / ntn) * kBTK, n0 = (tile % ntn) * kBTN;
-                *reinterpret_cast<v4i*>(qBt + (uint64_t)(n0 + n) * K + k0 + part * 16) = v;
+                store4(rsQB, (uint32_t)i < nt ? (n0 + n) * K + k0 + part * 16 : kOff, v);
             }
         }
-    }
-    // ---- A past the on-chip part: read again and quantize
-    for (uint64_t jr = a0 + kROnChip4 + t; jr < a1; jr += kRBatch * kRT) {
-        float4 v[kRBatch];
+        if (!F) load_rest();
 #pragma unroll
-        for (int u = 0; u < kRBatch; u++)
-            if (jr + u * kRT < a1) v[u] = A4[jr + u * kRT];
+        for (int u = 0; u < kRVA; u++)
+            if (kROnChip4 + u * kRT < nw)
+                store1(rsQ, (kROnChip4 + u * kRT + t) * 4u, q4(av[u].x, av[u].y, av[u].z, av[u].w, invA));
+        for (uint32_t base = kROnChip4 + kRVA * kRT; base < nw; base += kRBatch * kRT) {
+            float4 v[kRBatch];
 #pragma unroll
-        for (int u = 0; u < kRBatch; u++)
-            if (jr + u * kRT < a1) qA32[jr + u * kRT] = qa(v[u]);
-    }
+            for (int u = 0; u < kRBatch; u++) v[u] = load4(rsA, (base + u * kRT + t) * 16u);
+#pragma unroll
+            for (int u = 0; u < kRBatch; u++)
+                store1(rsQ, (base + u * kRT + t) * 4u, q4(v[u].x, v[u].y, v[u].z, v[u].w, invA));
+        }
+    };
+    if (!fast_quant_ok(__uint_as_float(pa), invA) || !fast_quant_ok(__uint_as_float(pb), invB))
+        phase2(BoolTag<false>{}, BoolTag<false>{});
+    else if (nw >= kROnChip4)
+        phase2(BoolTag<true>{}, BoolTag<true>{});
+    else
+        phase2(BoolTag<true>{}, BoolTag<false>{});
 }
 
 // The wait's slot in device memory: zero when the code object loads, left
@@ -521,6 +576,8 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     const uint32_t perT = (uint32_t)((nTiles + G - 1) / G);
     const uint64_t nA4 = (uint64_t)M * K / 4;
     const uint64_t perA4 = (nA4 + G - 1) / G;
+    // the kernel's buffer offsets are 32-bit byte offsets below kOff
+    if (perA4 * 16 >= kOff || (uint64_t)K * N * 4 >= kOff) return false;
     // Resident launches on one device are ordered: a launch on another
     // stream than the previous one waits for it.  A captured launch cannot
     // wait for work outside its graph, so under capture the route is taken
