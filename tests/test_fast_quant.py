@@ -3,14 +3,16 @@ ane_amd/csrc/common.hpp), checked on the CPU against the oracle's
 quantize_fp32_i8 (oracle/ane_oracle.c, bytecode_interpreter.s:1885-1950).
 
 When a tensor's max |x| and inv = 127 / max are both finite, t = fl(x * inv)
-is finite, and the handler's q = fcvtzs(frintn(clamp(t, -127, 127))) equals
-the low byte of the bits of fl(clamp(t) + 1.5 * 2^23): that sum lies in
-[2^23, 2^24), where the fp32 ulp is 1, so the one rounding of the addition
-is round-half-to-even to an integer (frintn), and the integer's
-two's-complement byte is the low byte of the float's bits.  numpy float32
-arithmetic rounds each operation to nearest-even, as the GPU's fmul, fmed3
-and fadd do, so the restatement below is the kernel's arithmetic, and the
-oracle is the reference's.  CPU only."""
+is finite with |t| <= 127 (1 + 2^-24)^2 < 127.5 for every element x, so the
+handler's clamp to [-127, 127] cannot bind after rounding, and its
+q = fcvtzs(frintn(clamp(t, -127, 127))) equals the low byte of the bits of
+fl(t + 1.5 * 2^23): that sum lies in [2^23, 2^24), where the fp32 ulp is 1,
+so the one rounding of the addition is round-half-to-even to an integer
+(frintn), and the integer's two's-complement byte is the low byte of the
+float's bits (which the kernel's SDWA add writes straight into its byte of
+the packed result).  numpy float32 arithmetic rounds each operation to
+nearest-even, as the GPU's fmul and fadd do, so the restatement below is the
+kernel's arithmetic, and the oracle is the reference's.  CPU only."""
 import numpy as np
 import pytest
 
@@ -22,8 +24,7 @@ def fast_q(x: np.ndarray, amax: np.float32) -> np.ndarray:
     inv = F32(127.0) / amax if amax != 0 else F32(127.0)
     assert np.isfinite(amax) and np.isfinite(inv)
     t = (x.astype(F32) * inv).astype(F32)
-    c = np.minimum(np.maximum(t, F32(-127.0)), F32(127.0))  # fmed3 on finite t
-    s = (c + MAGIC).astype(F32)
+    s = (t + MAGIC).astype(F32)  # no clamp: |t| < 127.5
     return (s.view(np.uint32) & 0xFF).astype(np.uint8).view(np.int8)
 
 
@@ -68,7 +69,7 @@ def test_fast_identity_every_tie_and_the_clamp(oracle):
 def test_fast_identity_scales(oracle, amax):
     """Tensors whose max sets inv to ordinary, very large (amax 1e-36: inv
     ~1.27e38, still finite) and very small values; the element at +-amax may
-    round just past 127 in t and is clamped."""
+    round just past 127 in t, and still rounds to +-127."""
     g = np.random.default_rng(int(np.log10(amax) + 50))
     x = (g.uniform(-1, 1, 8192) * amax).astype(F32)
     x[0], x[1] = F32(amax), F32(-amax)
@@ -86,3 +87,27 @@ def test_fast_path_condition_excludes_overflowing_inv():
     for amax in (F32(1e-40), F32(3e-39)):
         with np.errstate(over="ignore", divide="ignore"):
             assert not np.isfinite(F32(127.0) / amax)
+
+
+def test_fast_path_bound_at_the_max():
+    """The bound the missing clamp rests on: t = fl(amax * fl(127 / amax))
+    stays below 127.5 (it is 127 up to a few ulps) for maxima over the whole
+    fp32 range where inv is finite (amax >= 127 / FLT_MAX; random bit
+    patterns, whose subnormals and tiny normals drop out with an infinite
+    inv), including every power of two and its neighbours."""
+    g = np.random.default_rng(7)
+    bits = g.integers(1, 0x7F7FFFFF, 400_000, dtype=np.uint32)  # positive finite floats
+    pow2 = (np.arange(1, 255, dtype=np.uint32) << 23)
+    edges = np.concatenate([pow2 - 1, pow2, pow2 + 1]).astype(np.uint32)
+    amax = np.concatenate([bits, edges]).view(F32)
+    with np.errstate(over="ignore", divide="ignore"):
+        inv = (F32(127.0) / amax).astype(F32)
+    ok = np.isfinite(inv)
+    t = (amax[ok] * inv[ok]).astype(F32)
+    assert ok.sum() > 390_000
+    assert np.all(np.abs(t) < F32(127.5)), np.abs(t).max()
+    assert np.abs(t - F32(127.0)).max() <= F32(127.0) * F32(2.0 ** -22)
+    # and the fast form at x = +-amax is +-127 exactly
+    q = (((t + MAGIC).astype(F32)).view(np.uint32) & 0xFF).astype(np.uint8).view(np.int8)
+    assert np.all(q == 127)
+
