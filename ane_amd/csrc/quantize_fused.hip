@@ -307,18 +307,24 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
     const uint32_t t = threadIdx.x, wv = t >> 6, lane = t & 63;
     const uint32_t G = gridDim.x, w = blockIdx.x;
     const uint32_t ntn = N / kBTN;
+    // Share index: workgroups go to the eight XCDs round-robin (w % 8), and
+    // shares that are contiguous per XCD (one block of A and one run of B's
+    // tiles for each XCD) measured faster to read than shares interleaved
+    // across the XCDs (4096^3: phase 1 about 3 us sooner).  Any order is
+    // correct; this one is a permutation of 0 .. G-1.
+    const uint32_t ws = G % 8 == 0 ? (w % 8) * (G / 8) + w / 8 : w;
 
     // ---- phase 1: every operand byte read once.  Vector-memory loads
     // complete in issue order, so the copies of A's LDS part go first: they
     // are waited for (by count) and reduced while the B tiles, A's VGPR part
     // and the first batch of A's rest are still in flight.
-    //   A: this workgroup's nw float4s from a0.  The first kRLdsA4 are copied
+    //   A: share ws's nw float4s from a0.  The first kRLdsA4 are copied
     //      into LDS (a wave copies only whole 64-slot runs that start below
     //      nres, so no copy writes past As), the next kRVA per thread are
     //      loaded into VGPRs, and the rest is read for the maximum here and
     //      read again in phase 2.
-    //   B: perT tiles into VGPRs (tiles past this workgroup's read as zeros).
-    const uint64_t a0 = (uint64_t)w * perA4;
+    //   B: share ws's perT tiles into VGPRs (tiles past the last read as zeros).
+    const uint64_t a0 = (uint64_t)ws * perA4;
     const uint32_t nw = a0 < nA4 ? (uint32_t)(a0 + perA4 < nA4 ? perA4 : nA4 - a0) : 0;
     const uint32_t nres = nw < kRLdsA4 ? nw : kRLdsA4;
     const __amdgpu_buffer_rsrc_t rsA = make_rsrc(A + 4 * a0, nw * 16u);
@@ -327,7 +333,7 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         if (s * kRT + wv * kWave < nres) copy16_to_lds(rsA, &As[s * kRT + wv * kWave], (s * kRT + t) * 16u);
     asm volatile("" ::: "memory");  // keeps the loads below after the copies
 
-    const uint32_t tb0 = w * perT;
+    const uint32_t tb0 = ws * perT;
     const uint32_t nt = nTiles > tb0 ? (nTiles - tb0 < perT ? nTiles - tb0 : perT) : 0;
     const uint32_t kq = t >> 4, nq = t & 15;
     const __amdgpu_buffer_rsrc_t rsB = make_rsrc(B, K * N * 4u);
