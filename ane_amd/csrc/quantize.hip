@@ -72,13 +72,19 @@ k_quantize(const float* __restrict__ src, uint64_t n, int8_t* __restrict__ dst,
         const uint64_t n4 = n >> 2;
         const float4* s4 = reinterpret_cast<const float4*>(src);
         uint32_t* d4 = reinterpret_cast<uint32_t*>(dst);
-        for (uint64_t i = tid; i < n4; i += stride) {
-            float4 v = s4[i];
-            uint32_t q = (uint32_t)(quant1(v.x, inv) & 0xff) |
-                         ((uint32_t)(quant1(v.y, inv) & 0xff) << 8) |
-                         ((uint32_t)(quant1(v.z, inv) & 0xff) << 16) |
-                         ((uint32_t)(quant1(v.w, inv) & 0xff) << 24);
-            d4[i] = q;
+        // every value is one whose max |x| was just folded, so pack4_fast
+        // (bit-identical, two VALU per value) applies whenever that max and
+        // inv are finite
+        if (fast_quant_ok(__uint_as_float(m), inv)) {
+            for (uint64_t i = tid; i < n4; i += stride) {
+                const float4 v = s4[i];
+                d4[i] = pack4_fast(v.x, v.y, v.z, v.w, inv);
+            }
+        } else {
+            for (uint64_t i = tid; i < n4; i += stride) {
+                const float4 v = s4[i];
+                d4[i] = pack4(v.x, v.y, v.z, v.w, inv);
+            }
         }
         head = n4 << 2;
     }

@@ -95,6 +95,9 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
     float scale, inv;
     quant_params(amax, scale, inv);
     if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == nqA)) scales[isA ? 0 : 1] = scale;
+    // the values quantized here are the tensor's own, whose max was just
+    // folded: pack4_fast applies whenever that max and inv are finite
+    const bool fast = fast_quant_ok(amax, inv);
 
     if (isA) {
         const uint64_t chunks_per_row = Kp / 16;
@@ -113,10 +116,17 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
                 const float4 v1 = reinterpret_cast<const float4*>(src)[1];
                 const float4 v2 = reinterpret_cast<const float4*>(src)[2];
                 const float4 v3 = reinterpret_cast<const float4*>(src)[3];
-                w[0] = pack4(v0.x, v0.y, v0.z, v0.w, inv);
-                w[1] = pack4(v1.x, v1.y, v1.z, v1.w, inv);
-                w[2] = pack4(v2.x, v2.y, v2.z, v2.w, inv);
-                w[3] = pack4(v3.x, v3.y, v3.z, v3.w, inv);
+                if (fast) {
+                    w[0] = pack4_fast(v0.x, v0.y, v0.z, v0.w, inv);
+                    w[1] = pack4_fast(v1.x, v1.y, v1.z, v1.w, inv);
+                    w[2] = pack4_fast(v2.x, v2.y, v2.z, v2.w, inv);
+                    w[3] = pack4_fast(v3.x, v3.y, v3.z, v3.w, inv);
+                } else {
+                    w[0] = pack4(v0.x, v0.y, v0.z, v0.w, inv);
+                    w[1] = pack4(v1.x, v1.y, v1.z, v1.w, inv);
+                    w[2] = pack4(v2.x, v2.y, v2.z, v2.w, inv);
+                    w[3] = pack4(v3.x, v3.y, v3.z, v3.w, inv);
+                }
             } else {
                 for (int e = 0; e < 16; e++)
                     if (k + e < K) w[e >> 2] |= (uint32_t)(quant1(src[e], inv) & 0xff) << (8 * (e & 3));
@@ -150,7 +160,8 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
         // column j of the 4 x 4 block = 4 consecutive k of output row n = gn + j
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            tileT[(4 * nq + j) * kTileRowDw + g * 16 + kq] = pack4(v[0][j], v[1][j], v[2][j], v[3][j], inv);
+            tileT[(4 * nq + j) * kTileRowDw + g * 16 + kq] =
+                fast ? pack4_fast(v[0][j], v[1][j], v[2][j], v[3][j], inv) : pack4(v[0][j], v[1][j], v[2][j], v[3][j], inv);
     }
     __syncthreads();
     {
