@@ -13,6 +13,7 @@
 namespace ane {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
@@ -229,6 +230,12 @@ __device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, void* ds
 // the buffer instruction's cache-policy field): for weight streams read once
 // per launch, measured 3-8 % faster on the Q8_0 matvecs.
 constexpr int kCpolNt = 2;
+// The gfx940+ "sc1" bit (agent scope) on a store: the line is written
+// through the XCD's L2 to the memory side instead of being left dirty there,
+// so a kernel that writes its output last does not end with a write-back
+// burst of its L2s (the operand quantizer: 1.5 us of a 30 us launch, and
+// the contraction reading its output next is no slower).
+constexpr int kCpolSc1 = 16;
 __device__ __forceinline__ void copy16_to_lds_nt(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voffset, 0, 0, kCpolNt);
 }

@@ -285,22 +285,22 @@ __device__ __forceinline__ void grid_arrive_wait(uint32_t* sync, uint32_t* parti
 }
 
 // Range-checked buffer access (make_rsrc): a load past the resource's
-// range returns zeros and a store past it is dropped, so the resident
+// range returns zeros and a store past it is dropped (stores write through
+// the L2, kCpolSc1), so the resident
 // kernel's per-lane edge cases need no branches, and the compiler's
 // s_waitcnt counts stay exact (a branch around a load makes it drain
 // every load in flight at the join).  kOff is past every range.
 constexpr uint32_t kOff = 0x80000000u;
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     return make_float4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void store1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
-    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kCpolSc1);
 }
 __device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t r, uint32_t off, v4i v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, kCpolSc1);
 }
 template <bool B_>
 struct BoolTag {
