@@ -245,10 +245,12 @@ def main() -> int:
     # ------------------------------------------------------------ headline
     # The K timed steps are K full dense_fused_i8 calls (both quantize passes
     # and the contraction, on fresh fp32 operands each time), captured once
-    # into a HIP graph and replayed once between two synchronisations, so
-    # the host's per-call launch work stays outside the timed region; the
-    # wall clock brackets the replay.  --eager launches the K calls from
-    # Python instead.
+    # into a HIP graph and replayed between two synchronisations, so the
+    # host's per-call launch work stays outside the timed region; the wall
+    # clock brackets the replay.  The warmup replays a graph of W steps and
+    # then the timed graph once, untimed: a graph's first replay carries
+    # one-time setup (measured ~5 us per step of a 100-step graph).  --eager
+    # launches the K calls from Python instead.
     log(f"dense_fused_i8 M={M} N={N} K={K}: warmup {args.warmup}, steps {args.steps}"
         f"{' (eager launches)' if args.eager else ' (one HIP graph of the steps)'}")
     if args.eager:
@@ -273,6 +275,7 @@ def main() -> int:
                 for _ in range(args.steps):
                     fused(gs)
             warm.replay()
+            timed.replay()
             gs.synchronize()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -384,7 +387,8 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic: A, B ~ N(0,1) fp32 (seeded), quantized per tensor on the GPU each step",
         "timing": ("eager launches from Python" if args.eager else
-                   "the K steps captured as one HIP graph and replayed once between synchronisations"),
+                   "the K steps captured as one HIP graph, replayed once untimed after the warmup and "
+                   "then once between synchronisations"),
         "config": {"workload": f"dense_fused_i8 M={M} N={N} K={K} scale=1.0 relu (config 2)",
                    "M": M, "N": N, "K": K},
         "roofline": roofline,
