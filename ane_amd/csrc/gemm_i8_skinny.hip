@@ -7,12 +7,19 @@
 //  * One workgroup per 16 output columns: ceil(N/16) workgroups of 4 waves
 //    (256 for N = 4096).  The workgroup holds every output row (up to 8
 //    16-row blocks, MB) of its columns.
-//  * K advances in 64-byte steps; wave w takes steps w, w+4, w+8, ... (the
-//    four waves together read each Bt row front to back).  A step is one
-//    v_mfma_i32_16x16x64_i8 per row block: lane l loads 16 bytes of column
-//    n0 + l%16 (Bt row) and of row 16rb + l%16 (A row) at k = 64s + 16(l/16).
-//    A and B place the same k in the same lane and byte, so the int32 sums
-//    are the exact dot products whatever order the instruction adds in.
+//  * K advances in 128-byte steps; wave w takes steps w, w+4, w+8, ... (the
+//    four waves together read each Bt row front to back).  A step is two
+//    v_mfma_i32_16x16x64_i8 per row block: lane l loads the 32 contiguous
+//    bytes of column n0 + l%16 (Bt row) and of row 16rb + l%16 (A row) at
+//    k = 128s + 32(l/16), and gives the first 16 to one instruction and the
+//    next 16 to the other (so a pair of loads covers whole 128-byte lines;
+//    measured 7 % faster than 64-byte steps at M = 16).  A and B place the
+//    same k in the same lane and byte, so the int32 sums are the exact dot
+//    products whatever order the instructions add in.
+//  * With 4+ row blocks, the workgroups start their walks over K at four
+//    different phases (a rotation of the steps, which changes no sum), so
+//    the workgroups of an XCD do not all read the same lines of A at once
+//    (M = 128: 20.6 -> 19.7 us).
 //  * Operands are read straight into VGPRs with range-checked 16-byte buffer
 //    loads (rows past M or N and k past Kp read as zeros), two steps per
 //    batch, the next batch in flight while the current one is multiplied.
@@ -27,8 +34,6 @@
 namespace ane {
 namespace {
 
-constexpr int kSkU = 2;  // steps per load batch
-
 template <int MB>
 __global__ void __launch_bounds__(256) k_gemm_skinny(GemmParams p) {
     __shared__ v4i red[4][MB][64];
@@ -37,43 +42,47 @@ __global__ void __launch_bounds__(256) k_gemm_skinny(GemmParams p) {
     const uint32_t n0 = blockIdx.x * 16;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.rowsA * p.lda));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(p.colsB * p.ldb));
-    const uint32_t nsteps = (p.Kp + 63) / 64;  // the last step may be partial: k < Kp decides per lane
+    const uint32_t nsteps = (p.Kp + 127) / 128;  // the last step may be partial: k < Kp decides per chunk
     const uint32_t nj = (nsteps + 3) / 4;  // this wave's steps, rounded up (extra steps read zeros)
-    const uint32_t offB = (n0 + c16) * (uint32_t)p.ldb + 16 * g;
+    // the rotation of this workgroup's walk (4+ row blocks)
+    const uint32_t phase = MB >= 4 ? (blockIdx.x & 3) * (nsteps / 4) : 0;
+    const uint32_t offB = (n0 + c16) * (uint32_t)p.ldb + 32 * g;
     uint32_t offA[MB];
 #pragma unroll
-    for (int r = 0; r < MB; r++) offA[r] = (16 * r + c16) * (uint32_t)p.lda + 16 * g;
+    for (int r = 0; r < MB; r++) offA[r] = (16 * r + c16) * (uint32_t)p.lda + 32 * g;
 
-    auto load = [&](uint32_t j0, v4i (&b)[kSkU], v4i (&a)[kSkU][MB]) {
+    // step j of this wave: 16-byte chunks h = 0, 1 at k = 128 S + 32 g + 16 h
+    auto load = [&](uint32_t j, v4i (&b)[2], v4i (&a)[2][MB]) {
+        uint32_t S = wave + 4 * j;
+        const bool in = S < nsteps;
+        if (in) S = (S + phase) % nsteps;
 #pragma unroll
-        for (int u = 0; u < kSkU; u++) {
-            const uint32_t s = wave + 4 * (j0 + u);
-            const uint32_t k = 64 * s + 16 * g;
-            const bool live = s < nsteps && k < p.Kp;
-            b[u] = __builtin_bit_cast(
-                v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, live ? offB + 64 * s : 0x80000000u, 0, kCpolNt));
+        for (int h = 0; h < 2; h++) {
+            const bool live = in && 128 * S + 32 * g + 16 * h < p.Kp;
+            b[h] = __builtin_bit_cast(
+                v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, live ? offB + 128 * S + 16 * h : 0x80000000u, 0, kCpolNt));
 #pragma unroll
             for (int r = 0; r < MB; r++)
-                a[u][r] = __builtin_bit_cast(
-                    v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, live ? offA[r] + 64 * s : 0x80000000u, 0, 0));
+                a[h][r] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, live ? offA[r] + 128 * S + 16 * h : 0x80000000u, 0, 0));
         }
     };
-    auto mma = [&](v4i (&acc)[MB], const v4i (&b)[kSkU], const v4i (&a)[kSkU][MB]) {
+    auto mma = [&](v4i (&acc)[MB], const v4i (&b)[2], const v4i (&a)[2][MB]) {
 #pragma unroll
-        for (int u = 0; u < kSkU; u++)
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int r = 0; r < MB; r++) acc[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u][r], b[u], acc[r], 0, 0, 0);
+            for (int r = 0; r < MB; r++) acc[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[h][r], b[h], acc[r], 0, 0, 0);
     };
 
     v4i acc[MB];
 #pragma unroll
     for (int r = 0; r < MB; r++) acc[r] = v4i{0, 0, 0, 0};
-    v4i b0[kSkU], b1[kSkU], a0[kSkU][MB], a1[kSkU][MB];
+    v4i b0[2], b1[2], a0[2][MB], a1[2][MB];
     load(0, b0, a0);
-    for (uint32_t j0 = 0; j0 < nj; j0 += 2 * kSkU) {
-        load(j0 + kSkU, b1, a1);
+    for (uint32_t j = 0; j < nj; j += 2) {
+        load(j + 1, b1, a1);
         mma(acc, b0, a0);
-        load(j0 + 2 * kSkU, b0, a0);
+        load(j + 2, b0, a0);
         mma(acc, b1, a1);
     }
 
@@ -112,7 +121,7 @@ bool skinny_eligible(const GemmParams& p) {
     // 32-bit buffer offsets; 0x80000000 marks an empty load: every row a
     // workgroup may touch (up to 16 past the last column, 128 A rows) and
     // every step stay below it
-    const uint64_t kspan = ceil_to(p.Kp, 256) + 64;
+    const uint64_t kspan = ceil_to(p.Kp, 256) + 128;
     if ((uint64_t)ceil_to(p.Nout, 16) * p.ldb + kspan >= (1ull << 31)) return false;
     if (128ull * p.lda + kspan >= (1ull << 31)) return false;
     if ((uint64_t)p.rowsA * p.lda >= (1ull << 31) || (uint64_t)p.colsB * p.ldb >= (1ull << 31)) return false;
