@@ -7,27 +7,35 @@
 //    wave owns FM x FN blocks of v_mfma_i32_32x32x32_i8 accumulators.  With
 //    8 or 16 waves, 2 or 4 share each SIMD, so one wave's barrier or LDS
 //    wait is covered by the others' MFMAs.
-//  * K advances in 64-byte slices through a 4-stage LDS ring (4 x 32 KB).
-//    Slice kt is computed from stage kt%4 while slices kt+1 and kt+2 are in
-//    flight; slice kt+2 goes into the stage of slice kt-2, which every wave
-//    finished reading before the barrier that preceded the last k-step of
-//    slice kt-1.  Slices are copied with buffer_load_dwordx4 ... lds (direct
-//    global -> LDS, no VGPR staging; rows past the operand's end and the
-//    out-of-range tail slices read as zeros through the buffer resource's
-//    range check, so every slice issues the same number of copies).  The
-//    copies are spread over the MFMAs so the vector-memory queue never
-//    stalls MFMA issue.
+//  * 256-tiles: K advances in 128-byte slices through a 2-stage LDS ring
+//    (2 x 64 KB).  Each slice starts with a barrier (every wave's copies of
+//    slice kt have landed, and every wave has finished slice kt-1), after
+//    which the copies of slice kt+1 go into slice kt-1's stage.  Those copies
+//    are pinned one between every two MFMAs of the slice's first two k-steps
+//    (sched_barrier): issuing a buffer_load ... lds occupies the issuing
+//    wave for tens of cycles, and issued back to back, 8 of them drained
+//    the MFMA pipe after every barrier (4096^3: the K loop about 2-3 us
+//    faster; copies issued over all four k-steps land too late and the loop
+//    stalls).  The next k-step's fragment reads sit between the MFMAs the
+//    same way.
+//  * 128-tiles: 64-byte slices through a 4-stage ring (4 x 16 KB).  Slice kt
+//    is computed from stage kt%4 while slices kt+1 and kt+2 are in flight;
+//    slice kt+2 goes into the stage of slice kt-2, which every wave finished
+//    reading before the barrier that preceded the last k-step of slice kt-1.
+//  * Slices are copied with buffer_load_dwordx4 ... lds (direct global ->
+//    LDS, no VGPR staging; rows past the operand's end and the out-of-range
+//    tail slices read as zeros through the buffer resource's range check, so
+//    every slice issues the same number of copies).
 //  * Synchronisation is s_waitcnt vmcnt + a bare s_barrier.  __syncthreads()
 //    would add a release fence, i.e. vmcnt(0), draining the slices that are
-//    meant to stay in flight.  The barrier for slice kt+1 is taken before the
-//    last k-step of slice kt, whose MFMAs then cover the LDS reads of slice
-//    kt+1's first fragments.
-//  * LDS layout per stage: [256 rows][64 bytes] for A then for Bt; the
-//    16-byte chunk c of row r sits in slot c ^ ((r ^ r>>2) & 3).  A
-//    ds_read_b128 serves 16 lanes (16 consecutive rows, same chunk) per LDS
-//    cycle (64 banks x 4 bytes); the swizzle gives them 16 distinct bank
-//    groups.  Each copy wave-instruction writes 1 KB of consecutive LDS, so
-//    the swizzle is applied on the global side.
+//    meant to stay in flight.
+//  * LDS layout per stage: [rows][TK bytes] for A then for Bt; the 16-byte
+//    chunk c of row r sits in slot c ^ g(r), g(r) = (r >> 1) & 7 for 128-byte
+//    rows and (r ^ r>>2) & 3 for 64-byte rows.  A ds_read_b128 serves 16
+//    lanes (16 consecutive rows, same chunk) per LDS cycle (64 banks x 4
+//    bytes); g gives them 16 distinct bank groups.  Each copy
+//    wave-instruction writes 1 KB of consecutive LDS, so the swizzle is
+//    applied on the global side.
 //  * Tiles are assigned XCD-major: dispatch round-robins workgroups over the
 //    8 XCDs, so workgroup w is remapped to logical tile (w%8)*(T/8) + w/8 and
 //    each XCD's L2 sees a compact 4 x 8 block of tiles.
@@ -65,8 +73,8 @@ namespace {
 #endif
 
 constexpr int TM = ANE_TILE, TN = ANE_TILE;
-constexpr int TK = 64;                        // bytes of K per slice
-constexpr int STAGES = 4;                     // LDS ring depth
+constexpr int TK = TM == 256 ? 128 : 64;      // bytes of K per slice
+constexpr int STAGES = TM == 256 ? 2 : 4;     // LDS ring depth
 constexpr int NW = ANE_TILE_WAVES;            // waves per workgroup
 constexpr int kWavesPerEu = TM == 128 ? 2 : NW / 4;  // 128-tiles: two workgroups per CU
 constexpr int kThreads = NW * 64;
@@ -88,6 +96,7 @@ static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
 static_assert(kLdsBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
 static_assert(kSteps % 2 == 0, "fragment double-buffering needs an even k-step count");
 static_assert(kDmaPerStep * kSteps == 2 * kDmaPerWave, "copies must split evenly over k-steps");
+static_assert(STAGES == 4 || STAGES == 2, "4-stage ring with early barriers, or 2-stage with copies pinned");
 // Epilogue staging: per wave EPR rows x (FN*32) fp32 per pass, rows padded
 // by 32 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
 // staging write land in different bank halves).
@@ -99,7 +108,10 @@ constexpr int kRowsPerStore = 64 / kLanesPerRow;
 constexpr int kEpiWaveBytes = EPR * kEpiRowBytes;
 static_assert(NW * kEpiWaveBytes <= kLdsBytes, "epilogue staging does not fit");
 
-__device__ __forceinline__ uint32_t swz_g(uint32_t row) { return (row ^ (row >> 2)) & 3; }
+__device__ __forceinline__ uint32_t swz_g(uint32_t row) {
+    if constexpr (TK == 128) return (row >> 1) & 7;
+    return (row ^ (row >> 2)) & 3;
+}
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
     return row * TK + ((chunk ^ swz_g(row)) << 4);
 }
@@ -128,6 +140,17 @@ __device__ __forceinline__ void issue_part(const SliceCopy& c, const uint32_t (&
     }
 }
 
+// Copy d of a slice (d < kDmaPerWave: A, else Bt); unrolled callers pass a
+// constant d.
+__device__ __forceinline__ void issue_one(const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
+                                          const uint32_t (&offB)[kDmaPerWave], int d) {
+    const int i = d % kDmaPerWave;
+    const bool isB = d >= kDmaPerWave;
+    int8_t* dst = c.stage + (c.wave * kRowsPerWave + i * kRowsPerDma) * TK + (isB ? kStageA : 0);
+    const uint32_t o = c.live ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
+    copy16_to_lds(isB ? c.rb : c.ra, dst, o);
+}
+
 struct Frags {
     v4i a[FM], b[FN];
 };
@@ -148,6 +171,43 @@ __device__ __forceinline__ void mfmas(v16i (&acc)[FM][FN], const Frags& f) {
 #pragma unroll
         for (int ni = 0; ni < FN; ni++)
             acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+}
+
+// One of the FM + FN fragment reads of a k-step, by index.
+__device__ __forceinline__ void load_frag(const int8_t* stage, uint32_t rA, uint32_t rB, uint32_t chunk,
+                                          Frags& f, int idx) {
+    if (idx < FM)
+        f.a[idx] = *reinterpret_cast<const v4i*>(stage + swz(rA + idx * 32, chunk));
+    else
+        f.b[idx - FM] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(rB + (idx - FM) * 32, chunk));
+}
+
+// 2-stage ring (256-tiles): one slice, copies of the next slice and the
+// next k-step's fragment reads pinned between the MFMAs.  f0 holds the
+// slice's first fragments on entry.
+__device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Frags& f1, const int8_t* cur,
+                                             uint32_t rA, uint32_t rB, uint32_t chalf, const SliceCopy& c,
+                                             const uint32_t (&offA)[kDmaPerWave],
+                                             const uint32_t (&offB)[kDmaPerWave]) {
+    constexpr int nM = FM * FN, nD = FM + FN;
+    constexpr int kCopySteps = 2;                       // k-steps that carry the copies
+    constexpr int kPerStep = 2 * kDmaPerWave / kCopySteps;
+    constexpr int kStride = nM / kPerStep;              // MFMAs per copy
+    static_assert(kPerStep * kCopySteps == 2 * kDmaPerWave && kStride * kPerStep == nM && kCopySteps <= kSteps,
+                  "copies must spread evenly over the MFMAs");
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ks++) {
+        Frags& fc = (ks & 1) ? f1 : f0;
+        Frags& fn = (ks & 1) ? f0 : f1;
+#pragma unroll
+        for (int g = 0; g < nM; g++) {
+            const int mi = g / FN, ni = g % FN;
+            acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fc.a[mi], fc.b[ni], acc[mi][ni], 0, 0, 0);
+            if (ks + 1 < kSteps && g < nD) load_frag(cur, rA, rB, 2 * (ks + 1) + chalf, fn, g);
+            if (ks < kCopySteps && g % kStride == kStride - 1) issue_one(c, offA, offB, ks * kPerStep + g / kStride);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 }
 
 // The MFMAs of one k-step with the LDS reads of the next k-step's fragments
@@ -264,34 +324,51 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     const uint32_t nk = p.Kp / TK;
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-        const SliceCopy c{ra, rb, smem + s * kStage, wave, (uint32_t)s * TK, (uint32_t)s < nk};
-        issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
-    }
     Frags f0, f1;
-    wait_vmcnt<2 * kDmaPerWave>();  // slice 0 landed (slice 1 may be in flight)
-    lds_barrier();
-    load_frags(smem, rA, rB, chalf, f0);
+    if constexpr (STAGES == 2) {
+        {
+            const SliceCopy c{ra, rb, smem, wave, 0, 0 < nk};
+            issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
+        }
+        for (uint32_t kt = 0; kt < nk; kt++) {
+            const uint32_t st = kt & 1;
+            wait_vmcnt<0>();  // this wave's copies of slice kt landed
+            lds_barrier();    // everyone's did; everyone finished slice kt-1
+            const int8_t* cur = smem + st * kStage;
+            const SliceCopy c{ra, rb, smem + (st ^ 1) * kStage, wave, (kt + 1) * TK, kt + 1 < nk};
+            load_frags(cur, rA, rB, chalf, f0);
+            __builtin_amdgcn_sched_barrier(0);
+            slice_pinned(acc, f0, f1, cur, rA, rB, chalf, c, offA, offB);
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const SliceCopy c{ra, rb, smem + s * kStage, wave, (uint32_t)s * TK, (uint32_t)s < nk};
+            issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
+        }
+        wait_vmcnt<2 * kDmaPerWave>();  // slice 0 landed (slice 1 may be in flight)
+        lds_barrier();
+        load_frags(smem, rA, rB, chalf, f0);
 
-    uint32_t st = 0;
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const uint32_t st1 = st + 1 == STAGES ? 0 : st + 1;
-        const uint32_t st2 = st1 + 1 == STAGES ? 0 : st1 + 1;
-        const uint32_t k2 = kt + 2;
-        const SliceCopy c{ra, rb, smem + st2 * kStage, wave, k2 * TK, k2 < nk};
-        const bool more = kt + 1 < nk;
-        auto boundary = [&]() {
-            if (more) {
-                // slice kt+1 landed for this wave: the only younger copies are
-                // the ones of slice kt+2 issued in this slice's earlier k-steps
-                wait_vmcnt<(kSteps - 1) * kDmaPerStep>();
-                lds_barrier();
-            }
-        };
-        ksteps<0>(acc, f0, f1, smem + st * kStage, smem + (more ? st1 : st) * kStage, rA, rB, chalf,
-                  c, offA, offB, boundary);
-        st = st1;
+        uint32_t st = 0;
+        for (uint32_t kt = 0; kt < nk; kt++) {
+            const uint32_t st1 = st + 1 == STAGES ? 0 : st + 1;
+            const uint32_t st2 = st1 + 1 == STAGES ? 0 : st1 + 1;
+            const uint32_t k2 = kt + 2;
+            const SliceCopy c{ra, rb, smem + st2 * kStage, wave, k2 * TK, k2 < nk};
+            const bool more = kt + 1 < nk;
+            auto boundary = [&]() {
+                if (more) {
+                    // slice kt+1 landed for this wave: the only younger copies are
+                    // the ones of slice kt+2 issued in this slice's earlier k-steps
+                    wait_vmcnt<(kSteps - 1) * kDmaPerStep>();
+                    lds_barrier();
+                }
+            };
+            ksteps<0>(acc, f0, f1, smem + st * kStage, smem + (more ? st1 : st) * kStage, rA, rB, chalf,
+                      c, offA, offB, boundary);
+            st = st1;
+        }
     }
     wait_vmcnt<0>();
     __syncthreads();  // all fragment reads done: the ring becomes epilogue staging
