@@ -31,9 +31,10 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
                           uint32_t Kp, uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales,
                           hipStream_t s);
 
-// 256 x 256 tile kernel (gemm_i8_tile256.hip): Bt layout, signed A, whole
-// 128-byte K slices, 16-byte aligned rows, and enough rows/columns to fill
-// 256-wide tiles reasonably.
+// 256 x 256 tile kernel (gemm_i8_tile256.hip): Bt layout, signed A, K a
+// multiple of 64 (run as 128-byte slices, an odd last half read as zeros),
+// 16-byte aligned rows, and enough rows/columns to fill 256-wide tiles
+// reasonably.
 bool tile256_eligible(const GemmParams& p);
 int launch_gemm_tile256(const GemmParams& p, hipStream_t s);
 

@@ -7,21 +7,19 @@
 //    wave owns FM x FN blocks of v_mfma_i32_32x32x32_i8 accumulators.  With
 //    8 or 16 waves, 2 or 4 share each SIMD, so one wave's barrier or LDS
 //    wait is covered by the others' MFMAs.
-//  * 256-tiles: K advances in 128-byte slices through a 2-stage LDS ring
-//    (2 x 64 KB).  Each slice starts with a barrier (every wave's copies of
-//    slice kt have landed, and every wave has finished slice kt-1), after
-//    which the copies of slice kt+1 go into slice kt-1's stage.  Those copies
-//    are pinned one between every two MFMAs of the slice's first two k-steps
-//    (sched_barrier): issuing a buffer_load ... lds occupies the issuing
-//    wave for tens of cycles, and issued back to back, 8 of them drained
-//    the MFMA pipe after every barrier (4096^3: the K loop about 2-3 us
-//    faster; copies issued over all four k-steps land too late and the loop
-//    stalls).  The next k-step's fragment reads sit between the MFMAs the
-//    same way.
-//  * 128-tiles: 64-byte slices through a 4-stage ring (4 x 16 KB).  Slice kt
-//    is computed from stage kt%4 while slices kt+1 and kt+2 are in flight;
-//    slice kt+2 goes into the stage of slice kt-2, which every wave finished
-//    reading before the barrier that preceded the last k-step of slice kt-1.
+//  * K advances in 128-byte slices through a 2-stage LDS ring (2 x 64 KB
+//    for 256-tiles, 2 x 32 KB for 128-tiles).  Each slice starts with a
+//    barrier (every wave's copies of slice kt have landed, and every wave
+//    has finished slice kt-1), after which the copies of slice kt+1 go into
+//    slice kt-1's stage.  Those copies are pinned one between MFMAs of the
+//    slice's first two k-steps (sched_barrier): issuing a buffer_load ...
+//    lds occupies the issuing wave for tens of cycles, and issued back to
+//    back they drained the MFMA pipe after every barrier (4096^3: the K loop
+//    about 2-3 us faster than a 4-stage ring of 64-byte slices whose copies
+//    the compiler bunched; copies spread over all four k-steps land too
+//    late).  The next k-step's fragment reads sit between the MFMAs the same
+//    way.  When Kp is an odd multiple of 64, the last slice's upper half is
+//    sent out of range per lane and lands as zeros.
 //  * Slices are copied with buffer_load_dwordx4 ... lds (direct global ->
 //    LDS, no VGPR staging; rows past the operand's end and the out-of-range
 //    tail slices read as zeros through the buffer resource's range check, so
@@ -29,9 +27,8 @@
 //  * Synchronisation is s_waitcnt vmcnt + a bare s_barrier.  __syncthreads()
 //    would add a release fence, i.e. vmcnt(0), draining the slices that are
 //    meant to stay in flight.
-//  * LDS layout per stage: [rows][TK bytes] for A then for Bt; the 16-byte
-//    chunk c of row r sits in slot c ^ g(r), g(r) = (r >> 1) & 7 for 128-byte
-//    rows and (r ^ r>>2) & 3 for 64-byte rows.  A ds_read_b128 serves 16
+//  * LDS layout per stage: [rows][128 bytes] for A then for Bt; the 16-byte
+//    chunk c of row r sits in slot c ^ ((r >> 1) & 7).  A ds_read_b128 serves 16
 //    lanes (16 consecutive rows, same chunk) per LDS cycle (64 banks x 4
 //    bytes); g gives them 16 distinct bank groups.  Each copy
 //    wave-instruction writes 1 KB of consecutive LDS, so the swizzle is
@@ -73,8 +70,8 @@ namespace {
 #endif
 
 constexpr int TM = ANE_TILE, TN = ANE_TILE;
-constexpr int TK = TM == 256 ? 128 : 64;      // bytes of K per slice
-constexpr int STAGES = TM == 256 ? 2 : 4;     // LDS ring depth
+constexpr int TK = 128;                       // bytes of K per slice
+constexpr int STAGES = 2;                     // LDS ring depth
 constexpr int NW = ANE_TILE_WAVES;            // waves per workgroup
 constexpr int kWavesPerEu = TM == 128 ? 2 : NW / 4;  // 128-tiles: two workgroups per CU
 constexpr int kThreads = NW * 64;
@@ -91,12 +88,8 @@ constexpr int kRowsPerDma = 1024 / TK;        // rows covered by one copy wave-i
 constexpr int kRowsPerWave = TM / NW;         // rows of A (and of Bt) each wave copies
 constexpr int kDmaPerWave = kRowsPerWave / kRowsPerDma;
 constexpr int kSteps = TK / 32;
-constexpr int kDmaPerStep = 2 * kDmaPerWave / kSteps;
 static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
 static_assert(kLdsBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
-static_assert(kSteps % 2 == 0, "fragment double-buffering needs an even k-step count");
-static_assert(kDmaPerStep * kSteps == 2 * kDmaPerWave, "copies must split evenly over k-steps");
-static_assert(STAGES == 4 || STAGES == 2, "4-stage ring with early barriers, or 2-stage with copies pinned");
 // Epilogue staging: per wave EPR rows x (FN*32) fp32 per pass, rows padded
 // by 32 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
 // staging write land in different bank halves).
@@ -108,46 +101,32 @@ constexpr int kRowsPerStore = 64 / kLanesPerRow;
 constexpr int kEpiWaveBytes = EPR * kEpiRowBytes;
 static_assert(NW * kEpiWaveBytes <= kLdsBytes, "epilogue staging does not fit");
 
-__device__ __forceinline__ uint32_t swz_g(uint32_t row) {
-    if constexpr (TK == 128) return (row >> 1) & 7;
-    return (row ^ (row >> 2)) & 3;
-}
+__device__ __forceinline__ uint32_t swz_g(uint32_t row) { return (row >> 1) & 7; }
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
     return row * TK + ((chunk ^ swz_g(row)) << 4);
 }
 
 // One slice copy: wave w copies rows [w*kRowsPerWave, (w+1)*kRowsPerWave)
 // of the tile's A rows and of its Bt rows; wave-instruction i covers
-// kRowsPerDma rows (1 KB of consecutive LDS).  `live` false sends every lane
-// out of range: the copy then writes zeros without touching memory.
+// kRowsPerDma rows (1 KB of consecutive LDS).  A lane whose 16 bytes lie at
+// or past `kmax` bytes into the slice (kmax 0: the slice is past K) is sent
+// out of range: its copy writes zeros without touching memory.
 struct SliceCopy {
     __amdgpu_buffer_rsrc_t ra, rb;
     int8_t* stage;
-    uint32_t wave, k0;
-    bool live;
+    uint32_t wave, k0, kmax;
 };
 
-template <int first, int count>
-__device__ __forceinline__ void issue_part(const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
-                                           const uint32_t (&offB)[kDmaPerWave]) {
-#pragma unroll
-    for (int d = first; d < first + count; d++) {
-        const int i = d % kDmaPerWave;
-        const bool isB = d >= kDmaPerWave;
-        int8_t* dst = c.stage + (c.wave * kRowsPerWave + i * kRowsPerDma) * TK + (isB ? kStageA : 0);
-        const uint32_t o = c.live ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
-        copy16_to_lds(isB ? c.rb : c.ra, dst, o);
-    }
-}
-
 // Copy d of a slice (d < kDmaPerWave: A, else Bt); unrolled callers pass a
-// constant d.
+// constant d.  kofs[i]: this lane's byte offset inside the slice for copy i
+// (its swizzled 16-byte chunk), the same for A and Bt.
 __device__ __forceinline__ void issue_one(const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
-                                          const uint32_t (&offB)[kDmaPerWave], int d) {
+                                          const uint32_t (&offB)[kDmaPerWave],
+                                          const uint32_t (&kofs)[kDmaPerWave], int d) {
     const int i = d % kDmaPerWave;
     const bool isB = d >= kDmaPerWave;
     int8_t* dst = c.stage + (c.wave * kRowsPerWave + i * kRowsPerDma) * TK + (isB ? kStageA : 0);
-    const uint32_t o = c.live ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
+    const uint32_t o = kofs[i] < c.kmax ? (isB ? offB[i] : offA[i]) + c.k0 : 0x80000000u;
     copy16_to_lds(isB ? c.rb : c.ra, dst, o);
 }
 
@@ -182,13 +161,14 @@ __device__ __forceinline__ void load_frag(const int8_t* stage, uint32_t rA, uint
         f.b[idx - FM] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(rB + (idx - FM) * 32, chunk));
 }
 
-// 2-stage ring (256-tiles): one slice, copies of the next slice and the
-// next k-step's fragment reads pinned between the MFMAs.  f0 holds the
-// slice's first fragments on entry.
+// One slice: the copies of the next slice and the next k-step's fragment
+// reads pinned between the MFMAs.  f0 holds the slice's first fragments on
+// entry.
 __device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Frags& f1, const int8_t* cur,
                                              uint32_t rA, uint32_t rB, uint32_t chalf, const SliceCopy& c,
                                              const uint32_t (&offA)[kDmaPerWave],
-                                             const uint32_t (&offB)[kDmaPerWave]) {
+                                             const uint32_t (&offB)[kDmaPerWave],
+                                             const uint32_t (&kofs)[kDmaPerWave]) {
     constexpr int nM = FM * FN, nD = FM + FN;
     constexpr int kCopySteps = 2;                       // k-steps that carry the copies
     constexpr int kPerStep = 2 * kDmaPerWave / kCopySteps;
@@ -204,55 +184,9 @@ __device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Fra
             const int mi = g / FN, ni = g % FN;
             acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fc.a[mi], fc.b[ni], acc[mi][ni], 0, 0, 0);
             if (ks + 1 < kSteps && g < nD) load_frag(cur, rA, rB, 2 * (ks + 1) + chalf, fn, g);
-            if (ks < kCopySteps && g % kStride == kStride - 1) issue_one(c, offA, offB, ks * kPerStep + g / kStride);
+            if (ks < kCopySteps && g % kStride == kStride - 1) issue_one(c, offA, offB, kofs, ks * kPerStep + g / kStride);
             __builtin_amdgcn_sched_barrier(0);
         }
-    }
-}
-
-// The MFMAs of one k-step with the LDS reads of the next k-step's fragments
-// and this k-step's share of slice copies spread between them;
-// sched_barrier keeps k-steps in order so consecutive MFMAs never
-// accumulate into the same registers.
-template <int ks>
-__device__ __forceinline__ void kstep(v16i (&acc)[FM][FN], const Frags& cur, Frags& nxt,
-                                      const int8_t* src, uint32_t rA, uint32_t rB, uint32_t chunk,
-                                      const SliceCopy& c, const uint32_t (&offA)[kDmaPerWave],
-                                      const uint32_t (&offB)[kDmaPerWave]) {
-    constexpr int nM = FM * FN, nD = FM + FN, nV = kDmaPerStep;
-    load_frags(src, rA, rB, chunk, nxt);
-    issue_part<ks * kDmaPerStep, kDmaPerStep>(c, offA, offB);
-    mfmas(acc, cur);
-#pragma unroll
-    for (int i = 0; i < nM; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // 1 MFMA
-        if (i < nD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // 1 LDS read
-        if ((i * nV) / nM != ((i + 1) * nV) / nM)
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);               // 1 slice copy
-    }
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// One slice: its first k-step's fragments are in f0 (prefetched during the
-// previous slice).  Before the last k-step, `boundary()` makes the next
-// slice visible (copy wait + barrier); the last k-step then prefetches the
-// next slice's first fragments from `next_stage` into f0.
-template <int ks, typename Boundary>
-__device__ __forceinline__ void ksteps(v16i (&acc)[FM][FN], Frags& f0, Frags& f1, const int8_t* stage,
-                                       const int8_t* next_stage, uint32_t rA, uint32_t rB,
-                                       uint32_t chalf, const SliceCopy& c,
-                                       const uint32_t (&offA)[kDmaPerWave],
-                                       const uint32_t (&offB)[kDmaPerWave], Boundary boundary) {
-    if constexpr (ks < kSteps) {
-        constexpr bool last = ks + 1 == kSteps;
-        if constexpr (last) boundary();
-        const int8_t* src = last ? next_stage : stage;
-        const uint32_t chunk = last ? chalf : 2 * (ks + 1) + chalf;
-        if constexpr (ks % 2 == 0)
-            kstep<ks>(acc, f0, f1, src, rA, rB, chunk, c, offA, offB);
-        else
-            kstep<ks>(acc, f1, f0, src, rA, rB, chunk, c, offA, offB);
-        ksteps<ks + 1>(acc, f0, f1, stage, next_stage, rA, rB, chalf, c, offA, offB, boundary);
     }
 }
 
@@ -292,7 +226,7 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.rowsA * p.lda));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(p.colsB * p.ldb));
-    uint32_t offA[kDmaPerWave], offB[kDmaPerWave];
+    uint32_t offA[kDmaPerWave], offB[kDmaPerWave], kofs[kDmaPerWave];
     {
         // lane l fills slot l % kChunks of row wave*kRowsPerWave + i*kRowsPerDma + l/kChunks
         const uint32_t r = wave * kRowsPerWave + lane / kChunks;
@@ -300,8 +234,9 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
         for (int i = 0; i < kDmaPerWave; i++) {
             const uint32_t row = r + i * kRowsPerDma;
             const uint32_t chunk = (lane % kChunks) ^ swz_g(row);
-            offA[i] = (row0 + row) * (uint32_t)p.lda + chunk * 16;
-            offB[i] = (col0 + row) * (uint32_t)p.ldb + chunk * 16;
+            kofs[i] = chunk * 16;
+            offA[i] = (row0 + row) * (uint32_t)p.lda + kofs[i];
+            offB[i] = (col0 + row) * (uint32_t)p.ldb + kofs[i];
         }
     }
 
@@ -323,52 +258,26 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    const uint32_t nk = p.Kp / TK;
+    const uint32_t nk = (p.Kp + TK - 1) / TK;
+    auto kmax = [&](uint32_t k) -> uint32_t {  // bytes of slice k inside Kp (0 past it)
+        const uint32_t k0 = k * TK;
+        return k0 >= p.Kp ? 0u : (p.Kp - k0 < (uint32_t)TK ? p.Kp - k0 : (uint32_t)TK);
+    };
     Frags f0, f1;
-    if constexpr (STAGES == 2) {
-        {
-            const SliceCopy c{ra, rb, smem, wave, 0, 0 < nk};
-            issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
-        }
-        for (uint32_t kt = 0; kt < nk; kt++) {
-            const uint32_t st = kt & 1;
-            wait_vmcnt<0>();  // this wave's copies of slice kt landed
-            lds_barrier();    // everyone's did; everyone finished slice kt-1
-            const int8_t* cur = smem + st * kStage;
-            const SliceCopy c{ra, rb, smem + (st ^ 1) * kStage, wave, (kt + 1) * TK, kt + 1 < nk};
-            load_frags(cur, rA, rB, chalf, f0);
-            __builtin_amdgcn_sched_barrier(0);
-            slice_pinned(acc, f0, f1, cur, rA, rB, chalf, c, offA, offB);
-        }
-    } else {
+    {
+        const SliceCopy c{ra, rb, smem, wave, 0, kmax(0)};
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const SliceCopy c{ra, rb, smem + s * kStage, wave, (uint32_t)s * TK, (uint32_t)s < nk};
-            issue_part<0, 2 * kDmaPerWave>(c, offA, offB);
-        }
-        wait_vmcnt<2 * kDmaPerWave>();  // slice 0 landed (slice 1 may be in flight)
-        lds_barrier();
-        load_frags(smem, rA, rB, chalf, f0);
-
-        uint32_t st = 0;
-        for (uint32_t kt = 0; kt < nk; kt++) {
-            const uint32_t st1 = st + 1 == STAGES ? 0 : st + 1;
-            const uint32_t st2 = st1 + 1 == STAGES ? 0 : st1 + 1;
-            const uint32_t k2 = kt + 2;
-            const SliceCopy c{ra, rb, smem + st2 * kStage, wave, k2 * TK, k2 < nk};
-            const bool more = kt + 1 < nk;
-            auto boundary = [&]() {
-                if (more) {
-                    // slice kt+1 landed for this wave: the only younger copies are
-                    // the ones of slice kt+2 issued in this slice's earlier k-steps
-                    wait_vmcnt<(kSteps - 1) * kDmaPerStep>();
-                    lds_barrier();
-                }
-            };
-            ksteps<0>(acc, f0, f1, smem + st * kStage, smem + (more ? st1 : st) * kStage, rA, rB, chalf,
-                      c, offA, offB, boundary);
-            st = st1;
-        }
+        for (int d = 0; d < 2 * kDmaPerWave; d++) issue_one(c, offA, offB, kofs, d);
+    }
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const uint32_t st = kt & 1;
+        wait_vmcnt<0>();  // this wave's copies of slice kt landed
+        lds_barrier();    // everyone's did; everyone finished slice kt-1
+        const int8_t* cur = smem + st * kStage;
+        const SliceCopy c{ra, rb, smem + (st ^ 1) * kStage, wave, (kt + 1) * TK, kmax(kt + 1)};
+        load_frags(cur, rA, rB, chalf, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        slice_pinned(acc, f0, f1, cur, rA, rB, chalf, c, offA, offB, kofs);
     }
     wait_vmcnt<0>();
     __syncthreads();  // all fragment reads done: the ring becomes epilogue staging
@@ -438,12 +347,13 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 
 bool ANE_TILE_ELIGIBLE(const GemmParams& p) {
     if (p.Mout < TM || p.Nout < TN) return false;
-    if (p.Kp == 0 || (p.Kp % TK) != 0) return false;
+    if (p.Kp == 0 || (p.Kp % 64) != 0) return false;
     if ((p.lda & 15) || (p.ldb & 15)) return false;
     if ((((uintptr_t)p.A) & 15) || (((uintptr_t)p.B) & 15)) return false;
     if (p.rowsA < p.Mout || p.colsB < p.Nout) return false;
     // buffer offsets are 32-bit and 0x80000000 marks an empty copy: every
-    // row of every tile, in range or not, stays below it
+    // row of every tile, in range or not, stays below it (a lane's K offset
+    // is sent only below Kp)
     const uint64_t rows_a = ceil_to(p.Mout, TM) + TM, rows_b = ceil_to(p.Nout, TN) + TN;
     if (rows_a * p.lda + p.Kp >= (1ull << 31) || rows_b * p.ldb + p.Kp >= (1ull << 31)) return false;
     return true;

@@ -56,7 +56,11 @@ def assert_f32_identical(got, want):
                                    (5, 17, 80), (100, 1000, 2064), (128, 1024, 4096), (17, 33, 16),
                                    (48, 300, 592),
                                    # 256-tiles again once they fill every CU: full and ragged grids
-                                   (4096, 4096, 128), (4352, 4096, 64)])
+                                   (4096, 4096, 128), (4352, 4096, 64),
+                                   # K an odd multiple of 64: the last 128-byte slice half zeros
+                                   # (256-tiles, 128-tiles, both with a ragged grid)
+                                   (4096, 4096, 192), (4100, 4096, 4160), (1000, 600, 960),
+                                   (513, 257, 4160)])
 def test_gemm_s8_i32_exact(ane, M, N, K):
     import torch
 
