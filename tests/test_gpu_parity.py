@@ -73,6 +73,26 @@ def test_gemm_s8_i32_exact(ane, M, N, K):
     np.testing.assert_array_equal(host(acc), want.astype(np.int32))
 
 
+@pytest.mark.parametrize("M,N,K,pad", [(4096, 4096, 192, 64), (1000, 600, 960, 48), (4100, 4096, 4160, 16)])
+def test_gemm_s8_i32_padded_rows(ane, M, N, K, pad):
+    """Rows wider than K (lda = ldb = K + pad) filled with nonzero bytes past
+    K, K an odd multiple of 64: the contraction kernels run 128-byte K slices
+    and must send the last slice's upper half out of range rather than read
+    the padding (256-tiles, then 128-tiles)."""
+    import torch
+
+    g = np.random.default_rng(M + 7 * K)
+    ld = K + pad
+    A = g.integers(-128, 128, size=(M, ld), dtype=np.int8)
+    Bt = g.integers(-128, 128, size=(N, ld), dtype=np.int8)
+    A[:, K:] = 77
+    Bt[:, K:] = -91
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    ane.gemm_s8_i32(dev(A), dev(Bt), acc, M, N, K, lda=ld, ldb=ld)
+    want = A[:, :K].astype(np.int64) @ Bt[:, :K].astype(np.int64).T
+    np.testing.assert_array_equal(host(acc), want.astype(np.int32))
+
+
 # ---------------------------------------------------------------- quantize
 @pytest.mark.parametrize("count", [1, 16, 17, 1000, 4096 + 5, 1 << 20])
 def test_quantize_opcode_parity(ane, oracle, count):
