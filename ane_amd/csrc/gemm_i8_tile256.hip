@@ -144,14 +144,6 @@ __device__ __forceinline__ void load_frags(const int8_t* stage, uint32_t rA, uin
         f.b[ni] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(rB + ni * 32, chunk));
 }
 
-__device__ __forceinline__ void mfmas(v16i (&acc)[FM][FN], const Frags& f) {
-#pragma unroll
-    for (int mi = 0; mi < FM; mi++)
-#pragma unroll
-        for (int ni = 0; ni < FN; ni++)
-            acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
-}
-
 // One of the FM + FN fragment reads of a k-step, by index.
 __device__ __forceinline__ void load_frag(const int8_t* stage, uint32_t rA, uint32_t rB, uint32_t chunk,
                                           Frags& f, int idx) {
@@ -184,7 +176,8 @@ __device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Fra
             const int mi = g / FN, ni = g % FN;
             acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fc.a[mi], fc.b[ni], acc[mi][ni], 0, 0, 0);
             if (ks + 1 < kSteps && g < nD) load_frag(cur, rA, rB, 2 * (ks + 1) + chalf, fn, g);
-            if (ks < kCopySteps && g % kStride == kStride - 1) issue_one(c, offA, offB, kofs, ks * kPerStep + g / kStride);
+            if (ks < kCopySteps && g % kStride == kStride - 1)
+                issue_one(c, offA, offB, kofs, ks * kPerStep + g / kStride);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
