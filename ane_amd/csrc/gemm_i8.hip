@@ -18,6 +18,7 @@
 #include "gemm_i8.hpp"
 
 #include <atomic>
+#include <vector>
 
 namespace ane {
 
@@ -259,11 +260,16 @@ extern "C" int ane_hip_gemm_s8_i32(uint32_t M, uint32_t N, uint32_t K, const int
 // so both contraction kernels run whole 128-byte K slices.
 static uint64_t fused_kp(int32_t K) { return ceil_to((uint64_t)(K > 0 ? K : 0), 128); }
 
+// Workspace layout: scales {sa, sb} at 0; at 256 the absmax partials
+// (2 x kFusedPartials uint32) followed by the quantizer's wait record
+// (1 + kFusedPartials uint32); then qA and qBt, each rounded up to 256 bytes.
+static uint64_t fused_partials_bytes() { return ceil_to((uint64_t)(3 * kFusedPartials + 1) * 4, 256); }
+
 extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K) {
     if (M < 0 || N < 0 || K < 0) return 0;
     const uint64_t Kp = fused_kp(K);
     uint64_t bytes = 256;                                  // scales + alignment slack
-    bytes += ceil_to((uint64_t)kFusedPartials * 2 * 4, 256);  // absmax partials
+    bytes += fused_partials_bytes();                      // absmax partials + wait record
     bytes += ceil_to((uint64_t)M * Kp, 256);               // qA
     bytes += ceil_to((uint64_t)N * Kp, 256);               // qBt
     return (size_t)bytes;
@@ -274,6 +280,7 @@ struct FusedLayout {
     uint64_t Kp;
     float* scales;
     uint32_t* partials;
+    uint32_t* wstatus;
     int8_t* qA;
     int8_t* qBt;
 };
@@ -284,7 +291,8 @@ static FusedLayout fused_layout(int32_t M, int32_t K, void* workspace) {
     uint8_t* ws = (uint8_t*)workspace;
     L.scales = (float*)ws;
     L.partials = (uint32_t*)(ws + 256);
-    L.qA = (int8_t*)(ws + 256 + ceil_to((uint64_t)kFusedPartials * 2 * 4, 256));
+    L.wstatus = L.partials + 2 * kFusedPartials;
+    L.qA = (int8_t*)(ws + 256 + fused_partials_bytes());
     L.qBt = L.qA + ceil_to((uint64_t)M * L.Kp, 256);
     return L;
 }
@@ -308,7 +316,7 @@ extern "C" int ane_hip_dense_fused_i8_quantize(int32_t M, int32_t N, int32_t K, 
     const FusedLayout L = fused_layout(M, K, workspace);
     const uint64_t Kp = L.Kp;
     st = launch_fused_quantize(A, B, (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, L.partials,
-                               L.qA, L.qBt, L.scales, s);
+                               L.qA, L.qBt, L.scales, L.wstatus, s);
     if (st != ANE_OK) return st;
     if (scales_out) {
         hipError_t e = hipMemcpyAsync(scales_out, L.scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
@@ -353,4 +361,36 @@ extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float sca
                                              stream);
     if (st != ANE_OK) return st;
     return ane_hip_dense_fused_i8_gemm(M, N, K, scale, relu, C, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ane_hip_dense_fused_i8_status(const void* workspace, void* stream) {
+    if (!workspace || !aligned16(workspace)) return ANE_ERR_WORKSPACE;
+    if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    const uint32_t* rec = (const uint32_t*)((const uint8_t*)workspace + 256) + 2 * kFusedPartials;
+    uint32_t n = 0;
+    if (hipMemcpy(&n, rec, 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    if (n > kFusedPartials) return ANE_ERR_INVALID_ARG;  // no quantize call wrote this workspace
+    uint32_t bits = 0;
+    if (n) {
+        std::vector<uint32_t> h(n);
+        if (hipMemcpy(h.data(), rec + 1, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+            (void)hipGetLastError();
+            return ANE_ERR_HIP;
+        }
+        for (uint32_t v : h) bits |= v;
+    }
+    // A launch whose wait was completed by another launch's arrivals does
+    // not see that itself: the arrival that completed it recorded it on the
+    // device, so the device's record is read (and cleared) as well.
+    uint32_t dev_bits = 0;
+    const int st = resident_slot_check(&dev_bits);
+    if (st != ANE_OK) return st;
+    if (bits || resident_mixed_bit(dev_bits)) return ANE_ERR_GRID_WAIT;
+    return ANE_OK;
 }

@@ -25,11 +25,20 @@ struct GemmParams {
 };
 
 // dense_fused_i8 operand preparation (quantize_fused.hip): absmax partials
-// (kFusedPartials per tensor), qA (M x Kp), qBt (N x Kp), scales {sa, sb}.
+// (kFusedPartials per tensor), qA (M x Kp), qBt (N x Kp), scales {sa, sb},
+// and the launch's wait record wstatus: wstatus[0] = the number of
+// workgroups that met at the grid-wide wait (0 on the two-pass route, which
+// has none), wstatus[1 + w] = what workgroup w saw there (0, or timed-out /
+// mixed-arrival bits).  Every launch writes it, so no clearing is needed.
 constexpr uint32_t kFusedPartials = 1024;
 int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t Kp, uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales,
-                          hipStream_t s);
+                          uint32_t* wstatus, hipStream_t s);
+// The current device's record of failed grid-wide waits (sticky bits; 0 if
+// the resident route never ran): read, and cleared together with the
+// counters once the device is idle when nonzero.
+int resident_slot_check(uint32_t* bits);
+bool resident_mixed_bit(uint32_t bits);
 
 // 256 x 256 tile kernel (gemm_i8_tile256.hip): Bt layout, signed A, K a
 // multiple of 64 (run as 128-byte slices, an odd last half read as zeros),

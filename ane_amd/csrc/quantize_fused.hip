@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(kT)
 k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_t M, uint32_t N,
                uint32_t K, uint32_t Kp, const uint32_t* __restrict__ partials, uint32_t nbA,
                uint32_t nbB, uint32_t nqA, int8_t* __restrict__ qA, int8_t* __restrict__ qBt,
-               float* __restrict__ scales) {
+               float* __restrict__ scales, uint32_t* __restrict__ wstatus) {
     __shared__ uint32_t red[4];
     __shared__ uint32_t tileT[kBTN * kTileRowDw];
     const bool isA = blockIdx.x < nqA;
@@ -95,6 +95,7 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
     float scale, inv;
     quant_params(amax, scale, inv);
     if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == nqA)) scales[isA ? 0 : 1] = scale;
+    if (threadIdx.x == 0 && blockIdx.x == 0) wstatus[0] = 0;  // no grid-wide wait on this route
     // the values quantized here are the tensor's own, whose max was just
     // folded: pack4_fast applies whenever that max and inv are finite
     const bool fast = fast_quant_ok(amax, inv);
@@ -215,32 +216,116 @@ constexpr uint64_t kResidentMinBytes = (uint64_t)12 << 20;
 // vmcnt(0) orders each workgroup's partial stores before its arrival.
 // Arrivals are counted in kSyncGroups groups (workgroup w in group
 // w % kSyncGroups, each counter on its own 128-byte line) so no line takes
-// more than ~G/kSyncGroups atomics; the last arrival of a group bumps the
-// top counter, and the last group's last arrival advances every group's
-// generation word, which the waiting workgroups poll (gen0 read before
-// arriving, so the advance cannot be missed).  Group counters return to
-// zero and the top counter to a multiple of the group count, so the slot
-// needs no reset between launches (a launch's resets complete before the
-// kernel does).  The wait gives up after timeout_ticks of the 100 MHz
-// realtime counter and records that in the error word.
+// more than ~G/kSyncGroups atomics; the last arrival of a group adds to the
+// top counter, and the last group's last arrival writes every group's
+// release word, which the waiting workgroups poll (each read its group's
+// word before arriving, so the release cannot be missed).  The last
+// arrivals reset the group and top counters to zero, so the slot is at rest
+// between launches (a launch's resets complete before the kernel does).
+//
+// Every launch carries a nonzero 32-bit tag (the host numbers launches
+// 1, 2, 3, ...), so that two launches sharing the slot at once (a replayed
+// graph overlapping another call) cannot pass each other's workgroups
+// silently:
+//  * each arrival adds (tag << 32) | 1 to a 64-bit counter; a counter that
+//    reaches its member count holds members * tag in its high half when all
+//    its arrivals are one launch's, and a different sum when two launches'
+//    arrivals mixed in it, unless their tags differ by a multiple of 2^27 (a
+//    counter has at most 64 members): the arrival that completes it records
+//    kSyncMixed in the error word;
+//  * a release word is (epoch << 32) | tag of the releasing launch, and a
+//    waiter passes only on a release carrying its own tag: one by another
+//    launch is recorded (kSyncMixed) and the wait goes on for its own.
+// The wait gives up after timeout_ticks of the 100 MHz realtime counter and
+// records kSyncTimeout.  Returns this workgroup's view: 0, or the bits it
+// recorded.  Two launches with the same tag (one captured graph replayed
+// twice at once, on the same workspace) are not told apart.
 constexpr uint32_t kSyncGroups = 16;
 constexpr uint32_t kSyncLineDw = 32;                       // 128-byte lines
 constexpr uint32_t kSyncSlotDw = (1 + 2 * kSyncGroups) * kSyncLineDw;
-__device__ __forceinline__ uint32_t* sync_top(uint32_t* sync) { return sync; }
-__device__ __forceinline__ uint32_t* sync_err(uint32_t* sync) { return sync + 1; }
-__device__ __forceinline__ uint32_t* sync_gen(uint32_t* sync, uint32_t g) { return sync + (1 + g) * kSyncLineDw; }
-__device__ __forceinline__ uint32_t* sync_sub(uint32_t* sync, uint32_t g) {
-    return sync + (1 + kSyncGroups + g) * kSyncLineDw;
+constexpr uint32_t kSyncTimeout = 1u, kSyncMixed = 2u;
+__device__ __forceinline__ uint64_t* sync_top(uint32_t* sync) { return reinterpret_cast<uint64_t*>(sync); }
+__device__ __forceinline__ uint32_t* sync_err(uint32_t* sync) { return sync + 2; }
+__device__ __forceinline__ uint64_t* sync_gen(uint32_t* sync, uint32_t g) {
+    return reinterpret_cast<uint64_t*>(sync + (1 + g) * kSyncLineDw);
+}
+__device__ __forceinline__ uint64_t* sync_sub(uint32_t* sync, uint32_t g) {
+    return reinterpret_cast<uint64_t*>(sync + (1 + kSyncGroups + g) * kSyncLineDw);
 }
 
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint64_t ld_agent64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
+__device__ __forceinline__ void st_agent64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t add_agent64(uint64_t* p, uint64_t v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void or_err(uint32_t* sync, uint32_t bits) {
+    __hip_atomic_fetch_or(sync_err(sync), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True when a counter that has just reached `members` arrivals (old is its
+// value before the last add of `tag`) holds only arrivals tagged `tag`.
+__device__ __forceinline__ bool sync_tags_match(uint64_t old, uint32_t tag, uint32_t members) {
+    return (uint32_t)(old >> 32) + tag == members * tag;
+}
+
+__device__ __forceinline__ uint32_t grid_arrive_wait(uint32_t* sync, uint32_t* partials, uint32_t ma,
+                                                     uint32_t mb, uint32_t w, uint32_t G, uint32_t tag,
+                                                     uint64_t timeout_ticks) {
+    const uint32_t ng = G < kSyncGroups ? G : kSyncGroups;
+    const uint32_t g = w % ng, members = (G - g + ng - 1) / ng;
+    uint64_t* gen = sync_gen(sync, g);
+    const uint64_t gen0 = ld_agent64(gen);
+    st_agent(&partials[w], ma);
+    st_agent(&partials[G + w], mb);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint64_t inc = ((uint64_t)tag << 32) | 1u;
+    uint32_t bad = 0;
+    const uint64_t old = add_agent64(sync_sub(sync, g), inc);
+    if ((uint32_t)old == members - 1) {
+        if (!sync_tags_match(old, tag, members)) bad = kSyncMixed;
+        // the group's counter is reset after the top counter's add, so that
+        // add does not queue behind the store
+        const uint64_t top = add_agent64(sync_top(sync), inc);
+        const bool last = (uint32_t)top == ng - 1;
+        if (last && !sync_tags_match(top, tag, ng)) bad = kSyncMixed;
+        if (bad) or_err(sync, bad);
+        st_agent64(sync_sub(sync, g), 0u);
+        if (last) {
+            st_agent64(sync_top(sync), 0u);
+            const uint64_t rel = (((gen0 >> 32) + 1) << 32) | tag;
+            for (uint32_t i = 0; i < ng; i++) st_agent64(sync_gen(sync, i), rel);
+            return bad;
+        }
+    }
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        const uint64_t v = ld_agent64(gen);
+        if (v != gen0) {
+            if ((uint32_t)v == tag) break;  // this launch's release
+            if (!(bad & kSyncMixed)) {
+                bad |= kSyncMixed;          // another launch's release
+                or_err(sync, kSyncMixed);
+            }
+        }
+        __builtin_amdgcn_s_sleep(4);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > timeout_ticks) {
+            or_err(sync, kSyncTimeout);
+            bad |= kSyncTimeout;
+            break;
+        }
+    }
+    asm volatile("" ::: "memory");
+    return bad;
 }
 
 // max over the 64 lanes, every lane gets it: DPP within each 16-lane row,
@@ -253,35 +338,6 @@ __device__ __forceinline__ uint32_t wave_max_dpp(uint32_t m) {
     const uint32_t r0 = __builtin_amdgcn_readlane(m, 0), r1 = __builtin_amdgcn_readlane(m, 16);
     const uint32_t r2 = __builtin_amdgcn_readlane(m, 32), r3 = __builtin_amdgcn_readlane(m, 48);
     return umax(umax(r0, r1), umax(r2, r3));
-}
-
-__device__ __forceinline__ void grid_arrive_wait(uint32_t* sync, uint32_t* partials, uint32_t ma, uint32_t mb,
-                                                 uint32_t w, uint32_t G, uint64_t timeout_ticks) {
-    const uint32_t ng = G < kSyncGroups ? G : kSyncGroups;
-    const uint32_t g = w % ng, members = (G - g + ng - 1) / ng;
-    uint32_t* gen = sync_gen(sync, g);
-    const uint32_t gen0 = ld_agent(gen);
-    st_agent(&partials[w], ma);
-    st_agent(&partials[G + w], mb);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (add_agent(sync_sub(sync, g), 1u) == members - 1) {
-        // the group's counter is reset after the top counter's add, so that
-        // add does not queue behind the store
-        const bool last = add_agent(sync_top(sync), 1u) % ng == ng - 1;
-        if (last)
-            for (uint32_t i = 0; i < ng; i++) st_agent(sync_gen(sync, i), gen0 + 1);
-        st_agent(sync_sub(sync, g), 0u);
-        if (last) return;
-    }
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (ld_agent(gen) == gen0) {
-        __builtin_amdgcn_s_sleep(4);
-        if (__builtin_amdgcn_s_memrealtime() - t0 > timeout_ticks) {
-            __hip_atomic_fetch_or(sync_err(sync), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-    }
-    asm volatile("" ::: "memory");
 }
 
 // Range-checked buffer access (make_rsrc): a load past the resource's
@@ -311,7 +367,8 @@ __global__ void __launch_bounds__(kRT)
 k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, uint32_t N, uint32_t K,
                     uint64_t nA4, uint64_t perA4, uint32_t nTiles, uint32_t perT,
                     uint32_t* __restrict__ partials, int8_t* __restrict__ qA, int8_t* __restrict__ qBt,
-                    float* __restrict__ scales, uint32_t* __restrict__ sync, uint64_t timeout_ticks) {
+                    float* __restrict__ scales, uint32_t* __restrict__ sync, uint32_t tag,
+                    uint64_t timeout_ticks, uint32_t* __restrict__ status) {
     __shared__ float4 As[kRLdsA4];
     __shared__ uint32_t red[2 * (kRT / kWave)];
     uint32_t* tileT = reinterpret_cast<uint32_t*>(As);  // phase 2, once A's LDS part is written out
@@ -402,7 +459,12 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
             ma = umax(ma, red[i]);
             mb = umax(mb, red[kRT / kWave + i]);
         }
-        grid_arrive_wait(sync, partials, ma, mb, w, G, timeout_ticks);
+        // this launch's record in the workspace: entry w = what workgroup w
+        // saw at the wait, the count of entries at status[0] (written by
+        // every launch, so no clearing is needed)
+        const uint32_t bad = grid_arrive_wait(sync, partials, ma, mb, w, G, tag, timeout_ticks);
+        st_agent(&status[1 + w], bad);
+        if (w == 0) st_agent(&status[0], G);
     }
     __syncthreads();
     uint32_t pa = 0, pb = 0;
@@ -530,6 +592,7 @@ struct ResidentDevice {
     hipEvent_t last = nullptr;
     hipStream_t last_stream = nullptr;
     bool last_valid = false;
+    uint32_t tag = 0;  // the last launch's tag (launches are numbered from 1)
 };
 std::mutex g_res_mu;
 ResidentDevice g_res_dev[64];
@@ -567,8 +630,8 @@ ResidentDevice* resident_device(hipStream_t s, int* dev_out) {
 // (K % 128 == 0, N % 64 == 0), 16-byte aligned operands, and at most kRNT
 // B tiles per workgroup.  Returns true when it launched.
 bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
-                     uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales, hipStream_t s,
-                     int* status) {
+                     uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales, uint32_t* wstatus,
+                     hipStream_t s, int* status) {
     *status = ANE_OK;
     if (K == 0 || M == 0 || N == 0 || (K % kBTK) || (N % kBTN)) return false;
     // below ~12 MiB of operands the two launches of the two-pass route are
@@ -613,12 +676,36 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
             return false;
         }
     }
-    hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, A, B, N, K, nA4, perA4,
-                       (uint32_t)nTiles, perT, partials, qA, qBt, scales, d.sync,
-                       g_wait_limit.load(std::memory_order_relaxed));
-    if (hipGetLastError() != hipSuccess) {
-        *status = ANE_ERR_HIP;
-        return true;
+    // Outside capture the grid goes out as a cooperative launch: the runtime
+    // then starts it only with every workgroup resident at once, or refuses
+    // it (the two-pass route runs instead).  A captured launch is a plain
+    // one; the ordering above and the bounded, tagged wait cover it.
+    if (++d.tag == 0) d.tag = 1;
+    const float* kA = A;
+    const float* kB = B;
+    uint32_t kN = N, kK = K, kTiles = (uint32_t)nTiles, kPerT = perT, kTag = d.tag;
+    uint64_t kNA4 = nA4, kPerA4 = perA4, kLimit = g_wait_limit.load(std::memory_order_relaxed);
+    uint32_t* kPartials = partials;
+    int8_t* kQA = qA;
+    int8_t* kQBt = qBt;
+    float* kScales = scales;
+    uint32_t* kSync = d.sync;
+    uint32_t* kStatus = wstatus;
+    if (!capturing) {
+        void* args[] = {&kA, &kB, &kN, &kK, &kNA4, &kPerA4, &kTiles, &kPerT, &kPartials, &kQA, &kQBt,
+                        &kScales, &kSync, &kTag, &kLimit, &kStatus};
+        if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_quantize_resident), dim3(G), dim3(kRT),
+                                       args, 0, s) != hipSuccess) {
+            (void)hipGetLastError();  // refused before anything was queued
+            return false;
+        }
+    } else {
+        hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, kA, kB, kN, kK, kNA4, kPerA4, kTiles,
+                           kPerT, kPartials, kQA, kQBt, kScales, kSync, kTag, kLimit, kStatus);
+        if (hipGetLastError() != hipSuccess) {
+            *status = ANE_ERR_HIP;
+            return true;
+        }
     }
     if (!capturing) {
         if (hipEventRecord(d.last, s) != hipSuccess) {
@@ -651,9 +738,9 @@ uint32_t blocks_for(uint64_t n) {
 
 int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t Kp, uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales,
-                          hipStream_t s) {
+                          uint32_t* wstatus, hipStream_t s) {
     int st = ANE_OK;
-    if (Kp == K && launch_resident(A, B, M, N, K, partials, qA, qBt, scales, s, &st)) return st;
+    if (Kp == K && launch_resident(A, B, M, N, K, partials, qA, qBt, scales, wstatus, s, &st)) return st;
     const uint64_t nA = (uint64_t)M * K, nB = (uint64_t)K * N;
     const uint32_t nbA = blocks_for(nA), nbB = blocks_for(nB);
     hipLaunchKernelGGL(k_absmax_two, dim3(nbA + nbB), dim3(kT), 0, s, A, nA, nbA, B, nB, nbB, partials);
@@ -663,7 +750,7 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
     const uint64_t nqB = Kp ? ((uint64_t)Kp / kBTK) * (((uint64_t)N + kBTN - 1) / kBTN) : 1;
     if (nqA + nqB > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
     hipLaunchKernelGGL(k_quantize_two, dim3((uint32_t)(nqA + nqB)), dim3(kT), 0, s, A, B, M, N, K, Kp,
-                       partials, nbA, nbB, (uint32_t)nqA, qA, qBt, scales);
+                       partials, nbA, nbB, (uint32_t)nqA, qA, qBt, scales, wstatus);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -674,21 +761,50 @@ extern "C" void ane_hip_set_grid_wait_limit(uint64_t ticks) {
     ane::g_wait_limit.store(ticks ? ticks : ane::kSyncTimeoutTicks, std::memory_order_relaxed);
 }
 
-extern "C" int ane_hip_grid_wait_status(void* stream) {
-    hipStream_t s = (hipStream_t)stream;
-    uint32_t* slot = ane::resident_slot_of();
+namespace ane {
+
+int resident_slot_check(uint32_t* bits) {
+    *bits = 0;
+    uint32_t* slot = resident_slot_of();
     if (!slot) return ANE_OK;
-    if (hipStreamSynchronize(s) != hipSuccess) {
-        (void)hipGetLastError();
-        return ANE_ERR_HIP;
-    }
     uint32_t err = 0;
-    if (hipMemcpy(&err, slot + 1, 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (hipMemcpy(&err, slot + 2, 4, hipMemcpyDeviceToHost) != hipSuccess) {
         (void)hipGetLastError();
         return ANE_ERR_HIP;
     }
+    *bits = err;
     if (!err) return ANE_OK;
-    const uint32_t zero = 0;
-    if (hipMemcpy(slot + 1, &zero, 4, hipMemcpyHostToDevice) != hipSuccess) (void)hipGetLastError();
-    return ANE_ERR_HIP;
+    // Back to rest: once every launch on the device has ended, the top and
+    // group counters and the error word are zeroed (the generation words
+    // keep counting).  Arrivals of two launches mixed in one counter can
+    // leave it short of, or past, a whole launch's count.
+    if (hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    static const uint32_t zeros[4] = {0, 0, 0, 0};
+    bool ok = hipMemcpy(slot, zeros, 3 * sizeof(uint32_t), hipMemcpyHostToDevice) == hipSuccess;
+    for (uint32_t g = 0; g < kSyncGroups && ok; g++)
+        ok = hipMemcpy(slot + (1 + kSyncGroups + g) * kSyncLineDw, zeros, 2 * sizeof(uint32_t),
+                       hipMemcpyHostToDevice) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    return ANE_OK;
+}
+
+bool resident_mixed_bit(uint32_t bits) { return (bits & kSyncMixed) != 0; }
+
+}  // namespace ane
+
+extern "C" int ane_hip_grid_wait_status(void* stream) {
+    if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return ANE_ERR_HIP;
+    }
+    uint32_t bits = 0;
+    const int st = ane::resident_slot_check(&bits);
+    if (st != ANE_OK) return st;
+    return bits ? ANE_ERR_GRID_WAIT : ANE_OK;
 }
