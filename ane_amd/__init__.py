@@ -77,6 +77,7 @@ STATUS = {
     6: "ANE_ERR_HIP",
     7: "ANE_ERR_NO_DEVICE",
     8: "ANE_ERR_WORKSPACE",
+    9: "ANE_ERR_GRID_WAIT",
 }
 
 # Symbols include/ane_hip.h, include/ggml-ane-hip.h and include/ane_decode.h
@@ -86,6 +87,7 @@ EXPORTS = (
     "ane_last_error",
     "ane_last_error_message",
     "ane_set_stream",
+    "ane_set_host_staging",
     "ane_stream_exec_async",
     "ane_hip_quantize_workspace_size",
     "ane_hip_quantize_fp32_i8",
@@ -98,6 +100,7 @@ EXPORTS = (
     "ane_hip_dense_fused_i8",
     "ane_hip_dense_fused_i8_quantize",
     "ane_hip_dense_fused_i8_gemm",
+    "ane_hip_dense_fused_i8_status",
     "ane_hip_grid_wait_status",
     "ane_hip_set_grid_wait_limit",
     "ane_hip_gemm_s8_i32",
@@ -161,6 +164,7 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_last_error": (_c.c_int, []),
     "ane_last_error_message": (_c.c_char_p, []),
     "ane_set_stream": (None, [_P]),
+    "ane_set_host_staging": (None, [_c.c_int]),
     "ane_stream_exec_async": (_c.c_int, [_P, _c.c_size_t, _P]),
     "ane_hip_quantize_workspace_size": (_c.c_size_t, [_c.c_uint64]),
     "ane_hip_quantize_fp32_i8": (_c.c_int, [_c.c_uint64, _c.c_int, _P, _P, _P, _P, _c.c_size_t, _P]),
@@ -182,6 +186,7 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
         _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _P, _P, _P, _P, _c.c_size_t, _P]),
     "ane_hip_dense_fused_i8_gemm": (
         _c.c_int, [_c.c_int32, _c.c_int32, _c.c_int32, _c.c_float, _c.c_int, _P, _P, _c.c_size_t, _P]),
+    "ane_hip_dense_fused_i8_status": (_c.c_int, [_P, _P]),
     "ane_hip_grid_wait_status": (_c.c_int, [_P]),
     "ane_hip_set_grid_wait_limit": (None, [_c.c_uint64]),
     "ane_hip_gemm_s8_i32": (
@@ -551,18 +556,55 @@ def quantize_fp32_i8(src, dst, scale_out, count=None, pad16=True, workspace=None
                                      _stream_handle(stream)), "quantize_fp32_i8")
 
 
-def dense_fused_i8(M, N, K, scale, relu, A, B, C, scales_out=None, workspace=None, stream=None):
+def _capturing(stream: Any = None) -> bool:
+    """True when ``stream`` (default: torch's current stream) is capturing a graph."""
+    import torch
+
+    if stream is None:
+        return torch.cuda.is_current_stream_capturing()
+    if not isinstance(stream, torch.cuda.Stream):
+        h = _stream_handle(stream)
+        if h == 0:
+            return False  # the null stream never captures
+        stream = torch.cuda.ExternalStream(h)
+    s = stream
+    with torch.cuda.stream(s):
+        return torch.cuda.is_current_stream_capturing()
+
+
+def dense_fused_i8_status(workspace, stream=None) -> None:
+    """Raise AneError(ANE_ERR_GRID_WAIT) if the last quantize call made with
+    ``workspace`` ran a grid-wide wait that gave up or was completed by
+    another launch's arrivals (its outputs are then not valid).
+    Synchronizes the stream; not allowed while it is capturing."""
+    check(lib().ane_hip_dense_fused_i8_status(_p(workspace), _stream_handle(stream)), "dense_fused_i8")
+
+
+def _want_check(check_arg, stream) -> bool:
+    return (not _capturing(stream)) if check_arg is None else bool(check_arg)
+
+
+def dense_fused_i8(M, N, K, scale, relu, A, B, C, scales_out=None, workspace=None, stream=None, check_wait=None):
+    """Op::dense_fused_i8 on the kernel ABI.  check_wait: None (default)
+    checks the quantizer's wait record after the call (dense_fused_i8_status,
+    which synchronizes the stream) unless the stream is capturing; False
+    leaves that to the caller; True always checks."""
     L = lib()
     wsb = L.ane_hip_dense_fused_i8_workspace_size(M, N, K)
     ws = workspace if workspace is not None else _scratch(wsb, A.device, stream)
     check(L.ane_hip_dense_fused_i8(M, N, K, scale, 1 if relu else 0, _p(A), _p(B), _p(C), _p(scales_out),
                                    _p(ws), wsb, _stream_handle(stream)), "dense_fused_i8")
+    if M > 0 and N > 0 and _want_check(check_wait, stream):
+        dense_fused_i8_status(ws, stream)
 
 
-def dense_fused_i8_quantize(M, N, K, A, B, workspace, scales_out=None, stream=None):
+def dense_fused_i8_quantize(M, N, K, A, B, workspace, scales_out=None, stream=None, check_wait=None):
+    """The quantize phase of dense_fused_i8; check_wait as for dense_fused_i8."""
     check(lib().ane_hip_dense_fused_i8_quantize(M, N, K, _p(A), _p(B), _p(scales_out), _p(workspace),
                                                 workspace.numel(), _stream_handle(stream)),
           "dense_fused_i8_quantize")
+    if M > 0 and N > 0 and _want_check(check_wait, stream):
+        dense_fused_i8_status(workspace, stream)
 
 
 def dense_fused_i8_gemm(M, N, K, scale, relu, C, workspace, stream=None):

@@ -12,6 +12,11 @@
 //  * operands are device pointers; every operand extent is checked against
 //    its HIP allocation before anything is launched, so a short or host
 //    buffer becomes an error instead of a GPU memory fault;
+//  * opt-in host staging (ane_set_host_staging, or ANE_HOST_STAGING=1 in
+//    the environment): operands in plain host memory (malloc,
+//    aligned_alloc) are copied to a device staging buffer, the record runs
+//    on the copies, and its outputs are copied back before the record
+//    returns, so the reference's callers can keep their host allocations;
 //  * scalar outputs (quantize scale_out, channelwise scales) may also be
 //    host memory: they are computed on the device and copied back;
 //  * errors are recorded per thread (ane_last_error) since the signature
@@ -20,8 +25,10 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <algorithm>
 #include <cstring>
+#include <functional>
 #include <vector>
 #include <map>
 #include <mutex>
@@ -37,6 +44,15 @@ thread_local int t_status = ANE_OK;
 thread_local std::string t_message;
 thread_local hipStream_t t_stream = nullptr;
 thread_local bool t_ran_fused = false;  // a dense_fused_i8 record ran in this stream_exec call
+thread_local int t_staging = -1;        // host staging: -1 = ANE_HOST_STAGING, 0 off, 1 on
+
+bool staging_on() {
+    if (t_staging < 0) {
+        const char* e = std::getenv("ANE_HOST_STAGING");
+        t_staging = (e && e[0] && std::strcmp(e, "0") != 0) ? 1 : 0;
+    }
+    return t_staging == 1;
+}
 
 int fail(int status, const char* fmt, ...) {
     char buf[512];
@@ -62,21 +78,22 @@ struct Workspace {
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace>* g_ws = nullptr;
+// pool 0: the records' workspaces; pool 1: host staging copies
+std::map<std::pair<int, hipStream_t>, Workspace>* g_ws[2] = {nullptr, nullptr};
 
 struct Lease {
     std::unique_lock<std::mutex> lock;
     void* ptr = nullptr;
 };
 
-int get_workspace(hipStream_t s, size_t bytes, Lease& lease) {
+int get_workspace(hipStream_t s, size_t bytes, Lease& lease, int pool = 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(ANE_ERR_HIP, "hipGetDevice failed");
     Workspace* w = nullptr;
     {
         std::lock_guard<std::mutex> lock(g_ws_mu);
-        if (!g_ws) g_ws = new std::map<std::pair<int, hipStream_t>, Workspace>();
-        w = &(*g_ws)[{dev, s}];  // map nodes never move
+        if (!g_ws[pool]) g_ws[pool] = new std::map<std::pair<int, hipStream_t>, Workspace>();
+        w = &(*g_ws[pool])[{dev, s}];  // map nodes never move
     }
     lease.lock = std::unique_lock<std::mutex>(w->mu);
     if (w->bytes < bytes) {
@@ -141,6 +158,80 @@ int check_range(const void* p, uint64_t bytes, const char* name, bool host_ok, W
         if (st__ != ANE_OK) return st__; \
     } while (0)
 
+// ------------------------------------------------------------ host staging
+// A record's operands, checked and (in staging mode) mapped.  operand()
+// checks one operand's extent as before; in staging mode an operand in
+// unregistered host memory is instead given a slot in the stream's staging
+// buffer, and commit() then copies the inputs there and repoints the
+// record's pointers at the copies.  finish() copies the outputs back and
+// waits for them.  Without staging, host memory stays an error.
+enum Dir { kIn = 1, kOut = 2, kInOut = 3 };
+
+class Stager {
+  public:
+    explicit Stager(hipStream_t s) : s_(s) {}
+
+    template <typename T>
+    int operand(T*& p, uint64_t bytes, const char* name, Dir dir) {
+        if (bytes == 0) return ANE_OK;
+        Where w = Where::kDevice;
+        CHECK(check_range(p, bytes, name, staging_on(), &w));
+        if (w == Where::kHost) {
+            T** slot = &p;
+            items_.push_back({(void*)p, 0, bytes, dir, [slot](void* d) { *slot = reinterpret_cast<T*>(d); }});
+        }
+        return ANE_OK;
+    }
+
+    int commit() {
+        if (items_.empty()) return ANE_OK;
+        size_t total = 0;
+        for (Item& it : items_) {
+            it.offset = total;
+            total += (it.bytes + 255) & ~(size_t)255;
+        }
+        CHECK(get_workspace(s_, total, lease_, 1));
+        for (Item& it : items_) {
+            void* d = (uint8_t*)lease_.ptr + it.offset;
+            if ((it.dir & kIn) && hipMemcpyAsync(d, it.host, it.bytes, hipMemcpyHostToDevice, s_) != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(ANE_ERR_HIP, "host staging: copy of %zu input bytes failed", it.bytes);
+            }
+            it.set(d);
+        }
+        return ANE_OK;
+    }
+
+    int finish(int st) {
+        if (items_.empty() || st != ANE_OK) return st;
+        for (Item& it : items_) {
+            if (!(it.dir & kOut)) continue;
+            const void* d = (uint8_t*)lease_.ptr + it.offset;
+            if (hipMemcpyAsync(it.host, d, it.bytes, hipMemcpyDeviceToHost, s_) != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(ANE_ERR_HIP, "host staging: copy of %zu output bytes failed", it.bytes);
+            }
+        }
+        if (hipStreamSynchronize(s_) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(ANE_ERR_HIP, "host staging: stream synchronize failed");
+        }
+        return st;
+    }
+
+  private:
+    struct Item {
+        void* host;
+        size_t offset;
+        uint64_t bytes;
+        Dir dir;
+        std::function<void(void*)> set;
+    };
+    hipStream_t s_;
+    std::vector<Item> items_;
+    Lease lease_;
+};
+
 uint64_t ceil_u(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
 
 // ------------------------------------------------------------ record reader
@@ -194,9 +285,11 @@ int op_quantize(Reader& r, hipStream_t s) {
     uint64_t n = ceil_u(count, 16);
     if (n == 0) n = 16;
     Where w;
-    CHECK(check_range(src, n * 4, "quantize_fp32_i8 src", false, nullptr));
-    CHECK(check_range(dst, n, "quantize_fp32_i8 dst", false, nullptr));
+    Stager st(s);
+    CHECK(st.operand(src, n * 4, "quantize_fp32_i8 src", kIn));
+    CHECK(st.operand(dst, n, "quantize_fp32_i8 dst", kOut));
     CHECK(check_range(scale_out, 4, "quantize_fp32_i8 scale_out", true, &w));
+    CHECK(st.commit());
     const size_t wsb = ane_hip_quantize_workspace_size(n) + 256;
     Lease lease;
     CHECK(get_workspace(s, wsb, lease));
@@ -206,7 +299,7 @@ int op_quantize(Reader& r, hipStream_t s) {
     CHECK(hip_status(ane_hip_quantize_fp32_i8(count, 1, src, dst, dev_scale, part, wsb - 256, s),
                      "quantize_fp32_i8"));
     if (w == Where::kHost) CHECK(copy_back(s, scale_out, dev_scale, 4));
-    return ANE_OK;
+    return st.finish(ANE_OK);
 }
 
 // 0x1A [count:u32][scale:f32][src][dst]  (bytecode_interpreter.s:1959-1963)
@@ -217,9 +310,11 @@ int op_dequantize(Reader& r, hipStream_t s) {
     float* dst = r.ptr<float>();
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "dequantize_i8_fp32 record truncated");
     const uint64_t n = ceil_u(count, 16);
-    CHECK(check_range(src, n, "dequantize_i8_fp32 src", false, nullptr));
-    CHECK(check_range(dst, n * 4, "dequantize_i8_fp32 dst", false, nullptr));
-    return hip_status(ane_hip_dequantize_i8_fp32(count, scale, src, dst, s), "dequantize_i8_fp32");
+    Stager st(s);
+    CHECK(st.operand(src, n, "dequantize_i8_fp32 src", kIn));
+    CHECK(st.operand(dst, n * 4, "dequantize_i8_fp32 dst", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_dequantize_i8_fp32(count, scale, src, dst, s), "dequantize_i8_fp32"));
 }
 
 // 0x1B [K:u32][N:u32][src][dst]  (bytecode_interpreter.s:2460-2464)
@@ -229,9 +324,11 @@ int op_pack_b(Reader& r, hipStream_t s) {
     const int8_t* src = r.ptr<const int8_t>();
     int8_t* dst = r.ptr<int8_t>();
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "pack_b_i8 record truncated");
-    CHECK(check_range(src, (uint64_t)K * N, "pack_b_i8 src", false, nullptr));
-    CHECK(check_range(dst, ane_hip_packed_b_size(K, N), "pack_b_i8 dst", false, nullptr));
-    return hip_status(ane_hip_pack_b_i8(K, N, src, dst, s), "pack_b_i8");
+    Stager st(s);
+    CHECK(st.operand(src, (uint64_t)K * N, "pack_b_i8 src", kIn));
+    CHECK(st.operand(dst, ane_hip_packed_b_size(K, N), "pack_b_i8 dst", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_pack_b_i8(K, N, src, dst, s), "pack_b_i8"));
 }
 
 // 0x1C [rows:u32][cols:u32][src][dst][scales]  (bytecode_interpreter.s:2592-2597)
@@ -246,9 +343,11 @@ int op_channelwise(Reader& r, hipStream_t s) {
     uint64_t cpad = ceil_u(cols, 16);
     if (cpad == 0) cpad = 16;
     Where w;
-    CHECK(check_range(src, (uint64_t)rows * cpad * 4, "channelwise src", false, nullptr));
-    CHECK(check_range(dst, (uint64_t)rows * cpad, "channelwise dst", false, nullptr));
+    Stager st(s);
+    CHECK(st.operand(src, (uint64_t)rows * cpad * 4, "channelwise src", kIn));
+    CHECK(st.operand(dst, (uint64_t)rows * cpad, "channelwise dst", kOut));
     CHECK(check_range(scales, (uint64_t)rows * 4, "channelwise scales", true, &w));
+    CHECK(st.commit());
     float* dev_scales = scales;
     Lease lease;
     if (w == Where::kHost) {
@@ -258,7 +357,7 @@ int op_channelwise(Reader& r, hipStream_t s) {
     CHECK(hip_status(ane_hip_quantize_channelwise(rows, cols, src, dst, dev_scales, s),
                      "quantize_fp32_i8_channelwise"));
     if (w == Where::kHost) CHECK(copy_back(s, scales, dev_scales, (size_t)rows * 4));
-    return ANE_OK;
+    return st.finish(ANE_OK);
 }
 
 // 0x18 / 0x1E [M][N][K][sa][sb][flags:u8][A][Bp][bias][C]
@@ -283,12 +382,14 @@ int op_dense(Reader& r, hipStream_t s, bool a_unsigned) {
     const uint64_t P = ceil_u(N, 16) / 16, G = Kp / 4;
     if (((uintptr_t)A & 15) || ((uintptr_t)Bp & 15))
         return fail(ANE_ERR_INVALID_ARG, "%s: A and B_packed must be 16-byte aligned", nm);
-    CHECK(check_range(A, Mp * Kp, "dense A", false, nullptr));
-    CHECK(check_range(Bp, P * G * 64, "dense B_packed", false, nullptr));
-    CHECK(check_range(bias, (uint64_t)N * 4, "dense bias", false, nullptr));
-    CHECK(check_range(C, Mp * N * 4, "dense C", false, nullptr));
-    return hip_status(ane_hip_dense_i8(M, N, K, sa, sb, flags, A, Bp, bias, C, a_unsigned ? 1 : 0, s),
-                      nm);
+    Stager st(s);
+    CHECK(st.operand(A, Mp * Kp, "dense A", kIn));
+    CHECK(st.operand(Bp, P * G * 64, "dense B_packed", kIn));
+    CHECK(st.operand(bias, (uint64_t)N * 4, "dense bias", kIn));
+    CHECK(st.operand(C, Mp * N * 4, "dense C", kOut));
+    CHECK(st.commit());
+    return st.finish(
+        hip_status(ane_hip_dense_i8(M, N, K, sa, sb, flags, A, Bp, bias, C, a_unsigned ? 1 : 0, s), nm));
 }
 
 // 0x57 [M:u32][K:u32][x][W][y]  (bytecode_interpreter.s:7017-7023)
@@ -301,11 +402,13 @@ int op_q8_0_gemv(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "q8_0_gemv record truncated");
     if (M == 0) return ANE_OK;
     const uint64_t nb = K >> 5;
-    CHECK(check_range(x, nb * 32 * 4, "q8_0_gemv x", false, nullptr));
-    CHECK(check_range(W, (uint64_t)M * nb * 34, "q8_0_gemv W", false, nullptr));
-    CHECK(check_range(y, (uint64_t)M * 4, "q8_0_gemv y", false, nullptr));
     if ((uintptr_t)W & 1) return fail(ANE_ERR_INVALID_ARG, "q8_0_gemv: W must be 2-byte aligned");
-    return hip_status(ane_hip_q8_0_gemv(M, K, x, W, y, s), "q8_0_gemv");
+    Stager st(s);
+    CHECK(st.operand(x, nb * 32 * 4, "q8_0_gemv x", kIn));
+    CHECK(st.operand(W, (uint64_t)M * nb * 34, "q8_0_gemv W", kIn));
+    CHECK(st.operand(y, (uint64_t)M * 4, "q8_0_gemv y", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_q8_0_gemv(M, K, x, W, y, s), "q8_0_gemv"));
 }
 
 // 0x80 [M:i32][N:i32][K:i32][scale:f32][relu:bool][A][B][C]  (README.md:87-97)
@@ -321,15 +424,17 @@ int op_dense_fused(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "dense_fused_i8 record truncated");
     if (M < 0 || N < 0 || K < 0) return fail(ANE_ERR_INVALID_ARG, "dense_fused_i8: negative shape");
     if (M == 0 || N == 0) return ANE_OK;
-    CHECK(check_range(A, (uint64_t)M * K * 4, "dense_fused_i8 A", false, nullptr));
-    CHECK(check_range(B, (uint64_t)K * N * 4, "dense_fused_i8 B", false, nullptr));
-    CHECK(check_range(C, (uint64_t)M * N * 4, "dense_fused_i8 C", false, nullptr));
+    Stager st(s);
+    CHECK(st.operand(A, (uint64_t)M * K * 4, "dense_fused_i8 A", kIn));
+    CHECK(st.operand(B, (uint64_t)K * N * 4, "dense_fused_i8 B", kIn));
+    CHECK(st.operand(C, (uint64_t)M * N * 4, "dense_fused_i8 C", kOut));
+    CHECK(st.commit());
     const size_t wsb = ane_hip_dense_fused_i8_workspace_size(M, N, K);
     Lease lease;
     CHECK(get_workspace(s, wsb, lease));
     t_ran_fused = true;
-    return hip_status(ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, lease.ptr, wsb, s),
-                      "dense_fused_i8");
+    return st.finish(hip_status(
+        ane_hip_dense_fused_i8(M, N, K, scale, relu & 1, A, B, C, nullptr, lease.ptr, wsb, s), "dense_fused_i8"));
 }
 
 // 0x61 / 0x62 / 0x63 [flags:u8][M][N][K][lda][ldb][ldc:u32][alpha:f32][beta:f32][A][B][C]
@@ -357,6 +462,7 @@ int op_cblas_igemm(Reader& r, hipStream_t s, int variant) {
     if (ldc < N) return fail(ANE_ERR_INVALID_ARG, "%s: ldc %u < N %u (overlapping output rows)", nm, ldc, N);
     if ((uintptr_t)C & 3) return fail(ANE_ERR_INVALID_ARG, "%s: C must be 4-byte aligned", nm);
     const uint64_t Ke = (uint64_t)(K / 64) * 64;
+    Stager st(s);
     if (Ke) {
         uint64_t a_ext;
         if (!(flags & 1)) {
@@ -368,16 +474,18 @@ int op_cblas_igemm(Reader& r, hipStream_t s, int variant) {
             a_ext = mx + Ke;
         }
         const uint64_t b_ext = (flags & 2) ? (uint64_t)(N - 1) * ldb + Ke : (Ke - 1) * ldb + N;
-        CHECK(check_range(A, a_ext, nm, false, nullptr));
-        CHECK(check_range(B, b_ext, nm, false, nullptr));
+        CHECK(st.operand(A, a_ext, nm, kIn));
+        CHECK(st.operand(B, b_ext, nm, kIn));
     }
-    CHECK(check_range(C, ((uint64_t)(M - 1) * ldc + N) * 4, nm, false, nullptr));
+    // C is read too (beta, and the gaps between rows when ldc > N)
+    CHECK(st.operand(C, ((uint64_t)(M - 1) * ldc + N) * 4, nm, kInOut));
+    CHECK(st.commit());
     const size_t wsb = ane_hip_cblas_igemm_workspace_size(M, N, K);
     Lease lease;
     CHECK(get_workspace(s, wsb, lease));
-    return hip_status(ane_hip_cblas_igemm(variant, ANE_IGEMM_REFERENCE, flags, M, N, K, lda, ldb, ldc, alpha, beta,
-                                          A, B, C, lease.ptr, wsb, s),
-                      nm);
+    return st.finish(hip_status(ane_hip_cblas_igemm(variant, ANE_IGEMM_REFERENCE, flags, M, N, K, lda, ldb, ldc,
+                                                    alpha, beta, A, B, C, lease.ptr, wsb, s),
+                                nm));
 }
 
 // The decode-step handlers (bytecode_interpreter.s:6508-7009).  Their loops
@@ -393,10 +501,12 @@ int op_rms_norm(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "rms_norm_fp32 record truncated");
     if (dim == 0) return ANE_OK;
     if (dim % 16) return fail(ANE_ERR_INVALID_ARG, "rms_norm_fp32: dim %u is not a multiple of 16", dim);
-    CHECK(check_range(in, (uint64_t)dim * 4, "rms_norm_fp32 in", false, nullptr));
-    CHECK(check_range(w, (uint64_t)dim * 4, "rms_norm_fp32 weight", false, nullptr));
-    CHECK(check_range(out, (uint64_t)dim * 4, "rms_norm_fp32 out", false, nullptr));
-    return hip_status(ane_hip_rms_norm_fp32(1, dim, eps, in, w, out, s), "rms_norm_fp32");
+    Stager st(s);
+    CHECK(st.operand(in, (uint64_t)dim * 4, "rms_norm_fp32 in", kIn));
+    CHECK(st.operand(w, (uint64_t)dim * 4, "rms_norm_fp32 weight", kIn));
+    CHECK(st.operand(out, (uint64_t)dim * 4, "rms_norm_fp32 out", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_rms_norm_fp32(1, dim, eps, in, w, out, s), "rms_norm_fp32"));
 }
 
 // 0x54 [count:u32][in][out]  (:6618-6621)
@@ -407,9 +517,11 @@ int op_silu(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "silu_fp32 record truncated");
     if (count == 0) return ANE_OK;
     if (count % 16) return fail(ANE_ERR_INVALID_ARG, "silu_fp32: count %u is not a multiple of 16", count);
-    CHECK(check_range(in, (uint64_t)count * 4, "silu_fp32 in", false, nullptr));
-    CHECK(check_range(out, (uint64_t)count * 4, "silu_fp32 out", false, nullptr));
-    return hip_status(ane_hip_silu_fp32(count, in, out, s), "silu_fp32");
+    Stager st(s);
+    CHECK(st.operand(in, (uint64_t)count * 4, "silu_fp32 in", kIn));
+    CHECK(st.operand(out, (uint64_t)count * 4, "silu_fp32 out", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_silu_fp32(count, in, out, s), "silu_fp32"));
 }
 
 // 0x55 [dim:u32][pos:u32][theta:f32][in][out]  (:6715-6720); pairs dim/2
@@ -422,9 +534,11 @@ int op_rope(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "rope_fp32 record truncated");
     const uint64_t n = (uint64_t)(dim / 2) * 2;
     if (n == 0) return ANE_OK;
-    CHECK(check_range(in, n * 4, "rope_fp32 in", false, nullptr));
-    CHECK(check_range(out, n * 4, "rope_fp32 out", false, nullptr));
-    return hip_status(ane_hip_rope_fp32(1, dim, pos, theta, in, out, s), "rope_fp32");
+    Stager st(s);
+    CHECK(st.operand(in, n * 4, "rope_fp32 in", kIn));
+    CHECK(st.operand(out, n * 4, "rope_fp32 out", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_rope_fp32(1, dim, pos, theta, in, out, s), "rope_fp32"));
 }
 
 // 0x56 [dim:u32][in][out]  (:6914-6917)
@@ -435,9 +549,11 @@ int op_softmax(Reader& r, hipStream_t s) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "softmax_fp32 record truncated");
     if (dim == 0) return ANE_OK;
     if (dim % 16) return fail(ANE_ERR_INVALID_ARG, "softmax_fp32: dim %u is not a multiple of 16", dim);
-    CHECK(check_range(in, (uint64_t)dim * 4, "softmax_fp32 in", false, nullptr));
-    CHECK(check_range(out, (uint64_t)dim * 4, "softmax_fp32 out", false, nullptr));
-    return hip_status(ane_hip_softmax_fp32(1, dim, in, out, s), "softmax_fp32");
+    Stager st(s);
+    CHECK(st.operand(in, (uint64_t)dim * 4, "softmax_fp32 in", kIn));
+    CHECK(st.operand(out, (uint64_t)dim * 4, "softmax_fp32 out", kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(ane_hip_softmax_fp32(1, dim, in, out, s), "softmax_fp32"));
 }
 
 // 0x58, 0x75-0x79 [M:u32][K:u32][x][W][y]: the other weight formats' GEMVs
@@ -467,10 +583,12 @@ int op_q_gemv(Reader& r, hipStream_t s, const QGemv& f) {
     if (!r.ok) return fail(ANE_ERR_TRUNCATED, "%s record truncated", f.name);
     if (M == 0) return ANE_OK;
     const uint64_t nsb = K / f.values;
-    CHECK(check_range(x, nsb * f.values * 4, f.name, false, nullptr));
-    CHECK(check_range(W, (uint64_t)M * nsb * f.bytes, f.name, false, nullptr));
-    CHECK(check_range(y, (uint64_t)M * 4, f.name, false, nullptr));
-    return hip_status(f.fn(M, K, x, W, y, s), f.name);
+    Stager st(s);
+    CHECK(st.operand(x, nsb * f.values * 4, f.name, kIn));
+    CHECK(st.operand(W, (uint64_t)M * nsb * f.bytes, f.name, kIn));
+    CHECK(st.operand(y, (uint64_t)M * 4, f.name, kOut));
+    CHECK(st.commit());
+    return st.finish(hip_status(f.fn(M, K, x, W, y, s), f.name));
 }
 
 // 0x7C / 0x7D [n_rows:u32][dim:u32][table][indices][out]
@@ -488,9 +606,9 @@ int op_get_rows(Reader& r, hipStream_t s, bool q4) {
     const uint64_t nb = dim >> 5;
     if (n == 0 || nb == 0) return ANE_OK;
     if (dim & 31) return fail(ANE_ERR_INVALID_ARG, "%s: dim %u is not a multiple of 32", name, dim);
-    CHECK(check_range(idx, (uint64_t)n * 4, name, false, nullptr));
-    CHECK(check_range(out, (uint64_t)n * nb * 32 * 4, name, false, nullptr));
-    CHECK(check_range(table, 1, name, false, nullptr));
+    CHECK(check_range(idx, (uint64_t)n * 4, name, staging_on(), nullptr));
+    CHECK(check_range(out, (uint64_t)n * nb * 32 * 4, name, staging_on(), nullptr));
+    CHECK(check_range(table, 1, name, staging_on(), nullptr));
     std::vector<uint32_t> h(n);
     if (hipStreamSynchronize(s) != hipSuccess || hipMemcpy(h.data(), idx, (size_t)n * 4, hipMemcpyDefault) != hipSuccess) {
         (void)hipGetLastError();
@@ -499,11 +617,15 @@ int op_get_rows(Reader& r, hipStream_t s, bool q4) {
     uint32_t mx = 0;
     for (uint32_t v : h) mx = v > mx ? v : mx;
     const uint64_t rb = nb * (q4 ? 18 : 34);
-    CHECK(check_range(table, ((uint64_t)mx + 1) * rb, name, false, nullptr));
+    Stager st(s);
+    CHECK(st.operand(table, ((uint64_t)mx + 1) * rb, name, kIn));
+    CHECK(st.operand(idx, (uint64_t)n * 4, name, kIn));
+    CHECK(st.operand(out, (uint64_t)n * nb * 32 * 4, name, kOut));
+    CHECK(st.commit());
     const uint64_t rows = (uint64_t)mx + 1;
-    return hip_status(q4 ? ane_hip_get_rows_q4_0(n, dim, table, rows, idx, out, s)
-                         : ane_hip_get_rows_q8_0(n, dim, table, rows, idx, out, s),
-                      name);
+    return st.finish(hip_status(q4 ? ane_hip_get_rows_q4_0(n, dim, table, rows, idx, out, s)
+                                   : ane_hip_get_rows_q8_0(n, dim, table, rows, idx, out, s),
+                                name));
 }
 
 int run(const uint8_t* data, size_t size, hipStream_t s) {
@@ -566,8 +688,12 @@ extern "C" void stream_exec(const uint8_t* data, size_t size) {
         (void)hipGetLastError();
         if (st == ANE_OK) st = fail(ANE_ERR_HIP, "hipStreamSynchronize failed");
     }
-    if (t_ran_fused && ane_hip_grid_wait_status(s) != ANE_OK && st == ANE_OK)
-        st = fail(ANE_ERR_HIP, "dense_fused_i8: the quantizer's grid-wide wait gave up; C is not valid");
+    if (t_ran_fused) {
+        const int ws = ane_hip_grid_wait_status(s);
+        if (ws != ANE_OK && st == ANE_OK)
+            st = fail(ws, "dense_fused_i8: the quantizer's grid-wide wait gave up or saw another launch's "
+                          "arrivals; C is not valid");
+    }
     t_status = st;
 }
 
@@ -584,6 +710,8 @@ extern "C" const char* ane_last_error_message(void) {
 }
 
 extern "C" void ane_set_stream(void* stream) { t_stream = (hipStream_t)stream; }
+
+extern "C" void ane_set_host_staging(int mode) { t_staging = mode < 0 ? -1 : (mode ? 1 : 0); }
 
 extern "C" int ane_hip_device_check(void) {
     int n = 0;

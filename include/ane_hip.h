@@ -47,7 +47,9 @@ enum ane_status {
     ANE_ERR_TRUNCATED = 5,        /* record runs past the end of the stream   */
     ANE_ERR_HIP = 6,              /* a HIP runtime call failed                */
     ANE_ERR_NO_DEVICE = 7,        /* no gfx950 device                         */
-    ANE_ERR_WORKSPACE = 8         /* workspace pointer null or too small      */
+    ANE_ERR_WORKSPACE = 8,        /* workspace pointer null or too small      */
+    ANE_ERR_GRID_WAIT = 9         /* dense_fused_i8's grid-wide wait failed:  */
+                                  /* its outputs are not valid                */
 };
 
 /* Opcodes served by this build (values identical to the reference's
@@ -93,6 +95,18 @@ const char* ane_last_error_message(void);
 
 /* Stream used by stream_exec on this thread (void* = hipStream_t). */
 void ane_set_stream(void* stream);
+
+/* Host staging for stream_exec on this thread: 1 on, 0 off, -1 (the
+ * default) follows the environment variable ANE_HOST_STAGING (on when set
+ * to anything but "" or "0").  With staging on, an operand in plain host
+ * memory (malloc, aligned_alloc, a stack array: the reference's callers,
+ * tests/test_mnist_i8.cpp) is copied to a device staging buffer, the record
+ * runs on the copy, and its outputs are copied back before the record
+ * returns; records with staged operands are synchronous also under
+ * ane_stream_exec_async.  With staging off, such an operand is refused
+ * (ANE_ERR_BAD_POINTER).  Device memory is never staged.  No reference
+ * counterpart: the reference reads and writes host memory directly. */
+void ane_set_host_staging(int mode);
 
 /* stream_exec without the final synchronisation and with an explicit
  * stream; returns the status instead of storing it.  Host-memory scalar
@@ -148,20 +162,35 @@ int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
 /* The operand quantizer of dense_fused_i8 runs, for large shapes (K % 128
  * == 0, N % 64 == 0, at least 12 MiB of operands), as one launch whose
  * workgroups (one per CU) exchange their maxima through a grid-wide wait.
- * Every workgroup is resident at once, so the wait ends; it is bounded all
- * the same, and a workgroup that gives up leaves C invalid and records it.
- * Two such launches must not run at once on one device (each needs every
- * CU): calls on different streams are ordered by the library (a call waits
- * for the previous call's launch), and under stream capture the route is
- * taken only on the stream of the previous call.  Replays of captured
- * graphs are not ordered by the library: a caller replaying graphs that
- * hold this op on several streams at once orders them itself.
+ * Outside stream capture it is a cooperative launch: the runtime starts it
+ * only with every workgroup resident, or refuses it and the two-pass route
+ * (no wait) runs instead.  Under capture it is a plain launch.  Two such
+ * launches must not run at once on one device (each needs every CU): calls
+ * on different streams are ordered by the library (a call waits for the
+ * previous call's launch), and under capture the route is taken only on the
+ * stream of the previous call.  Replays of captured graphs are not ordered
+ * by the library: a replay that overlaps another replay or an eager call on
+ * another stream makes the waits of both either time out or count each
+ * other's arrivals.  Neither is silent: the wait is bounded (2 s by
+ * default), every launch is tagged, and a counter completed by arrivals of
+ * two launches is detected; the outputs of such a call are not valid, and
+ * the status calls below report it (ANE_ERR_GRID_WAIT).
+ *
+ * ane_hip_dense_fused_i8_status(workspace, stream) synchronizes the stream
+ * and reports the last quantize call made with this workspace: every such
+ * call writes a wait record into the workspace (one word per workgroup),
+ * which this reads; it also reads, and clears, the device's record of
+ * counters completed by mixed arrivals, which a call whose wait another
+ * launch completed cannot see in its own record.  ANE_ERR_INVALID_ARG: no
+ * quantize call has written this workspace.
  * ane_hip_grid_wait_status(stream) synchronizes the stream and returns
- * ANE_ERR_HIP (and clears the record) if such a launch on the current
- * device gave up since the last call, else ANE_OK; stream_exec checks it
- * itself.
+ * ANE_ERR_GRID_WAIT (and clears the device's record) if any such launch on
+ * the current device gave up or saw mixed arrivals since the last call, else
+ * ANE_OK; stream_exec checks it itself.  After a failure the device's
+ * counters are returned to rest once the device is idle.
  * ane_hip_set_grid_wait_limit sets the bound, in ticks of the 100 MHz
  * realtime counter, for launches made after it (0: the default, 2 s). */
+int ane_hip_dense_fused_i8_status(const void* workspace, void* stream);
 int ane_hip_grid_wait_status(void* stream);
 void ane_hip_set_grid_wait_limit(uint64_t ticks);
 

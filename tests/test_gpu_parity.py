@@ -307,20 +307,29 @@ def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
-@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny"])
-@pytest.mark.parametrize("M,N,K", [(129, 257, 1000), (256, 512, 2048), (256, 2048, 2048)])
+_SPECIAL = [(c, *shape) for c in ("a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny")
+            for shape in ((129, 257, 1000), (256, 512, 2048), (256, 2048, 2048))]
+_SPECIAL += [("a_nan", 5000, 64, 4096), ("b_inf", 5000, 64, 4096), ("a_neg_inf", 5000, 64, 4096)]
+
+
+@pytest.mark.parametrize("case,M,N,K", _SPECIAL)
 def test_dense_fused_special_operands(ane, oracle, case, M, N, K):
     """The fused max|x| and quantize passes on operands the quantizer
     special-cases: a NaN or an infinity (NaN or infinite per-tensor scale),
     an all-zero tensor (the zero guard) and a tensor of denormals and signed
     zeros only (127 / amax overflows to +inf, so 0 * inf reaches the
     quantizer).  256 x 2048 x 2048 (18 MiB of operands) takes the one-launch
-    resident quantizer, the others the two-pass one."""
+    resident quantizer, the others the two-pass one.  5000 x 64 x 4096 takes
+    the resident quantizer with A's share larger than LDS and registers hold
+    (its rest re-read after the B tiles on the exact pack4 route that a
+    non-finite scale selects); the NaN sits in that re-read rest."""
     import torch
 
     A, B = data.gemm_inputs(M, N, K, seed=M + K)
     if case == "a_nan":
         A[M // 2, K // 3] = np.nan
+        if M == 5000:  # in workgroup 0's re-read rest: float4 15232 + 3 * 512 onward of its share
+            A.ravel()[4 * (15232 + 3 * 512) + 7] = np.nan
     elif case == "b_inf":
         B[K - 1, N // 2] = np.inf
     elif case == "a_neg_inf":
@@ -369,8 +378,10 @@ def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
     resident quantizer (1 row; 5000 rows, whose workgroup shares run past
     LDS and registers), the last the two-pass one (K % 128 != 0).
     Workspace layout (gemm_i8.hip, fused_layout): scales at 0, the partial
-    maxima at 256 (2 x 1024 uint32), qA at 8448, qBt after qA rounded up to
-    256 bytes; Kp = ceil(K / 128) * 128."""
+    maxima at 256 (2 x 1024 uint32) and the wait record after them
+    (1 + 1024 uint32), qA at 12800, qBt after qA rounded up to 256 bytes;
+    Kp = ceil(K / 128) * 128.  The wait record holds 0 entries on the
+    two-pass route and one zero per workgroup on the resident one."""
     import torch
 
     A, B = data.gemm_inputs(M, N, K, seed=M + N + 5)
@@ -385,7 +396,11 @@ def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
     sc = zeros(2, torch.float32)
     ane.dense_fused_i8_quantize(M, N, K, dev(A), dev(B), ws, scales_out=sc)
     w = host(ws)
-    off_a = 8448
+    rec = w[256 + 8192: 256 + 8192 + 4 * 1025].view(np.uint32)
+    resident = K % 128 == 0 and N % 64 == 0 and 4 * (M * K + K * N) >= 12 << 20
+    assert (rec[0] > 0) == resident and rec[0] <= 1024
+    assert not rec[1: 1 + rec[0]].any()
+    off_a = 12800
     off_b = off_a + -(-(M * Kp) // 256) * 256
     got_a = w[off_a: off_a + M * Kp].view(np.int8).reshape(M, Kp)
     got_b = w[off_b: off_b + N * Kp].view(np.int8).reshape(N, Kp)
@@ -397,9 +412,10 @@ def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
 def test_dense_fused_grid_wait_limit(ane, oracle):
     """The resident quantizer's bounded grid-wide wait, forced from the host
     to a one-tick limit: every workgroup still finishes, and a launch whose
-    workgroups gave up is reported by stream_exec (C is then not valid);
-    one that did not is exact.  Restored to the default, the same record is
-    exact and reports nothing."""
+    workgroups gave up is reported (C is then not valid) by stream_exec, by
+    the kernel ABI's wait record (ane_hip_dense_fused_i8_status) and by the
+    Python wrapper, each with ANE_ERR_GRID_WAIT; one that did not is exact.
+    Restored to the default, the same calls are exact and report nothing."""
     import torch
 
     M, N, K = 256, 2048, 2048
@@ -412,20 +428,65 @@ def test_dense_fused_grid_wait_limit(ane, oracle):
     dA, dB = dev(A), dev(B)
     lib = ane.lib()
     C = zeros(M * N, torch.float32)
+    wsb = ane.dense_fused_i8_workspace_size(M, N, K)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    stream = ane._stream_handle(None)
+    grid_wait = 9  # ANE_ERR_GRID_WAIT
     try:
         lib.ane_hip_set_grid_wait_limit(1)
+        # opcode boundary
         try:
             ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dA, dB, C))
         except ane.AneError as e:
-            assert e.status == 6 and "grid-wide wait" in str(e)  # ANE_ERR_HIP
+            assert e.status == grid_wait and "grid-wide wait" in str(e)
         else:
             assert_f32_identical(host(C).reshape(M, N), ref)
+        # kernel ABI: the wait record in the caller's workspace
+        C.zero_()
+        assert lib.ane_hip_dense_fused_i8(M, N, K, 1.0, 1, ane._p(dA), ane._p(dB), ane._p(C), 0, ane._p(ws),
+                                          wsb, stream) == 0
+        st = lib.ane_hip_dense_fused_i8_status(ane._p(ws), stream)
+        assert st in (0, grid_wait)
+        if st == 0:
+            assert_f32_identical(host(C).reshape(M, N), ref)
+        assert lib.ane_hip_grid_wait_status(stream) == 0  # the status call cleared the device record
+        # Python wrapper: checks after the call by default
+        C.zero_()
+        try:
+            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws)
+        except ane.AneError as e:
+            assert e.status == grid_wait
+        else:
+            assert_f32_identical(host(C).reshape(M, N), ref)
+        assert lib.ane_hip_grid_wait_status(stream) == 0
     finally:
         lib.ane_hip_set_grid_wait_limit(0)
-    C.zero_()
-    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dA, dB, C))
-    assert lib.ane_hip_grid_wait_status(ane._stream_handle(None)) == 0
-    assert_f32_identical(host(C).reshape(M, N), ref)
+    for how in ("stream_exec", "abi", "python"):
+        C.zero_()
+        if how == "stream_exec":
+            ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dA, dB, C))
+        elif how == "abi":
+            assert lib.ane_hip_dense_fused_i8(M, N, K, 1.0, 1, ane._p(dA), ane._p(dB), ane._p(C), 0, ane._p(ws),
+                                              wsb, stream) == 0
+            assert lib.ane_hip_dense_fused_i8_status(ane._p(ws), stream) == 0
+        else:
+            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws)
+        assert lib.ane_hip_grid_wait_status(stream) == 0
+        assert_f32_identical(host(C).reshape(M, N), ref)
+
+
+def test_dense_fused_status_unwritten_workspace(ane):
+    """ane_hip_dense_fused_i8_status on a workspace no quantize call wrote
+    (its record count word past the largest grid) is ANE_ERR_INVALID_ARG;
+    a misaligned or null workspace is ANE_ERR_WORKSPACE."""
+    import torch
+
+    ws = torch.full((16384,), 0xFF, dtype=torch.uint8, device="cuda")
+    lib = ane.lib()
+    stream = ane._stream_handle(None)
+    assert lib.ane_hip_dense_fused_i8_status(ane._p(ws), stream) == 1
+    assert lib.ane_hip_dense_fused_i8_status(ane._p(ws) + 4, stream) == 8
+    assert lib.ane_hip_dense_fused_i8_status(0, stream) == 8
 
 
 def test_dense_fused_resident_two_streams(ane, oracle):
@@ -449,9 +510,9 @@ def test_dense_fused_resident_two_streams(ane, oracle):
     torch.cuda.synchronize()
     for rep in range(3):
         for (dA, dB, C, ws), st in zip(bufs, streams):
-            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws, stream=st)
-        for st in streams:
-            st.synchronize()
+            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws, stream=st, check_wait=False)
+        for (dA, dB, C, ws), st in zip(bufs, streams):
+            ane.dense_fused_i8_status(ws, stream=st)
             assert ane.lib().ane_hip_grid_wait_status(ane._stream_handle(st)) == 0
         for (dA, dB, C, ws), ref in zip(bufs, refs):
             assert_f32_identical(host(C).reshape(M, N), ref)
