@@ -110,6 +110,24 @@ def build_ggml_adapter(verbose: bool = False) -> Path:
     return GGML_TEST_LIB
 
 
+DISPATCH_SRC = ROOT / "tests" / "cpp" / "mnist_i8_dispatch.cpp"
+DISPATCH_BIN = ROOT / "tests" / "cpp" / "mnist_i8_dispatch"
+
+
+def build_dispatch_program(verbose: bool = False) -> Path:
+    """tests/cpp/mnist_i8_dispatch: the reference's MNIST-i8 call sequence
+    written against include/ane/ane.hpp, linked against libane_amd.so (a GPU
+    test runs it as a child process)."""
+    tmp = DISPATCH_BIN.with_suffix(".tmp")
+    _run(["g++", "-std=c++20", "-O1", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+          f"-I{ROOT / 'include'}", str(DISPATCH_SRC), "-o", str(tmp), f"-L{PKG}", "-lane_amd",
+          "-Wl,-rpath,$ORIGIN/../../ane_amd", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"])
+    os.replace(tmp, DISPATCH_BIN)
+    if verbose:
+        print(f"built {DISPATCH_BIN}")
+    return DISPATCH_BIN
+
+
 def build_oracle(verbose: bool = False) -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     out = ROOT / "oracle" / "libane_oracle.so"
@@ -123,6 +141,7 @@ def build_all(verbose: bool = False) -> None:
     build_library(verbose)
     build_peaks(verbose)
     build_ggml_adapter(verbose)
+    build_dispatch_program(verbose)
 
 
 if __name__ == "__main__":
