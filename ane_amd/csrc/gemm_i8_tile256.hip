@@ -190,9 +190,12 @@ __device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Fra
 // global_store).  Inline assembly, as no builtin sets the bit on a plain
 // store.  The compiler does not count these stores in vmcnt; since vector
 // memory operations complete in issue order, uncounted stores can only
-// make its later vmcnt waits stricter, never release one early.
+// make its later vmcnt waits stricter, never release one early.  A VALU
+// write to the data registers of a store wider than 8 bytes needs one wait
+// state after the store; the compiler's hazard recognizer does not see
+// inside the asm, so the s_nop provides it.
 __device__ __forceinline__ void store16_sc1(uint32_t* dst, v4i v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" ::"v"(dst), "v"(v) : "memory");
 }
 
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu)))

@@ -64,7 +64,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--eager", action="store_true",
                     help="launch every step from Python instead of replaying the steps as one HIP graph")
     ap.add_argument("--only", choices=["gemm", "fused", "q8g", "q8r", "copy", "decode", "qformats", "ceilings",
-                             "mulmat", "msweep", "mnist", "mfma_loop", "vendor_int8"],
+                             "mulmat", "msweep", "mnist", "mfma_loop", "vendor_int8", "igemm", "rotating"],
                     default=None,
                     help="profiling mode: launch only this workload --steps times, print timing")
     return ap.parse_args()
@@ -162,14 +162,16 @@ def main() -> int:
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     scales = torch.empty(2, dtype=torch.float32, device=dev)
 
+    # the wait record of the quantizer is checked once after each timed
+    # section (ane_amd.dense_fused_i8_status), not after every call
     def fused(st=stream):
-        ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st)
+        ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st, check_wait=False)
 
     def gemm_phase(st=stream):
         ane_amd.dense_fused_i8_gemm(M, N, K, 1.0, True, C, ws, stream=st)
 
     def quant_phase(st=stream):
-        ane_amd.dense_fused_i8_quantize(M, N, K, A, B, ws, stream=st)
+        ane_amd.dense_fused_i8_quantize(M, N, K, A, B, ws, stream=st, check_wait=False)
 
     ops = 2.0 * M * N * K
 
@@ -190,6 +192,12 @@ def main() -> int:
         return 0
     if args.only == "mnist":
         print(json.dumps(bench_mnist(args)), flush=True)
+        return 0
+    if args.only == "igemm":
+        print(json.dumps(bench_igemm(args)), flush=True)
+        return 0
+    if args.only == "rotating":
+        print(json.dumps(headline_rotating(args, M, N, K, ops)), flush=True)
         return 0
     if args.only == "mulmat":
         print(json.dumps(bench_mul_mat(args)), flush=True)
@@ -245,21 +253,27 @@ def main() -> int:
     # ------------------------------------------------------------ headline
     # The K timed steps are K full dense_fused_i8 calls (both quantize passes
     # and the contraction, on fresh fp32 operands each time), captured once
-    # into a HIP graph and replayed between two synchronisations, so the
-    # host's per-call launch work stays outside the timed region; the wall
-    # clock brackets the replay.  The warmup replays a graph of W steps and
-    # then the timed graph once, untimed: a graph's first replay carries
-    # one-time setup (measured ~5 us per step of a 100-step graph).  --eager
-    # launches the K calls from Python instead.
+    # into a HIP graph.  The warmup replays a graph of W steps and then the
+    # timed graph once, untimed (a graph's first replay carries one-time
+    # setup).  The timed replay is bracketed by synchronisations, and its
+    # time is read from HIP events recorded on the replay stream just before
+    # and after it: all K steps of GPU work, without the host's launch and
+    # synchronisation latency (the wall clock around the same replay is
+    # reported too).  --eager launches the K calls from Python instead,
+    # between the same two events.
     log(f"dense_fused_i8 M={M} N={N} K={K}: warmup {args.warmup}, steps {args.steps}"
         f"{' (eager launches)' if args.eager else ' (one HIP graph of the steps)'}")
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     if args.eager:
         for _ in range(args.warmup):
             fused()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        ev0.record(stream)
         for _ in range(args.steps):
             fused()
+        ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     else:
@@ -279,13 +293,19 @@ def main() -> int:
             gs.synchronize()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
+            ev0.record(gs)
             timed.replay()
+            ev1.record(gs)
             gs.synchronize()
             torch.cuda.synchronize()
             wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
+    ane_amd.dense_fused_i8_status(ws)  # every quantize of the timed steps met its grid-wide wait
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    wall_ms_per_step = wall * 1e3 / args.steps
     value = ops / (ms_per_step * 1e-3) / 1e12
-    log(f"whole op: {ms_per_step * 1e3:.2f} us/step = {value:.1f} TOPS")
+    log(f"whole op: {ms_per_step * 1e3:.2f} us/step = {value:.1f} TOPS "
+        f"(wall clock around the replay: {wall_ms_per_step * 1e3:.2f} us/step)")
+    rotating = headline_rotating(args, M, N, K, ops)
 
     # ------------------------------------------------------------ kernel roofline
     # The contraction's launch duration: kernel_reps launches captured into
@@ -306,6 +326,7 @@ def main() -> int:
         if e1 is not None:
             e1.record(stream)
     torch.cuda.synchronize()
+    ane_amd.dense_fused_i8_status(ws)
     in_op = sorted(e0.elapsed_time(e1) for e0, e1 in marks)
     in_op_ms = sum(in_op) / len(in_op)
     gemm_ms = graph_time(gemm_phase, args.kernel_reps)
@@ -366,6 +387,7 @@ def main() -> int:
     qformats = bench_qformats(args) if not args.no_q8 else None
     m_sweep = bench_m_sweep(args, N, K) if not args.no_sweep else None
     mnist = bench_mnist(args) if not args.no_sweep else None
+    igemm = bench_igemm(args) if not args.no_sweep else None
     decode = bench_decode(args) if not args.no_decode else None
 
     # ------------------------------------------------------------ CPU baseline
@@ -386,9 +408,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic: A, B ~ N(0,1) fp32 (seeded), quantized per tensor on the GPU each step",
-        "timing": ("eager launches from Python" if args.eager else
+        "timing": ("eager launches from Python between HIP events" if args.eager else
                    "the K steps captured as one HIP graph, replayed once untimed after the warmup and "
-                   "then once between synchronisations"),
+                   "then once between synchronisations; ms_per_step from HIP events recorded on the "
+                   "replay stream around that replay"),
+        "wall_ms_per_step": round(wall_ms_per_step, 5),
+        "rotating_operands": rotating,
         "config": {"workload": f"dense_fused_i8 M={M} N={N} K={K} scale=1.0 relu (config 2)",
                    "M": M, "N": N, "K": K},
         "roofline": roofline,
@@ -399,11 +424,64 @@ def main() -> int:
         "other_formats_gemv": qformats,
         "dense_fused_m_sweep": m_sweep,
         "mnist_mlp_config1": mnist,
+        "cblas_igemm_1024": igemm,
         "decode_config5": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def headline_rotating(args, M, N, K, ops) -> dict:
+    """The headline step again with the operands rotating over three A/B
+    sets (3 x 128 MiB of fp32 at 4096^3, more than the 256 MB Infinity
+    Cache), each set with its own output and workspace, so the quantize
+    phase reads operands that the previous steps did not leave in the
+    cache.  Same graph capture and HIP-event timing as the headline."""
+    import torch
+
+    import ane_amd
+
+    dev = torch.device("cuda:0")
+    nsets = 3
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    wsb = ane_amd.dense_fused_i8_workspace_size(M, N, K)
+    sets = [(torch.randn((M, K), generator=g, device=dev), torch.randn((K, N), generator=g, device=dev),
+             torch.empty((M, N), device=dev), torch.empty(wsb, dtype=torch.uint8, device=dev))
+            for _ in range(nsets)]
+    steps = max(args.steps, nsets)
+    steps -= steps % nsets
+    gs = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(gs):
+        for A, B, C, ws in sets:
+            ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=gs, check_wait=False)
+        gs.synchronize()
+        with torch.cuda.graph(graph, stream=gs):
+            for i in range(steps):
+                A, B, C, ws = sets[i % nsets]
+                ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=gs, check_wait=False)
+        graph.replay()
+        gs.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(gs)
+        graph.replay()
+        e1.record(gs)
+        gs.synchronize()
+    for *_, ws in sets:
+        ane_amd.dense_fused_i8_status(ws)
+    ms = e0.elapsed_time(e1) / steps
+    log(f"whole op, operands rotating over {nsets} sets: {ms * 1e3:.2f} us/step = {ops / ms / 1e9:.1f} TOPS")
+    res = {"us_per_step": round(ms * 1e3, 3), "TOPS": round(ops / ms / 1e9, 2), "sets": nsets,
+           "steps": steps, "operand_bytes_per_set": 4 * (M * K + K * N),
+           "how": ("A, B (fp32), C and the workspace rotate over 3 sets, step i using set i % 3, one HIP "
+                   "graph replayed between HIP events")}
+    del sets, graph
+    torch.cuda.empty_cache()
+    return res
 
 
 def profile_q8(args, stream) -> int:
@@ -705,8 +783,8 @@ def bench_mnist(args) -> dict:
     ws2 = torch.empty(ane_amd.dense_fused_i8_workspace_size(50, 10, 128), dtype=torch.uint8, device=dev)
 
     def fwd(st):
-        ane_amd.dense_fused_i8(50, 128, 784, 1.0, True, xd, w1d, h, workspace=ws1, stream=st)
-        ane_amd.dense_fused_i8(50, 10, 128, 1.0, False, h, w2d, o, workspace=ws2, stream=st)
+        ane_amd.dense_fused_i8(50, 128, 784, 1.0, True, xd, w1d, h, workspace=ws1, stream=st, check_wait=False)
+        ane_amd.dense_fused_i8(50, 10, 128, 1.0, False, h, w2d, o, workspace=ws2, stream=st, check_wait=False)
 
     graph_us = graph_time(fwd, 50) * 1e3
     o_graph = o.clone()
@@ -927,15 +1005,44 @@ def bench_m_sweep(args, N, K) -> dict:
         ws = torch.empty(ane_amd.dense_fused_i8_workspace_size(M, N, K), dtype=torch.uint8, device="cuda")
 
         def fn(st):
-            ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st)
+            ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=st, check_wait=False)
 
         ms = graph_time(fn, 20)
+        ane_amd.dense_fused_i8_status(ws)
         ops = 2.0 * M * N * K
         alg = 4.0 * (M * K + K * N + M * N)
         out[f"M{M}"] = {"us": round(ms * 1e3, 2), "TOPS": round(ops / ms / 1e9, 2),
                         "GB_s_fp32_io": round(alg / ms / 1e6, 1)}
         log(f"dense_fused_i8 M={M}: {ms * 1e3:.2f} us = {ops / ms / 1e9:.1f} TOPS")
     return {"workload": "config 2 M sweep: dense_fused_i8 M x 4096 x 4096, whole op", "shapes": out}
+
+
+def bench_igemm(args) -> dict:
+    """cblas_igemm (opcode 0x61, the handler's arithmetic) at 1024^3 with
+    transB: int8 A (1024 x 1024), int8 B stored N x K, fp32 C, alpha 1,
+    beta 0, on the kernel ABI, HIP-graph replayed."""
+    import torch
+
+    import ane_amd
+
+    M = N = K = 1024
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    A = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+    B = torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8)
+    C = torch.zeros((M, N), device="cuda", dtype=torch.float32)
+    ws = torch.empty(max(1, int(ane_amd.lib().ane_hip_cblas_igemm_workspace_size(M, N, K))), dtype=torch.uint8,
+                     device="cuda")
+
+    def fn(st):
+        ane_amd.cblas_igemm("igemm", 2, M, N, K, K, K, N, 1.0, 0.0, A, B, C, workspace=ws, stream=st)
+
+    ms = graph_time(fn, 50)
+    ops = 2.0 * M * N * K
+    log(f"cblas_igemm 1024^3 transB: {ms * 1e3:.2f} us = {ops / ms / 1e9:.1f} TOPS")
+    return {"workload": "cblas_igemm (0x61) 1024^3, transB, alpha 1, beta 0, handler arithmetic",
+            "us": round(ms * 1e3, 3), "TOPS": round(ops / ms / 1e9, 2),
+            "frac_int8_peak": round(ops / ms / 1e9 / PEAK_INT8_TOPS, 4)}
 
 
 def _host_threads() -> int:
