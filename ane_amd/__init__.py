@@ -116,6 +116,7 @@ EXPORTS = (
     "ane_hip_get_rows_q8_0",
     "ane_hip_get_rows_q4_0",
     "ane_hip_q8_0_mul_mat_workspace_size",
+    "ane_hip_q8_0_mul_mat_workspace_size_n",
     "ane_hip_q8_0_mul_mat",
     "ane_hip_q8_0_mul_mat_noalloc_max_bytes",
     "ane_hip_q8_0_mul_mat_noalloc",
@@ -204,6 +205,7 @@ _SIGS: dict[str, tuple[Any, list[Any]]] = {
     "ane_hip_get_rows_q8_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
     "ane_hip_get_rows_q4_0": (_c.c_int, [_c.c_uint32, _c.c_uint32, _P, _c.c_uint64, _P, _P, _P]),
     "ane_hip_q8_0_mul_mat_workspace_size": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),
+    "ane_hip_q8_0_mul_mat_workspace_size_n": (_c.c_size_t, [_c.c_uint32, _c.c_uint32, _c.c_uint32]),
     "ane_hip_q8_0_mul_mat": (
         _c.c_int,
         [_c.c_uint32, _c.c_uint32, _c.c_uint32, _P, _P, _P, _P, _c.c_size_t, _P],
@@ -653,14 +655,24 @@ def get_rows(fmt, n_rows, dim, table, table_rows, indices, out, stream=None):
                                                      _stream_handle(stream)), f"get_rows_{fmt}")
 
 
-def q8_0_mul_mat_workspace_size(K, T) -> int:
-    return int(lib().ane_hip_q8_0_mul_mat_workspace_size(K, T))
+def q8_0_mul_mat_workspace_size(K, T, N=None) -> int:
+    """Workspace bytes for q8_0_mul_mat: with N, enough for every route of
+    an N-row matrix (ane_hip_q8_0_mul_mat_workspace_size_n); without, the
+    minimum (some routes are then not taken; results are the same)."""
+    if N is None:
+        return int(lib().ane_hip_q8_0_mul_mat_workspace_size(K, T))
+    return int(lib().ane_hip_q8_0_mul_mat_workspace_size_n(N, K, T))
 
 
 def q8_0_mul_mat(N, K, T, x, W, y, workspace=None, stream=None):
     L = lib()
-    wsb = L.ane_hip_q8_0_mul_mat_workspace_size(K, T)
-    ws = workspace if workspace is not None else _scratch(wsb, W.device, stream)
+    if workspace is None:
+        wsb = L.ane_hip_q8_0_mul_mat_workspace_size_n(N, K, T)
+        ws = _scratch(wsb, W.device, stream)
+    else:
+        ws = workspace
+        wsb = (workspace.numel() * workspace.element_size() if hasattr(workspace, "numel")
+               else L.ane_hip_q8_0_mul_mat_workspace_size(K, T))
     check(L.ane_hip_q8_0_mul_mat(N, K, T, _p(x), _p(W), _p(y), _p(ws), wsb, _stream_handle(stream)),
           "q8_0_mul_mat")
 

@@ -104,7 +104,7 @@ int mul_mat_rows(ane_ggml_backend* be, int type, uint32_t N, uint32_t K, uint32_
     if (T == 0 || N == 0) return ANE_OK;
     const bool xc = xs == (uint64_t)K * 4, yc = ys == (uint64_t)N * 4;
     const bool g = type == ANE_GGML_TYPE_Q8_0 && be->q8_mode == ANE_GGML_Q8_G;
-    const size_t qws = g ? ane_hip_q8_0_mul_mat_workspace_size(K, T) : 0;
+    const size_t qws = g ? ane_hip_q8_0_mul_mat_workspace_size_n(N, K, T) : 0;
     const size_t xoff = ceil_to(qws, 256);
     const size_t xbytes = xc ? 0 : ceil_to((uint64_t)T * K * 4, 256);
     const size_t yoff = xoff + xbytes;

@@ -1387,6 +1387,271 @@ int mmt_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* w
     return ANE_OK;
 }
 
+// ====================================================== MFMA mul_mat, residue-split workgroups
+// Token-stationary like k_q8_0_mmt (lane (g, c16) computes weight row c16
+// for tokens 4g..4g+3 of a token tile), for matrices with few rows: the 16
+// residues b % 16 of the blocks are split over KW = 16 / NR workgroups.
+// Workgroup q of a row group takes residues NR*q .. NR*q + NR - 1, which are
+// NR consecutive blocks of every 16-block group, so it copies only those
+// bytes of its rows' weights and of the activations; it has one wave per
+// (row tile, residue), and each wave's chain runs over its residue's blocks
+// in order.  The NR leaves of a row tile meet in LDS for the lower levels
+// of the FADDV tree (an aligned NR-leaf subtree); the KW subtotals meet in
+// k_q8_0_mmr_reduce for the top levels.  A 4096-row matrix then keeps every
+// CU busy with its weights read once and the activations copied once per
+// 64 rows (k_q8_0_mma copies them once per 16 rows, k_q8_0_mmt has too few
+// workgroups there).
+//
+// Stage s holds G 16-block groups.  Per group, a weight row contributes
+// kWGroupChunks 16-byte chunks starting at chunk floor(34*NR*q / 16) of the
+// group (the window's 34*NR bytes start o0 = 0 or 8 bytes in); a token
+// contributes the 2*NR chunks of its qx blocks; the scales are block-major
+// dx[b][t] (k_q8_act_quantize_bm), NR*G runs of the workgroup's tokens.
+template <int RT, int TT, int NR, int G>
+struct MmrLayout {
+    static constexpr int kNw = RT * NR;
+    static constexpr uint32_t kTok = TT * 16;
+    static constexpr uint32_t kWGroupChunks = (8 + 34 * NR + 15) / 16;
+    // row strides of 12 (weights) and 4 (tokens) dwords mod 64, as in k_q8_0_mmt
+    static constexpr uint32_t kWRowChunks = G * kWGroupChunks + (3 + 16 - (G * kWGroupChunks) % 16) % 16;
+    static constexpr uint32_t kXGroupChunks = 2 * NR;
+    static constexpr uint32_t kXRowChunks = G * kXGroupChunks + (1 + 16 - (G * kXGroupChunks) % 16) % 16;
+    static constexpr uint32_t kWChunks = RT * 16 * kWRowChunks;
+    static constexpr uint32_t kXChunks = kTok * kXRowChunks;
+    static constexpr uint32_t kDChunks = G * NR * kTok / 4;
+    static constexpr uint32_t kWInstr = (kWChunks + 63) / 64, kXInstr = (kXChunks + 63) / 64,
+                              kDInstr = (kDChunks + 63) / 64;
+    static constexpr uint32_t kWSlots = (kWInstr + kNw - 1) / kNw, kXSlots = (kXInstr + kNw - 1) / kNw,
+                              kDSlots = (kDInstr + kNw - 1) / kNw;
+    static constexpr uint32_t kSlots = kWSlots + kXSlots + kDSlots;
+    static constexpr uint32_t kXOff = kWChunks * 16, kDOff = kXOff + kXChunks * 16;
+    static constexpr uint32_t kStageBytes = kDOff + kDChunks * 16;
+    static_assert((kWRowChunks * 4) % 64 == 12 && (kXRowChunks * 4) % 64 == 4, "row strides");
+};
+
+template <int RT, int TT, int NR, int G, int S>
+__global__ void __launch_bounds__(RT * NR * 64)
+k_q8_0_mmr(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, const uint8_t* __restrict__ qws,
+           uint32_t dx_off, uint32_t T4, uint32_t n_tgroups, uint32_t n_units, float* __restrict__ out) {
+    using L = MmrLayout<RT, TT, NR, G>;
+    constexpr int NW = L::kNw;
+    constexpr uint32_t KW = 16 / NR;
+    static_assert(16 % NR == 0 && NR >= 2, "NR divides the 16 residues");
+    static_assert((S - 1) * L::kSlots < 64, "copies in flight exceed the vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t* trash = smem + S * L::kStageBytes;  // 1 KB, the target of padding copies
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const uint32_t r = wave % NR, rt = wave / NR;
+
+    // Workgroups go to the 8 XCDs round-robin; the KW windows of one unit
+    // (row group x token group) are consecutive slots of one XCD, so the
+    // cache lines that two windows share are fetched into one L2.  The grid
+    // is KW x the units rounded up to a multiple of 8; the surplus exits.
+    const uint32_t xcd = blockIdx.x & 7, xslot = blockIdx.x >> 3;
+    const uint32_t wq = xslot % KW, unit = xcd + 8 * (xslot / KW);
+    if (unit >= n_units) return;
+    const uint32_t wg_t = unit % n_tgroups, wg_r = unit / n_tgroups;
+    const uint32_t row_base = wg_r * RT * 16, tok_base = wg_t * L::kTok;
+    const uint32_t rb = nb * 34;
+    const uint32_t c0 = (34 * NR * wq) / 16, o0 = 34 * NR * wq - 16 * c0;  // window start: chunk, byte
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W, N * rb);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(qws, dx_off + nb * T4 * 4);
+    const uint32_t nst = nb / (16 * G);
+
+    uint32_t ow[L::kWSlots], ox[L::kXSlots], od[L::kDSlots];
+#pragma unroll
+    for (uint32_t q = 0; q < L::kWSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, rr = c / L::kWRowChunks, sub = c - rr * L::kWRowChunks;
+        const uint32_t gi = sub / L::kWGroupChunks, cc = sub - gi * L::kWGroupChunks;
+        const uint32_t row = row_base + rr;
+        ow[q] = (c < L::kWChunks && gi < (uint32_t)G && row < N) ? row * rb + gi * 544 + 16 * (c0 + cc)
+                                                                   : 0x80000000u;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < L::kXSlots; q++) {
+        const uint32_t c = 64 * (q * NW + wave) + lane, t = c / L::kXRowChunks, sub = c - t * L::kXRowChunks;
+        const uint32_t gi = sub / L::kXGroupChunks, cc = sub - gi * L::kXGroupChunks;
+        const uint32_t tok = tok_base + t;
+        ox[q] = (c < L::kXChunks && gi < (uint32_t)G && tok < T)
+                    ? tok * nb * 32 + gi * 512 + 32 * NR * wq + 16 * cc
+                    : 0x80000000u;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < L::kDSlots; q++) {
+        // chunk c: group gi, residue rr of the window, tokens 4*t4 .. of the workgroup
+        const uint32_t c = 64 * (q * NW + wave) + lane, gi = c / (NR * L::kTok / 4);
+        const uint32_t rem = c - gi * (NR * L::kTok / 4), rr = rem / (L::kTok / 4), t4 = rem - rr * (L::kTok / 4);
+        const uint32_t tok = tok_base + 4 * t4, b = 16 * gi + NR * wq + rr;
+        od[q] = (c < L::kDChunks && tok < T4) ? dx_off + (b * T4 + tok) * 4 : 0x80000000u;
+    }
+    auto slot = [&](__amdgpu_buffer_rsrc_t rs, int8_t* region, uint32_t ninstr, uint32_t nchunks, uint32_t q,
+                    uint32_t src) {
+        const uint32_t i = q * NW + wave;
+        if (i < ninstr) {
+            if (nchunks % 64 == 0 || i + 1 < ninstr || lane < nchunks % 64) copy16_to_lds(rs, region + 1024 * i, src);
+        } else if (S > 2) {  // padding that keeps vmcnt counts uniform (none with two stages)
+            copy16_to_lds(rs, trash, 0x80000000u);
+        }
+    };
+    auto issue = [&](uint32_t s) {
+        int8_t* st = smem + (s % S) * L::kStageBytes;
+        const bool on = s < nst;
+#pragma unroll
+        for (uint32_t q = 0; q < L::kWSlots; q++)
+            slot(wr, st, L::kWInstr, L::kWChunks, q,
+                 on && ow[q] != 0x80000000u ? ow[q] + s * (G * 544) : 0x80000000u);
+#pragma unroll
+        for (uint32_t q = 0; q < L::kXSlots; q++)
+            slot(xr, st + L::kXOff, L::kXInstr, L::kXChunks, q,
+                 on && ox[q] != 0x80000000u ? ox[q] + s * (G * 512) : 0x80000000u);
+#pragma unroll
+        for (uint32_t q = 0; q < L::kDSlots; q++)
+            slot(xr, st + L::kDOff, L::kDInstr, L::kDChunks, q,
+                 on && od[q] != 0x80000000u ? od[q] + s * (16 * G * T4 * 4) : 0x80000000u);
+    };
+
+    float p[TT][4];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) p[tt][i] = 0.0f;
+    // this wave's block inside a group's window, and whether its quants are 4-byte aligned
+    const uint32_t bofs = o0 + 34 * r;
+    const bool odd = ((bofs + 2) & 3) == 0;
+#pragma unroll
+    for (int s = 0; s < S - 1; s++) issue(s);
+    for (uint32_t s = 0; s < nst; s++) {
+        wait_vmcnt<(S - 2) * L::kSlots>();  // this wave's copies of stage s have landed
+        __builtin_amdgcn_s_barrier();       // everyone's have; everyone is done with stage s-1
+        issue(s + S - 1);                    // refills the slot of stage s-1
+        const int8_t* st = smem + (s % S) * L::kStageBytes;
+        const int8_t* wrow = st + (rt * 16 + c16) * (L::kWRowChunks * 16) + bofs;       // B: weight row c16
+        const int8_t* xt = st + L::kXOff + c16 * (L::kXRowChunks * 16) + 32 * r + 8 * g;  // A: token c16
+        const float* dd = reinterpret_cast<const float*>(st + L::kDOff) + r * L::kTok + 4 * g;
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) {
+            const int8_t* wb = wrow + gi * (L::kWGroupChunks * 16);
+            const uint32_t o = 2 + 8 * g;
+            uint32_t w0, w1;
+            if (odd) {
+                const uint32_t* a32 = reinterpret_cast<const uint32_t*>(wb + o);
+                w0 = a32[0];
+                w1 = a32[1];
+            } else {
+                const uint32_t* a32 = reinterpret_cast<const uint32_t*>(wb + o - 2);
+                const uint32_t d0 = a32[0], d1 = a32[1], d2 = a32[2];
+                w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                w1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+            }
+            const uint64_t wv = (uint64_t)w0 | ((uint64_t)w1 << 32);
+            const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wb));
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+                const uint64_t xv = *reinterpret_cast<const uint64_t*>(
+                    xt + tt * 16 * (L::kXRowChunks * 16) + gi * (L::kXGroupChunks * 16));
+                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float4 d4 = *reinterpret_cast<const float4*>(dd + gi * (NR * L::kTok) + tt * 16);
+                const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
+                    p[tt][i] = __builtin_fmaf((float)acc[i], __fmul_rn(dw, dx[i]), p[tt][i]);
+            }
+        }
+    }
+    wait_vmcnt<0>();
+    // leaves [rt][tt][r][lane] over the ring; wave (rt, tt % NR) takes the
+    // subtree of token tile tt
+    __syncthreads();
+    float4* ex = reinterpret_cast<float4*>(smem);
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+        ex[((rt * TT + tt) * NR + r) * 64 + lane] = make_float4(p[tt][0], p[tt][1], p[tt][2], p[tt][3]);
+    __syncthreads();
+    const uint32_t row = row_base + rt * 16 + c16;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        if ((uint32_t)(tt % NR) != r) continue;
+        float q[4][NR];
+#pragma unroll
+        for (int k = 0; k < NR; k++) {
+            const float4 e = ex[((rt * TT + tt) * NR + k) * 64 + lane];
+            q[0][k] = e.x;
+            q[1][k] = e.y;
+            q[2][k] = e.z;
+            q[3][k] = e.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float v = tree_sum(q[i]);
+            const uint32_t t = tok_base + tt * 16 + 4 * g + i;
+            // subtotal wq of y[t][row]: out[(wq * T + t) * N + row]
+            if (row < N && t < T) out[((uint64_t)wq * T + t) * N + row] = v;
+        }
+    }
+}
+
+// y[t][row] = the top KW levels of the FADDV tree over the KW subtotals,
+// four outputs per thread (16-byte loads and stores where n % 4 == 0 and y
+// is 16-byte aligned; one output per lane step otherwise).
+template <int KW>
+__global__ void __launch_bounds__(256)
+k_q8_0_mmr_reduce(uint64_t n, const float* __restrict__ part, float* __restrict__ y) {
+    const uint64_t i4 = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i4 >= n) return;
+    if ((n & 3) == 0 && (((uintptr_t)y) & 15) == 0) {
+        float4 a[KW];
+#pragma unroll
+        for (int k = 0; k < KW; k++) a[k] = *reinterpret_cast<const float4*>(part + k * n + i4);
+        float c[4][KW];
+#pragma unroll
+        for (int k = 0; k < KW; k++) {
+            c[0][k] = a[k].x;
+            c[1][k] = a[k].y;
+            c[2][k] = a[k].z;
+            c[3][k] = a[k].w;
+        }
+        const float4 v = make_float4(tree_sum(c[0]), tree_sum(c[1]), tree_sum(c[2]), tree_sum(c[3]));
+        *reinterpret_cast<float4*>(y + i4) = v;
+        return;
+    }
+    for (uint64_t i = i4; i < i4 + 4 && i < n; i++) {
+        float a[KW];
+#pragma unroll
+        for (int k = 0; k < KW; k++) a[k] = part[k * n + i];
+        y[i] = tree_sum(a);
+    }
+}
+
+template <int RT, int TT, int NR, int G, int S>
+int mmr_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* ws, uint32_t dx_off, uint32_t T4,
+               float* part, float* y, hipStream_t s) {
+    using L = MmrLayout<RT, TT, NR, G>;
+    constexpr uint32_t KW = 16 / NR;
+    if (nb % (16 * G)) return -1;
+    const uint64_t ring = (uint64_t)S * L::kStageBytes;
+    const uint64_t exch = (uint64_t)RT * TT * NR * 64 * 16;
+    const uint32_t lds = (uint32_t)((ring > exch ? ring : exch) + 1024);
+    if (lds > kLdsLimit) return -1;
+    auto fn = k_q8_0_mmr<RT, TT, NR, G, S>;
+    static StreamLaunchCache cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ANE_ERR_HIP;
+    const int occ = stream_occupancy(cache, reinterpret_cast<const void*>(fn), dev, L::kNw * 64, lds);
+    if (occ < 0) return occ;
+    const uint32_t rgroups = (N + RT * 16 - 1) / (RT * 16), tgroups = (T + L::kTok - 1) / L::kTok;
+    const uint64_t units = (uint64_t)rgroups * tgroups;
+    const uint64_t grid = KW * ceil_to(units, 8);
+    if (grid > 0x7fffffffull) return -1;
+    hipLaunchKernelGGL(fn, dim3((uint32_t)grid), dim3(L::kNw * 64), lds, s, N, nb, T, (const uint8_t*)W,
+                       (const uint8_t*)ws, dx_off, T4, tgroups, (uint32_t)units, part);
+    ANE_HIP_CHECK_LAUNCH();
+    const uint64_t n = (uint64_t)T * N;
+    hipLaunchKernelGGL(k_q8_0_mmr_reduce<KW>, dim3((uint32_t)((n + 1023) / 1024)), dim3(256), 0, s, n, part, y);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
 // The MFMA path: rows 16-byte aligned (as the streaming kernels need) and
 // whole 16-block stages.  x is quantized into the workspace first.
 //
@@ -1400,8 +1665,24 @@ int mmt_launch(uint32_t N, uint32_t nb, uint32_t T, const void* W, const void* w
 //    groups of 2x2 tiles);
 //  * k_q8_0_mma otherwise (at most one row tile per CU, where its split-K
 //    over residues keeps 16+ waves per CU).
+//  * k_q8_0_mmr (the residue windows of a 64-row group split over four
+//    workgroups) for matrices with fewer rows, when the workspace holds its
+//    subtotals (ane_hip_q8_0_mul_mat_workspace_size_n).
+// Offset of k_q8_0_mmr's subtotals in the workspace: after the activation
+// form with block-major scales.
+uint64_t mmr_part_off(uint32_t nb, uint32_t T) {
+    const uint64_t T4 = ((uint64_t)T + 3) & ~3ull;
+    return ceil_to(ceil_to((uint64_t)T * nb * 32, 256) + (uint64_t)nb * T4 * 4, 256);
+}
+constexpr uint32_t kMmrWindows = 4;  // workgroups per row group on the residue-split route
+// ... taken from this many blocks per row: measured on config 4 (XCD-grouped
+// windows), down 4096 x 14336 (448 blocks) T = 16 / 32 / 64: 30.9 / 37.3 /
+// 42.0 -> 26.9 / 29.6 / 36.9 us; at 128 blocks (o, qkv) the four 32-block
+// stages do not repay the subtotal pass (o T = 64 17.2 -> 18.3 us).
+constexpr uint32_t kMmrMinBlocks = 256;
+
 int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
-                void* workspace, hipStream_t s) {
+                void* workspace, size_t workspace_bytes, hipStream_t s) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t cus = cu_count(dev);
@@ -1412,19 +1693,32 @@ int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     const uint32_t ttiles = (T + 15) / 16;
     const uint32_t T4 = (T + 3) & ~3u;
     const bool many = rtiles >= 4 * cus;
-    const bool mmt = (many || (ttiles > 2 && rtiles > cus)) && dx_off + (uint64_t)nb * T4 * 4 < 0x80000000ull;
-    if (mmt) {
+    const bool bm_ok = dx_off + (uint64_t)nb * T4 * 4 < 0x80000000ull;
+    const uint64_t part_off = mmr_part_off(nb, T);
+    const bool mmr = !many && bm_ok && nb % 32 == 0 && nb >= kMmrMinBlocks &&
+                     part_off + (uint64_t)kMmrWindows * T * N * 4 <= workspace_bytes;
+    const bool mmt = !mmr && (many || (ttiles > 2 && rtiles > cus)) && bm_ok;
+    if (mmr || mmt) {
         // activation scales block-major: dx[b][t] at dx_off
         hipLaunchKernelGGL(k_q8_act_quantize_bm, dim3((nblocks * 8 + 255) / 256), dim3(256), 0, s, nblocks, nb, K,
                            T4, dxo, x, static_cast<uint8_t*>(workspace));
         ANE_HIP_CHECK_LAUNCH();
         int r;
-        if (ttiles == 1)
+        if (mmr) {
+            float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + part_off);
+            if (ttiles == 1)
+                r = mmr_launch<4, 1, 4, 2, 2>(N, nb, T, W, workspace, dxo, T4, part, y, s);
+            else if (ttiles == 2)
+                r = mmr_launch<4, 2, 4, 2, 2>(N, nb, T, W, workspace, dxo, T4, part, y, s);
+            else
+                r = mmr_launch<4, 4, 4, 2, 2>(N, nb, T, W, workspace, dxo, T4, part, y, s);
+        } else if (ttiles == 1) {
             r = mmt_launch<2, 1, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
-        else if (ttiles == 2 || !many)
+        } else if (ttiles == 2 || !many) {
             r = mmt_launch<2, 2, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
-        else
+        } else {
             r = mmt_launch<4, 4, 4, 2>(N, nb, T, W, workspace, dxo, T4, y, s);
+        }
         if (r != -1) return r;
         // not launched: the token-major form below overwrites the workspace
     }
@@ -1581,6 +1875,13 @@ extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {
     return (size_t)(ceil_to((uint64_t)T * nb * 32, 256) + ceil_to(nb * (((uint64_t)T + 3) & ~3ull) * 4, 256) + 256);
 }
 
+extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size_n(uint32_t N, uint32_t K, uint32_t T) {
+    const size_t base = ane_hip_q8_0_mul_mat_workspace_size(K, T);
+    if (T <= kMaxStreamTokens) return base;
+    const uint64_t with_part = mmr_part_off(K >> 5, T) + (uint64_t)kMmrWindows * T * N * 4;
+    return with_part > base ? (size_t)with_part : base;
+}
+
 extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,
                                     const void* W, float* y, void* workspace,
                                     size_t workspace_bytes, void* stream) {
@@ -1611,7 +1912,7 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
         if (r >= 0) return r;
     }
     if (T > kMaxStreamTokens && nb % kMmaSb == 0 && stream_eligible(N, nb, K, T, W)) {
-        const int r = mma_mul_mat(N, nb, K, T, x, W, y, workspace, s);
+        const int r = mma_mul_mat(N, nb, K, T, x, W, y, workspace, workspace_bytes, s);
         if (r >= 0) return r;
     }
     int8_t* qx = (int8_t*)workspace;

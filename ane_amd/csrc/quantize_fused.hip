@@ -15,6 +15,8 @@
 //    every block first folds its tensor's partials.  It takes the shapes
 //    the resident route does not.
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -598,6 +600,17 @@ std::mutex g_res_mu;
 ResidentDevice g_res_dev[64];
 std::atomic<uint64_t> g_wait_limit{kSyncTimeoutTicks};
 
+// ANE_COOPERATIVE=0 in the environment makes the uncaptured launches plain
+// ones too (for tools that do not handle cooperative launches: rocprofv3's
+// teardown has crashed after them); read once.
+bool cooperative_launches() {
+    static const bool on = [] {
+        const char* e = std::getenv("ANE_COOPERATIVE");
+        return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
+}
+
 // The device's slot and grid (probed once per device, with it current);
 // null when the resident route is unavailable (then the two-pass route
 // runs).  Called with g_res_mu held.
@@ -691,7 +704,7 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     float* kScales = scales;
     uint32_t* kSync = d.sync;
     uint32_t* kStatus = wstatus;
-    if (!capturing) {
+    if (!capturing && cooperative_launches()) {
         void* args[] = {&kA, &kB, &kN, &kK, &kNA4, &kPerA4, &kTiles, &kPerT, &kPartials, &kQA, &kQBt,
                         &kScales, &kSync, &kTag, &kLimit, &kStatus};
         if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_quantize_resident), dim3(G), dim3(kRT),

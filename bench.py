@@ -70,6 +70,23 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
+WARM_S = 0.25  # seconds of warm-up replays before a timed region (the clock settles within ~20 ms)
+
+
+def warm_until(replay, stream, min_s: float = WARM_S) -> int:
+    """Call replay() (enqueueing GPU work on ``stream``) back to back until
+    at least min_s seconds have passed, at least once; returns the count."""
+    t0 = time.perf_counter()
+    n = 0
+    while n == 0 or time.perf_counter() - t0 < min_s:
+        replay()
+        n += 1
+        if n % 8 == 0:
+            stream.synchronize()  # keep the host within a few replays of the GPU
+    stream.synchronize()
+    return n
+
+
 def events_time(fn, reps: int, stream) -> float:
     """Average milliseconds per call of fn() over reps calls, HIP events on stream."""
     import torch
@@ -86,9 +103,10 @@ def events_time(fn, reps: int, stream) -> float:
 
 def graph_time(fn_s, reps: int, rounds: int = 5) -> float:
     """Median milliseconds per call of fn_s(stream): `reps` calls (fn_s may
-    rotate its inputs) are captured into one HIP graph on a side stream and
-    replayed `rounds` times on that stream between HIP events, so host
-    launch overhead is outside the timed region."""
+    rotate its inputs) are captured into one HIP graph on a side stream,
+    replayed back to back for 0.1 s to warm up, then replayed `rounds` times
+    on that stream between HIP events, so host launch overhead is outside
+    the timed region."""
     import torch
 
     gs = torch.cuda.Stream()
@@ -100,8 +118,7 @@ def graph_time(fn_s, reps: int, rounds: int = 5) -> float:
         with torch.cuda.graph(graph, stream=gs):
             for _ in range(reps):
                 fn_s(gs)
-        graph.replay()
-        gs.synchronize()
+        warm_until(graph.replay, gs, 0.1)
         times = []
         for _ in range(rounds):
             start = torch.cuda.Event(enable_timing=True)
@@ -253,11 +270,15 @@ def main() -> int:
     # ------------------------------------------------------------ headline
     # The K timed steps are K full dense_fused_i8 calls (both quantize passes
     # and the contraction, on fresh fp32 operands each time), captured once
-    # into a HIP graph.  The warmup replays a graph of W steps and then the
-    # timed graph once, untimed (a graph's first replay carries one-time
-    # setup).  The timed replay is bracketed by synchronisations, and its
-    # time is read from HIP events recorded on the replay stream just before
-    # and after it: all K steps of GPU work, without the host's launch and
+    # into a HIP graph.  The warmup replays a graph of W steps back to back
+    # until at least WARM_S seconds have passed, then the timed graph once,
+    # untimed (a graph's first replay carries one-time setup): the GPU's
+    # clock settles over the first ~20 ms of this workload (measured: a
+    # 20-step replay right after start 104 us/step, falling to 95 us/step
+    # over ten replays; after 0.3 s of warm replays, 95 us/step at once).
+    # The timed replay is bracketed by synchronisations, and its time is
+    # read from HIP events recorded on the replay stream just before and
+    # after it: all K steps of GPU work, without the host's launch and
     # synchronisation latency (the wall clock around the same replay is
     # reported too).  --eager launches the K calls from Python instead,
     # between the same two events.
@@ -266,8 +287,7 @@ def main() -> int:
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     if args.eager:
-        for _ in range(args.warmup):
-            fused()
+        warm_until(lambda: [fused() for _ in range(max(1, args.warmup))], stream)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0.record(stream)
@@ -288,7 +308,7 @@ def main() -> int:
             with torch.cuda.graph(timed, stream=gs):
                 for _ in range(args.steps):
                     fused(gs)
-            warm.replay()
+            warm_until(warm.replay, gs)
             timed.replay()
             gs.synchronize()
             torch.cuda.synchronize()
@@ -412,6 +432,8 @@ def main() -> int:
                    "the K steps captured as one HIP graph, replayed once untimed after the warmup and "
                    "then once between synchronisations; ms_per_step from HIP events recorded on the "
                    "replay stream around that replay"),
+        "warmup_how": (f"the W warmup steps (one HIP graph) replayed back to back for at least {WARM_S} s, "
+                       "so the GPU's clock has settled before the K timed steps"),
         "wall_ms_per_step": round(wall_ms_per_step, 5),
         "rotating_operands": rotating,
         "config": {"workload": f"dense_fused_i8 M={M} N={N} K={K} scale=1.0 relu (config 2)",
@@ -462,8 +484,7 @@ def headline_rotating(args, M, N, K, ops) -> dict:
             for i in range(steps):
                 A, B, C, ws = sets[i % nsets]
                 ane_amd.dense_fused_i8(M, N, K, 1.0, True, A, B, C, workspace=ws, stream=gs, check_wait=False)
-        graph.replay()
-        gs.synchronize()
+        warm_until(graph.replay, gs)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -739,7 +760,7 @@ def bench_mul_mat(args) -> dict:
         for T in (1, 4, 16, 64):
             x = torch.from_numpy(data.activations(T, Kc, seed=6)).cuda()
             y = torch.empty(T * Nr, device="cuda", dtype=torch.float32)
-            wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, T), dtype=torch.uint8, device="cuda")
+            wsq = torch.empty(ane_amd.q8_0_mul_mat_workspace_size(Kc, T, N=Nr), dtype=torch.uint8, device="cuda")
             it = [0]
 
             def fn(st):

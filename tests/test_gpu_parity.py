@@ -46,6 +46,23 @@ def assert_f32_identical(got, want):
     np.testing.assert_array_equal(bits(got)[~nan], bits(want)[~nan])
 
 
+def mul_mat_both_routes(ane, N, K, T, x, W):
+    """y of ane.q8_0_mul_mat twice: with the full workspace of an N-row
+    matrix (ane_hip_q8_0_mul_mat_workspace_size_n, every route allowed) and
+    with the minimum one (the residue-split route then not taken)."""
+    import torch
+
+    xd, Wd = dev(x), dev(W)
+    outs = []
+    for n_aware in (True, False):
+        wsb = ane.q8_0_mul_mat_workspace_size(K, T, N=N if n_aware else None)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device="cuda")
+        y = zeros(T * N, torch.float32)
+        ane.q8_0_mul_mat(N, K, T, xd, Wd, y, workspace=ws)
+        outs.append(host(y).reshape(T, N))
+    return outs
+
+
 # ---------------------------------------------------------------- MFMA core
 @pytest.mark.parametrize("M,N,K", [(1, 1, 16), (32, 32, 32), (50, 130, 784), (128, 128, 128),
                                    (300, 200, 1008), (257, 129, 4096), (64, 512, 48),
@@ -755,7 +772,13 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # rows and tokens, two token groups); 2 x 2 tiles at two token
                                    # tiles, and at three or four just past one row tile per CU
                                    (28672, 512, 64), (16392, 1024, 40), (16384, 512, 100),
-                                   (19990, 512, 20), (4100, 1024, 50)])
+                                   (19990, 512, 20), (4100, 1024, 50),
+                                   # residue-split kernel (256+ blocks per row, fewer than 64 row
+                                   # tiles per CU): ragged 64-row groups and token tiles, rows
+                                   # fewer than one group, the unit count not a multiple of 8,
+                                   # token groups past 64, one and two token tiles
+                                   (4100, 8192, 40), (300, 9216, 20), (37, 8192, 5), (1000, 16384, 64),
+                                   (200, 8192, 100), (4096, 14336, 32), (130, 8192, 16)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
@@ -766,9 +789,8 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
         ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
     finally:
         oracle.set_threads(1)
-    y = zeros(T * N, torch.float32)
-    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
-    assert_f32_identical(host(y).reshape(T, N), ref)
+    for got in mul_mat_both_routes(ane, N, K, T, x, W):
+        assert_f32_identical(got, ref)
 
 
 # config 4: the four Llama-3-8B projections (rows x K) at every token count
@@ -779,9 +801,9 @@ CONFIG4 = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "do
 @pytest.mark.parametrize("proj", list(CONFIG4))
 def test_q8_0_mul_mat_config4_shapes(ane, oracle, proj, T):
     """Config 4 at its exact shapes: every (projection, tokens) pair, every
-    output bit-identical to the oracle's G-mode definition."""
-    import torch
-
+    output bit-identical to the oracle's G-mode definition, on the routes
+    of both workspace sizes (the residue-split kernel at 16 and 64 tokens
+    on the 4096- and 6144-row projections, the older kernels otherwise)."""
     N, K = CONFIG4[proj]
     W = data.q8_0_weights(N, K, seed=N + K + 1)
     x = data.activations(T, K, seed=T + 200)
@@ -790,18 +812,18 @@ def test_q8_0_mul_mat_config4_shapes(ane, oracle, proj, T):
         ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
     finally:
         oracle.set_threads(1)
-    y = zeros(T * N, torch.float32)
-    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
-    assert_f32_identical(host(y).reshape(T, N), ref)
+    for got in mul_mat_both_routes(ane, N, K, T, x, W):
+        assert_f32_identical(got, ref)
 
 
 @pytest.mark.parametrize("T,K,N", [(2, 1024, 300), (20, 1024, 300), (1, 9216, 300), (3, 9216, 300),
-                                   (40, 512, 4100)])
+                                   (40, 512, 4100), (20, 9216, 300), (64, 8192, 130)])
 def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K, N):
     """Zero, NaN and infinite activation blocks (0x19 zero guard and NaN rules
     per block), on the streaming (T = 2, and the separately quantized T = 1
-    and 3 at K = 9216), MFMA (T = 20) and token-stationary MFMA (T = 40 over
-    4100 rows) kernels."""
+    and 3 at K = 9216), MFMA (T = 20), token-stationary MFMA (T = 40 over
+    4100 rows) and residue-split (T = 20 and 64 at K = 9216 / 8192)
+    kernels."""
     import torch
 
     W = data.q8_0_weights(N, K, seed=11)
@@ -811,20 +833,20 @@ def test_q8_0_mul_mat_g_special_values(ane, oracle, T, K, N):
     x[T - 1, 100] = np.inf
     x[T - 1, 200] = -1e-40  # denormal
     ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
-    y = zeros(T * N, torch.float32)
-    ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
-    assert_f32_identical(host(y).reshape(T, N), ref)
+    for got in mul_mat_both_routes(ane, N, K, T, x, W):
+        assert_f32_identical(got, ref)
 
 
 @pytest.mark.parametrize("mode,N,K,T", [("R", 300, 1024, 1), ("G", 300, 1024, 1), ("G", 300, 1024, 2),
                                         ("G", 300, 9216, 3), ("G", 300, 1024, 20), ("G", 4100, 1024, 40),
-                                        ("G", 16384, 512, 16)])
+                                        ("G", 16384, 512, 16), ("G", 300, 9216, 20), ("G", 200, 8192, 64)])
 def test_q8_0_special_weight_scales(ane, oracle, mode, N, K, T):
     """Weight block scales of every fp16 class (infinities, NaN, subnormals,
     signed zeros, the largest finite), with all-zero blocks among them so
     0 * inf reaches the fma, on the R matvec, the G streaming kernel (T = 1,
-    2, and 3 on separately quantized activations), the MFMA kernel (T = 20)
-    and the token-stationary MFMA kernel (2 x 2 and 2 x 1 tile shapes)."""
+    2, and 3 on separately quantized activations), the MFMA kernel (T = 20),
+    the token-stationary MFMA kernel (2 x 2 and 2 x 1 tile shapes) and the
+    residue-split kernel (T = 20 and 40 with the full workspace)."""
     import torch
 
     nb = K // 32
@@ -845,9 +867,8 @@ def test_q8_0_special_weight_scales(ane, oracle, mode, N, K, T):
         assert_f32_identical(host(y), ref)
     else:
         ref = oracle.q8_0_mul_mat_g(N, K, T, x, W)
-        y = zeros(T * N, torch.float32)
-        ane.q8_0_mul_mat(N, K, T, dev(x), dev(W), y)
-        assert_f32_identical(host(y).reshape(T, N), ref)
+        for got in mul_mat_both_routes(ane, N, K, T, x, W):
+            assert_f32_identical(got, ref)
     # the cases reach NaN, finite and (G: one isum per block) infinite outputs;
     # an R-mode infinite block mixes both signs across its lanes, giving NaN
     assert np.isnan(ref).any() and np.isfinite(ref).any() and (mode == "R" or np.isinf(ref).any())
