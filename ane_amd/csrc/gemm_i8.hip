@@ -262,8 +262,25 @@ static uint64_t fused_kp(int32_t K) { return ceil_to((uint64_t)(K > 0 ? K : 0), 
 
 // Workspace layout: scales {sa, sb} at 0; at 256 the absmax partials
 // (2 x kFusedPartials uint32) followed by the quantizer's wait record
-// (1 + kFusedPartials uint32); then qA and qBt, each rounded up to 256 bytes.
+// (1 + kFusedPartials uint32); then qA and qBt, each rounded up to 256
+// bytes; then, for few rows, the split contraction's int32 planes.
 static uint64_t fused_partials_bytes() { return ceil_to((uint64_t)(3 * kFusedPartials + 1) * 4, 256); }
+
+// Few rows (kSplitMinRows .. 128): the contraction on 128 x 128 tiles with K
+// split over up to kMaxSplit workgroups per tile, each writing an int32
+// plane, then k_split_epilogue adds the planes (int32, exact in any order)
+// and applies the epilogue.  A full-K workgroup per 16 columns
+// (k_gemm_skinny) re-reads all of A for every 16 columns; here each
+// workgroup reads A and Bt over its share of K only.  Measured whole op at
+// N = K = 4096 (skinny / 4 splits / 8 splits): M = 64 31.7 / 32.9 / 32.0 us,
+// M = 96 36.9 / 33.1 / 32.6, M = 128 39.4 / 33.2 / 33.3 (contraction alone
+// at M = 128: 20.1 / 13.5 / 16.0).
+constexpr uint32_t kSplitMinRows = 65;
+constexpr uint32_t kMaxSplit = 4;
+static uint64_t fused_split_bytes(int32_t M, int32_t N, int32_t K) {
+    if (M < (int32_t)kSplitMinRows || M > 128 || N < 128 || K <= 0) return 0;
+    return ceil_to((uint64_t)kMaxSplit * M * N * 4, 256);
+}
 
 extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K) {
     if (M < 0 || N < 0 || K < 0) return 0;
@@ -272,9 +289,40 @@ extern "C" size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, in
     bytes += fused_partials_bytes();                      // absmax partials + wait record
     bytes += ceil_to((uint64_t)M * Kp, 256);               // qA
     bytes += ceil_to((uint64_t)N * Kp, 256);               // qBt
+    bytes += fused_split_bytes(M, N, K);                   // split contraction planes
     return (size_t)bytes;
 }
 
+
+// C = fmaxA(fadd(fmul((float)acc, s), +0), lo) with acc the int32 sum
+// (wrapping, exact in any order) of the ksplit planes and s = (sa*sb)*smul:
+// the same operations as the contraction kernels' epilogue.  Four outputs
+// per thread.
+__global__ void __launch_bounds__(256)
+k_split_epilogue(const int32_t* __restrict__ planes, uint32_t ksplit, uint64_t n, const float* __restrict__ sdev,
+                 float smul, float lo, float* __restrict__ C) {
+    const uint64_t i4 = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i4 >= n) return;
+    const float s = __fmul_rn(__fmul_rn(sdev[0], sdev[1]), smul);
+    auto epi = [&](uint32_t acc) { return fmax_a(__fadd_rn(__fmul_rn((float)(int32_t)acc, s), 0.0f), lo); };
+    if ((n & 3) == 0 && (((uintptr_t)C) & 15) == 0) {
+        uint4 acc = make_uint4(0, 0, 0, 0);
+        for (uint32_t y = 0; y < ksplit; y++) {
+            const uint4 v = *reinterpret_cast<const uint4*>(planes + y * n + i4);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        *reinterpret_cast<float4*>(C + i4) = make_float4(epi(acc.x), epi(acc.y), epi(acc.z), epi(acc.w));
+        return;
+    }
+    for (uint64_t i = i4; i < i4 + 4 && i < n; i++) {
+        uint32_t acc = 0;
+        for (uint32_t y = 0; y < ksplit; y++) acc += (uint32_t)planes[y * n + i];
+        C[i] = epi(acc);
+    }
+}
 
 struct FusedLayout {
     uint64_t Kp;
@@ -283,9 +331,10 @@ struct FusedLayout {
     uint32_t* wstatus;
     int8_t* qA;
     int8_t* qBt;
+    int32_t* planes;  // split contraction (few rows), or null
 };
 
-static FusedLayout fused_layout(int32_t M, int32_t K, void* workspace) {
+static FusedLayout fused_layout(int32_t M, int32_t N, int32_t K, void* workspace) {
     FusedLayout L;
     L.Kp = fused_kp(K);
     uint8_t* ws = (uint8_t*)workspace;
@@ -294,6 +343,8 @@ static FusedLayout fused_layout(int32_t M, int32_t K, void* workspace) {
     L.wstatus = L.partials + 2 * kFusedPartials;
     L.qA = (int8_t*)(ws + 256 + fused_partials_bytes());
     L.qBt = L.qA + ceil_to((uint64_t)M * L.Kp, 256);
+    L.planes = fused_split_bytes(M, N, K) ? reinterpret_cast<int32_t*>(L.qBt + ceil_to((uint64_t)N * L.Kp, 256))
+                                          : nullptr;
     return L;
 }
 
@@ -313,7 +364,7 @@ extern "C" int ane_hip_dense_fused_i8_quantize(int32_t M, int32_t N, int32_t K, 
     if (M == 0 || N == 0) return ANE_OK;
     if (K > 0 && (!A || !B)) return ANE_ERR_BAD_POINTER;
     hipStream_t s = (hipStream_t)stream;
-    const FusedLayout L = fused_layout(M, K, workspace);
+    const FusedLayout L = fused_layout(M, N, K, workspace);
     const uint64_t Kp = L.Kp;
     st = launch_fused_quantize(A, B, (uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)Kp, L.partials,
                                L.qA, L.qBt, L.scales, L.wstatus, s);
@@ -332,7 +383,7 @@ extern "C" int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, floa
     if (st != ANE_OK) return st;
     if (M == 0 || N == 0) return ANE_OK;
     if (!C) return ANE_ERR_BAD_POINTER;
-    const FusedLayout L = fused_layout(M, K, (void*)workspace);
+    const FusedLayout L = fused_layout(M, N, K, (void*)workspace);
     GemmParams p{};
     p.A = L.qA;
     p.lda = L.Kp;
@@ -349,7 +400,28 @@ extern "C" int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, floa
     p.lo = relu ? 0.0f : -3.40282347e+38f;
     p.C = C;
     p.ldc = (uint64_t)N;
-    return launch_gemm<kBTransposed, false>(p, (hipStream_t)stream);
+    hipStream_t s = (hipStream_t)stream;
+    if (L.planes) {
+        // K split so that the tiles x splits fill the CUs, at least two
+        // 128-byte slices per split
+        const uint32_t tiles = (uint32_t)((N + 127) / 128), nk = (uint32_t)(L.Kp / 128);
+        uint32_t ksplit = (uint32_t)(tile256_min_tiles() / tiles);
+        if (ksplit > kMaxSplit) ksplit = kMaxSplit;
+        if (ksplit > nk / 2) ksplit = nk / 2;
+        GemmParams q = p;
+        q.C = nullptr;
+        q.Craw = L.planes;
+        if (ksplit >= 2 && tile128_eligible(q, true)) {
+            const int st = launch_gemm_tile128(q, s, ksplit);
+            if (st != ANE_OK) return st;
+            const uint64_t n = (uint64_t)M * N;
+            hipLaunchKernelGGL(k_split_epilogue, dim3((uint32_t)((n + 1023) / 1024)), dim3(256), 0, s, L.planes,
+                               ksplit, n, L.scales, scale, p.lo, C);
+            ANE_HIP_CHECK_LAUNCH();
+            return ANE_OK;
+        }
+    }
+    return launch_gemm<kBTransposed, false>(p, s);
 }
 
 extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale, int relu,

@@ -44,12 +44,15 @@ bool resident_mixed_bit(uint32_t bits);
 // multiple of 64 (run as 128-byte slices, an odd last half read as zeros),
 // 16-byte aligned rows, and enough rows/columns to fill 256-wide tiles
 // reasonably.
-bool tile256_eligible(const GemmParams& p);
-int launch_gemm_tile256(const GemmParams& p, hipStream_t s);
+// any_rows: also fewer rows than one tile (rows past Mout read as zeros).
+// ksplit > 1 splits K over gridDim.y workgroups per tile, each writing its
+// int32 plane y of Craw (Mout x ldc): raw output only.
+bool tile256_eligible(const GemmParams& p, bool any_rows = false);
+int launch_gemm_tile256(const GemmParams& p, hipStream_t s, uint32_t ksplit = 1);
 
 // The same loop at 128 x 128 tiles (gemm_i8_tile128.hip).
-bool tile128_eligible(const GemmParams& p);
-int launch_gemm_tile128(const GemmParams& p, hipStream_t s);
+bool tile128_eligible(const GemmParams& p, bool any_rows = false);
+int launch_gemm_tile128(const GemmParams& p, hipStream_t s, uint32_t ksplit = 1);
 
 // Few-row kernel (gemm_i8_skinny.hip): Bt layout, signed A, M <= 128, one
 // workgroup per 16 columns.

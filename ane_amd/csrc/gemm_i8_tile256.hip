@@ -254,19 +254,26 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
+    // Split K (gridDim.y > 1, raw int32 output only): workgroup (x, y) takes
+    // the slices [y * per, (y + 1) * per) and writes its int32 plane y of
+    // Craw (Mout x ldc each); the planes are added afterwards (exact).
     const uint32_t nk = (p.Kp + TK - 1) / TK;
-    auto kmax = [&](uint32_t k) -> uint32_t {  // bytes of slice k inside Kp (0 past it)
+    const uint32_t per = (nk + gridDim.y - 1) / gridDim.y;
+    const uint32_t kt0 = blockIdx.y * per < nk ? blockIdx.y * per : nk;
+    const uint32_t kt1 = kt0 + per < nk ? kt0 + per : nk;
+    int32_t* const craw = p.Craw ? p.Craw + (uint64_t)blockIdx.y * p.Mout * p.ldc : nullptr;
+    auto kmax = [&](uint32_t k) -> uint32_t {  // bytes of slice k inside this range of Kp (0 past it)
         const uint32_t k0 = k * TK;
-        return k0 >= p.Kp ? 0u : (p.Kp - k0 < (uint32_t)TK ? p.Kp - k0 : (uint32_t)TK);
+        return (k >= kt1 || k0 >= p.Kp) ? 0u : (p.Kp - k0 < (uint32_t)TK ? p.Kp - k0 : (uint32_t)TK);
     };
     Frags f0, f1;
     {
-        const SliceCopy c{ra, rb, smem, wave, 0, kmax(0)};
+        const SliceCopy c{ra, rb, smem, wave, kt0 * TK, kmax(kt0)};
 #pragma unroll
         for (int d = 0; d < 2 * kDmaPerWave; d++) issue_one(c, offA, offB, kofs, d);
     }
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const uint32_t st = kt & 1;
+    for (uint32_t kt = kt0; kt < kt1; kt++) {
+        const uint32_t st = (kt - kt0) & 1;
         wait_vmcnt<0>();  // this wave's copies of slice kt landed
         lds_barrier();    // everyone's did; everyone finished slice kt-1
         const int8_t* cur = smem + st * kStage;
@@ -285,8 +292,7 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
         bj[ni] = (p.bias && j < p.Nout) ? p.bias[j] : 0.0f;
     }
     int8_t* epi = smem + wave * kEpiWaveBytes;
-    const bool vec_ok =
-        (((uintptr_t)(p.Craw ? (void*)p.Craw : (void*)p.C)) & 15) == 0 && (p.ldc & 3) == 0;
+    const bool vec_ok = (((uintptr_t)(craw ? (void*)craw : (void*)p.C)) & 15) == 0 && (p.ldc & 3) == 0;
 
 #pragma unroll
     for (int mi = 0; mi < FM; mi++) {
@@ -302,7 +308,7 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
                     const uint32_t lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) - h * EPR;
                     const uint32_t lc = ni * 32 + (lane & 31);
                     uint32_t bitsv;
-                    if (p.Craw) {
+                    if (craw) {
                         bitsv = (uint32_t)acc[mi][ni][r];
                     } else {
                         const float f = __fadd_rn(__fmul_rn((float)acc[mi][ni][r], s), bj[ni]);
@@ -322,8 +328,8 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
                 const uint32_t i = row0 + wr0 + mi * 32 + h * EPR + lr;
                 const uint32_t j = col0 + wc0 + lc;
                 if (i >= p.Mout) continue;
-                uint32_t* dst = p.Craw ? reinterpret_cast<uint32_t*>(p.Craw) + (uint64_t)i * p.ldc + j
-                                       : reinterpret_cast<uint32_t*>(p.C) + (uint64_t)i * p.ldc + j;
+                uint32_t* dst = craw ? reinterpret_cast<uint32_t*>(craw) + (uint64_t)i * p.ldc + j
+                                     : reinterpret_cast<uint32_t*>(p.C) + (uint64_t)i * p.ldc + j;
                 if (vec_ok && j + 3 < p.Nout) {
                     store16_sc1(dst, v);
                 } else {
@@ -341,8 +347,8 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
 
 }  // namespace
 
-bool ANE_TILE_ELIGIBLE(const GemmParams& p) {
-    if (p.Mout < TM || p.Nout < TN) return false;
+bool ANE_TILE_ELIGIBLE(const GemmParams& p, bool any_rows) {
+    if ((!any_rows && p.Mout < TM) || p.Nout < TN) return false;
     if (p.Kp == 0 || (p.Kp % 64) != 0) return false;
     if ((p.lda & 15) || (p.ldb & 15)) return false;
     if ((((uintptr_t)p.A) & 15) || (((uintptr_t)p.B) & 15)) return false;
@@ -355,12 +361,13 @@ bool ANE_TILE_ELIGIBLE(const GemmParams& p) {
     return true;
 }
 
-int ANE_TILE_LAUNCH(const GemmParams& p, hipStream_t s) {
+int ANE_TILE_LAUNCH(const GemmParams& p, hipStream_t s, uint32_t ksplit) {
     const uint32_t tiles_m = (p.Mout + TM - 1) / TM;
     const uint32_t tiles_n = (p.Nout + TN - 1) / TN;
     const uint64_t total = (uint64_t)tiles_m * tiles_n;
-    if (total > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(ANE_TILE_KERNEL, dim3((uint32_t)total), dim3(kThreads), 0, s, p, tiles_m,
+    if (total > 0x7fffffffull || ksplit == 0 || ksplit > 65535) return ANE_ERR_INVALID_ARG;
+    if (ksplit > 1 && !p.Craw) return ANE_ERR_INVALID_ARG;  // split K writes int32 planes
+    hipLaunchKernelGGL(ANE_TILE_KERNEL, dim3((uint32_t)total, ksplit), dim3(kThreads), 0, s, p, tiles_m,
                        tiles_n);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;

@@ -313,8 +313,15 @@ def test_dense_fused_mnist_mlp(ane, oracle):
                                               (1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0),
                                               (129, 257, 1000, False, 0.75), (7, 9, 0, True, 1.0),
                                               (300, 700, 333, True, 1.0), (1024, 512, 4096, False, 1.0),
-                                              (128, 4096, 4096, True, 1.0), (33, 1000, 4000, True, 1.0)])
+                                              (128, 4096, 4096, True, 1.0), (33, 1000, 4000, True, 1.0),
+                                              # few rows on split K (65..128 rows): ragged columns and K,
+                                              # two to four splits, a range shorter than its share, and
+                                              # one 128-byte slice (no split)
+                                              (100, 1000, 4000, False, 1.0), (65, 130, 640, True, 0.5),
+                                              (127, 4100, 2048, True, 1.0), (96, 256, 128, False, 1.0),
+                                              (120, 640, 1200, True, 1.0), (70, 512, 1152, False, 1.0)])
 def test_dense_fused_parity(ane, oracle, M, N, K, relu, scale):
+    """dense_fused_i8 through stream_exec against the oracle, bit for bit."""
     A, B = data.gemm_inputs(M, N, K, seed=M + N + K)
     ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
     import torch
