@@ -711,12 +711,22 @@ class GgmlType:
     F16 = 1
     Q4_0 = 2
     Q8_0 = 8
+    I32 = 26
 
 
 class GgmlOp:
+    """enum ane_ggml_op (include/ggml-ane-hip.h)."""
     NONE = 0
     MUL_MAT = 1
     OTHER = 2
+    ADD = 3
+    MUL = 4
+    SCALE = 5
+    RMS_NORM = 6
+    SOFT_MAX = 7
+    SILU = 8
+    ROPE = 9
+    CPY = 10
 
 
 class GgmlTensor(ctypes.Structure):
@@ -730,13 +740,27 @@ GgmlTensor._fields_ = [
     ("op", ctypes.c_int32),
     ("src", ctypes.POINTER(GgmlTensor) * 10),
     ("data", ctypes.c_void_p),
+    ("op_params", ctypes.c_int32 * 16),
 ]
 
-_TYPE_SIZE = {GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.Q4_0: (32, 18), GgmlType.Q8_0: (32, 34)}
+_TYPE_SIZE = {GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.Q4_0: (32, 18), GgmlType.Q8_0: (32, 34),
+              GgmlType.I32: (1, 4)}
 
 
-def ggml_tensor(type_, ne, data=None, nb=None, op=GgmlOp.NONE, src=()) -> GgmlTensor:
-    """A node with ggml's default (contiguous) strides unless nb is given."""
+def ggml_op_params(*values) -> list:
+    """op_params words from ints and floats (floats stored as their fp32
+    bits, as ggml's memcpy into op_params does)."""
+    import struct
+
+    out = []
+    for v in values:
+        out.append(struct.unpack("<i", struct.pack("<f", v))[0] if isinstance(v, float) else int(v))
+    return out
+
+
+def ggml_tensor(type_, ne, data=None, nb=None, op=GgmlOp.NONE, src=(), op_params=()) -> GgmlTensor:
+    """A node with ggml's default (contiguous) strides unless nb is given;
+    op_params: int32 words (ggml_op_params packs floats)."""
     ne = list(ne) + [1] * (4 - len(ne))
     t = GgmlTensor()
     t.type = type_
@@ -751,7 +775,10 @@ def ggml_tensor(type_, ne, data=None, nb=None, op=GgmlOp.NONE, src=()) -> GgmlTe
     for i in range(4):
         t.nb[i] = nb[i]
     for i, s_ in enumerate(src):
-        t.src[i] = ctypes.pointer(s_)
+        if s_ is not None:
+            t.src[i] = ctypes.pointer(s_)
+    for i, w in enumerate(op_params):
+        t.op_params[i] = w
     t.data = _p(data) or None
     return t
 

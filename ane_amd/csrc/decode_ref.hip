@@ -24,6 +24,7 @@
 // meet in the FADDV tree, and the kernels below keep exactly those chains.
 #include "../../include/ane_decode.h"
 #include "common.hpp"
+#include "ggml_rows.hpp"
 
 namespace ane {
 namespace {
@@ -222,16 +223,13 @@ __device__ __forceinline__ float chain16(const float* v, uint32_t n, uint32_t l)
     return acc;
 }
 
-// 0x51, one workgroup (256 threads) per row; the row is staged in LDS when
-// it fits.  Every lane of wave 0 runs chain lane & 15 (four copies of the 16
-// chains), so the FADDV tree reads only active DPP rows.
-__global__ void __launch_bounds__(256)
-k_rms_norm_ref(uint32_t dim, float eps, const float* __restrict__ in, const float* __restrict__ w,
-               float* __restrict__ out, uint64_t stride) {
+// 0x51 over one row, by one workgroup (256 threads); the row is staged in
+// LDS when it fits.  Every lane of wave 0 runs chain lane & 15 (four copies
+// of the 16 chains), so the FADDV tree reads only active DPP rows.  w ==
+// nullptr multiplies by 1.0f (unit weights).  o may alias x.
+__device__ __forceinline__ void rms_norm_row(uint32_t dim, float eps, const float* x, const float* w, float* o) {
     __shared__ float rs;
     __shared__ float xs[kStageFloats];
-    const float* x = in + blockIdx.x * stride;
-    float* o = out + blockIdx.x * stride;
     const bool staged = dim <= kStageFloats;
     if (staged) {
         for (uint32_t i = threadIdx.x; i < dim; i += 256) xs[i] = x[i];
@@ -254,7 +252,12 @@ k_rms_norm_ref(uint32_t dim, float eps, const float* __restrict__ in, const floa
     }
     __syncthreads();
     const float r = rs;
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(__fmul_rn(x[i], r), w[i]);
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(__fmul_rn(x[i], r), w ? w[i] : 1.0f);
+}
+
+__global__ void __launch_bounds__(256)
+k_rms_norm_ref(uint32_t dim, float eps, const float* in, const float* __restrict__ w, float* out, uint64_t stride) {
+    rms_norm_row(dim, eps, in + blockIdx.x * stride, w, out + blockIdx.x * stride);
 }
 
 __global__ void __launch_bounds__(256) k_silu_ref(uint64_t n, const float* __restrict__ in, float* __restrict__ out) {
@@ -279,26 +282,34 @@ k_rope_ref(uint32_t rows, uint32_t dim, uint32_t pos, float theta, const float* 
     o[2 * p + 1] = v.y;
 }
 
-// 0x56, one workgroup per row: the max (any order: max is exact), e stored
-// in out, the 16 fadd chains (in wave 0, four copies), FADDV, 1/sum, scale.
-// A dim that is not a multiple of 16 leaves the last chains shorter.
-__global__ void __launch_bounds__(256)
-k_softmax_ref(uint32_t dim, const float* __restrict__ in, float* __restrict__ out, uint64_t stride) {
+// 0x56 over one row, by one workgroup: the max (any order: max is exact), e
+// stored in out, the 16 fadd chains (in wave 0, four copies), FADDV, 1/sum,
+// scale.  A dim that is not a multiple of 16 leaves the last chains
+// shorter.  o may alias x.  NODE (ggml's SOFT_MAX): the values are
+// fl(fl(x * scale) + m) (m from mrow, or no add when mrow is null), and an
+// element whose x - max is -inf gives e = 0 (the polynomial would give NaN
+// there: floor(-inf) - -inf).
+template <bool NODE>
+__device__ __forceinline__ void softmax_row(uint32_t dim, const float* x, float* o, float scale, const float* mrow) {
     __shared__ float red[4];
     __shared__ float sinv;
     __shared__ float es[kStageFloats];
-    const float* x = in + blockIdx.x * stride;
-    float* o = out + blockIdx.x * stride;
+    auto val = [&](uint32_t i) {
+        if (!NODE) return x[i];
+        const float v = __fmul_rn(x[i], scale);
+        return mrow ? __fadd_rn(v, mrow[i]) : v;
+    };
     const bool staged = dim <= kStageFloats;
     float m = -__builtin_inff();
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) m = fmax_nan(m, x[i]);
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) m = fmax_nan(m, val(i));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmax_nan(m, __shfl_xor(m, off, 64));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmax_nan(fmax_nan(red[0], red[1]), fmax_nan(red[2], red[3]));
     for (uint32_t i = threadIdx.x; i < dim; i += 256) {
-        const float e = exp_poly_a(__fsub_rn(x[i], m), true);
+        const float d = __fsub_rn(val(i), m);
+        const float e = NODE && d == -__builtin_inff() ? 0.0f : exp_poly_a(d, true);
         if (staged) es[i] = e;
         else o[i] = e;
     }
@@ -311,6 +322,48 @@ k_softmax_ref(uint32_t dim, const float* __restrict__ in, float* __restrict__ ou
     __syncthreads();
     const float inv = sinv;
     for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(staged ? es[i] : o[i], inv);
+}
+
+__global__ void __launch_bounds__(256) k_softmax_ref(uint32_t dim, const float* in, float* out, uint64_t stride) {
+    softmax_row<false>(dim, in + blockIdx.x * stride, out + blockIdx.x * stride, 1.0f, nullptr);
+}
+
+// ------------------------------------------------------ ggml node forms
+// One workgroup per row of the node (ggml_rows.hpp); the rows' operands
+// may sit anywhere their strides put them.
+__global__ void __launch_bounds__(256)
+k_rms_norm_node(uint32_t dim, float eps, const uint8_t* in, NodeRows src, uint8_t* out, NodeRows dst) {
+    const RowIdx i = row_index(dst, blockIdx.x);
+    rms_norm_row(dim, eps, reinterpret_cast<const float*>(in + row_offset(src, i)), nullptr,
+                 reinterpret_cast<float*>(out + row_offset(dst, i)));
+}
+
+__global__ void __launch_bounds__(256)
+k_softmax_node(uint32_t dim, float scale, const uint8_t* in, NodeRows src, const uint8_t* mask, NodeRows msk,
+               uint8_t* out, NodeRows dst) {
+    const RowIdx i = row_index(dst, blockIdx.x);
+    softmax_row<true>(dim, reinterpret_cast<const float*>(in + row_offset(src, i)),
+                      reinterpret_cast<float*>(out + row_offset(dst, i)), scale,
+                      mask ? reinterpret_cast<const float*>(mask + row_offset(msk, i)) : nullptr);
+}
+
+// One thread per pair, grid-stride over rows * dim/2 pairs.  Both values of
+// a pair are read before either is written, so out may alias in.
+__global__ void __launch_bounds__(256)
+k_rope_node(uint32_t dim, uint64_t total, float theta, const int32_t* __restrict__ pos, const uint8_t* in,
+            NodeRows src, uint8_t* out, NodeRows dst) {
+    const uint32_t pairs = dim / 2;
+    const float ratio = rope_ratio_a(dim, theta);
+    for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (uint64_t)gridDim.x * 256) {
+        const uint64_t row = t / pairs;
+        const uint32_t p = (uint32_t)(t - row * pairs);
+        const RowIdx i = row_index(dst, row);
+        const float* x = reinterpret_cast<const float*>(in + row_offset(src, i));
+        float* o = reinterpret_cast<float*>(out + row_offset(dst, i));
+        const float2 v = rope_pair_a(x[2 * p], x[2 * p + 1], p, ratio, (float)pos[i.i2]);
+        o[2 * p] = v.x;
+        o[2 * p + 1] = v.y;
+    }
 }
 
 __device__ __forceinline__ uint16_t f16_bits(float f) {
@@ -488,6 +541,37 @@ int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t
                        ctx, q, kc, sc);
     hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
     hipLaunchKernelGGL(k_attn_pv_ref, dim3(n_kv * 8), dim3(256), 0, s, len, ctx, pr, vc, out);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int rms_norm_node_launch(uint32_t dim, uint64_t rows, float eps, const uint8_t* in, const NodeRows& src,
+                         uint8_t* out, const NodeRows& dst, hipStream_t s) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (rows > 0x7fffffffu) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_rms_norm_node, dim3((uint32_t)rows), dim3(256), 0, s, dim, eps, in, src, out, dst);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int softmax_node_launch(uint32_t dim, uint64_t rows, float scale, const uint8_t* in, const NodeRows& src,
+                        const uint8_t* mask, const NodeRows& msk, uint8_t* out, const NodeRows& dst, hipStream_t s) {
+    if (rows == 0 || dim == 0) return ANE_OK;
+    if (rows > 0x7fffffffu) return ANE_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(k_softmax_node, dim3((uint32_t)rows), dim3(256), 0, s, dim, scale, in, src, mask, msk, out,
+                       dst);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+int rope_node_launch(uint32_t dim, uint64_t rows, float theta, const int32_t* pos, const uint8_t* in,
+                     const NodeRows& src, uint8_t* out, const NodeRows& dst, hipStream_t s) {
+    const uint64_t total = rows * (dim / 2);
+    if (total == 0) return ANE_OK;
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_rope_node, dim3((uint32_t)blocks), dim3(256), 0, s, dim, total, theta, pos, in, src, out,
+                       dst);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }

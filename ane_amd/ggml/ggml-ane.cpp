@@ -1,7 +1,9 @@
 // ggml-ane.cpp -- the ggml backend registry of ane_amd: device "ANE0", a
 // device-memory buffer type and a backend whose graph_compute runs
-// GGML_OP_MUL_MAT with Q8_0 / Q4_0 weights on the MI355X kernels behind
-// include/ggml-ane-hip.h (ane_ggml_supports_op / ane_ggml_compute_forward).
+// GGML_OP_MUL_MAT with Q8_0 / Q4_0 weights and the fp32 ops ADD, MUL, SCALE,
+// RMS_NORM, SOFT_MAX, SILU, ROPE and CPY/CONT/DUP on the MI355X kernels
+// behind include/ggml-ane-hip.h (ane_ggml_supports_op /
+// ane_ggml_compute_forward).
 //
 // Replaces src/ggml-backend/ggml-ane.cpp of the reference: registry
 // (:412-436), device (:302-410), buffer type (:29-95), backend (:97-104,
@@ -25,10 +27,13 @@
 //    downloads are hipMemcpy;
 //  - MUL_MAT computes every token (ne11) and broadcast batch with nb[]
 //    strides (the reference computes token 0 only); F32 weights (the
-//    reference's cblas_sgemm route) and the other ops it claims (ADD, MUL,
-//    SCALE, RMS_NORM, SOFT_MAX, SILU, ROPE, CPY) are not claimed, so ggml's
-//    scheduler runs them on its CPU backend; view ops are claimed and cost
-//    nothing;
+//    reference's cblas_sgemm route) are not claimed, so ggml's scheduler
+//    runs those products on its CPU backend;
+//  - ADD, MUL, SCALE, RMS_NORM, SOFT_MAX, SILU, ROPE and CPY/CONT/DUP are
+//    claimed only where the shim computes ggml's semantics (broadcasting,
+//    strides, the softmax scale and mask, RoPE's freq_base and per-token
+//    positions from ggml's op_params layout), which the reference's
+//    handlers do not (:155-277); view ops are claimed and cost nothing;
 //  - graph_compute launches every node on the backend's own HIP stream and
 //    synchronises once at the end; a node it cannot run fails the graph with
 //    GGML_STATUS_FAILED and one stderr line, like the reference (:291-295).
@@ -70,30 +75,71 @@ bool is_view_op(enum ggml_op op) {
            op == GGML_OP_TRANSPOSE;
 }
 
-// The shim's tensor for one ggml tensor (types keep ggml's on-disk values).
+// ggml_type -> the shim's type values (ggml's on-disk numbers for the
+// formats it knows; -1 for any other type, which nothing claims).
+int32_t ane_type(enum ggml_type t) {
+    switch (t) {
+        case GGML_TYPE_F32: return ANE_GGML_TYPE_F32;
+        case GGML_TYPE_F16: return ANE_GGML_TYPE_F16;
+        case GGML_TYPE_Q4_0: return ANE_GGML_TYPE_Q4_0;
+        case GGML_TYPE_Q8_0: return ANE_GGML_TYPE_Q8_0;
+        case GGML_TYPE_I32: return ANE_GGML_TYPE_I32;
+        default: return -1;
+    }
+}
+
+int32_t ane_op(const ggml_tensor* t) {
+    switch (t->op) {
+        case GGML_OP_MUL_MAT: return ANE_GGML_OP_MUL_MAT;
+        case GGML_OP_ADD: return ANE_GGML_OP_ADD;
+        case GGML_OP_MUL: return ANE_GGML_OP_MUL;
+        case GGML_OP_SCALE: return ANE_GGML_OP_SCALE;
+        case GGML_OP_RMS_NORM: return ANE_GGML_OP_RMS_NORM;
+        case GGML_OP_SOFT_MAX: return ANE_GGML_OP_SOFT_MAX;
+        case GGML_OP_ROPE: return ANE_GGML_OP_ROPE;
+        case GGML_OP_UNARY:
+            return ggml_get_unary_op(t) == GGML_UNARY_OP_SILU ? ANE_GGML_OP_SILU : ANE_GGML_OP_OTHER;
+        case GGML_OP_CPY:
+        case GGML_OP_CONT:
+        case GGML_OP_DUP: return ANE_GGML_OP_CPY;
+        default: return ANE_GGML_OP_OTHER;
+    }
+}
+
+// The shim's tensor for one ggml tensor.
 void to_ane(const ggml_tensor* t, ane_ggml_tensor* out) {
     std::memset(out, 0, sizeof(*out));
-    out->type = (int32_t)t->type;
+    out->type = ane_type(t->type);
     for (int d = 0; d < ANE_GGML_MAX_DIMS; d++) {
         out->ne[d] = t->ne[d];
         out->nb[d] = t->nb[d];
     }
-    out->op = t->op == GGML_OP_MUL_MAT ? ANE_GGML_OP_MUL_MAT : ANE_GGML_OP_OTHER;
+    out->op = ane_op(t);
+    static_assert(sizeof(out->op_params) <= sizeof(t->op_params), "ggml op_params smaller than the shim's");
+    std::memcpy(out->op_params, t->op_params, sizeof(out->op_params));
     out->data = t->data;
 }
 
-// MUL_MAT node with its two sources, in the shim's form.
-struct MulMat {
-    ane_ggml_tensor dst, src0, src1;
-    bool ok;
-    explicit MulMat(const ggml_tensor* node) : ok(false) {
-        if (node->op != GGML_OP_MUL_MAT || !node->src[0] || !node->src[1]) return;
+// A node with its first three sources (MUL_MAT's weights and activations,
+// a binary op's operands, SOFT_MAX's mask and sinks, ROPE's positions and
+// frequency factors), in the shim's form.
+struct Node {
+    static constexpr int kSrc = 3;
+    ane_ggml_tensor dst, src[kSrc];
+    explicit Node(const ggml_tensor* node) {
         to_ane(node, &dst);
-        to_ane(node->src[0], &src0);
-        to_ane(node->src[1], &src1);
-        dst.src[0] = &src0;
-        dst.src[1] = &src1;
-        ok = true;
+        for (int i = 0; i < kSrc; i++) {
+            if (!node->src[i]) continue;
+            to_ane(node->src[i], &src[i]);
+            dst.src[i] = &src[i];
+        }
+    }
+    // Sources past the third are not looked at by any op the shim claims;
+    // a node that has one is not claimed.
+    static bool fits(const ggml_tensor* node) {
+        for (int i = kSrc; i < GGML_MAX_SRC; i++)
+            if (node->src[i]) return false;
+        return true;
     }
 };
 
@@ -168,8 +214,8 @@ enum ggml_status be_graph_compute(ggml_backend_t backend, ggml_cgraph* cgraph) {
     for (int i = 0; i < n; i++) {
         ggml_tensor* node = ggml_graph_node(cgraph, i);
         if (ggml_is_empty(node) || is_view_op(node->op)) continue;
-        const MulMat mm(node);
-        const int st = mm.ok ? ane_ggml_compute_forward(c->be, &mm.dst) : (int)ANE_ERR_INVALID_ARG;
+        const Node nd(node);
+        const int st = Node::fits(node) ? ane_ggml_compute_forward(c->be, &nd.dst) : (int)ANE_ERR_INVALID_ARG;
         if (st != 0) {
             std::fprintf(stderr, "ANE backend: cannot compute node %d (%s, status %d)\n", i, ggml_op_name(node->op),
                          st);
@@ -221,8 +267,9 @@ ggml_backend_t dev_init_backend(ggml_backend_dev_t dev, const char*) {
 ggml_backend_buffer_type_t dev_buffer_type(ggml_backend_dev_t) { return &g_buft; }
 bool dev_supports_op(ggml_backend_dev_t, const ggml_tensor* op) {
     if (is_view_op(op->op)) return true;
-    const MulMat mm(op);
-    return mm.ok && ane_ggml_supports_op(&mm.dst) == 1;
+    if (!Node::fits(op)) return false;
+    const Node nd(op);
+    return ane_ggml_supports_op(&nd.dst) == 1;
 }
 bool dev_supports_buft(ggml_backend_dev_t, ggml_backend_buffer_type_t buft) { return buft == &g_buft; }
 

@@ -3,9 +3,10 @@
  * ane_amd/ggml/ggml-ane.cpp uses, so the adapter builds and runs in the
  * tests without a ggml tree.  It is not ggml: names and meanings follow
  * ggml's public header (the ggml_tensor members, the ggml_type values,
- * which are ggml's on-disk format; the graph accessors), the ggml_op values
- * here are this file's own, and the adapter depends on none of them by
- * value.  In a real build the adapter is compiled against ggml's headers.
+ * which are ggml's on-disk format; the graph accessors, ggml_get_unary_op),
+ * the ggml_op and ggml_unary_op values here are this file's own, and the
+ * adapter depends on none of them by value.  In a real build the adapter is
+ * compiled against ggml's headers.
  */
 #pragma once
 
@@ -36,6 +37,7 @@ enum ggml_type {
     GGML_TYPE_Q4_K = 12,
     GGML_TYPE_Q5_K = 13,
     GGML_TYPE_Q6_K = 14,
+    GGML_TYPE_I32 = 26,
 };
 
 enum ggml_op {
@@ -56,6 +58,21 @@ enum ggml_op {
     GGML_OP_ROPE,
     GGML_OP_UNARY,
     GGML_OP_COUNT,
+};
+
+enum ggml_unary_op {
+    GGML_UNARY_OP_ABS,
+    GGML_UNARY_OP_SGN,
+    GGML_UNARY_OP_NEG,
+    GGML_UNARY_OP_STEP,
+    GGML_UNARY_OP_TANH,
+    GGML_UNARY_OP_ELU,
+    GGML_UNARY_OP_RELU,
+    GGML_UNARY_OP_SIGMOID,
+    GGML_UNARY_OP_GELU,
+    GGML_UNARY_OP_GELU_QUICK,
+    GGML_UNARY_OP_SILU,
+    GGML_UNARY_OP_COUNT,
 };
 
 enum ggml_status {
@@ -94,6 +111,7 @@ GGML_API struct ggml_tensor* ggml_graph_node(struct ggml_cgraph* cgraph, int i);
 GGML_API bool ggml_is_empty(const struct ggml_tensor* tensor);
 GGML_API size_t ggml_nbytes(const struct ggml_tensor* tensor);
 GGML_API const char* ggml_op_name(enum ggml_op op);
+GGML_API enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor* tensor);
 
 #ifdef __cplusplus
 }

@@ -2,7 +2,9 @@
 // adapter calls (graph accessors, ggml_nbytes, ggml_backend_buffer_init ...),
 // restated after ggml's definitions, and C entry points that drive the
 // registry the way ggml's scheduler would (device -> buffer type -> buffer
-// -> tensors -> graph_compute), for tests/test_ggml_registry.py.
+// -> tensors -> graph_compute), for tests/test_ggml_registry.py and
+// tests/test_ggml_ops.py.
+#include <cstddef>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -45,16 +47,14 @@ size_t ggml_nbytes(const ggml_tensor* t) {
     return n;
 }
 
-const char* ggml_op_name(ggml_op op) {
-    switch (op) {
-        case GGML_OP_NONE: return "NONE";
-        case GGML_OP_ADD: return "ADD";
-        case GGML_OP_MUL_MAT: return "MUL_MAT";
-        case GGML_OP_VIEW: return "VIEW";
-        case GGML_OP_SOFT_MAX: return "SOFT_MAX";
-        default: return "OTHER";
-    }
-}
+static const char* const kOpNames[GGML_OP_COUNT] = {
+    "NONE", "DUP", "ADD", "MUL", "SCALE", "RMS_NORM", "MUL_MAT", "CPY", "CONT", "RESHAPE",
+    "VIEW", "PERMUTE", "TRANSPOSE", "SOFT_MAX", "ROPE", "UNARY"};
+
+const char* ggml_op_name(ggml_op op) { return op >= 0 && op < GGML_OP_COUNT ? kOpNames[op] : "?"; }
+
+// ggml keeps a unary node's op in op_params[0].
+ggml_unary_op ggml_get_unary_op(const ggml_tensor* t) { return (ggml_unary_op)t->op_params[0]; }
 
 ggml_backend_buffer_t ggml_backend_buffer_init(ggml_backend_buffer_type_t buft, ggml_backend_buffer_i iface,
                                                void* context, size_t size) {
@@ -68,6 +68,53 @@ ggml_backend_buffer_t ggml_backend_buffer_init(ggml_backend_buffer_type_t buft, 
 }
 
 // ---------------------------------------------------------------- harness
+// This header's ggml_op value for an op name (-1 if unknown), and the
+// value of GGML_UNARY_OP_SILU, for tests that build ggml_tensor nodes.
+int ggml_ane_test_op(const char* name) {
+    for (int i = 0; i < GGML_OP_COUNT; i++)
+        if (std::strcmp(kOpNames[i], name) == 0) return i;
+    return -1;
+}
+int ggml_ane_test_unary_silu(void) { return GGML_UNARY_OP_SILU; }
+
+// sizeof(ggml_tensor) and the offsets of its members, in declaration order.
+int ggml_ane_test_layout(size_t* out, int n) {
+    const size_t v[] = {sizeof(ggml_tensor), offsetof(ggml_tensor, type), offsetof(ggml_tensor, buffer),
+                        offsetof(ggml_tensor, ne), offsetof(ggml_tensor, nb), offsetof(ggml_tensor, op),
+                        offsetof(ggml_tensor, op_params), offsetof(ggml_tensor, flags), offsetof(ggml_tensor, src),
+                        offsetof(ggml_tensor, view_src), offsetof(ggml_tensor, view_offs),
+                        offsetof(ggml_tensor, data), offsetof(ggml_tensor, name), offsetof(ggml_tensor, extra),
+                        offsetof(ggml_tensor, padding)};
+    const int k = (int)(sizeof(v) / sizeof(v[0]));
+    for (int i = 0; i < k && i < n; i++) out[i] = v[i];
+    return k;
+}
+
+// The device's supports_op for a node built by the caller.
+int ggml_ane_test_supports_node(const ggml_tensor* node) {
+    ggml_backend_reg_t reg = ggml_backend_ane_reg();
+    ggml_backend_dev_t dev = reg->iface.get_device(reg, 0);
+    return dev->iface.supports_op(dev, node) ? 1 : 0;
+}
+
+// A backend of the device, and graph_compute over caller-built nodes whose
+// data already point to device memory (as tensors in the backend's buffers
+// do).
+void* ggml_ane_test_backend_new(void) {
+    ggml_backend_reg_t reg = ggml_backend_ane_reg();
+    ggml_backend_dev_t dev = reg->iface.get_device(reg, 0);
+    return dev->iface.init_backend(dev, nullptr);
+}
+void ggml_ane_test_backend_free(void* be) {
+    auto* b = static_cast<ggml_backend_t>(be);
+    if (b) b->iface.free(b);
+}
+int ggml_ane_test_graph(void* be, ggml_tensor** nodes, int n) {
+    auto* b = static_cast<ggml_backend_t>(be);
+    ggml_cgraph g{n, nodes};
+    return (int)b->iface.graph_compute(b, &g);
+}
+
 static void contiguous(ggml_tensor* t, ggml_type type, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3) {
     std::memset(t, 0, sizeof(*t));
     t->type = type;
@@ -169,18 +216,19 @@ int ggml_ane_test_mul_mat(int type0, int N, int K, int T, const void* W, const f
     return st;
 }
 
-// A graph holding a node the backend does not run (ADD) fails with
-// GGML_STATUS_FAILED before launching anything (the ADD is not touched).
+// A graph holding a node the backend does not run (MUL_MAT with F32
+// weights) fails with GGML_STATUS_FAILED before launching anything (the node
+// is not touched: its data stay null).
 int ggml_ane_test_unsupported_graph(void) {
     ggml_backend_reg_t reg = ggml_backend_ane_reg();
     ggml_backend_dev_t dev = reg->iface.get_device(reg, 0);
     ggml_backend_t be = dev->iface.init_backend(dev, nullptr);
     if (!be) return -101;
     ggml_tensor a, b, d;
-    contiguous(&a, GGML_TYPE_F32, 16, 1, 1, 1);
-    contiguous(&b, GGML_TYPE_F32, 16, 1, 1, 1);
+    contiguous(&a, GGML_TYPE_F32, 64, 16, 1, 1);
+    contiguous(&b, GGML_TYPE_F32, 64, 1, 1, 1);
     contiguous(&d, GGML_TYPE_F32, 16, 1, 1, 1);
-    d.op = GGML_OP_ADD;
+    d.op = GGML_OP_MUL_MAT;
     d.src[0] = &a;
     d.src[1] = &b;
     ggml_tensor* nodes[1] = {&d};

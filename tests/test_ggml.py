@@ -40,14 +40,15 @@ def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "ggml-ane-hip.h"\n'
-        "int main(void) { printf(\"%zu %zu %zu %zu %zu %zu\\n\", sizeof(struct ane_ggml_tensor),"
+        "int main(void) { printf(\"%zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(struct ane_ggml_tensor),"
         " offsetof(struct ane_ggml_tensor, ne), offsetof(struct ane_ggml_tensor, nb),"
         " offsetof(struct ane_ggml_tensor, op), offsetof(struct ane_ggml_tensor, src),"
-        " offsetof(struct ane_ggml_tensor, data)); return 0; }\n")
+        " offsetof(struct ane_ggml_tensor, data), offsetof(struct ane_ggml_tensor, op_params)); return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run([gcc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    want = [ctypes.sizeof(GgmlTensor)] + [getattr(GgmlTensor, f).offset for f in ("ne", "nb", "op", "src", "data")]
+    fields = ("ne", "nb", "op", "src", "data", "op_params")
+    want = [ctypes.sizeof(GgmlTensor)] + [getattr(GgmlTensor, f).offset for f in fields]
     assert got == want
 
 

@@ -9,7 +9,8 @@ names, counts, device type, buffer-type facts and supports_op decisions
 GPU: MUL_MAT through the registry (device buffer, set_tensor, a graph with
 a view node, graph_compute, get_tensor) bit-identical to the oracle, for
 Q8_0 (every token) and Q4_0 weights; a graph holding an op the backend does
-not run fails with GGML_STATUS_FAILED.
+not run (MUL_MAT with F32 weights) fails with GGML_STATUS_FAILED.  The fp32
+ops are covered in tests/test_ggml_ops.py.
 
 ggml's own behaviour around the backend (its scheduler, its op numbering)
 is not available here and stays unpinned.
@@ -83,7 +84,8 @@ def test_supports_op_decisions(fresh):
     assert not supports(t, typed=T_F16)
     assert not supports(t, A2=3, B2=4)       # not broadcastable
     assert supports(t, op=1, type0=T_F32, K=16, N=1, T=1)    # a view: no compute
-    assert not supports(t, op=2, type0=T_F32, K=16, N=1, T=1)  # ADD: not claimed
+    assert supports(t, op=2, type0=T_F32, K=16, N=16, T=16)  # ADD of equal shapes
+    assert not supports(t, op=2, type0=T_F32, K=16, N=1, T=1)  # ADD of src0 [16,1] into dst [1,1]
 
 
 # ------------------------------------------------------------------ GPU
