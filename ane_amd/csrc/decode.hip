@@ -582,6 +582,8 @@ struct MulMatNode {
 
 int rms_norm_ref_launch(uint32_t rows, uint32_t dim, float eps, const float* in, const float* w, float* out,
                         uint64_t stride, hipStream_t s);
+int add_rms_norm_ref_launch(uint32_t dim, float eps, float* x, const float* y, const float* w, float* xn,
+                            hipStream_t s);
 int rope_ref_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos, uint32_t ctx, float theta,
                        uint16_t* kc, uint16_t* vc, hipStream_t s);
 int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
@@ -778,8 +780,10 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
     };
     for (uint32_t l = 0; l < cfg->n_layers; l++) {
         const ane_decode_layer& L = layers[l];
-        if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.attn_norm, w.xn, H, s));
-        else if (l == 0) ANE_TRY(ane_hip_rms_norm(H, x, L.attn_norm, cfg->eps, w.xn, s));
+        if (l == 0) {
+            if (ref) ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.attn_norm, w.xn, H, s));
+            else ANE_TRY(ane_hip_rms_norm(H, x, L.attn_norm, cfg->eps, w.xn, s));
+        }
         {
             const MulMatNode n(L.w_qkv, nqkv, H, w.xn, w.qkv);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
@@ -798,8 +802,7 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
         }
         if (ref) {
-            hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
-            ANE_TRY(rms_norm_ref_launch(1, H, cfg->eps, x, L.ffn_norm, w.xn, H, s));
+            ANE_TRY(add_rms_norm_ref_launch(H, cfg->eps, x, w.y, L.ffn_norm, w.xn, s));
         } else {
             add_norm(w.y, L.ffn_norm);
         }
@@ -813,8 +816,14 @@ extern "C" int ane_decode_token_ggml(const ane_decode_config* cfg, const ane_dec
             const MulMatNode n(L.w_down, H, F, w.h, w.y);
             ANE_TRY(ane_ggml_compute_forward(backend, &n.d));
         }
-        if (!ref && l + 1 < cfg->n_layers) add_norm(w.y, layers[l + 1].attn_norm);
-        else hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+        // the residual add rides on the next layer's norm (the same fl(x + y)
+        // then the norm of the sum, in one launch)
+        if (l + 1 < cfg->n_layers) {
+            if (ref) ANE_TRY(add_rms_norm_ref_launch(H, cfg->eps, x, w.y, layers[l + 1].attn_norm, w.xn, s));
+            else add_norm(w.y, layers[l + 1].attn_norm);
+        } else {
+            hipLaunchKernelGGL(k_add, dim3(gA), dim3(256), 0, s, H, x, w.y, x);
+        }
         ANE_HIP_CHECK_LAUNCH();
     }
 #undef ANE_TRY

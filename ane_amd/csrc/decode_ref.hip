@@ -204,10 +204,11 @@ __device__ __forceinline__ float fmax_nan(float a, float b) {
     return a > b ? a : b;
 }
 
-constexpr uint32_t kStageFloats = 8192;  // rows up to this long are staged in LDS (32 KB)
+constexpr uint32_t kStageFloats = 8192;  // rows up to this long are held in registers and LDS
 
 // chain l of a 16-lane accumulation over v[0..n): acc = op(v[i], acc) for
 // i = l, l + 16, ... in order; 8 values are loaded ahead of each 8 steps.
+// (Rows longer than kStageFloats, read from global memory.)
 template <bool FMA_SQ>
 __device__ __forceinline__ float chain16(const float* v, uint32_t n, uint32_t l) {
     float acc = 0.0f;
@@ -223,41 +224,159 @@ __device__ __forceinline__ float chain16(const float* v, uint32_t n, uint32_t l)
     return acc;
 }
 
-// 0x51 over one row, by one workgroup (256 threads); the row is staged in
-// LDS when it fits.  Every lane of wave 0 runs chain lane & 15 (four copies
-// of the 16 chains), so the FADDV tree reads only active DPP rows.  w ==
-// nullptr multiplies by 1.0f (unit weights).  o may alias x.
-__device__ __forceinline__ void rms_norm_row(uint32_t dim, float eps, const float* x, const float* w, float* o) {
-    __shared__ float rs;
-    __shared__ float xs[kStageFloats];
-    const bool staged = dim <= kStageFloats;
-    if (staged) {
-        for (uint32_t i = threadIdx.x; i < dim; i += 256) xs[i] = x[i];
-        __syncthreads();
+// A row of up to kStageFloats values held by a workgroup of 256 threads:
+// thread t keeps elements t + 256u (u < kItems) in registers, and the row
+// is also written to LDS transposed by chain, element i at
+// ct[(i % 16) * kChainStride + i / 16], so chain l reads its elements in
+// order with 16-byte loads.  Slots from the row's end to the next multiple
+// of 64 hold +0, which adds nothing to a chain (every chain's partial is
+// +0 or positive: sums of squares, sums of exponentials).  kChainStride is 4
+// mod 64 words, so the 16 chains' rows start in distinct 4-bank groups.
+constexpr uint32_t kItems = kStageFloats / 256;
+constexpr uint32_t kChainStride = kStageFloats / 16 + 4;
+
+__device__ __forceinline__ void stage_chains(float* ct, uint32_t dim, const float (&v)[kItems]) {
+    const uint32_t nz = (dim + 63) & ~63u;
+#pragma unroll
+    for (uint32_t u = 0; u < kItems; u++) {
+        const uint32_t i = threadIdx.x + 256 * u;
+        if (i < nz) ct[(i & 15) * kChainStride + (i >> 4)] = i < dim ? v[u] : 0.0f;
     }
-    if (threadIdx.x < 64) {
-        const uint32_t l = threadIdx.x & 15;
-        const float acc = chain16<true>(staged ? xs : x, dim, l);
-        const float ss = faddv16(acc);
-        const float mean = __fdiv_rn(ss, (float)dim);
-        const float t = __fadd_rn(mean, eps);
-        float r = frsqrte_a(t);
-        float s = __fmul_rn(r, r);
-        s = frsqrts_a(t, s);
-        r = __fmul_rn(r, s);
-        s = __fmul_rn(r, r);
-        s = frsqrts_a(t, s);
-        r = __fmul_rn(r, s);
-        if (threadIdx.x == 0) rs = r;
+}
+
+template <bool FMA_SQ>
+__device__ __forceinline__ float chain16_staged(const float* ct, uint32_t dim, uint32_t l) {
+    const float4* c = reinterpret_cast<const float4*>(ct + l * kChainStride);
+    const uint32_t n4 = (dim + 63) / 64;  // 4-element groups per chain, zero tail included
+    float acc = 0.0f;
+    auto step = [&](float t) { acc = FMA_SQ ? __builtin_fmaf(t, t, acc) : __fadd_rn(acc, t); };
+    uint32_t q = 0;
+    for (; q + 4 <= n4; q += 4) {
+        float4 t[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) t[k] = c[q + k];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            step(t[k].x);
+            step(t[k].y);
+            step(t[k].z);
+            step(t[k].w);
+        }
+    }
+    for (; q < n4; q++) {
+        const float4 t = c[q];
+        step(t.x);
+        step(t.y);
+        step(t.z);
+        step(t.w);
+    }
+    return acc;
+}
+
+// 1/sqrt(mean + eps) as 0x51 computes it from the FADDV of the chains.
+__device__ __forceinline__ float rms_factor(float acc, uint32_t dim, float eps) {
+    const float ss = faddv16(acc);
+    const float mean = __fdiv_rn(ss, (float)dim);
+    const float t = __fadd_rn(mean, eps);
+    float r = frsqrte_a(t);
+    float s = __fmul_rn(r, r);
+    s = frsqrts_a(t, s);
+    r = __fmul_rn(r, s);
+    s = __fmul_rn(r, r);
+    s = frsqrts_a(t, s);
+    return __fmul_rn(r, s);
+}
+
+// f(u) for the items u of a staged row, in groups of 8 whose condition
+// (the group holds an element of the row) is the same for the whole
+// workgroup.  f loads element min(t + 256u, dim - 1) with no condition, so
+// a group's loads are all in flight before the first is used.
+template <class F>
+__device__ __forceinline__ void for_item_groups(uint32_t dim, F&& f) {
+#pragma unroll
+    for (uint32_t g = 0; g < kItems / 8; g++) {
+        if (g * 2048 < dim) {
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) f(g * 8 + k);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t item_index(uint32_t u, uint32_t dim) {
+    const uint32_t i = threadIdx.x + 256 * u;
+    return i < dim ? i : dim - 1;
+}
+
+// 0x51 over one row, by one workgroup (256 threads).  Every lane of wave 0
+// runs chain lane & 15 (four copies of the 16 chains), so the FADDV tree
+// reads only active DPP rows.  HAS_W: weights w (else 1.0f, unit weights).
+// HAS_Y: the row is fl(x + y) (a residual add), written back to xsum.  o
+// may alias x.
+template <bool HAS_W, bool HAS_Y>
+__device__ __forceinline__ void rms_norm_row(uint32_t dim, float eps, const float* x, const float* w, float* o,
+                                             const float* y, float* xsum) {
+    __shared__ float rs;
+    __shared__ __attribute__((aligned(16))) float ct[16 * kChainStride];
+    const uint32_t t = threadIdx.x;
+    if (dim <= kStageFloats) {
+        float v[kItems], wv[kItems], yv[kItems];
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++) v[u] = wv[u] = yv[u] = 0.0f;
+        for_item_groups(dim, [&](uint32_t u) {
+            const uint32_t i = item_index(u, dim);
+            v[u] = x[i];
+            if (HAS_W) wv[u] = w[i];
+            if (HAS_Y) yv[u] = y[i];
+        });
+        if (HAS_Y) {
+#pragma unroll
+            for (uint32_t u = 0; u < kItems; u++) v[u] = __fadd_rn(v[u], yv[u]);
+        }
+        stage_chains(ct, dim, v);
+        __syncthreads();
+        if (t < 64) {
+            const float r = rms_factor(chain16_staged<true>(ct, dim, t & 15), dim, eps);
+            if (t == 0) rs = r;
+        }
+        __syncthreads();
+        const float r = rs;
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++) {
+            const uint32_t i = t + 256 * u;
+            if (i < dim) {
+                o[i] = __fmul_rn(__fmul_rn(v[u], r), HAS_W ? wv[u] : 1.0f);
+                if (HAS_Y) xsum[i] = v[u];
+            }
+        }
+        return;
+    }
+    // longer rows: chains over global memory (the sum, if any, written first)
+    if (HAS_Y) {
+        for (uint32_t i = t; i < dim; i += 256) xsum[i] = __fadd_rn(x[i], y[i]);
+        __threadfence_block();
+        __syncthreads();
+        x = xsum;
+    }
+    if (t < 64) {
+        const float r = rms_factor(chain16<true>(x, dim, t & 15), dim, eps);
+        if (t == 0) rs = r;
     }
     __syncthreads();
     const float r = rs;
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(__fmul_rn(x[i], r), w ? w[i] : 1.0f);
+    for (uint32_t i = t; i < dim; i += 256) o[i] = __fmul_rn(__fmul_rn(x[i], r), HAS_W ? w[i] : 1.0f);
 }
 
 __global__ void __launch_bounds__(256)
 k_rms_norm_ref(uint32_t dim, float eps, const float* in, const float* __restrict__ w, float* out, uint64_t stride) {
-    rms_norm_row(dim, eps, in + blockIdx.x * stride, w, out + blockIdx.x * stride);
+    rms_norm_row<true, false>(dim, eps, in + blockIdx.x * stride, w, out + blockIdx.x * stride, nullptr, nullptr);
+}
+
+// x = fl(x + y), xn = 0x51(x) with weights w: one row (the residual add of
+// the reference-arithmetic decode, then its norm).
+__global__ void __launch_bounds__(256)
+k_add_rms_norm_ref(uint32_t dim, float eps, float* x, const float* __restrict__ y, const float* __restrict__ w,
+                   float* __restrict__ xn) {
+    rms_norm_row<true, true>(dim, eps, x, w, xn, y, x);
 }
 
 __global__ void __launch_bounds__(256) k_silu_ref(uint64_t n, const float* __restrict__ in, float* __restrict__ out) {
@@ -282,10 +401,10 @@ k_rope_ref(uint32_t rows, uint32_t dim, uint32_t pos, float theta, const float* 
     o[2 * p + 1] = v.y;
 }
 
-// 0x56 over one row, by one workgroup: the max (any order: max is exact), e
-// stored in out, the 16 fadd chains (in wave 0, four copies), FADDV, 1/sum,
-// scale.  A dim that is not a multiple of 16 leaves the last chains
-// shorter.  o may alias x.  NODE (ggml's SOFT_MAX): the values are
+// 0x56 over one row, by one workgroup: the max (any order: max is exact),
+// e = exp(x - max), the 16 fadd chains (in wave 0, four copies), FADDV,
+// 1/sum, fl(e * inv).  A dim that is not a multiple of 16 leaves the last
+// chains shorter.  o may alias x.  NODE (ggml's SOFT_MAX): the values are
 // fl(fl(x * scale) + m) (m from mrow, or no add when mrow is null), and an
 // element whose x - max is -inf gives e = 0 (the polynomial would give NaN
 // there: floor(-inf) - -inf).
@@ -293,35 +412,62 @@ template <bool NODE>
 __device__ __forceinline__ void softmax_row(uint32_t dim, const float* x, float* o, float scale, const float* mrow) {
     __shared__ float red[4];
     __shared__ float sinv;
-    __shared__ float es[kStageFloats];
+    __shared__ __attribute__((aligned(16))) float ct[16 * kChainStride];
+    const uint32_t t = threadIdx.x;
     auto val = [&](uint32_t i) {
         if (!NODE) return x[i];
         const float v = __fmul_rn(x[i], scale);
         return mrow ? __fadd_rn(v, mrow[i]) : v;
     };
-    const bool staged = dim <= kStageFloats;
-    float m = -__builtin_inff();
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) m = fmax_nan(m, val(i));
+    auto expd = [&](float v, float m) {
+        const float d = __fsub_rn(v, m);
+        return NODE && d == -__builtin_inff() ? 0.0f : exp_poly_a(d, true);
+    };
+    auto max_of = [&](float m) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmax_nan(m, __shfl_xor(m, off, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmax_nan(fmax_nan(red[0], red[1]), fmax_nan(red[2], red[3]));
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) {
-        const float d = __fsub_rn(val(i), m);
-        const float e = NODE && d == -__builtin_inff() ? 0.0f : exp_poly_a(d, true);
-        if (staged) es[i] = e;
-        else o[i] = e;
+        for (int off = 32; off >= 1; off >>= 1) m = fmax_nan(m, __shfl_xor(m, off, 64));
+        if ((t & 63) == 0) red[t >> 6] = m;
+        __syncthreads();
+        return fmax_nan(fmax_nan(red[0], red[1]), fmax_nan(red[2], red[3]));
+    };
+    auto inv_of = [&](float acc) {
+        if (t < 64) {
+            const float inv = __fdiv_rn(1.0f, faddv16(acc));
+            if (t == 0) sinv = inv;
+        }
+        __syncthreads();
+        return sinv;
+    };
+    if (dim <= kStageFloats) {
+        float v[kItems];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++) v[u] = 0.0f;
+        for_item_groups(dim, [&](uint32_t u) { v[u] = val(item_index(u, dim)); });
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++)
+            if (t + 256 * u < dim) m = fmax_nan(m, v[u]);
+        m = max_of(m);
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++)
+            if (t + 256 * u < dim) v[u] = expd(v[u], m);
+        stage_chains(ct, dim, v);
+        __syncthreads();
+        const float inv = inv_of(t < 64 ? chain16_staged<false>(ct, dim, t & 15) : 0.0f);
+#pragma unroll
+        for (uint32_t u = 0; u < kItems; u++)
+            if (t + 256 * u < dim) o[t + 256 * u] = __fmul_rn(v[u], inv);
+        return;
     }
+    // longer rows: e through o in global memory
+    float m = -__builtin_inff();
+    for (uint32_t i = t; i < dim; i += 256) m = fmax_nan(m, val(i));
+    m = max_of(m);
+    for (uint32_t i = t; i < dim; i += 256) o[i] = expd(val(i), m);
+    __threadfence_block();
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const float acc = chain16<false>(staged ? es : o, dim, threadIdx.x & 15);
-        const float inv = __fdiv_rn(1.0f, faddv16(acc));
-        if (threadIdx.x == 0) sinv = inv;
-    }
-    __syncthreads();
-    const float inv = sinv;
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) o[i] = __fmul_rn(staged ? es[i] : o[i], inv);
+    const float inv = inv_of(t < 64 ? chain16<false>(o, dim, t & 15) : 0.0f);
+    for (uint32_t i = t; i < dim; i += 256) o[i] = __fmul_rn(o[i], inv);
 }
 
 __global__ void __launch_bounds__(256) k_softmax_ref(uint32_t dim, const float* in, float* out, uint64_t stride) {
@@ -334,8 +480,8 @@ __global__ void __launch_bounds__(256) k_softmax_ref(uint32_t dim, const float* 
 __global__ void __launch_bounds__(256)
 k_rms_norm_node(uint32_t dim, float eps, const uint8_t* in, NodeRows src, uint8_t* out, NodeRows dst) {
     const RowIdx i = row_index(dst, blockIdx.x);
-    rms_norm_row(dim, eps, reinterpret_cast<const float*>(in + row_offset(src, i)), nullptr,
-                 reinterpret_cast<float*>(out + row_offset(dst, i)));
+    rms_norm_row<false, false>(dim, eps, reinterpret_cast<const float*>(in + row_offset(src, i)), nullptr,
+                               reinterpret_cast<float*>(out + row_offset(dst, i)), nullptr, nullptr);
 }
 
 __global__ void __launch_bounds__(256)
@@ -430,63 +576,102 @@ k_attn_scores_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, 
 
 // out[h][d] = FADDV over 16 chains, chain l = fma(p_j, v_j[d], acc) for
 // j = l mod 16 in increasing j.  One workgroup per (kv head g, block of 16
-// dimensions): its kPvHeads query heads share every V row.  Thread (hq, l)
-// runs chain l of head kPvHeads*g + hq/4 for the 4 dimensions 4(hq%4)..
-// of the block.  Positions pass through LDS in chunks of kPvChunk, copied
-// global -> LDS directly (V rows as 16-byte pieces, P as dwords; positions
-// at or past len read as zeros and are never folded), double-buffered so
-// chunk c+1 is in flight while chunk c is folded.
-constexpr uint32_t kPvHeads = 4, kPvChunk = 1024;
+// dimensions, query head hq of the group): thread t runs chain l = t / 16
+// of dimension d = t % 16.  Positions pass through LDS in chunks of
+// kPvChunk (V rows' 32-byte slices and P), double-buffered through
+// registers: chunk c+1's global loads are in flight while chunk c is folded
+// from LDS, then written to the other buffer (positions at or past len load
+// as zeros and are never folded).  Inside a chunk each thread's LDS reads
+// run one batch of 8 positions ahead of its fmas.  The 16 chains of a
+// dimension meet through LDS for the FADDV tree.
+constexpr uint32_t kPvHeads = 4, kPvChunk = 1024, kPvBatch = 8;
+constexpr uint32_t kPvVPieces = kPvChunk * 2 / 256;  // 16-byte V pieces per thread per chunk
 __global__ void __launch_bounds__(256)
 k_attn_pv_ref(uint32_t len, uint32_t ctx, const float* __restrict__ p, const uint16_t* __restrict__ v_cache,
               float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPvChunk * 16];    // 2 x 32 KB
-    __shared__ __attribute__((aligned(16))) float ps[2][kPvHeads * kPvChunk];  // 2 x 16 KB
-    const uint32_t g = blockIdx.x >> 3, db = blockIdx.x & 7;
-    const uint32_t t = threadIdx.x, l = t & 15, hq = t >> 4, hl = hq >> 2, d4 = (hq & 3) * 4;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
-    const uint16_t* vg = v_cache + (uint64_t)g * ctx * 128 + db * 16;
-    const float* pg = p + (uint64_t)g * kPvHeads * len;
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vg, len * 256);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pg, kPvHeads * len * 4);
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPvChunk * 16];  // 2 x 32 KB
+    __shared__ __attribute__((aligned(16))) float ps[2][kPvChunk];          // 2 x 4 KB
+    __shared__ float red[256];
+    const uint32_t hq = blockIdx.x % kPvHeads, db = (blockIdx.x / kPvHeads) & 7, g = blockIdx.x / (kPvHeads * 8);
+    const uint32_t t = threadIdx.x, l = t >> 4, d = t & 15;
+    const uint8_t* vg = reinterpret_cast<const uint8_t*>(v_cache + (uint64_t)g * ctx * 128 + db * 16);
+    const float* pg = p + (uint64_t)(g * kPvHeads + hq) * len;
     const uint32_t nch = (len + kPvChunk - 1) / kPvChunk;
-    auto issue = [&](uint32_t c) {
-        const uint32_t j0 = c * kPvChunk, buf = c & 1;
+    // thread t's share of a chunk: V pieces q = t + 256 i (row q / 2, half
+    // q % 2) and P positions 4t .. 4t + 3
+    v4i rv[kPvVPieces];
+    float4 rp;
+    auto load = [&](uint32_t c) {
+        const uint32_t j0 = c * kPvChunk;
 #pragma unroll
-        for (uint32_t i = 0; i < kPvChunk * 2 / 256; i++) {  // V: piece q = row q/2, half q%2
-            const uint32_t q = 64 * (wave + 4 * i) + lane, j = j0 + (q >> 1);
-            copy16_to_lds(rv, reinterpret_cast<int8_t*>(vs[buf]) + 1024 * (wave + 4 * i),
-                          j < len ? j * 256 + (q & 1) * 16 : 0x80000000u);
+        for (uint32_t i = 0; i < kPvVPieces; i++) {
+            const uint32_t q = t + 256 * i, j = j0 + (q >> 1);
+            rv[i] = j < len ? *reinterpret_cast<const v4i*>(vg + (uint64_t)j * 256 + (q & 1) * 16) : v4i{0, 0, 0, 0};
         }
-#pragma unroll
-        for (uint32_t i = 0; i < kPvHeads * kPvChunk / 256; i++) {  // P: element e = head e/kPvChunk
-            const uint32_t e = 64 * (wave + 4 * i) + lane, h = e / kPvChunk, j = j0 + e % kPvChunk;
-            copy4_to_lds(rp, ps[buf] + 64 * (wave + 4 * i), j < len ? (h * len + j) * 4 : 0x80000000u);
+        const uint32_t j = j0 + 4 * t;
+        if (j + 3 < len) {
+            rp = *reinterpret_cast<const float4*>(pg + j);
+        } else {
+            rp.x = j < len ? pg[j] : 0.0f;
+            rp.y = j + 1 < len ? pg[j + 1] : 0.0f;
+            rp.z = j + 2 < len ? pg[j + 2] : 0.0f;
+            rp.w = 0.0f;
         }
     };
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    issue(0);
+    auto store = [&](uint32_t buf) {
+#pragma unroll
+        for (uint32_t i = 0; i < kPvVPieces; i++)
+            reinterpret_cast<v4i*>(vs[buf])[t + 256 * i] = rv[i];
+        reinterpret_cast<float4*>(ps[buf])[t] = rp;
+    };
+    float acc = 0.0f;
+    load(0);
+    store(0);
+    __syncthreads();
     for (uint32_t c = 0; c < nch; c++) {
-        wait_vmcnt<0>();  // chunk c's copies of this wave
-        __syncthreads();  // everyone's; everyone is done with chunk c-1, whose buffer is refilled next
-        if (c + 1 < nch) issue(c + 1);
+        if (c + 1 < nch) load(c + 1);
         const uint32_t buf = c & 1, j0 = c * kPvChunk;
         const uint32_t nj = min(kPvChunk, len - j0);
-        for (uint32_t k = l; k < nj; k += 16) {
-            const float pj = ps[buf][hl * kPvChunk + k];
-            const uint2 raw = *reinterpret_cast<const uint2*>(vs[buf] + k * 16 + d4);
-            acc[0] = __builtin_fmaf(pj, h2f(raw.x & 0xffff), acc[0]);
-            acc[1] = __builtin_fmaf(pj, h2f(raw.x >> 16), acc[1]);
-            acc[2] = __builtin_fmaf(pj, h2f(raw.y & 0xffff), acc[2]);
-            acc[3] = __builtin_fmaf(pj, h2f(raw.y >> 16), acc[3]);
-        }
-    }
-    float* o = out + (uint64_t)(g * kPvHeads + hl) * 128 + db * 16 + d4;
+        const float* pc = ps[buf];
+        const uint16_t* vc = vs[buf];
+        uint32_t k = l;
+        if (k + (kPvBatch - 1) * 16 < nj) {
+            float pp[kPvBatch], pn[kPvBatch];
+            uint16_t vv[kPvBatch], vn[kPvBatch];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float v = faddv16(acc[i]);
-        if (l == 0) o[i] = v;
+            for (uint32_t u = 0; u < kPvBatch; u++) {
+                pp[u] = pc[k + 16 * u];
+                vv[u] = vc[(k + 16 * u) * 16 + d];
+            }
+            while (true) {
+                const uint32_t kn = k + 16 * kPvBatch;
+                const bool more = kn + (kPvBatch - 1) * 16 < nj;
+                if (more) {
+#pragma unroll
+                    for (uint32_t u = 0; u < kPvBatch; u++) {
+                        pn[u] = pc[kn + 16 * u];
+                        vn[u] = vc[(kn + 16 * u) * 16 + d];
+                    }
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < kPvBatch; u++) acc = __builtin_fmaf(pp[u], h2f(vv[u]), acc);
+                k = kn;
+                if (!more) break;
+#pragma unroll
+                for (uint32_t u = 0; u < kPvBatch; u++) {
+                    pp[u] = pn[u];
+                    vv[u] = vn[u];
+                }
+            }
+        }
+        for (; k < nj; k += 16) acc = __builtin_fmaf(pc[k], h2f(vc[k * 16 + d]), acc);
+        if (c + 1 < nch) store(buf ^ 1);  // every thread finished chunk c-1, whose buffer this is
+        __syncthreads();
     }
+    red[d * 16 + l] = acc;
+    __syncthreads();
+    const float v = faddv16(red[t]);  // lanes t..t+15 hold the 16 chains of dimension t / 16
+    if ((t & 15) == 0) out[(uint64_t)(g * kPvHeads + hq) * 128 + db * 16 + (t >> 4)] = v;
 }
 
 // h[i] = fl(silu_fp32(g_i) * u_i) on gate|up interleaved in 32-row groups.
@@ -506,6 +691,16 @@ int rms_norm_ref_launch(uint32_t rows, uint32_t dim, float eps, const float* in,
     if (rows == 0 || dim == 0) return ANE_OK;
     if (rows > 0x7fffffffu) return ANE_ERR_INVALID_ARG;
     hipLaunchKernelGGL(k_rms_norm_ref, dim3(rows), dim3(256), 0, s, dim, eps, in, w, out, stride);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+// x = fl(x + y) (written back), xn = rms_norm_fp32(x) with weights w: one
+// row of dim values.
+int add_rms_norm_ref_launch(uint32_t dim, float eps, float* x, const float* y, const float* w, float* xn,
+                            hipStream_t s) {
+    if (dim == 0) return ANE_OK;
+    hipLaunchKernelGGL(k_add_rms_norm_ref, dim3(1), dim3(256), 0, s, dim, eps, x, y, w, xn);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
@@ -540,7 +735,7 @@ int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t
     hipLaunchKernelGGL(k_attn_scores_ref, dim3((uint32_t)((ns + 255) / 256)), dim3(256), 0, s, n_heads, group, len,
                        ctx, q, kc, sc);
     hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
-    hipLaunchKernelGGL(k_attn_pv_ref, dim3(n_kv * 8), dim3(256), 0, s, len, ctx, pr, vc, out);
+    hipLaunchKernelGGL(k_attn_pv_ref, dim3(n_kv * 8 * kPvHeads), dim3(256), 0, s, len, ctx, pr, vc, out);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
