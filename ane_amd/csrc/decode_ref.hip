@@ -548,126 +548,172 @@ k_rope_ref_kv(float* __restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t
 
 __device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h); }
 
-// s[h][j] = fl(dot16(q_h, k_j) * fl(1/sqrt(128))), one thread per (h, j):
-// 16 chains of 8 fmas, then the FADDV tree in registers.
+// s[h][j] = fl(dot16(q_h, k_j) * fl(1/sqrt(128))): 16 chains of 8 fmas
+// (chain l over elements l, l + 16, ... in order), then the FADDV tree in
+// registers.  One workgroup per (kv head g, block of kScRows positions):
+// the block's K rows are copied global -> LDS (row r's 16-byte piece c at
+// slot c ^ (r mod 16), so the 16 rows a ds_read_b128 serves sit in distinct
+// banks) with the group's q rows; thread t takes position j0 + t % kScRows
+// for the group's query heads 2(t / kScRows) and 2(t / kScRows) + 1,
+// holding its K row in registers.
+constexpr uint32_t kScRows = 128, kScHeads = 4;
 __global__ void __launch_bounds__(256)
-k_attn_scores_ref(uint32_t n_heads, uint32_t group, uint32_t len, uint32_t ctx, const float* __restrict__ q,
-                  const uint16_t* __restrict__ k_cache, float* __restrict__ s) {
-    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (uint64_t)n_heads * len) return;
-    const uint32_t h = (uint32_t)(t / len), j = (uint32_t)(t - (uint64_t)h * len);
-    const float* qh = q + h * 128;
-    const uint16_t* kj = k_cache + ((uint64_t)(h / group) * ctx + j) * 128;
-    float acc[16];
+k_attn_scores_ref(uint32_t len, uint32_t ctx, const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
+                  float* __restrict__ s) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kScRows * 128];  // 32 KB
+    __shared__ __attribute__((aligned(16))) float qs[kScHeads * 128];     // 2 KB
+    const uint32_t nblk = (len + kScRows - 1) / kScRows;
+    const uint32_t g = blockIdx.x / nblk, j0 = (blockIdx.x % nblk) * kScRows;
+    const uint32_t t = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+    const uint32_t nrows = len - j0 < kScRows ? len - j0 : kScRows;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(k_cache + ((uint64_t)g * ctx + j0) * 128, nrows * 256);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + (uint64_t)g * kScHeads * 128, kScHeads * 128 * 4);
 #pragma unroll
-    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+    for (uint32_t i = wave; i < kScRows / 4; i += 4) {  // 4 rows per wave-instruction; rows past len -> zeros
+        const uint32_t r = 4 * i + lane / 16, c = (lane & 15) ^ (r & 15);
+        copy16_to_lds(rk, reinterpret_cast<int8_t*>(ks) + 1024 * i, r * 256 + c * 16);
+    }
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (uint32_t i = wave; i < kScHeads * 128 / 64; i += 4) copy4_to_lds(rq, qs + 64 * i, (64 * i + lane) * 4);
+    wait_vmcnt<0>();
+    __syncthreads();
+    const uint32_t r = t % kScRows, hp = t / kScRows, j = j0 + r;
+    v4i kr[16];  // this row's 128 halves, piece c = elements 8c .. 8c + 7
 #pragma unroll
-        for (int l = 0; l < 16; l++) acc[l] = __builtin_fmaf(qh[16 * i + l], h2f(kj[16 * i + l]), acc[l]);
-    float t8[8], t4[4];
+    for (uint32_t c = 0; c < 16; c++) kr[c] = *reinterpret_cast<const v4i*>(ks + r * 128 + ((c ^ (r & 15)) * 8));
+    auto kv = [&](uint32_t e) {  // element e of the row, as fp32
+        const uint32_t w = (uint32_t)kr[e / 8][(e % 8) / 2];
+        return h2f((uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff)));
+    };
 #pragma unroll
-    for (int l = 0; l < 8; l++) t8[l] = __fadd_rn(acc[2 * l], acc[2 * l + 1]);
+    for (uint32_t hh = 2 * hp; hh < 2 * hp + 2; hh++) {
+        const float* qh = qs + hh * 128;
+        float acc[16];
 #pragma unroll
-    for (int l = 0; l < 4; l++) t4[l] = __fadd_rn(t8[2 * l], t8[2 * l + 1]);
-    const float dot = __fadd_rn(__fadd_rn(t4[0], t4[1]), __fadd_rn(t4[2], t4[3]));
-    s[(uint64_t)h * len + j] = __fmul_rn(dot, f_of(0x3DB504F3u));
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            float4 qv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) qv[k] = *reinterpret_cast<const float4*>(qh + 16 * i + 4 * k);
+#pragma unroll
+            for (uint32_t l = 0; l < 16; l++) {
+                const float4& v = qv[l / 4];
+                const float qe = (l % 4) == 0 ? v.x : (l % 4) == 1 ? v.y : (l % 4) == 2 ? v.z : v.w;
+                acc[l] = __builtin_fmaf(qe, kv(16 * i + l), acc[l]);
+            }
+        }
+        float t8[8], t4[4];
+#pragma unroll
+        for (int l = 0; l < 8; l++) t8[l] = __fadd_rn(acc[2 * l], acc[2 * l + 1]);
+#pragma unroll
+        for (int l = 0; l < 4; l++) t4[l] = __fadd_rn(t8[2 * l], t8[2 * l + 1]);
+        const float dot = __fadd_rn(__fadd_rn(t4[0], t4[1]), __fadd_rn(t4[2], t4[3]));
+        if (j < len) s[(uint64_t)(g * kScHeads + hh) * len + j] = __fmul_rn(dot, f_of(0x3DB504F3u));
+    }
 }
 
 // out[h][d] = FADDV over 16 chains, chain l = fma(p_j, v_j[d], acc) for
 // j = l mod 16 in increasing j.  One workgroup per (kv head g, block of 16
 // dimensions, query head hq of the group): thread t runs chain l = t / 16
-// of dimension d = t % 16.  Positions pass through LDS in chunks of
-// kPvChunk (V rows' 32-byte slices and P), double-buffered through
-// registers: chunk c+1's global loads are in flight while chunk c is folded
-// from LDS, then written to the other buffer (positions at or past len load
-// as zeros and are never folded).  Inside a chunk each thread's LDS reads
-// run one batch of 8 positions ahead of its fmas.  The 16 chains of a
+// of dimension d = t % 16.  Positions pass through LDS in chunks of up to
+// kPvChunk (4096: the whole context of config 5 in one chunk), the V rows'
+// 32-byte slices as 16-byte pieces and the P row as dwords, copied global
+// -> LDS directly (positions at or past len read as zeros and are never
+// folded); one wait and one barrier per chunk.  Each chain folds its
+// positions in batches of 8, the next batch's LDS reads in flight during the
+// current batch's fmas (two register sets in turn).  The 16 chains of a
 // dimension meet through LDS for the FADDV tree.
-constexpr uint32_t kPvHeads = 4, kPvChunk = 1024, kPvBatch = 8;
-constexpr uint32_t kPvVPieces = kPvChunk * 2 / 256;  // 16-byte V pieces per thread per chunk
+// SOFTMAX (len <= kPvChunk): p holds the raw scores and the workgroup
+// turns its head's row into probabilities in LDS first, exactly as 0x56
+// does (softmax_row: any-order max, e = exp(s - max), 16 fadd chains in
+// wave 0, FADDV, 1/sum, fl(e * inv)); every workgroup of the head computes
+// the same row.
+constexpr uint32_t kPvHeads = 4, kPvChunk = 4096, kPvBatch = 8;
+template <bool SOFTMAX>
 __global__ void __launch_bounds__(256)
 k_attn_pv_ref(uint32_t len, uint32_t ctx, const float* __restrict__ p, const uint16_t* __restrict__ v_cache,
               float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPvChunk * 16];  // 2 x 32 KB
-    __shared__ __attribute__((aligned(16))) float ps[2][kPvChunk];          // 2 x 4 KB
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kPvChunk * 16];  // 128 KB
+    __shared__ __attribute__((aligned(16))) float ps[kPvChunk];          // 16 KB
     __shared__ float red[256];
     const uint32_t hq = blockIdx.x % kPvHeads, db = (blockIdx.x / kPvHeads) & 7, g = blockIdx.x / (kPvHeads * 8);
     const uint32_t t = threadIdx.x, l = t >> 4, d = t & 15;
-    const uint8_t* vg = reinterpret_cast<const uint8_t*>(v_cache + (uint64_t)g * ctx * 128 + db * 16);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+    const uint16_t* vg = v_cache + (uint64_t)g * ctx * 128 + db * 16;
     const float* pg = p + (uint64_t)(g * kPvHeads + hq) * len;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vg, len * 256);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pg, len * 4);
     const uint32_t nch = (len + kPvChunk - 1) / kPvChunk;
-    // thread t's share of a chunk: V pieces q = t + 256 i (row q / 2, half
-    // q % 2) and P positions 4t .. 4t + 3
-    v4i rv[kPvVPieces];
-    float4 rp;
-    auto load = [&](uint32_t c) {
-        const uint32_t j0 = c * kPvChunk;
-#pragma unroll
-        for (uint32_t i = 0; i < kPvVPieces; i++) {
-            const uint32_t q = t + 256 * i, j = j0 + (q >> 1);
-            rv[i] = j < len ? *reinterpret_cast<const v4i*>(vg + (uint64_t)j * 256 + (q & 1) * 16) : v4i{0, 0, 0, 0};
-        }
-        const uint32_t j = j0 + 4 * t;
-        if (j + 3 < len) {
-            rp = *reinterpret_cast<const float4*>(pg + j);
-        } else {
-            rp.x = j < len ? pg[j] : 0.0f;
-            rp.y = j + 1 < len ? pg[j + 1] : 0.0f;
-            rp.z = j + 2 < len ? pg[j + 2] : 0.0f;
-            rp.w = 0.0f;
-        }
-    };
-    auto store = [&](uint32_t buf) {
-#pragma unroll
-        for (uint32_t i = 0; i < kPvVPieces; i++)
-            reinterpret_cast<v4i*>(vs[buf])[t + 256 * i] = rv[i];
-        reinterpret_cast<float4*>(ps[buf])[t] = rp;
-    };
     float acc = 0.0f;
-    load(0);
-    store(0);
-    __syncthreads();
     for (uint32_t c = 0; c < nch; c++) {
-        if (c + 1 < nch) load(c + 1);
-        const uint32_t buf = c & 1, j0 = c * kPvChunk;
-        const uint32_t nj = min(kPvChunk, len - j0);
-        const float* pc = ps[buf];
-        const uint16_t* vc = vs[buf];
-        uint32_t k = l;
-        if (k + (kPvBatch - 1) * 16 < nj) {
-            float pp[kPvBatch], pn[kPvBatch];
-            uint16_t vv[kPvBatch], vn[kPvBatch];
+        const uint32_t j0 = c * kPvChunk, nj = min(kPvChunk, len - j0);
+        if (c > 0) __syncthreads();  // everyone is done with the previous chunk
+        // P first (the softmax needs it before the V rows): 64 positions per
+        // wave-instruction.  V: piece q of the chunk = row q / 2, half q % 2;
+        // 64 pieces (1 KB of LDS) per wave-instruction.
+        for (uint32_t i = wave; i < (nj + 63) / 64; i += 4) {
+            const uint32_t j = j0 + 64 * i + lane;
+            copy4_to_lds(rp, ps + 64 * i, j < len ? j * 4 : 0x80000000u);
+        }
+        if (SOFTMAX) {  // the row is needed first; V lands while it is computed
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+        for (uint32_t i = wave; i < (nj * 2 + 63) / 64; i += 4) {
+            const uint32_t q = 64 * i + lane, j = j0 + (q >> 1);
+            copy16_to_lds(rv, reinterpret_cast<int8_t*>(vs) + 1024 * i,
+                          j < len ? j * 256 + (q & 1) * 16 : 0x80000000u);
+        }
+        if (SOFTMAX) {
+            float m = -__builtin_inff();
+            for (uint32_t j = t; j < nj; j += 256) m = fmax_nan(m, ps[j]);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) m = fmax_nan(m, __shfl_xor(m, off, 64));
+            if (lane == 0) red[wave] = m;
+            wait_lgkmcnt0();  // LDS-only barriers here: the V copies stay in flight
+            lds_barrier();
+            m = fmax_nan(fmax_nan(red[0], red[1]), fmax_nan(red[2], red[3]));
+            for (uint32_t j = t; j < nj; j += 256) ps[j] = exp_poly_a(__fsub_rn(ps[j], m), true);
+            wait_lgkmcnt0();
+            lds_barrier();
+            if (t < 64) {
+                const float inv = __fdiv_rn(1.0f, faddv16(chain16<false>(ps, nj, t & 15)));
+                if (t == 0) red[4] = inv;
+            }
+            wait_lgkmcnt0();
+            lds_barrier();
+            const float inv = red[4];
+            for (uint32_t j = t; j < nj; j += 256) ps[j] = __fmul_rn(ps[j], inv);
+        }
+        wait_vmcnt<0>();  // this wave's copies landed
+        __syncthreads();  // everyone's did
+        auto ld = [&](float (&pq)[kPvBatch], uint16_t (&vq)[kPvBatch], uint32_t k0) {
 #pragma unroll
             for (uint32_t u = 0; u < kPvBatch; u++) {
-                pp[u] = pc[k + 16 * u];
-                vv[u] = vc[(k + 16 * u) * 16 + d];
+                pq[u] = ps[k0 + 16 * u];
+                vq[u] = vs[(k0 + 16 * u) * 16 + d];
             }
-            while (true) {
-                const uint32_t kn = k + 16 * kPvBatch;
-                const bool more = kn + (kPvBatch - 1) * 16 < nj;
-                if (more) {
+        };
+        auto fold = [&](const float (&pq)[kPvBatch], const uint16_t (&vq)[kPvBatch]) {
 #pragma unroll
-                    for (uint32_t u = 0; u < kPvBatch; u++) {
-                        pn[u] = pc[kn + 16 * u];
-                        vn[u] = vc[(kn + 16 * u) * 16 + d];
-                    }
-                }
-#pragma unroll
-                for (uint32_t u = 0; u < kPvBatch; u++) acc = __builtin_fmaf(pp[u], h2f(vv[u]), acc);
-                k = kn;
-                if (!more) break;
-#pragma unroll
-                for (uint32_t u = 0; u < kPvBatch; u++) {
-                    pp[u] = pn[u];
-                    vv[u] = vn[u];
-                }
-            }
+            for (uint32_t u = 0; u < kPvBatch; u++) acc = __builtin_fmaf(pq[u], h2f(vq[u]), acc);
+        };
+        // chain l holds positions l + 16 m, m < cnt; nb full batches of 8
+        const uint32_t cnt = l < nj ? (nj - l + 15) / 16 : 0, nb = cnt / kPvBatch;
+        float pa[kPvBatch], pb[kPvBatch];
+        uint16_t va[kPvBatch], vb[kPvBatch];
+        if (nb > 0) ld(pa, va, l);
+        for (uint32_t bt = 0; bt < nb; bt += 2) {
+            if (bt + 1 < nb) ld(pb, vb, l + 16 * kPvBatch * (bt + 1));
+            fold(pa, va);
+            if (bt + 2 < nb) ld(pa, va, l + 16 * kPvBatch * (bt + 2));
+            if (bt + 1 < nb) fold(pb, vb);
         }
-        for (; k < nj; k += 16) acc = __builtin_fmaf(pc[k], h2f(vc[k * 16 + d]), acc);
-        if (c + 1 < nch) store(buf ^ 1);  // every thread finished chunk c-1, whose buffer this is
-        __syncthreads();
+        for (uint32_t k = l + 16 * kPvBatch * nb; k < nj; k += 16) acc = __builtin_fmaf(ps[k], h2f(vs[k * 16 + d]), acc);
     }
+    __syncthreads();  // red's softmax slots are read before the chains' partials overwrite them
     red[d * 16 + l] = acc;
     __syncthreads();
     const float v = faddv16(red[t]);  // lanes t..t+15 hold the 16 chains of dimension t / 16
@@ -728,14 +774,17 @@ int rope_ref_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t pos
 int attention_ref_launch(uint32_t n_heads, uint32_t n_kv, uint32_t len, uint32_t ctx, const float* q,
                          const uint16_t* kc, const uint16_t* vc, float* out, float* ws, hipStream_t s) {
     const uint32_t group = n_heads / n_kv;
-    if (group != kPvHeads) return ANE_ERR_INVALID_ARG;
+    if (group != kPvHeads || group != kScHeads || n_heads != group * n_kv) return ANE_ERR_INVALID_ARG;
     float* sc = ws;
     float* pr = ws + (uint64_t)n_heads * len;
-    const uint64_t ns = (uint64_t)n_heads * len;
-    hipLaunchKernelGGL(k_attn_scores_ref, dim3((uint32_t)((ns + 255) / 256)), dim3(256), 0, s, n_heads, group, len,
-                       ctx, q, kc, sc);
-    hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
-    hipLaunchKernelGGL(k_attn_pv_ref, dim3(n_kv * 8 * kPvHeads), dim3(256), 0, s, len, ctx, pr, vc, out);
+    hipLaunchKernelGGL(k_attn_scores_ref, dim3(n_kv * ((len + kScRows - 1) / kScRows)), dim3(256), 0, s, len, ctx,
+                       q, kc, sc);
+    if (len <= kPvChunk) {  // the softmax inside the P.V workgroups
+        hipLaunchKernelGGL(k_attn_pv_ref<true>, dim3(n_kv * 8 * kPvHeads), dim3(256), 0, s, len, ctx, sc, vc, out);
+    } else {
+        hipLaunchKernelGGL(k_softmax_ref, dim3(n_heads), dim3(256), 0, s, len, sc, pr, (uint64_t)len);
+        hipLaunchKernelGGL(k_attn_pv_ref<false>, dim3(n_kv * 8 * kPvHeads), dim3(256), 0, s, len, ctx, pr, vc, out);
+    }
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }
