@@ -185,7 +185,12 @@ static int launch_gemm(const GemmParams& p, hipStream_t s) {
         const bool e256 = tile256_eligible(p);
         if (e256 && tiles256 >= tile256_min_tiles()) return launch_gemm_tile256(p, s);
         if (skinny_eligible(p)) return launch_gemm_skinny(p, s);
-        if (tile128_eligible(p)) return launch_gemm_tile128(p, s);
+        if (tile128_eligible(p)) {
+            // one 128-tile per CU or fewer: the deeper ring; more: two per CU
+            const uint64_t tiles128 = (uint64_t)((p.Mout + 127) / 128) * ((p.Nout + 127) / 128);
+            if (tiles128 <= tile256_min_tiles() && tile128d_eligible(p)) return launch_gemm_tile128d(p, s);
+            return launch_gemm_tile128(p, s);
+        }
         if (e256) return launch_gemm_tile256(p, s);
     }
     dim3 grid((p.Nout + kBN - 1) / kBN, (p.Mout + kBM - 1) / kBM);
@@ -412,7 +417,9 @@ extern "C" int ane_hip_dense_fused_i8_gemm(int32_t M, int32_t N, int32_t K, floa
         q.C = nullptr;
         q.Craw = L.planes;
         if (ksplit >= 2 && tile128_eligible(q, true)) {
-            const int st = launch_gemm_tile128(q, s, ksplit);
+            const int st = (uint64_t)tiles * ksplit <= tile256_min_tiles() && tile128d_eligible(q, true)
+                               ? launch_gemm_tile128d(q, s, ksplit)
+                               : launch_gemm_tile128(q, s, ksplit);
             if (st != ANE_OK) return st;
             const uint64_t n = (uint64_t)M * N;
             hipLaunchKernelGGL(k_split_epilogue, dim3((uint32_t)((n + 1023) / 1024)), dim3(256), 0, s, L.planes,

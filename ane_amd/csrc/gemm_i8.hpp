@@ -53,6 +53,10 @@ int launch_gemm_tile256(const GemmParams& p, hipStream_t s, uint32_t ksplit = 1)
 // The same loop at 128 x 128 tiles (gemm_i8_tile128.hip).
 bool tile128_eligible(const GemmParams& p, bool any_rows = false);
 int launch_gemm_tile128(const GemmParams& p, hipStream_t s, uint32_t ksplit = 1);
+// The same at 128 x 128 tiles on a 3-stage ring with 8 waves, one workgroup
+// per CU (gemm_i8_tile128d.hip): for launches of at most one workgroup per CU.
+bool tile128d_eligible(const GemmParams& p, bool any_rows = false);
+int launch_gemm_tile128d(const GemmParams& p, hipStream_t s, uint32_t ksplit = 1);
 
 // Few-row kernel (gemm_i8_skinny.hip): Bt layout, signed A, M <= 128, one
 // workgroup per 16 columns.

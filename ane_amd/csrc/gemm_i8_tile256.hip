@@ -7,11 +7,12 @@
 //    wave owns FM x FN blocks of v_mfma_i32_32x32x32_i8 accumulators.  With
 //    8 or 16 waves, 2 or 4 share each SIMD, so one wave's barrier or LDS
 //    wait is covered by the others' MFMAs.
-//  * K advances in 128-byte slices through a 2-stage LDS ring (2 x 64 KB
-//    for 256-tiles, 2 x 32 KB for 128-tiles).  Each slice starts with a
-//    barrier (every wave's copies of slice kt have landed, and every wave
-//    has finished slice kt-1), after which the copies of slice kt+1 go into
-//    slice kt-1's stage.  Those copies are pinned one between MFMAs of the
+//  * K advances in 128-byte slices through an LDS ring of STAGES stages
+//    (2 x 64 KB for 256-tiles, 2 x 32 KB for 128-tiles, 3 x 32 KB for the
+//    128-tiles of gemm_i8_tile128d.hip).  Each slice starts with a barrier
+//    (every wave's copies of slice kt have landed, and every wave has
+//    finished slice kt-1), after which the copies of slice kt+STAGES-1 go
+//    into slice kt-1's stage.  Those copies are pinned one between MFMAs of the
 //    slice's first two k-steps (sched_barrier): issuing a buffer_load ...
 //    lds occupies the issuing wave for tens of cycles, and issued back to
 //    back they drained the MFMA pipe after every barrier (4096^3: the K loop
@@ -52,28 +53,36 @@ namespace {
 #define ANE_TILE 256
 #endif
 #if ANE_TILE == 256
+#ifndef ANE_TILE_KERNEL
 #define ANE_TILE_KERNEL k_gemm_i8_tile256
 #define ANE_TILE_ELIGIBLE tile256_eligible
 #define ANE_TILE_LAUNCH launch_gemm_tile256
+#endif
 #ifndef ANE_TILE_WAVES
 #define ANE_TILE_WAVES 8
 #endif
 #elif ANE_TILE == 128
+#ifndef ANE_TILE_KERNEL
 #define ANE_TILE_KERNEL k_gemm_i8_tile128
 #define ANE_TILE_ELIGIBLE tile128_eligible
 #define ANE_TILE_LAUNCH launch_gemm_tile128
+#endif
 #ifndef ANE_TILE_WAVES
 #define ANE_TILE_WAVES 4
 #endif
 #else
 #error "ANE_TILE is 256 or 128"
 #endif
+// ANE_TILE_STAGES: LDS ring depth (2 by default).  Slice kt+STAGES-1 is
+// copied while slice kt is multiplied, so STAGES-1 slices are in flight.
+#ifndef ANE_TILE_STAGES
+#define ANE_TILE_STAGES 2
+#endif
 
 constexpr int TM = ANE_TILE, TN = ANE_TILE;
 constexpr int TK = 128;                       // bytes of K per slice
-constexpr int STAGES = 2;                     // LDS ring depth
+constexpr int STAGES = ANE_TILE_STAGES;       // LDS ring depth
 constexpr int NW = ANE_TILE_WAVES;            // waves per workgroup
-constexpr int kWavesPerEu = TM == 128 ? 2 : NW / 4;  // 128-tiles: two workgroups per CU
 constexpr int kThreads = NW * 64;
 constexpr int WN = NW == 16 ? 4 : 2;          // waves along N
 constexpr int WM = NW / WN;                   // waves along M
@@ -84,11 +93,14 @@ constexpr int kStageA = TM * TK;
 constexpr int kStageB = TN * TK;
 constexpr int kStage = kStageA + kStageB;
 constexpr int kLdsBytes = STAGES * kStage;
+constexpr int kWgPerCu = 2 * kLdsBytes <= 160 * 1024 ? 2 : 1;  // 128-tiles on a 2-stage ring: two per CU
+constexpr int kWavesPerEu = kWgPerCu * NW / 4;
 constexpr int kRowsPerDma = 1024 / TK;        // rows covered by one copy wave-instruction
 constexpr int kRowsPerWave = TM / NW;         // rows of A (and of Bt) each wave copies
 constexpr int kDmaPerWave = kRowsPerWave / kRowsPerDma;
 constexpr int kSteps = TK / 32;
 static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
+static_assert(STAGES >= 2 && (STAGES - 2) * 2 * kDmaPerWave < 64, "ring depth fits the vmcnt field");
 static_assert(kLdsBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
 // Epilogue staging: per wave EPR rows x (FN*32) fp32 per pass, rows padded
 // by 32 bytes (4 rows apart = 128 bytes mod 256: the two half-waves of a
@@ -180,6 +192,12 @@ __device__ __forceinline__ void slice_pinned(v16i (&acc)[FM][FN], Frags& f0, Fra
                 issue_one(c, offA, offB, kofs, ks * kPerStep + g / kStride);
             __builtin_amdgcn_sched_barrier(0);
         }
+        // fewer MFMAs than fragments per k-step (1 x 2 blocks per wave): the
+        // rest of the next k-step's fragments after the last MFMA
+#pragma unroll
+        for (int g = nM; g < nD; g++)
+            if (ks + 1 < kSteps) load_frag(cur, rA, rB, 2 * (ks + 1) + chalf, fn, g);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -267,17 +285,22 @@ ANE_TILE_KERNEL(GemmParams p, uint32_t tiles_m, uint32_t tiles_n) {
         return (k >= kt1 || k0 >= p.Kp) ? 0u : (p.Kp - k0 < (uint32_t)TK ? p.Kp - k0 : (uint32_t)TK);
     };
     Frags f0, f1;
-    {
-        const SliceCopy c{ra, rb, smem, wave, kt0 * TK, kmax(kt0)};
+#pragma unroll
+    for (int j = 0; j < STAGES - 1; j++) {
+        const SliceCopy c{ra, rb, smem + j * kStage, wave, (kt0 + j) * TK, kmax(kt0 + j)};
 #pragma unroll
         for (int d = 0; d < 2 * kDmaPerWave; d++) issue_one(c, offA, offB, kofs, d);
     }
+    uint32_t st = 0;  // stage of slice kt
     for (uint32_t kt = kt0; kt < kt1; kt++) {
-        const uint32_t st = (kt - kt0) & 1;
-        wait_vmcnt<0>();  // this wave's copies of slice kt landed
+        // this wave's copies of slice kt landed (those of the STAGES-2
+        // slices after it may still be in flight; copies complete in order)
+        wait_vmcnt<(STAGES - 2) * 2 * kDmaPerWave>();
         lds_barrier();    // everyone's did; everyone finished slice kt-1
         const int8_t* cur = smem + st * kStage;
-        const SliceCopy c{ra, rb, smem + (st ^ 1) * kStage, wave, (kt + 1) * TK, kmax(kt + 1)};
+        const uint32_t sn = st == 0 ? STAGES - 1 : st - 1;  // slice kt-1's stage takes slice kt+STAGES-1
+        const SliceCopy c{ra, rb, smem + sn * kStage, wave, (kt + STAGES - 1) * TK, kmax(kt + STAGES - 1)};
+        st = st + 1 == STAGES ? 0 : st + 1;
         load_frags(cur, rA, rB, chalf, f0);
         __builtin_amdgcn_sched_barrier(0);
         slice_pinned(acc, f0, f1, cur, rA, rB, chalf, c, offA, offB, kofs);

@@ -77,7 +77,10 @@ def mul_mat_both_routes(ane, N, K, T, x, W):
                                    # K an odd multiple of 64: the last 128-byte slice half zeros
                                    # (256-tiles, 128-tiles, both with a ragged grid)
                                    (4096, 4096, 192), (4100, 4096, 4160), (1000, 600, 960),
-                                   (513, 257, 4160)])
+                                   (513, 257, 4160),
+                                   # more 128-tiles than CUs (the 2-stage ring, two per CU;
+                                   # the shapes above with fewer take the 3-stage ring)
+                                   (2048, 2304, 192), (1100, 4000, 320)])
 def test_gemm_s8_i32_exact(ane, M, N, K):
     import torch
 
