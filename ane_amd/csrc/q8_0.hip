@@ -21,6 +21,7 @@
 #include "../../include/ane_decode.h"
 #include "common.hpp"
 #include "qformats.hpp"
+#include "q8_0_mmv.hpp"
 
 #include <atomic>
 #include <map>
@@ -1683,6 +1684,11 @@ constexpr uint32_t kMmrMinBlocks = 256;
 
 int mma_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x, const void* W, float* y,
                 void* workspace, size_t workspace_bytes, hipStream_t s) {
+    {
+        // 16+ tokens at K = 4096 or 14336: activations held in VGPRs (q8_0_mmv.hip)
+        const int r = mmv_mul_mat(N, nb, K, T, x, W, y, workspace, workspace_bytes, s);
+        if (r != -1) return r;
+    }
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ANE_ERR_HIP;
     const uint64_t cus = cu_count(dev);
@@ -1871,8 +1877,11 @@ constexpr uint32_t kQ8InlineQuantBlocks = ANE_Q8_INLINE_QUANT_BLOCKS;
 
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {
     const uint64_t nb = K >> 5;
-    // qx, then the scales: token-major [T][nb] or block-major [nb][ceil(T, 4)]
-    return (size_t)(ceil_to((uint64_t)T * nb * 32, 256) + ceil_to(nb * (((uint64_t)T + 3) & ~3ull) * 4, 256) + 256);
+    // qx, then the scales: token-major [T][nb] or block-major [nb][ceil(T, 4)];
+    // for 16+ tokens, or the block-major form of ceil(T, 16) tokens (q8_0_mmv.hip)
+    const uint64_t a = ceil_to((uint64_t)T * nb * 32, 256) + ceil_to(nb * (((uint64_t)T + 3) & ~3ull) * 4, 256) + 256;
+    const uint64_t b = T >= 16 ? ceil_to(mmv_workspace_bound((uint32_t)nb, T), 256) : 0;
+    return (size_t)(a > b ? a : b);
 }
 
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size_n(uint32_t N, uint32_t K, uint32_t T) {

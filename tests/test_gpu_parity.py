@@ -788,7 +788,14 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # fewer than one group, the unit count not a multiple of 8,
                                    # token groups past 64, one and two token tiles
                                    (4100, 8192, 40), (300, 9216, 20), (37, 8192, 5), (1000, 16384, 64),
-                                   (200, 8192, 100), (4096, 14336, 32), (130, 8192, 16)])
+                                   (200, 8192, 100), (4096, 14336, 32), (130, 8192, 16),
+                                   # activation-stationary kernel (K 4096 with 16-64 tokens, K 14336
+                                   # with 16): three token groups of one tile, two groups of two
+                                   # tiles with ragged rows, several row tiles per workgroup, four
+                                   # tiles on 8 waves with ragged rows and tokens, K 14336 with
+                                   # ragged rows
+                                   (4100, 4096, 48), (6000, 4096, 64), (20000, 4096, 32),
+                                   (28677, 4096, 60), (5000, 14336, 16)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
