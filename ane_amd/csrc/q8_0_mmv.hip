@@ -14,8 +14,7 @@
 //    levels it adds itself.  Lane (g, c16) of a
 //    v_mfma_i32_16x16x32_i8 receives token c16 of a token tile as A and weight
 //    row c16 of a row tile as B, so it holds the isums of weight row c16 for
-//    tokens 4g..4g+3 (as in k_q8_0_mmt).  8 waves give each wave 256 VGPRs
-//    (two residues' activations for 64 tokens at K = 4096).
+//    tokens 4g..4g+3 (as in k_q8_0_mmt).
 //  * The workgroup serves one token group (TT token tiles of 16 tokens) for
 //    a run of row tiles.  Each wave loads, once, the activation bytes its
 //    MFMAs use -- for every block b = r + 16j and token tile, lane (g, c16)'s
@@ -97,11 +96,13 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
     constexpr uint32_t nsk = nb / kMvSbk;       // stages per row tile
     constexpr uint32_t kJps = kMvSbk / 16;      // a residue's blocks per stage
     constexpr int RPW = 16 / NW;                // residues per wave
+    constexpr int kEx = TT < 32 / NW ? TT : 32 / NW;  // token tiles per subtotal exchange
+    static_assert(TT % kEx == 0, "whole exchanges");
     static_assert(NW == 8 || NW == 16, "8 or 16 waves");
     static_assert(nb % kMvSbk == 0, "whole stages per row");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     float* const dxs = reinterpret_cast<float*>(smem + kMvStages * kMvStageBytes);  // [nb][kTok]
-    float4* const ex = reinterpret_cast<float4*>(smem + kMvStages * kMvStageBytes + nb * kTok * 4);  // [TT][NW][64]
+    float4* const ex = reinterpret_cast<float4*>(smem + kMvStages * kMvStageBytes + nb * kTok * 4);  // [kEx][NW][64]
 
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
@@ -249,35 +250,40 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
             }
         }
         // the FADDV tree: each wave's RPW leaves first (the lower levels), then
-        // the NW wave subtotals of every (row, token) meet in LDS (the upper)
+        // the NW wave subtotals of every (row, token) meet in LDS (the upper),
+        // kEx token tiles at a time (32 KB of subtotals)
 #pragma unroll
-        for (int tt = 0; tt < TT; tt++) {
-            float v[4];
+        for (int t0 = 0; t0 < TT; t0 += kEx) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float a[RPW];
+            for (int te = 0; te < kEx; te++) {
+                const int tt = t0 + te;
+                float v[4];
 #pragma unroll
-                for (int q = 0; q < RPW; q++) a[q] = p[q][tt][i];
-                v[i] = tree_sum<RPW>(a);
+                for (int i = 0; i < 4; i++) {
+                    float a[RPW];
+#pragma unroll
+                    for (int q = 0; q < RPW; q++) a[q] = p[q][tt][i];
+                    v[i] = tree_sum<RPW>(a);
+                }
+                ex[(te * NW + wave) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
             }
-            ex[(tt * NW + wave) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
-        }
-        __syncthreads();
+            __syncthreads();
 #pragma unroll
-        for (uint32_t o0 = 0; o0 < TT * 256; o0 += NW * 64) {
-            const uint32_t o = o0 + threadIdx.x;
-            if (TT * 256 % (NW * 64) == 0 || o < TT * 256) {
-                const uint32_t tt = o >> 8, c = o & 15, u = (o >> 4) & 15;  // row c, token u of tile tt
-                const uint32_t ln = 16 * (u >> 2) + c, e = u & 3;
-                float a[NW];
+            for (uint32_t o0 = 0; o0 < kEx * 256; o0 += NW * 64) {
+                const uint32_t o = o0 + threadIdx.x;
+                if (kEx * 256 % (NW * 64) == 0 || o < kEx * 256) {
+                    const uint32_t te = o >> 8, c = o & 15, u = (o >> 4) & 15;  // row c, token u of tile t0+te
+                    const uint32_t ln = 16 * (u >> 2) + c, e = u & 3;
+                    float a[NW];
 #pragma unroll
-                for (int k = 0; k < NW; k++) a[k] = reinterpret_cast<const float*>(ex + (tt * NW + k) * 64 + ln)[e];
-                const float v = tree_sum<NW>(a);
-                const uint32_t row = rt * 16 + c, tok = tok0 + tt * 16 + u;
-                if (row < N && tok < T) y[(uint64_t)tok * N + row] = v;
+                    for (int k = 0; k < NW; k++) a[k] = reinterpret_cast<const float*>(ex + (te * NW + k) * 64 + ln)[e];
+                    const float v = tree_sum<NW>(a);
+                    const uint32_t row = rt * 16 + c, tok = tok0 + (t0 + te) * 16 + u;
+                    if (row < N && tok < T) y[(uint64_t)tok * N + row] = v;
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 }
 
@@ -285,7 +291,8 @@ template <int NBR, int TT, int NW>
 int mmv_launch(uint32_t N, uint32_t T, uint32_t Tp, uint32_t n_tg, uint32_t rt_per_wg, const void* W,
                const uint8_t* qxb, const float* dxb, float* y, hipStream_t s) {
     constexpr uint32_t nb = NBR * 16;
-    const uint32_t lds = kMvStages * kMvStageBytes + nb * TT * 16 * 4 + TT * NW * 1024;
+    constexpr uint32_t kEx = TT < 32 / NW ? TT : 32 / NW;
+    const uint32_t lds = kMvStages * kMvStageBytes + nb * TT * 16 * 4 + kEx * NW * 1024;
     if (lds > 160 * 1024) return -1;
     // the dynamic-LDS limit is a per-device attribute of the function
     static std::atomic<bool> attr_set[64];
@@ -324,8 +331,8 @@ int cus_of_current_device() {
 // tokens): one token tile: TT = 1 on 16 waves (K = 4096) or 8 (K = 14336);
 // at K = 4096 with two or four token tiles, TT = 2 on 16 waves, except for
 // many row tiles (four per CU and more: gate_up 28672 x 4096 at 64 tokens,
-// 59.9 us against 64.4), where TT = 4 on 8 waves reads the activations once
-// per workgroup.  Row tiles are dealt so that workgroups number at most one
+// 52.9 us against 64.4 for TT = 2 and 59.8 for TT = 4 on 8 waves), where
+// TT = 4 on 16 waves reads the activations once per workgroup.  Row tiles are dealt so that workgroups number at most one
 // per CU.  Other shapes (K = 14336 with 17+ tokens, more than 64 tokens, other
 // K) keep the older kernels, measured faster or not measured here.
 MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
@@ -340,7 +347,7 @@ MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
         if (ttiles == 1)
             tt = 1, nw = 16;
         else if (ttiles % 4 == 0 && rtiles >= 4 * cus)
-            tt = 4, nw = 8;
+            tt = 4, nw = 16;
         else if (ttiles % 2 == 0)
             tt = 2, nw = 16;
         else
@@ -381,7 +388,7 @@ int mmv_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
                        dxb);
     ANE_HIP_CHECK_LAUNCH();
     if (nb / 16 == 28) return mmv_launch<28, 1, 8>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
-    if (pl.TT == 4) return mmv_launch<8, 4, 8>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
+    if (pl.TT == 4) return mmv_launch<8, 4, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
     if (pl.TT == 2) return mmv_launch<8, 2, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
     return mmv_launch<8, 1, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
 }
