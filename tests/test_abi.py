@@ -55,6 +55,28 @@ def test_pure_host_queries():
     assert L.ane_hip_q8_0_mul_mat_workspace_size(4096, 1) >= 4096 + 128 * 4
 
 
+def test_mul_mat_workspace_covers_both_activation_forms():
+    """ane_hip_q8_0_mul_mat_workspace_size(K, T) must hold the token-major
+    Q8 form (T x nb x 32 bytes, then scales over ceil4(T) tokens) and, from
+    16 tokens, the block-major form of ceil16(T) tokens that the
+    activation-stationary kernel writes (nb x Tp x 32 bytes at a 256-byte
+    boundary, then nb x Tp scales), ragged T included."""
+    L = ane_amd.lib()
+    L.ane_hip_q8_0_mul_mat_workspace_size.restype = ctypes.c_size_t
+
+    def ceil(x, m):
+        return (x + m - 1) // m * m
+
+    for K in (4096, 14336, 8192, 512):
+        nb = K // 32
+        for T in (1, 4, 5, 15, 16, 17, 20, 33, 48, 60, 64, 100):
+            got = L.ane_hip_q8_0_mul_mat_workspace_size(K, T)
+            assert got >= ceil(T * nb * 32, 256) + ceil(nb * ceil(T, 4) * 4, 256), (K, T)
+            if T >= 16:
+                tp = ceil(T, 16)
+                assert got >= ceil(nb * tp * 32, 256) + nb * tp * 4, (K, T)
+
+
 def test_record_sizes():
     """Appendix of the opcode table: dense 54 B, quantize 29, dequantize 25,
     pack 25, channelwise 33, q8_0_gemv 33, dense_fused_i8 42."""
