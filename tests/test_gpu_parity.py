@@ -795,7 +795,9 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    # tiles on 8 waves with ragged rows and tokens, K 14336 with
                                    # ragged rows
                                    (4100, 4096, 48), (6000, 4096, 64), (20000, 4096, 32),
-                                   (28677, 4096, 60), (5000, 14336, 16)])
+                                   (28677, 4096, 60), (5000, 14336, 16),
+                                   # ... with a remainder of K past the last whole block (ignored)
+                                   (300, 4100, 16), (33, 14350, 16)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
