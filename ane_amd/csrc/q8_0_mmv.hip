@@ -328,13 +328,16 @@ int cus_of_current_device() {
 }  // namespace
 
 // Shape plan, from measurements on the config-4 projections (16 and 64
-// tokens): one token tile: TT = 1 on 16 waves (K = 4096) or 8 (K = 14336);
+// tokens): one token tile: TT = 1 on 16 waves (K = 14336 on 8 waves: 24.0
+// against 21.7 us for down 4096 x 14336);
 // at K = 4096 with two or four token tiles, TT = 2 on 16 waves, except for
 // many row tiles (four per CU and more: gate_up 28672 x 4096 at 64 tokens,
 // 52.9 us against 64.4 for TT = 2 and 59.8 for TT = 4 on 8 waves), where
 // TT = 4 on 16 waves reads the activations once per workgroup.  Row tiles are dealt so that workgroups number at most one
 // per CU.  Other shapes (K = 14336 with 17+ tokens, more than 64 tokens, other
-// K) keep the older kernels, measured faster or not measured here.
+// K) keep the older kernels, measured faster (down at 32 / 64 tokens: 29.7 /
+// 37.0 us against 31.5 / 52.9 here with two / four token groups) or not
+// measured here.
 MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
     MmvPlan pl{};
     if (T < 16 || nb % kMvSbk != 0) return pl;
@@ -342,7 +345,7 @@ MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
     const uint32_t ttiles = (T + 15) / 16, rtiles = (N + 15) / 16, cus = (uint32_t)cus_of_current_device();
     uint32_t tt = 0, nw = 0;
     if (nbr == 28 && ttiles == 1) {
-        tt = 1, nw = 8;
+        tt = 1, nw = 16;
     } else if (nbr == 8 && ttiles <= 4) {
         if (ttiles == 1)
             tt = 1, nw = 16;
@@ -387,7 +390,7 @@ int mmv_mul_mat(uint32_t N, uint32_t nb, uint32_t K, uint32_t T, const float* x,
     hipLaunchKernelGGL(k_q8_act_quantize_bt, dim3((nthreads + 255) / 256), dim3(256), 0, s, T, pl.Tp, nb, K, x, qxb,
                        dxb);
     ANE_HIP_CHECK_LAUNCH();
-    if (nb / 16 == 28) return mmv_launch<28, 1, 8>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
+    if (nb / 16 == 28) return mmv_launch<28, 1, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
     if (pl.TT == 4) return mmv_launch<8, 4, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
     if (pl.TT == 2) return mmv_launch<8, 2, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
     return mmv_launch<8, 1, 16>(N, T, pl.Tp, pl.n_tg, pl.rt_per_wg, W, qxb, dxb, y, s);
