@@ -265,6 +265,26 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "me
 // s_waitcnt lgkmcnt(0) only (LDS and scalar memory), leaving stores in flight.
 __device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// LDS loads of bytes whose copies to LDS the caller has already waited for
+// (its ring wait and barrier).  Before an ordinary load from LDS the
+// compiler's wait insertion cannot always tell that no outstanding
+// buffer_load ... lds writes those bytes, and then waits for every
+// outstanding copy (vmcnt(0)); in a copy ring that includes the stage issued
+// just before, so each stage's math would start only once the next stage has
+// landed.  These loads wait for their own data only (lgkmcnt(0)).  The
+// "memory" clobber keeps them after the caller's wait and barrier.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
+__device__ __forceinline__ float4 lds_load_settled_f4(const void* p) {
+    float4 v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_offset(p)) : "memory");
+    return v;
+}
+__device__ __forceinline__ float lds_load_settled_f32(const void* p) {
+    float v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_offset(p)) : "memory");
+    return v;
+}
+
 }  // namespace ane
 
 namespace ane {

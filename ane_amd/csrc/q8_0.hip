@@ -1056,7 +1056,7 @@ k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             const uint64_t av = (uint64_t)a0 | ((uint64_t)a1 << 32);
             const uint64_t bv = *reinterpret_cast<const uint64_t*>(xb + 32 * bb + 8 * g);
             const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)av, (long)bv, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const float dx = dxs[bb];
+            const float dx = lds_load_settled_f32(dxs + bb);
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // output row 4g + i of the tile, token c16
                 const uint16_t dwb = *reinterpret_cast<const uint16_t*>(wrow + i * (kMmaWRowChunks * 16) + 34 * bb);
@@ -1284,7 +1284,7 @@ k_q8_0_mmt(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
                 const uint64_t xv =
                     *reinterpret_cast<const uint64_t*>(xt + tt * 16 * (kMmtXRowChunks * 16) + 32 * bb);
                 const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const float4 d4 = *reinterpret_cast<const float4*>(dd + bb * L::kTok + tt * 16);
+                const float4 d4 = lds_load_settled_f4(dd + bb * L::kTok + tt * 16);
                 const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
@@ -1552,7 +1552,7 @@ k_q8_0_mmr(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
                 const uint64_t xv = *reinterpret_cast<const uint64_t*>(
                     xt + tt * 16 * (L::kXRowChunks * 16) + gi * (L::kXGroupChunks * 16));
                 const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const float4 d4 = *reinterpret_cast<const float4*>(dd + gi * (NR * L::kTok) + tt * 16);
+                const float4 d4 = lds_load_settled_f4(dd + gi * (NR * L::kTok) + tt * 16);
                 const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16

@@ -234,7 +234,7 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
                 for (int tt = 0; tt < TT; tt++) {
                     const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv[q][j][tt], (long)wv,
                                                                           v4i{0, 0, 0, 0}, 0, 0, 0);
-                    const float4 d4 = *reinterpret_cast<const float4*>(dd + tt * 16);
+                    const float4 d4 = lds_load_settled_f4(dd + tt * 16);
                     const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
