@@ -472,11 +472,15 @@ __device__ __forceinline__ float compute_r4(const int8_t* rowp, uint32_t l, uint
 
 // K-quant GEMVs: lane l's fmas over each staged super-block in order, with
 // the format's decoder (the same code as k_qgemv, so the same bits).
+// The staged rows start 16-byte aligned, so super-block p sits at the
+// alignment gcd(kBytes, 16) and the decoders read its fields with typed loads.
 template <class F>
 __device__ __forceinline__ float compute_qf(const int8_t* rowp, uint32_t l, uint32_t sbk, uint32_t gsb0,
                                             const float* xs, float acc) {
+    constexpr int kAlign = F::kBytes % 16 == 0 ? 16 : F::kBytes % 4 == 0 ? 4 : F::kBytes % 2 == 0 ? 2 : 1;
     for (uint32_t p = 0; p < sbk; p++)
-        F::acc(reinterpret_cast<const uint8_t*>(rowp) + p * F::kBytes, xs + (gsb0 + p) * 256, l, acc);
+        F::template acc<kAlign>(reinterpret_cast<const uint8_t*>(rowp) + p * F::kBytes, xs + (gsb0 + p) * 256, l,
+                                acc);
     return acc;
 }
 
@@ -1048,6 +1052,7 @@ k_q8_0_mma(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             if (j & 1) {  // 34bb + 2 is 4-byte aligned for odd bb
                 a0 = a32[0];
                 a1 = a32[1];
+                asm("" : "+v"(a0));  // two loads, not one fused load without alias information
             } else {
                 const uint32_t d0 = a32[0], d1 = a32[1], d2 = a32[2];
                 a0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
@@ -1272,6 +1277,9 @@ k_q8_0_mmt(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             if (bb & 1) {  // 34bb + 2 is 4-byte aligned for odd bb
                 w0 = a32[0];
                 w1 = a32[1];
+                // two loads, not one fused 64-bit load without alias information
+                // (before which the compiler would wait for every copy to LDS)
+                asm("" : "+v"(w0));
             } else {
                 const uint32_t d0 = a32[0], d1 = a32[1], d2 = a32[2];
                 w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);

@@ -17,6 +17,32 @@ __device__ __forceinline__ uint32_t lu16(const uint8_t* p) { return lu8(p) | (lu
 __device__ __forceinline__ uint32_t lu32(const uint8_t* p) { return lu16(p) | (lu16(p + 2) << 16); }
 __device__ __forceinline__ float lh(const uint8_t* p) { return half_bits_to_float(lu16(p)); }
 
+// Multi-byte fields of a super-block in LDS whose base is A-byte aligned.
+// A = 1 (k_qgemv, whose rows sit at any byte offset): composed from bytes.
+// A = 2, 4 or 16 (the streaming kernel: super-blocks laid out from 16-byte
+// aligned rows): single typed 16- or 32-bit reads of the aligned fields.  A
+// load the compiler composes from bytes loses its alias information, and
+// before such an LDS load it waits for every outstanding copy to LDS, the
+// ring's next items included; the typed reads keep it.
+template <int A>
+__device__ __forceinline__ uint32_t fld16(const uint8_t* p) {
+    if constexpr (A >= 2) return *reinterpret_cast<const uint16_t*>(p);
+    else return lu16(p);
+}
+template <int A>
+__device__ __forceinline__ uint32_t fld32(const uint8_t* p) {
+    if constexpr (A >= 4) {
+        return *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (A == 2) {
+        return (uint32_t)*reinterpret_cast<const uint16_t*>(p) |
+               ((uint32_t)*reinterpret_cast<const uint16_t*>(p + 2) << 16);
+    } else {
+        return lu32(p);
+    }
+}
+template <int A>
+__device__ __forceinline__ float fldh(const uint8_t* p) { return half_bits_to_float(fld16<A>(p)); }
+
 // v of lane J of this lane's 16-lane row (DPP row_newbcast).  The 16 lanes
 // of a weight row form one DPP row in every caller, and all of them are
 // active where the decoders run, so a sub-block's scales can be decoded by
@@ -74,9 +100,10 @@ struct Q40 {
 
 struct Q4K {
     static constexpr uint32_t kBytes = 144, kValues = 256, kStage = 4;
+    template <int A = 1>
     __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
         // lane l decodes sub-block l % 8's fl(d * sc) and fl(-dmin * m)
-        const float d = lh(s), nmin = -lh(s + 2);
+        const float d = fldh<A>(s), nmin = -fldh<A>(s + 2);
         uint32_t scl, ml;
         scale_min6(s + 4, (int)(l & 7), scl, ml);
         const float dsl = __fmul_rn(d, (float)scl), dml = __fmul_rn(nmin, (float)ml);
@@ -92,9 +119,10 @@ struct Q4K {
 
 struct Q2K {
     static constexpr uint32_t kBytes = 84, kValues = 256, kStage = 4;
+    template <int A = 1>
     __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
         // lane l decodes sub-block l's fl(d * sc) and fl(-dmin * m)
-        const float d = lh(s + 80), nmin = -lh(s + 82);
+        const float d = fldh<A>(s + 80), nmin = -fldh<A>(s + 82);
         // (the qs words stay per-lane LDS reads: broadcasting them as well
         // measured slower for this format)
         const uint32_t scb = lu8(s + l);
@@ -102,7 +130,7 @@ struct Q2K {
         static_for<16>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             const float ds = row_bcast<j>(dsl), dm = row_bcast<j>(dml);
-            const uint32_t q = (lu32(s + 16 + 4 * j) >> (2 * l)) & 3u;
+            const uint32_t q = (fld32<A>(s + 16 + 4 * j) >> (2 * l)) & 3u;
             a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)q, ds), dm), xs[16 * j + l], a);
         });
     }
@@ -113,15 +141,16 @@ struct Q2K {
 // the handler does with the register its input load reused (:11323-11329).
 struct Q3K {
     static constexpr uint32_t kBytes = 110, kValues = 256, kStage = 4;
+    template <int A = 1>
     __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
         // lane l decodes sub-block l % 8's fl(d * (sc - 32))
-        const float d = lh(s + 108);
+        const float d = fldh<A>(s + 108);
         const uint32_t jl = l & 7;
         const uint32_t scl = jl < 4 ? (lu8(s + 96 + jl) & 63u)
                                     : ((lu8(s + 100 + jl) & 15u) | ((lu8(s + 92 + jl) >> 6) << 4));
         const float dsl = __fmul_rn(d, (float)((int)scl - 32));
         // dword l of qs and dword l % 8 of hmask, which every lane of the row reads
-        const uint32_t qsl = lu32(s + 32 + 4 * l), hml = lu32(s + 4 * jl);
+        const uint32_t qsl = fld32<A>(s + 32 + 4 * l), hml = fld32<A>(s + 4 * jl);
         static_for<8>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             const float ds = row_bcast<j>(dsl);
@@ -142,9 +171,10 @@ struct Q3K {
 
 struct Q5K {
     static constexpr uint32_t kBytes = 176, kValues = 256, kStage = 4;
+    template <int A = 1>
     __device__ static void acc(const uint8_t* s, const float* xs, uint32_t l, float& a) {
         // lane l decodes sub-block l % 8's fl(d * sc) and fl(-dmin * m)
-        const float d = lh(s), nmin = -lh(s + 2);
+        const float d = fldh<A>(s), nmin = -fldh<A>(s + 2);
         uint32_t scl, ml;
         scale_min6(s + 4, (int)(l & 7), scl, ml);
         const float dsl = __fmul_rn(d, (float)scl), dml = __fmul_rn(nmin, (float)ml);
@@ -152,7 +182,7 @@ struct Q5K {
             constexpr int j = decltype(jc)::value;
             const float ds = row_bcast<j>(dsl), dm = row_bcast<j>(dml);
             // (qh stays a per-lane LDS read: broadcasting it measured slower)
-            const uint32_t b = lu8(s + 48 + 16 * j + l), h = lu32(s + 16 + 4 * j);
+            const uint32_t b = lu8(s + 48 + 16 * j + l), h = fld32<A>(s + 16 + 4 * j);
             const uint32_t q0 = (b & 15u) | ((((h & 0xffffu) >> l) & 1u) << 4);
             const uint32_t q1 = (b >> 4) | ((((h >> 16) >> l) & 1u) << 4);
             a = __builtin_fmaf(__fadd_rn(__fmul_rn((float)q0, ds), dm), xs[32 * j + l], a);
