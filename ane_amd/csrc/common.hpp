@@ -284,6 +284,12 @@ __device__ __forceinline__ float lds_load_settled_f32(const void* p) {
     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_offset(p)) : "memory");
     return v;
 }
+// The store counterpart, for LDS bytes no outstanding copy targets: an
+// ordinary LDS store may otherwise wait for every outstanding copy first.
+__device__ __forceinline__ void lds_store_settled_f4(void* p, float4 v) {
+    const v4u u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+    asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(lds_offset(p)), "v"(u) : "memory");
+}
 
 }  // namespace ane
 

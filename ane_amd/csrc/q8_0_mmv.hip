@@ -250,39 +250,48 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
             }
         }
         // the FADDV tree: each wave's RPW leaves first (the lower levels), then
-        // the NW wave subtotals of every (row, token) meet in LDS (the upper),
-        // kEx token tiles at a time (32 KB of subtotals)
+        // the NW wave subtotals of every (row, token) meet in LDS (the upper).
+        // Token tiles [0, kEx) go to ex (32 KB); with TT = 2 kEx, tiles
+        // [kEx, TT) go to the ring slot of the stage just finished, which no
+        // wave reads once all are past the barrier after the first writes.
+        // No barrier follows the reads: the next writes to either region come
+        // after the next stage's barrier (the slot's refill is issued there).
+        static_assert(TT == kEx || TT == 2 * kEx, "one or two exchange regions");
+        static_assert(kEx * NW * 1024 <= kMvStageBytes, "a ring slot holds an exchange region");
+        float4* const ex2 = reinterpret_cast<float4*>(smem + ((s - 1) % kMvStages) * kMvStageBytes);
+        auto leaves = [&](int tt, float4* dst) {
+            float v[4];
 #pragma unroll
-        for (int t0 = 0; t0 < TT; t0 += kEx) {
+            for (int i = 0; i < 4; i++) {
+                float a[RPW];
 #pragma unroll
-            for (int te = 0; te < kEx; te++) {
-                const int tt = t0 + te;
-                float v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float a[RPW];
-#pragma unroll
-                    for (int q = 0; q < RPW; q++) a[q] = p[q][tt][i];
-                    v[i] = tree_sum<RPW>(a);
-                }
-                ex[(te * NW + wave) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
+                for (int q = 0; q < RPW; q++) a[q] = p[q][tt][i];
+                v[i] = tree_sum<RPW>(a);
             }
-            __syncthreads();
+            lds_store_settled_f4(dst + wave * 64 + lane, make_float4(v[0], v[1], v[2], v[3]));
+        };
 #pragma unroll
-            for (uint32_t o0 = 0; o0 < kEx * 256; o0 += NW * 64) {
-                const uint32_t o = o0 + threadIdx.x;
-                if (kEx * 256 % (NW * 64) == 0 || o < kEx * 256) {
-                    const uint32_t te = o >> 8, c = o & 15, u = (o >> 4) & 15;  // row c, token u of tile t0+te
-                    const uint32_t ln = 16 * (u >> 2) + c, e = u & 3;
-                    float a[NW];
+        for (int te = 0; te < kEx; te++) leaves(te, ex + te * NW * 64);
+        lds_barrier();  // the stores waited for themselves; y needs no fence here
+        if constexpr (TT == 2 * kEx) {
 #pragma unroll
-                    for (int k = 0; k < NW; k++) a[k] = reinterpret_cast<const float*>(ex + (te * NW + k) * 64 + ln)[e];
-                    const float v = tree_sum<NW>(a);
-                    const uint32_t row = rt * 16 + c, tok = tok0 + (t0 + te) * 16 + u;
-                    if (row < N && tok < T) y[(uint64_t)tok * N + row] = v;
-                }
+            for (int te = 0; te < kEx; te++) leaves(kEx + te, ex2 + te * NW * 64);
+            lds_barrier();
+        }
+#pragma unroll
+        for (uint32_t o0 = 0; o0 < TT * 256; o0 += NW * 64) {
+            const uint32_t o = o0 + threadIdx.x;
+            if (TT * 256 % (NW * 64) == 0 || o < TT * 256) {
+                const uint32_t tt = o >> 8, c = o & 15, u = (o >> 4) & 15;  // row c, token u of tile tt
+                const uint32_t ln = 16 * (u >> 2) + c, e = u & 3;
+                const float4* src = tt < (uint32_t)kEx ? ex + tt * NW * 64 : ex2 + (tt - kEx) * NW * 64;
+                float a[NW];
+#pragma unroll
+                for (int k = 0; k < NW; k++) a[k] = reinterpret_cast<const float*>(src + k * 64 + ln)[e];
+                const float v = tree_sum<NW>(a);
+                const uint32_t row = rt * 16 + c, tok = tok0 + tt * 16 + u;
+                if (row < N && tok < T) y[(uint64_t)tok * N + row] = v;
             }
-            __syncthreads();
         }
     }
 }
