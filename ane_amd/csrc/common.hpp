@@ -284,6 +284,33 @@ __device__ __forceinline__ float lds_load_settled_f32(const void* p) {
     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_offset(p)) : "memory");
     return v;
 }
+// N settled float4 loads at p, p + 64, ..., p + 64 (N - 1) bytes with one
+// wait for all of them.
+template <int N>
+__device__ __forceinline__ void lds_load_settled_f4x(const void* p, float4 (&o)[N]) {
+    static_assert(N == 1 || N == 2 || N == 4, "1, 2 or 4 loads");
+    v4u u[N];
+    if constexpr (N == 1) {
+        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(u[0]) : "v"(lds_offset(p)) : "memory");
+    } else if constexpr (N == 2) {
+        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:64\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(u[0]), "=&v"(u[1])
+                     : "v"(lds_offset(p))
+                     : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\tds_read_b128 %2, %4 offset:128\n\t"
+            "ds_read_b128 %3, %4 offset:192\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(u[0]), "=&v"(u[1]), "=&v"(u[2]), "=&v"(u[3])
+            : "v"(lds_offset(p))
+            : "memory");
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        o[i] = make_float4(__uint_as_float(u[i].x), __uint_as_float(u[i].y), __uint_as_float(u[i].z),
+                           __uint_as_float(u[i].w));
+}
+
 // The store counterpart, for LDS bytes no outstanding copy targets: an
 // ordinary LDS store may otherwise wait for every outstanding copy first.
 __device__ __forceinline__ void lds_store_settled_f4(void* p, float4 v) {

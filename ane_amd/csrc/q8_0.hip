@@ -1287,12 +1287,14 @@ k_q8_0_mmt(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             }
             const uint64_t wv = (uint64_t)w0 | ((uint64_t)w1 << 32);
             const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wrow + 34 * bb));
+            float4 d4s[TT];  // d_x of every token tile: 64 bytes apart
+            lds_load_settled_f4x<TT>(dd + bb * L::kTok, d4s);
 #pragma unroll
             for (int tt = 0; tt < TT; tt++) {
                 const uint64_t xv =
                     *reinterpret_cast<const uint64_t*>(xt + tt * 16 * (kMmtXRowChunks * 16) + 32 * bb);
                 const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const float4 d4 = lds_load_settled_f4(dd + bb * L::kTok + tt * 16);
+                const float4 d4 = d4s[tt];
                 const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
@@ -1555,12 +1557,14 @@ k_q8_0_mmr(uint32_t N, uint32_t nb, uint32_t T, const uint8_t* __restrict__ W, c
             }
             const uint64_t wv = (uint64_t)w0 | ((uint64_t)w1 << 32);
             const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wb));
+            float4 d4s[TT];  // d_x of every token tile: 64 bytes apart
+            lds_load_settled_f4x<TT>(dd + gi * (NR * L::kTok), d4s);
 #pragma unroll
             for (int tt = 0; tt < TT; tt++) {
                 const uint64_t xv = *reinterpret_cast<const uint64_t*>(
                     xt + tt * 16 * (L::kXRowChunks * 16) + gi * (L::kXGroupChunks * 16));
                 const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv, (long)wv, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const float4 d4 = lds_load_settled_f4(dd + gi * (NR * L::kTok) + tt * 16);
+                const float4 d4 = d4s[tt];
                 const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16

@@ -230,11 +230,15 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
                 const uint64_t wv = (uint64_t)w0 | ((uint64_t)w1 << 32);
                 const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wb));
                 const float* dd = dxs + (r + 16 * j) * kTok + 4 * g;
+                // d_x of the token tiles (64 bytes apart), two tiles per wait
+                constexpr int kDB = TT < 2 ? TT : 2;
+                float4 d4s[kDB];
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
                     const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xv[q][j][tt], (long)wv,
                                                                           v4i{0, 0, 0, 0}, 0, 0, 0);
-                    const float4 d4 = lds_load_settled_f4(dd + tt * 16);
+                    if (tt % kDB == 0) lds_load_settled_f4x<kDB>(dd + tt * 16, d4s);
+                    const float4 d4 = d4s[tt % kDB];
                     const float dx[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++)  // token 4g + i of tile tt, weight row c16
