@@ -22,10 +22,11 @@
 //    tiles x 2 VGPRs), from a block-major activation form (qxb[b][Tp][32],
 //    so each load is 512 contiguous bytes).  The activations are read from
 //    L2 once per workgroup instead of once per ring stage.
-//  * Only the weights stream through LDS: a 2-stage ring of 16 rows x 64
-//    blocks (the row stride padded to 12 dwords mod 64, as in k_q8_0_mmt),
-//    copied by buffer_load_dwordx4 ... lds and read by all 16 waves, each
-//    taking its residue's 4 blocks of the stage.  The token scales d_x of the
+//  * Only the weights stream through LDS: a ring of 16 rows x 64 blocks in 2
+//    stages, or x 32 blocks in 3 stages for one token tile (the row stride
+//    padded to 12 dwords mod 64, as in k_q8_0_mmt), copied by
+//    buffer_load_dwordx4 ... lds and read by all 16 waves, each taking its
+//    residue's blocks of the stage.  The token scales d_x of the
 //    group (block-major, nb x 16TT floats) are copied into LDS once.
 //  * After a row tile's last stage the NW wave subtotals of every (row,
 //    token) meet in LDS for the tree's upper levels.
@@ -43,14 +44,23 @@
 namespace ane {
 namespace {
 
-constexpr uint32_t kMvSbk = 64;                                     // blocks per weight stage
-constexpr uint32_t kMvStages = 2;                                   // ring depth
-constexpr uint32_t kMvRowData = kMvSbk * 34 / 16;                   // 136 chunks of a row's stage
-constexpr uint32_t kMvRowChunks = kMvRowData + (3 + 16 - kMvRowData % 16) % 16;  // 147: 12 dwords mod 64
-constexpr uint32_t kMvWChunks = 16 * kMvRowChunks;
-constexpr uint32_t kMvWInstr = (kMvWChunks + 63) / 64;
-constexpr uint32_t kMvStageBytes = kMvWChunks * 16;
-static_assert((kMvRowChunks * 4) % 64 == 12, "row stride");
+// The weight ring: kStages stages of 16 rows x kSbk blocks, the row stride
+// padded to 12 dwords mod 64.  Measured: with one token tile (the least math
+// per stage) 3 stages of 32 blocks, so that two stages' copies are in flight
+// (gate_up T = 16 27.8 -> 26.5 us, down 19.7 -> 18.0); with more token tiles
+// 2 stages of 64 (smaller stages measured 5-20 % slower there).
+template <int TT>
+struct MvRing {
+    static constexpr uint32_t kSbk = TT == 1 ? 32 : 64;  // blocks per stage
+    static constexpr uint32_t kStages = TT == 1 ? 3 : 2;
+    static constexpr uint32_t kRowData = kSbk * 34 / 16;  // chunks of a row's stage
+    static constexpr uint32_t kRowChunks = kRowData + (3 + 16 - kRowData % 16) % 16;
+    static constexpr uint32_t kWChunks = 16 * kRowChunks;
+    static constexpr uint32_t kWInstr = (kWChunks + 63) / 64;
+    static constexpr uint32_t kStageBytes = kWChunks * 16;
+    static_assert((kRowChunks * 4) % 64 == 12, "row stride");
+};
+constexpr uint32_t kMvMaxSbk = 64;  // every ring's stages divide rows of a multiple of 64 blocks
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // ((a0+a1)+(a2+a3)) + ... over n adjacent values: levels of the FADDV tree.
@@ -93,6 +103,10 @@ k_q8_0_mmv(uint32_t N, uint32_t Tp, const uint8_t* __restrict__ W, const uint8_t
            float* __restrict__ y) {
     constexpr uint32_t nb = NBR * 16;
     constexpr uint32_t kTok = TT * 16;
+    using R = MvRing<TT>;
+    constexpr uint32_t kMvSbk = R::kSbk, kMvStages = R::kStages, kMvRowData = R::kRowData;
+    constexpr uint32_t kMvRowChunks = R::kRowChunks, kMvWChunks = R::kWChunks, kMvWInstr = R::kWInstr;
+    constexpr uint32_t kMvStageBytes = R::kStageBytes;
     constexpr uint32_t nsk = nb / kMvSbk;       // stages per row tile
     constexpr uint32_t kJps = kMvSbk / 16;      // a residue's blocks per stage
     constexpr int RPW = 16 / NW;                // residues per wave
@@ -305,7 +319,7 @@ int mmv_launch(uint32_t N, uint32_t T, uint32_t Tp, uint32_t n_tg, uint32_t rt_p
                const uint8_t* qxb, const float* dxb, float* y, hipStream_t s) {
     constexpr uint32_t nb = NBR * 16;
     constexpr uint32_t kEx = TT < 32 / NW ? TT : 32 / NW;
-    const uint32_t lds = kMvStages * kMvStageBytes + nb * TT * 16 * 4 + kEx * NW * 1024;
+    const uint32_t lds = MvRing<TT>::kStages * MvRing<TT>::kStageBytes + nb * TT * 16 * 4 + kEx * NW * 1024;
     if (lds > 160 * 1024) return -1;
     // the dynamic-LDS limit is a per-device attribute of the function
     static std::atomic<bool> attr_set[64];
@@ -353,7 +367,7 @@ int cus_of_current_device() {
 // measured here.
 MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
     MmvPlan pl{};
-    if (T < 16 || nb % kMvSbk != 0) return pl;
+    if (T < 16 || nb % kMvMaxSbk != 0) return pl;
     const uint32_t nbr = nb / 16;
     const uint32_t ttiles = (T + 15) / 16, rtiles = (N + 15) / 16, cus = (uint32_t)cus_of_current_device();
     uint32_t tt = 0, nw = 0;
