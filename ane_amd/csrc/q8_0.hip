@@ -1890,9 +1890,9 @@ constexpr uint32_t kQ8InlineQuantBlocks = ANE_Q8_INLINE_QUANT_BLOCKS;
 extern "C" size_t ane_hip_q8_0_mul_mat_workspace_size(uint32_t K, uint32_t T) {
     const uint64_t nb = K >> 5;
     // qx, then the scales: token-major [T][nb] or block-major [nb][ceil(T, 4)];
-    // for 16+ tokens, or the block-major form of ceil(T, 16) tokens (q8_0_mmv.hip)
+    // for 2+ tokens, or the block-major form of ceil(T, 16) tokens (q8_0_mmv.hip)
     const uint64_t a = ceil_to((uint64_t)T * nb * 32, 256) + ceil_to(nb * (((uint64_t)T + 3) & ~3ull) * 4, 256) + 256;
-    const uint64_t b = T >= 16 ? ceil_to(mmv_workspace_bound((uint32_t)nb, T), 256) : 0;
+    const uint64_t b = T >= 2 ? ceil_to(mmv_workspace_bound((uint32_t)nb, T), 256) : 0;
     return (size_t)(a > b ? a : b);
 }
 
@@ -1914,6 +1914,12 @@ extern "C" int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const fl
         workspace_bytes < ane_hip_q8_0_mul_mat_workspace_size(K, T))
         return ANE_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
+    if (T >= 2 && T <= kMaxStreamTokens && nb % kMmaSb == 0 && stream_eligible(N, nb, K, T, W) &&
+        mmv_fills_cus(N)) {
+        // 2-4 tokens padded to one token tile of the activation-stationary kernel
+        const int r = mmv_mul_mat(N, nb, K, T, x, W, y, workspace, workspace_bytes, s);
+        if (r >= 0) return r;
+    }
     if (T <= kMaxStreamTokens && stream_eligible(N, nb, K, T, W)) {
         int r;
         if (T == 1 && nb <= kQ8InlineQuantBlocks) {

@@ -354,8 +354,9 @@ int cus_of_current_device() {
 
 }  // namespace
 
-// Shape plan, from measurements on the config-4 projections (16 and 64
-// tokens): one token tile: TT = 1 on 16 waves (K = 14336 on 8 waves: 24.0
+// Shape plan, from measurements on the config-4 projections (2-64 tokens;
+// fewer than 16 tokens are padded to one token tile, the padding quantized
+// from zeros and never stored): one token tile: TT = 1 on 16 waves (K = 14336 on 8 waves: 24.0
 // against 21.7 us for down 4096 x 14336);
 // at K = 4096 with two or four token tiles, TT = 2 on 16 waves, except for
 // many row tiles (four per CU and more: gate_up 28672 x 4096 at 64 tokens,
@@ -367,7 +368,7 @@ int cus_of_current_device() {
 // measured here.
 MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
     MmvPlan pl{};
-    if (T < 16 || nb % kMvMaxSbk != 0) return pl;
+    if (T < 2 || nb % kMvMaxSbk != 0) return pl;
     const uint32_t nbr = nb / 16;
     const uint32_t ttiles = (T + 15) / 16, rtiles = (N + 15) / 16, cus = (uint32_t)cus_of_current_device();
     uint32_t tt = 0, nw = 0;
@@ -391,6 +392,15 @@ MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T) {
     pl.rt_per_wg = (rtiles + per_tg - 1) / per_tg;
     pl.Tp = ttiles * 16;
     return pl;
+}
+
+// Whether the row tiles of N rows deal evenly over the CUs (a whole number
+// per CU, or four and more per CU).  For 2-4 tokens the padded token tile
+// pays only then (measured: o, gate_up, down 8.6 / 31.7 / 18.5 -> 8.3 / 25.5
+// / 17.9 us at 2 tokens; qkv's 384 row tiles on 256 CUs 10.3 -> 11.0 us).
+bool mmv_fills_cus(uint32_t N) {
+    const uint32_t rtiles = (N + 15) / 16, cus = (uint32_t)cus_of_current_device();
+    return rtiles % cus == 0 || rtiles >= 4 * cus;
 }
 
 uint64_t mmv_workspace_bytes(uint32_t nb, const MmvPlan& pl) {

@@ -15,6 +15,7 @@ struct MmvPlan {
 };
 MmvPlan mmv_plan(uint32_t N, uint32_t nb, uint32_t T);
 // Workspace bytes the plan's activation form takes.
+bool mmv_fills_cus(uint32_t N);
 uint64_t mmv_workspace_bytes(uint32_t nb, const MmvPlan& pl);
 // The same for any plan of T tokens (the activation form of ceil16(T) tokens).
 uint64_t mmv_workspace_bound(uint32_t nb, uint32_t T);

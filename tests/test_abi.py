@@ -58,7 +58,7 @@ def test_pure_host_queries():
 def test_mul_mat_workspace_covers_both_activation_forms():
     """ane_hip_q8_0_mul_mat_workspace_size(K, T) must hold the token-major
     Q8 form (T x nb x 32 bytes, then scales over ceil4(T) tokens) and, from
-    16 tokens, the block-major form of ceil16(T) tokens that the
+    2 tokens, the block-major form of ceil16(T) tokens that the
     activation-stationary kernel writes (nb x Tp x 32 bytes at a 256-byte
     boundary, then nb x Tp scales), ragged T included."""
     L = ane_amd.lib()
@@ -72,7 +72,7 @@ def test_mul_mat_workspace_covers_both_activation_forms():
         for T in (1, 4, 5, 15, 16, 17, 20, 33, 48, 60, 64, 100):
             got = L.ane_hip_q8_0_mul_mat_workspace_size(K, T)
             assert got >= ceil(T * nb * 32, 256) + ceil(nb * ceil(T, 4) * 4, 256), (K, T)
-            if T >= 16:
+            if T >= 2:
                 tp = ceil(T, 16)
                 assert got >= ceil(nb * tp * 32, 256) + nb * tp * 4, (K, T)
 

@@ -797,7 +797,12 @@ def test_q8_0_gemv_r_parity(ane, oracle, M, K):
                                    (4100, 4096, 48), (6000, 4096, 64), (20000, 4096, 32),
                                    (28677, 4096, 60), (5000, 14336, 16),
                                    # ... with a remainder of K past the last whole block (ignored)
-                                   (300, 4100, 16), (33, 14350, 16)])
+                                   (300, 4100, 16), (33, 14350, 16),
+                                   # ... for 2-15 tokens padded to one token tile (2-4 tokens where
+                                   # the row tiles fill the CUs): ragged rows, K 14336, and rows
+                                   # that keep 2-4 tokens on the streaming kernel
+                                   (4096, 4096, 2), (28672, 4096, 3), (4096, 14336, 4), (6144, 4096, 5),
+                                   (4100, 4096, 8), (300, 4096, 12), (5000, 14336, 7), (4100, 4096, 4)])
 def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
     import torch
 
@@ -816,7 +821,7 @@ def test_q8_0_mul_mat_g_parity(ane, oracle, N, K, T):
 CONFIG4 = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 64])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 16, 64])
 @pytest.mark.parametrize("proj", list(CONFIG4))
 def test_q8_0_mul_mat_config4_shapes(ane, oracle, proj, T):
     """Config 4 at its exact shapes: every (projection, tokens) pair, every
