@@ -153,7 +153,12 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
     }
 
     // ---- every K and V row of the chunk (non-temporal loads: the cache is
-    // streamed once per token)
+    // streamed once per token).  The loads stay in this order (small
+    // operands, K, V): vector-memory loads complete in order, so a score
+    // waits only for its K row and the loads before it, while V lands
+    // during the scores and the softmax; left free, the scheduler put V
+    // (and part of q) ahead of K.
+    __builtin_amdgcn_sched_barrier(0);
     uint4 kraw[kChunk / 16];
 #pragma unroll
     for (uint32_t st = 0; st < kChunk / 16; st++) {
@@ -162,6 +167,7 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
         const v4i t = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kc + ((uint64_t)g * ctx + jc) * kHD + sub * 8));
         kraw[st] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
     }
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t vraw[kChunk / 4];
 #pragma unroll
     for (uint32_t jj = 0; jj < kChunk / 4; jj++) {
@@ -169,6 +175,7 @@ k_attention(const float* __restrict__ q, const float* __restrict__ cs, uint16_t*
         const uint32_t jc = j < len ? j : len - 1;
         vraw[jj] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vc + ((uint64_t)g * ctx + jc) * kHD + 2 * lane));
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- q (rotated), and this token's k and v as fp16
     float qv[kGroup][8];
