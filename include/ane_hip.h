@@ -253,9 +253,11 @@ int ane_hip_q8_0_mul_mat(uint32_t N, uint32_t K, uint32_t T, const float* x,
                          const void* W, float* y, void* workspace,
                          size_t workspace_bytes, void* stream);
 /* The workspace for every route of an N-row matrix: at 5+ tokens on
- * matrices with few rows (fewer than 4 x 16 rows per CU), the fastest
- * kernel splits each 64-row group's block residues over four workgroups and
- * keeps their subtotals (4 x T x N fp32) in the workspace.  A workspace of
+ * matrices with few rows (fewer than 4 x 16 rows per CU) and rows of 256+
+ * blocks, where the activation-stationary kernel does not take the shape
+ * (e.g. 17+ tokens at K = 14336), the fastest kernel splits each 64-row
+ * group's block residues over four workgroups and keeps their subtotals
+ * (4 x T x N fp32) in the workspace.  A workspace of
  * ane_hip_q8_0_mul_mat_workspace_size(K, T) bytes is still valid: that
  * route is then not taken.  The result is bit-identical either way. */
 size_t ane_hip_q8_0_mul_mat_workspace_size_n(uint32_t N, uint32_t K, uint32_t T);
