@@ -436,6 +436,21 @@ extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float sca
                                       float* scales_out, void* workspace,
                                       size_t workspace_bytes, void* stream) {
     if (M > 0 && N > 0 && !C) return ANE_ERR_BAD_POINTER;
+    if (M > 0 && N > 0 && K > 0 && small_fused_eligible((uint32_t)M, (uint32_t)N, (uint32_t)K)) {
+        // small operands: the absmax pass and one quantize-and-contract launch
+        int st = fused_check(M, N, K, workspace, workspace_bytes);
+        if (st != ANE_OK) return st;
+        if (!A || !B) return ANE_ERR_BAD_POINTER;
+        hipStream_t s = (hipStream_t)stream;
+        const FusedLayout L = fused_layout(M, N, K, workspace);
+        st = launch_fused_small(A, B, (uint32_t)M, (uint32_t)N, (uint32_t)K, scale, relu ? 0.0f : -3.40282347e+38f, C,
+                                L.partials, L.scales, L.wstatus, s);
+        if (st != ANE_OK) return st;
+        if (scales_out && hipMemcpyAsync(scales_out, L.scales, 2 * sizeof(float), hipMemcpyDeviceToDevice, s) !=
+                              hipSuccess)
+            return ANE_ERR_HIP;
+        return ANE_OK;
+    }
     int st = ane_hip_dense_fused_i8_quantize(M, N, K, A, B, scales_out, workspace, workspace_bytes,
                                              stream);
     if (st != ANE_OK) return st;

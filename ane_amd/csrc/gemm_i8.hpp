@@ -34,6 +34,13 @@ constexpr uint32_t kFusedPartials = 1024;
 int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t Kp, uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales,
                           uint32_t* wstatus, hipStream_t s);
+// The whole of dense_fused_i8 for small operands (K <= 1024, at most 512
+// tiles of 16 x 16): the absmax pass, then one launch that quantizes each tile's rows
+// and columns into LDS and contracts them (quantize_fused.hip).  Writes C,
+// the scales and the wait record, not qA / qBt.
+bool small_fused_eligible(uint32_t M, uint32_t N, uint32_t K);
+int launch_fused_small(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K, float smul, float lo,
+                       float* C, uint32_t* partials, float* scales, uint32_t* wstatus, hipStream_t s);
 // The current device's record of failed grid-wide waits (sticky bits; 0 if
 // the resident route never ran): read, and cleared together with the
 // counters once the device is idle when nonzero.

@@ -180,6 +180,140 @@ k_quantize_two(const float* __restrict__ A, const float* __restrict__ B, uint32_
     }
 }
 
+// ------------------------------------------------------------ few-tile route
+// dense_fused_i8 on small operands in two launches instead of three:
+// k_absmax_two, then k_fused_small with one workgroup per 16 x 16 tile of C.
+// The workgroup folds the partial maxima, quantizes its 16 rows of A and 16
+// columns of B straight into LDS (pack4 / pack4_fast under the same
+// condition as k_quantize_two, so the same bytes; zeros past M, N and K),
+// and multiplies them with v_mfma_i32_16x16x64_i8: lane (g, c16) gives row
+// c16 of A and column c16 of B the same 16 bytes of each 64-byte step, so
+// the int32 sums are the exact dot products, and the four waves take every
+// fourth step, their sums meeting in LDS (exact in any order).  The
+// epilogue is the contraction kernels' fmaxA(fadd(fmul((float)acc, s), +0),
+// lo) with s = (sa * sb) * smul.  qA and qBt are not written: nothing after
+// the op reads them (the quantize entry point keeps the two-launch route).
+constexpr uint32_t kSmallMaxK = 1024;
+// Measured against the three-launch route (tiles, fp32 elements read by all
+// workgroups, µs): 128 / 2M (128x128x1000) 15.7 -> 10.0, 256 / 8M
+// (256x256x1024) 14.2 -> 10.0, 512 / 16M (256x512x1024) 14.5 -> 11.2; past
+// one workgroup per CU and a half, slower: 1024 / 8M (512x512x256) 12.0 ->
+// 13.7, 1024 / 32M (256x1024x1024) 15.0 -> 18.0.
+constexpr uint64_t kSmallMaxReads = 16u << 20;
+constexpr uint64_t kSmallMaxTiles = 512;
+constexpr uint32_t kSmallStride = kSmallMaxK + 16;  // bytes per staged row; rows 4 banks apart
+
+__global__ void __launch_bounds__(kT)
+k_fused_small(const float* __restrict__ A, const float* __restrict__ B, uint32_t M, uint32_t N, uint32_t K,
+              const uint32_t* __restrict__ partials, uint32_t nbA, uint32_t nbB, float smul, float lo,
+              float* __restrict__ C, float* __restrict__ scales, uint32_t* __restrict__ wstatus) {
+    __shared__ uint32_t red[4];
+    __shared__ __attribute__((aligned(16))) int8_t qa[16 * kSmallStride];
+    __shared__ __attribute__((aligned(16))) int8_t qb[16 * kSmallStride];
+    __shared__ v4i part[4][64];
+    const float amaxA = fold_partials(partials, nbA, red);
+    const float amaxB = fold_partials(partials + nbA, nbB, red);
+    float sa, ia, sb, ib;
+    quant_params(amaxA, sa, ia);
+    quant_params(amaxB, sb, ib);
+    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0) {
+        scales[0] = sa;
+        scales[1] = sb;
+        wstatus[0] = 0;  // no grid-wide wait on this route
+    }
+    const bool fa = fast_quant_ok(amaxA, ia), fb = fast_quant_ok(amaxB, ib);
+    const uint32_t m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+    const uint32_t Kp = (K + 63) & ~63u;  // whole 64-byte steps
+    const uint32_t kq = Kp / 4;
+
+    // Every load is issued before any is quantized (one memory round trip):
+    // range-checked buffer loads, an offset past the buffer reading zeros.
+    // A: 16 rows x Kp, four consecutive k per thread and step.
+    constexpr int kAIt = 16 * (kSmallMaxK / 4) / kT, kBIt = 4 * (kSmallMaxK / 4) / kT;
+    constexpr uint32_t kNone = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, M * K * 4), rb = make_rsrc(B, K * N * 4);
+    const bool va = (K & 3) == 0 && (((uintptr_t)A) & 15) == 0;  // whole float4s (uniform)
+    float a4[kAIt][4];
+#pragma unroll
+    for (int it = 0; it < kAIt; it++) {
+        const uint32_t c = threadIdx.x + it * kT, r = c / kq, k = (c - r * kq) * 4, m = m0 + r;
+        const bool live = c < 16 * kq && m < M;
+        if (va) {
+            const float4 f = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(ra, live && k < K ? (m * K + k) * 4 : kNone, 0, 0));
+            a4[it][0] = f.x, a4[it][1] = f.y, a4[it][2] = f.z, a4[it][3] = f.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                a4[it][e] = __uint_as_float(
+                    __builtin_amdgcn_raw_buffer_load_b32(ra, live && k + e < K ? (m * K + k + e) * 4 : kNone, 0, 0));
+        }
+    }
+    // B: 4 k x 4 columns per thread and step, transposed in registers so
+    // each staged row is one column of B
+    const bool vb = (N & 3) == 0 && (((uintptr_t)B) & 15) == 0;
+    float b4[kBIt][4][4];  // [step][k + i][n + j]
+#pragma unroll
+    for (int it = 0; it < kBIt; it++) {
+        const uint32_t c = threadIdx.x + it * kT, k = (c >> 2) * 4, n = n0 + (c & 3) * 4;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool live = c < 4 * kq && k + i < K;
+            if (vb) {
+                const float4 f = __builtin_bit_cast(
+                    float4,
+                    __builtin_amdgcn_raw_buffer_load_b128(rb, live && n < N ? ((k + i) * N + n) * 4 : kNone, 0, 0));
+                b4[it][i][0] = f.x, b4[it][i][1] = f.y, b4[it][i][2] = f.z, b4[it][i][3] = f.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    b4[it][i][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        rb, live && n + j < N ? ((k + i) * N + n + j) * 4 : kNone, 0, 0));
+            }
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < kAIt; it++) {
+        const uint32_t c = threadIdx.x + it * kT, r = c / kq, k = (c - r * kq) * 4;
+        if (c < 16 * kq)
+            *reinterpret_cast<uint32_t*>(qa + r * kSmallStride + k) =
+                fa ? pack4_fast(a4[it][0], a4[it][1], a4[it][2], a4[it][3], ia)
+                   : pack4(a4[it][0], a4[it][1], a4[it][2], a4[it][3], ia);
+    }
+#pragma unroll
+    for (int it = 0; it < kBIt; it++) {
+        const uint32_t c = threadIdx.x + it * kT, k = (c >> 2) * 4, j4 = (c & 3) * 4;
+        if (c < 4 * kq) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *reinterpret_cast<uint32_t*>(qb + (j4 + j) * kSmallStride + k) =
+                    fb ? pack4_fast(b4[it][0][j], b4[it][1][j], b4[it][2][j], b4[it][3][j], ib)
+                       : pack4(b4[it][0][j], b4[it][1][j], b4[it][2][j], b4[it][3][j], ib);
+        }
+    }
+    __syncthreads();
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+    v4i acc = {0, 0, 0, 0};
+    for (uint32_t k0 = wave * 64; k0 < Kp; k0 += 256) {
+        const v4i a = *reinterpret_cast<const v4i*>(qa + c16 * kSmallStride + k0 + 16 * g);
+        const v4i b = *reinterpret_cast<const v4i*>(qb + c16 * kSmallStride + k0 + 16 * g);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        const v4i t = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+        const float s = __fmul_rn(__fmul_rn(sa, sb), smul);
+        const uint32_t n = n0 + c16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // D lane (g, c16), register i: row 4g + i, column c16
+            const uint32_t m = m0 + 4 * g + i;
+            if (m < M && n < N) C[(uint64_t)m * N + n] = fmax_a(__fadd_rn(__fmul_rn((float)t[i], s), 0.0f), lo);
+        }
+    }
+}
+
 // ------------------------------------------------------------ resident route
 // Grid: one 512-thread workgroup per CU (its 158 KB of LDS allows no
 // second), every workgroup resident at once, so the grid-wide barrier
@@ -764,6 +898,27 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
     if (nqA + nqB > 0x7fffffffull) return ANE_ERR_INVALID_ARG;
     hipLaunchKernelGGL(k_quantize_two, dim3((uint32_t)(nqA + nqB)), dim3(kT), 0, s, A, B, M, N, K, Kp,
                        partials, nbA, nbB, (uint32_t)nqA, qA, qBt, scales, wstatus);
+    ANE_HIP_CHECK_LAUNCH();
+    return ANE_OK;
+}
+
+bool small_fused_eligible(uint32_t M, uint32_t N, uint32_t K) {
+    if (M == 0 || N == 0 || K == 0 || K > kSmallMaxK) return false;
+    // every workgroup reads its 16 rows of A and 16 columns of B whole: the
+    // route is for few tiles and operands small enough that those re-reads
+    // stay cheap
+    const uint64_t tm = (M + 15) / 16, tn = (N + 15) / 16;
+    return tm * tn <= kSmallMaxTiles && (uint64_t)M * K * tn + (uint64_t)K * N * tm <= kSmallMaxReads;
+}
+
+int launch_fused_small(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K, float smul, float lo,
+                       float* C, uint32_t* partials, float* scales, uint32_t* wstatus, hipStream_t s) {
+    if (!small_fused_eligible(M, N, K)) return ANE_ERR_INVALID_ARG;
+    const uint64_t nA = (uint64_t)M * K, nB = (uint64_t)K * N;
+    const uint32_t nbA = blocks_for(nA), nbB = blocks_for(nB);
+    hipLaunchKernelGGL(k_absmax_two, dim3(nbA + nbB), dim3(kT), 0, s, A, nA, nbA, B, nB, nbB, partials);
+    hipLaunchKernelGGL(k_fused_small, dim3((N + 15) / 16, (M + 15) / 16), dim3(kT), 0, s, A, B, M, N, K, partials,
+                       nbA, nbB, smul, lo, C, scales, wstatus);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
 }

@@ -376,6 +376,71 @@ def test_dense_fused_special_operands(ane, oracle, case, M, N, K):
     assert_f32_identical(host(C).reshape(M, N), ref)
 
 
+_FEW_TILE = [(50, 128, 784, True, 1.0, True), (50, 10, 128, False, 1.0, True), (1, 1, 1, True, 1.0, True),
+             (3, 5, 7, False, 2.5, True), (17, 33, 1023, True, 0.75, True), (16, 16, 1024, False, 1.0, True),
+             (64, 100, 64, True, 1.0, True), (31, 47, 65, False, 1.0, True), (128, 128, 1000, True, 1.0, True),
+             (100, 1, 513, False, 1.0, True), (256, 512, 1024, True, 1.0, True),
+             # past the route's bounds: K > 1024, more than 512 tiles
+             (17, 33, 1025, True, 0.75, False), (512, 512, 256, False, 1.0, False)]
+
+
+@pytest.mark.parametrize("M,N,K,relu,scale,few", _FEW_TILE)
+def test_dense_fused_few_tile_route(ane, oracle, M, N, K, relu, scale, few):
+    """dense_fused_i8 on small operands (K <= 1024, at most 512 tiles of
+    16 x 16 in C: the MNIST layers among them) runs as the absmax pass plus
+    one launch that quantizes each tile's rows and columns into LDS and
+    contracts them.  Bit for bit against the oracle (C and the two scales),
+    with ragged M, N and K (K % 4 != 0 reads A element by element), the
+    largest K, one column.  That launch leaves the workspace's qA bytes as
+    they were (filled with 0x5A here), which shows the route was taken; the
+    shapes past its bounds take the two-launch quantizer, which writes them."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M * 7 + N + K)
+    ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
+    _, sa = oracle.quantize_exact(A.ravel())
+    _, sb = oracle.quantize_exact(B.ravel())
+    wsb = ane.dense_fused_i8_workspace_size(M, N, K)
+    ws = torch.full((wsb,), 0x5A, dtype=torch.uint8, device="cuda")
+    C = zeros(M * N, torch.float32)
+    sc = zeros(2, torch.float32)
+    ane.dense_fused_i8(M, N, K, scale, relu, dev(A), dev(B), C, scales_out=sc, workspace=ws)
+    assert_f32_identical(host(C).reshape(M, N), ref)
+    assert host(sc).tobytes() == np.array([sa, sb], F32).tobytes()
+    qa = host(ws)[12800: 12800 + M * K]  # qA of the workspace layout (gemm_i8.hip, fused_layout)
+    assert (qa == 0x5A).all() == few
+
+
+@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny", "b_nan_tail"])
+def test_dense_fused_few_tile_special_operands(ane, oracle, case):
+    """The few-tile route on the operands the quantizer special-cases (as
+    test_dense_fused_special_operands): a NaN or an infinity (the exact
+    pack4 route), an all-zero tensor, a tensor of denormals and signed zeros
+    (127 / amax = +inf), and a NaN in B's last row and column (the ragged
+    edge of the last tile), through stream_exec at 50 x 130 x 783."""
+    import torch
+
+    M, N, K = 50, 130, 783
+    A, B = data.gemm_inputs(M, N, K, seed=11)
+    if case == "a_nan":
+        A[M // 2, K // 3] = np.nan
+    elif case == "b_inf":
+        B[K - 1, N // 2] = np.inf
+    elif case == "a_neg_inf":
+        A[0, 0] = -np.inf
+    elif case == "a_zero":
+        A[:] = 0.0
+    elif case == "b_tiny":
+        B[:] = np.where(np.arange(K * N).reshape(K, N) % 3 == 0, -0.0, F32(1e-40))
+        B[1, 2] = F32(-3e-39)
+    else:
+        B[K - 1, N - 1] = np.nan
+    ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 2048, 2048), (5000, 64, 4096), (777, 2048, 4096), (64, 2048, 2048)])
 def test_dense_fused_resident_quantizer_shapes(ane, oracle, M, N, K):
     """Shapes on the one-launch resident quantizer (K % 128 == 0, N % 64 == 0,
