@@ -152,7 +152,10 @@ int ane_hip_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
  * with the 0x19 arithmetic, int8 x int8 -> int32 on MFMA, then
  * C = fmaxA((float)acc * ((sa*sb)*scale) + 0.0f, relu ? +0 : -FLT_MAX).
  * Writes exactly M x N.  Optional outputs (may be null): the quantized
- * operands' scales (device float[2] = {sa, sb}). */
+ * operands' scales (device float[2] = {sa, sb}).  The workspace is scratch:
+ * small shapes (K <= 1024, at most 512 tiles of 16 x 16 in C) quantize
+ * straight into each tile's LDS and leave the workspace's quantized-operand
+ * area unwritten; ane_hip_dense_fused_i8_quantize always writes it. */
 size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K);
 int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
                            int relu, const float* A, const float* B, float* C,
