@@ -451,6 +451,22 @@ extern "C" int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float sca
             return ANE_ERR_HIP;
         return ANE_OK;
     }
+    if (M > 0 && N > 0 && K > 0 && strip_fused_eligible((uint32_t)M, (uint32_t)N, (uint32_t)K, A, B)) {
+        // at most 16 rows: one launch holding a 16-column strip of B per CU
+        // (when the device's grid has a workgroup for every strip)
+        int st = fused_check(M, N, K, workspace, workspace_bytes);
+        if (st != ANE_OK) return st;
+        hipStream_t s = (hipStream_t)stream;
+        const FusedLayout L = fused_layout(M, N, K, workspace);
+        if (launch_fused_strip(A, B, (uint32_t)M, (uint32_t)N, (uint32_t)K, scale, relu ? 0.0f : -3.40282347e+38f,
+                               C, L.partials, L.scales, L.wstatus, s, &st)) {
+            if (st != ANE_OK) return st;
+            if (scales_out && hipMemcpyAsync(scales_out, L.scales, 2 * sizeof(float), hipMemcpyDeviceToDevice,
+                                             s) != hipSuccess)
+                return ANE_ERR_HIP;
+            return ANE_OK;
+        }
+    }
     int st = ane_hip_dense_fused_i8_quantize(M, N, K, A, B, scales_out, workspace, workspace_bytes,
                                              stream);
     if (st != ANE_OK) return st;

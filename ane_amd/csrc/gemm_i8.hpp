@@ -41,6 +41,17 @@ int launch_fused_quantize(const float* A, const float* B, uint32_t M, uint32_t N
 bool small_fused_eligible(uint32_t M, uint32_t N, uint32_t K);
 int launch_fused_small(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K, float smul, float lo,
                        float* C, uint32_t* partials, float* scales, uint32_t* wstatus, hipStream_t s);
+// The whole of dense_fused_i8 for at most 16 rows of A in one launch with a
+// grid-wide wait (quantize_fused.hip, k_fused_strip): M <= 16, K % 512 == 0,
+// K <= 4096, N % 16 == 0, at most one 16-column strip of B per workgroup,
+// 16-byte aligned operands and at least 12 MiB of B.  Writes C, the scales
+// and the wait record, not qA / qBt.  Returns false when the route cannot
+// run (nothing queued); true when it was queued (*status = ANE_ERR_HIP if the
+// launch failed after that).
+bool strip_fused_eligible(uint32_t M, uint32_t N, uint32_t K, const float* A, const float* B);
+bool launch_fused_strip(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K, float smul, float lo,
+                        float* C, uint32_t* partials, float* scales, uint32_t* wstatus, hipStream_t s,
+                        int* status);
 // The current device's record of failed grid-wide waits (sticky bits; 0 if
 // the resident route never ran): read, and cleared together with the
 // counters once the device is idle when nonzero.

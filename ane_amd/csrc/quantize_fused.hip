@@ -712,19 +712,250 @@ k_quantize_resident(const float* __restrict__ A, const float* __restrict__ B, ui
         phase2(BoolTag<true>{}, BoolTag<false>{});
 }
 
+// ------------------------------------------------------------ strip route
+// dense_fused_i8 with at most 16 rows of A, in one launch.  Workgroup w (one
+// per CU, all resident, the grid-wide wait above) holds strip ws of B -- its
+// 16 columns n0 = 16 ws .. n0 + 15 over all K rows -- in VGPRs, and a share
+// of A for the maximum; after the wait it quantizes the strip into LDS as
+// 16 qBt rows and all of A as 16 qA rows (zeros past M), with pack4 /
+// pack4_fast under the resident route's condition (so the same bytes), and
+// contracts them with v_mfma_i32_16x16x64_i8 as k_fused_small does (lane
+// (g, c16) gives row c16 of qA and column c16 of the strip the same 16
+// bytes of each 64-byte step; the eight waves take every eighth step and
+// their int32 sums meet in LDS, exact in any order).  Then the contraction
+// kernels' epilogue for C's 16 columns.  B is read once and qBt never goes
+// through memory: against the resident quantizer plus a contraction launch
+// this saves qBt's write and re-read and one launch.  qA and qBt are not
+// written (the quantize entry point keeps the resident route).
+//   B: thread (rq = t / 4, cq = t % 4) holds rows 512 i + 4 rq + j (j < 4)
+//      x columns n0 + 4 cq .. +3, one float4 each: 4 consecutive k of a
+//      column pack into one qBt dword.
+//   A: rows m < M, float4 c = t and t + 512 of each row (K / 4 <= 1024);
+//      rows 0-7 are loaded before the wait (into VGPRs beside the strip),
+//      rows 8-15 once the strip is packed.
+// Shapes: M <= 16, K % 512 == 0, K <= 4096, N % 16 == 0, N / 16 <= the
+// grid, 16-byte aligned A and B, and K * N * 4 < 2^31.
+constexpr uint32_t kSMaxK = 4096;
+constexpr int kSNI = kSMaxK / 512;          // float4 row groups per thread of the strip
+constexpr uint32_t kSStride = kSMaxK + 16;  // bytes per staged row: rows 4 banks apart
+constexpr int kSPre = 4;                    // rows of A loaded before the wait: 2 x kSPre
+
+__global__ void __launch_bounds__(kRT)
+k_fused_strip(const float* __restrict__ A, const float* __restrict__ B, uint32_t M, uint32_t N, uint32_t K,
+              uint32_t perA4, float smul, float lo, float* __restrict__ C, uint32_t* __restrict__ partials,
+              float* __restrict__ scales, uint32_t* __restrict__ sync, uint32_t tag, uint64_t timeout_ticks,
+              uint32_t* __restrict__ status) {
+    __shared__ __attribute__((aligned(16))) int8_t qa[16 * kSStride];
+    __shared__ __attribute__((aligned(16))) int8_t qb[16 * kSStride];
+    __shared__ v4i part[kRT / kWave][kWave];
+    __shared__ uint32_t red[2 * (kRT / kWave)];
+    const uint32_t t = threadIdx.x, wv = t >> 6, lane = t & 63;
+    const uint32_t G = gridDim.x, w = blockIdx.x;
+    // strips contiguous per XCD, as the resident quantizer's shares
+    const uint32_t ws = G % 8 == 0 ? (w % 8) * (G / 8) + w / 8 : w;
+    const bool has = ws < N / 16;
+    const uint32_t n0 = ws * 16, ni = K / 512, K4 = K / 4;
+
+    // ---- phase 1: the strip, A's share (for the maximum) and A's first rows
+    const uint32_t rq = t >> 2, cq = t & 3;
+    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(B, K * N * 4u);
+    float4 bv[kSNI][4];
+#pragma unroll
+    for (int i = 0; i < kSNI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            bv[i][j] = load4(rsB, has && (uint32_t)i < ni ? ((512 * i + 4 * rq + j) * N + n0 + 4 * cq) * 4u : kOff);
+    const uint32_t nA4 = M * K4;
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(A, nA4 * 16u);
+    const uint32_t a0 = w * perA4;
+    const float4 ash = load4(rsA, t < perA4 && a0 + t < nA4 ? (a0 + t) * 16u : kOff);
+    auto a_off = [&](uint32_t m, uint32_t h) {
+        const uint32_t c = t + 512 * h;
+        return m < M && c < K4 ? (m * K4 + c) * 16u : kOff;
+    };
+    float4 ap[kSPre][2], ab[4][2];
+#pragma unroll
+    for (int m = 0; m < kSPre; m++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) ap[m][h] = load4(rsA, a_off(m, h));
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) ab[m][h] = load4(rsA, a_off(kSPre + m, h));
+    // qA rows past M read as zeros in the contraction
+    for (uint32_t r = M; r < 16; r++)
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++)
+            if (t + 512 * h < K4) *reinterpret_cast<uint32_t*>(qa + r * kSStride + 4 * (t + 512 * h)) = 0;
+
+    uint32_t mA = absmax4(ash), mB = 0;
+#pragma unroll
+    for (int i = 0; i < kSNI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) mB = umax(mB, absmax4(bv[i][j]));
+    mA = wave_max_dpp(mA);
+    mB = wave_max_dpp(mB);
+    if (lane == 0) {
+        red[wv] = mA;
+        red[kRT / kWave + wv] = mB;
+    }
+    __syncthreads();
+    if (t == 0) {
+        uint32_t ma = 0, mb = 0;
+        for (int i = 0; i < kRT / kWave; i++) {
+            ma = umax(ma, red[i]);
+            mb = umax(mb, red[kRT / kWave + i]);
+        }
+        const uint32_t bad = grid_arrive_wait(sync, partials, ma, mb, w, G, tag, timeout_ticks);
+        st_agent(&status[1 + w], bad);
+        if (w == 0) st_agent(&status[0], G);
+    }
+    __syncthreads();
+    uint32_t pa = 0, pb = 0;
+    for (uint32_t i = t; i < G; i += kRT) {
+        pa = umax(pa, ld_agent(&partials[i]));
+        pb = umax(pb, ld_agent(&partials[G + i]));
+    }
+    pa = wave_max_dpp(pa);
+    pb = wave_max_dpp(pb);
+    if (lane == 0) {
+        red[wv] = pa;
+        red[kRT / kWave + wv] = pb;
+    }
+    __syncthreads();
+    pa = 0;
+    pb = 0;
+#pragma unroll
+    for (int i = 0; i < kRT / kWave; i++) {
+        pa = umax(pa, red[i]);
+        pb = umax(pb, red[kRT / kWave + i]);
+    }
+    float sa, ia, sb, ib;
+    quant_params(__uint_as_float(pa), sa, ia);
+    quant_params(__uint_as_float(pb), sb, ib);
+    if (w == 0 && t == 0) {
+        scales[0] = sa;
+        scales[1] = sb;
+    }
+    const bool fa = fast_quant_ok(__uint_as_float(pa), ia), fb = fast_quant_ok(__uint_as_float(pb), ib);
+
+    // ---- phase 2: the strip and A packed into LDS, each tensor with pack4_fast
+    // or pack4 (one instantiation each, chosen per tensor as the resident
+    // route does: the same bytes either way)
+    auto pack_b = [&](auto ftag) {
+        constexpr bool F = decltype(ftag)::value;
+#pragma unroll
+        for (int i = 0; i < kSNI; i++) {
+            if ((uint32_t)i < ni) {
+                int8_t* dst = qb + 4 * cq * kSStride + 512 * i + 4 * rq;
+                auto q4 = [&](float a, float b, float c, float d) {
+                    return F ? pack4_fast(a, b, c, d, ib) : pack4(a, b, c, d, ib);
+                };
+                *reinterpret_cast<uint32_t*>(dst) = q4(bv[i][0].x, bv[i][1].x, bv[i][2].x, bv[i][3].x);
+                *reinterpret_cast<uint32_t*>(dst + kSStride) = q4(bv[i][0].y, bv[i][1].y, bv[i][2].y, bv[i][3].y);
+                *reinterpret_cast<uint32_t*>(dst + 2 * kSStride) =
+                    q4(bv[i][0].z, bv[i][1].z, bv[i][2].z, bv[i][3].z);
+                *reinterpret_cast<uint32_t*>(dst + 3 * kSStride) =
+                    q4(bv[i][0].w, bv[i][1].w, bv[i][2].w, bv[i][3].w);
+            }
+        }
+    };
+    if (has) {
+        if (fb)
+            pack_b(BoolTag<true>{});
+        else
+            pack_b(BoolTag<false>{});
+    }
+    auto pack_a = [&](auto ftag) {
+        constexpr bool F = decltype(ftag)::value;
+        auto put = [&](uint32_t m, uint32_t h, float4 v) {
+            const uint32_t c = t + 512 * h;
+            if (m < M && c < K4)
+                *reinterpret_cast<uint32_t*>(qa + m * kSStride + 4 * c) =
+                    F ? pack4_fast(v.x, v.y, v.z, v.w, ia) : pack4(v.x, v.y, v.z, v.w, ia);
+        };
+#pragma unroll
+        for (int m = 0; m < kSPre; m++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) put(m, h, ap[m][h]);
+        if (M > kSPre + 4) {
+            float4 ar[8][2];
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) ar[m][h] = load4(rsA, a_off(kSPre + 4 + m, h));
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) put(kSPre + m, h, ab[m][h]);
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) put(kSPre + 4 + m, h, ar[m][h]);
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) put(kSPre + m, h, ab[m][h]);
+        }
+    };
+    if (fa)
+        pack_a(BoolTag<true>{});
+    else
+        pack_a(BoolTag<false>{});
+    __syncthreads();
+    if (!has) return;
+
+    // ---- the contraction: wave wv takes 64-byte steps wv, wv + 8, ... (at
+    // most kSMaxK / 512 of them), every fragment read issued first
+    const uint32_t g = lane >> 4, c16 = lane & 15;
+    constexpr int kSSteps = kSMaxK / (64 * (kRT / kWave));
+    v4i fa4[kSSteps], fb4[kSSteps];
+#pragma unroll
+    for (int u = 0; u < kSSteps; u++) {
+        const uint32_t k0 = (wv + (kRT / kWave) * u) * 64;
+        if (k0 < K) {
+            fa4[u] = *reinterpret_cast<const v4i*>(qa + c16 * kSStride + k0 + 16 * g);
+            fb4[u] = *reinterpret_cast<const v4i*>(qb + c16 * kSStride + k0 + 16 * g);
+        }
+    }
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < kSSteps; u++)
+        if ((wv + (kRT / kWave) * u) * 64 < K) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa4[u], fb4[u], acc, 0, 0, 0);
+    part[wv][lane] = acc;
+    __syncthreads();
+    if (wv == 0) {
+        v4i s4 = part[0][lane];
+#pragma unroll
+        for (int i = 1; i < kRT / kWave; i++) s4 += part[i][lane];
+        const float s = __fmul_rn(__fmul_rn(sa, sb), smul);
+        const uint32_t n = n0 + c16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // D lane (g, c16), register i: row 4g + i, column c16
+            const uint32_t m = 4 * g + i;
+            if (m < M) C[(uint64_t)m * N + n] = fmax_a(__fadd_rn(__fmul_rn((float)s4[i], s), 0.0f), lo);
+        }
+    }
+}
+
 // The wait's slot in device memory: zero when the code object loads, left
-// with its counters at rest by every launch.  Resident launches on a device
-// are ordered (launch_resident), so one slot per device serves them all.
+// with its counters at rest by every launch.  Launches that wait on it
+// (k_quantize_resident, k_fused_strip) are ordered per device
+// (launch_grid_wait), so one slot per device serves them all.
 __device__ __align__(256) uint32_t resident_sync[kSyncSlotDw];
 
 struct ResidentDevice {
     uint32_t* sync = nullptr;  // device address of resident_sync
-    uint32_t grid = 0;         // CUs x resident workgroups per CU (0: route unusable)
+    // CUs x resident workgroups per CU of each kernel that waits on the
+    // slot (0: that route is unusable)
+    uint32_t grid = 0;        // k_quantize_resident
+    uint32_t grid_strip = 0;  // k_fused_strip
     bool probed = false;
-    // The last resident launch made by a host call: two grids that each need
-    // every CU must not run at once (their workgroups would split the CUs
-    // and neither grid could pass its wait), so a launch on another stream
-    // first waits for this event.
+    // The last grid-wide-wait launch made by a host call: two grids that
+    // each need every CU must not run at once (their workgroups would split
+    // the CUs and neither grid could pass its wait), so a launch on another
+    // stream first waits for this event.
     hipEvent_t last = nullptr;
     hipStream_t last_stream = nullptr;
     bool last_valid = false;
@@ -745,9 +976,9 @@ bool cooperative_launches() {
     return on;
 }
 
-// The device's slot and grid (probed once per device, with it current);
-// null when the resident route is unavailable (then the two-pass route
-// runs).  Called with g_res_mu held.
+// The device's slot and grids (probed once per device, with it current);
+// null when the slot is unavailable (then the routes without a grid-wide
+// wait run).  Called with g_res_mu held.
 ResidentDevice* resident_device(hipStream_t s, int* dev_out) {
     if (s == hipStreamPerThread) return nullptr;
     int dev = 0;
@@ -756,36 +987,34 @@ ResidentDevice* resident_device(hipStream_t s, int* dev_out) {
     if (!d.probed) {
         d.probed = true;
         void* p = nullptr;
-        int cus = 0, occ = 0;
+        int cus = 0, occ = 0, occ_strip = 0;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(resident_sync)) != hipSuccess || !p ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_quantize_resident, kRT, 0) != hipSuccess) {
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_quantize_resident, kRT, 0) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_strip, k_fused_strip, kRT, 0) != hipSuccess) {
             (void)hipGetLastError();
             return nullptr;
         }
-        if (cus > 0 && occ > 0 && (uint64_t)cus * occ <= kFusedPartials) {
-            d.sync = (uint32_t*)p;
-            d.grid = (uint32_t)(cus * occ);
-        }
+        d.sync = (uint32_t*)p;
+        if (cus > 0 && occ > 0 && (uint64_t)cus * occ <= kFusedPartials) d.grid = (uint32_t)(cus * occ);
+        if (cus > 0 && occ_strip > 0 && (uint64_t)cus * occ_strip <= kFusedPartials)
+            d.grid_strip = (uint32_t)(cus * occ_strip);
     }
-    if (!d.grid) return nullptr;
+    if (!d.sync) return nullptr;
     *dev_out = dev;
     return &d;
 }
 
-// The resident route, when the shape allows it: whole 128 x 64 B tiles
-// (K % 128 == 0, N % 64 == 0), 16-byte aligned operands, and at most kRNT
-// B tiles per workgroup.  Returns true when it launched.
-bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
-                     uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales, uint32_t* wstatus,
-                     hipStream_t s, int* status) {
+// What the grid-wide-wait launches share: the capture check, the ordering
+// of such launches per device, the launch tag and the choice of a
+// cooperative launch.  `fits(G)` checks the shape against the kernel's grid
+// G (d.*grid_of); `go(G, sync, tag, limit, coop)` queues the kernel and
+// returns the launch call's error.  Returns true when the kernel was queued
+// (*status = ANE_ERR_HIP if it failed after that), false when the route
+// cannot run (nothing queued: the caller takes another route).
+template <class Fits, class Go>
+bool launch_grid_wait(hipStream_t s, uint32_t ResidentDevice::*grid_of, Fits fits, Go go, int* status) {
     *status = ANE_OK;
-    if (K == 0 || M == 0 || N == 0 || (K % kBTK) || (N % kBTN)) return false;
-    // below ~12 MiB of operands the two launches of the two-pass route are
-    // faster than one grid-wide wait (measured: 1024^3 7.7 against 9.0 us,
-    // 64 x 2048 x 2048 10.0 against 9.4 us)
-    if (((uint64_t)M * K + (uint64_t)K * N) * 4 < kResidentMinBytes) return false;
-    if ((((uintptr_t)A) | ((uintptr_t)B)) & 15) return false;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
         (void)hipGetLastError();
@@ -797,15 +1026,9 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     ResidentDevice* dp = resident_device(s, &dev);
     if (!dp) return false;
     ResidentDevice& d = *dp;
-    const uint32_t G = d.grid;
-    const uint64_t nTiles = (uint64_t)(K / kBTK) * (N / kBTN);
-    if (nTiles > (uint64_t)kRNT * G) return false;
-    const uint32_t perT = (uint32_t)((nTiles + G - 1) / G);
-    const uint64_t nA4 = (uint64_t)M * K / 4;
-    const uint64_t perA4 = (nA4 + G - 1) / G;
-    // the kernel's buffer offsets are 32-bit byte offsets below kOff
-    if (perA4 * 16 >= kOff || (uint64_t)K * N * 4 >= kOff) return false;
-    // Resident launches on one device are ordered: a launch on another
+    const uint32_t G = d.*grid_of;
+    if (!G || !fits(G)) return false;
+    // Grid-wide-wait launches on one device are ordered: a launch on another
     // stream than the previous one waits for it.  A captured launch cannot
     // wait for work outside its graph, so under capture the route is taken
     // only on the stream of the previous launch (graph replays are ordered
@@ -825,34 +1048,15 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
     }
     // Outside capture the grid goes out as a cooperative launch: the runtime
     // then starts it only with every workgroup resident at once, or refuses
-    // it (the two-pass route runs instead).  A captured launch is a plain
-    // one; the ordering above and the bounded, tagged wait cover it.
+    // it (another route runs instead).  A captured launch is a plain one;
+    // the ordering above and the bounded, tagged wait cover it.
     if (++d.tag == 0) d.tag = 1;
-    const float* kA = A;
-    const float* kB = B;
-    uint32_t kN = N, kK = K, kTiles = (uint32_t)nTiles, kPerT = perT, kTag = d.tag;
-    uint64_t kNA4 = nA4, kPerA4 = perA4, kLimit = g_wait_limit.load(std::memory_order_relaxed);
-    uint32_t* kPartials = partials;
-    int8_t* kQA = qA;
-    int8_t* kQBt = qBt;
-    float* kScales = scales;
-    uint32_t* kSync = d.sync;
-    uint32_t* kStatus = wstatus;
-    if (!capturing && cooperative_launches()) {
-        void* args[] = {&kA, &kB, &kN, &kK, &kNA4, &kPerA4, &kTiles, &kPerT, &kPartials, &kQA, &kQBt,
-                        &kScales, &kSync, &kTag, &kLimit, &kStatus};
-        if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_quantize_resident), dim3(G), dim3(kRT),
-                                       args, 0, s) != hipSuccess) {
-            (void)hipGetLastError();  // refused before anything was queued
-            return false;
-        }
-    } else {
-        hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, kA, kB, kN, kK, kNA4, kPerA4, kTiles,
-                           kPerT, kPartials, kQA, kQBt, kScales, kSync, kTag, kLimit, kStatus);
-        if (hipGetLastError() != hipSuccess) {
-            *status = ANE_ERR_HIP;
-            return true;
-        }
+    const bool coop = !capturing && cooperative_launches();
+    if (go(G, d.sync, d.tag, g_wait_limit.load(std::memory_order_relaxed), coop) != hipSuccess) {
+        (void)hipGetLastError();
+        if (coop) return false;  // refused before anything was queued
+        *status = ANE_ERR_HIP;
+        return true;
     }
     if (!capturing) {
         if (hipEventRecord(d.last, s) != hipSuccess) {
@@ -864,6 +1068,54 @@ bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uin
         d.last_valid = true;
     }
     return true;
+}
+
+// The resident route, when the shape allows it: whole 128 x 64 B tiles
+// (K % 128 == 0, N % 64 == 0), 16-byte aligned operands, and at most kRNT
+// B tiles per workgroup.  Returns true when it launched.
+bool launch_resident(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K,
+                     uint32_t* partials, int8_t* qA, int8_t* qBt, float* scales, uint32_t* wstatus,
+                     hipStream_t s, int* status) {
+    *status = ANE_OK;
+    if (K == 0 || M == 0 || N == 0 || (K % kBTK) || (N % kBTN)) return false;
+    // below ~12 MiB of operands the two launches of the two-pass route are
+    // faster than one grid-wide wait (measured: 1024^3 7.7 against 9.0 us,
+    // 64 x 2048 x 2048 10.0 against 9.4 us)
+    if (((uint64_t)M * K + (uint64_t)K * N) * 4 < kResidentMinBytes) return false;
+    if ((((uintptr_t)A) | ((uintptr_t)B)) & 15) return false;
+    const uint64_t nTiles = (uint64_t)(K / kBTK) * (N / kBTN);
+    const uint64_t nA4 = (uint64_t)M * K / 4;
+    uint32_t perT = 0;
+    uint64_t perA4 = 0;
+    auto fits = [&](uint32_t G) {
+        if (nTiles > (uint64_t)kRNT * G) return false;
+        perT = (uint32_t)((nTiles + G - 1) / G);
+        perA4 = (nA4 + G - 1) / G;
+        // the kernel's buffer offsets are 32-bit byte offsets below kOff
+        return perA4 * 16 < kOff && (uint64_t)K * N * 4 < kOff;
+    };
+    auto go = [&](uint32_t G, uint32_t* sync, uint32_t tag, uint64_t limit, bool coop) {
+        const float* kA = A;
+        const float* kB = B;
+        uint32_t kN = N, kK = K, kTiles = (uint32_t)nTiles, kPerT = perT, kTag = tag;
+        uint64_t kNA4 = nA4, kPerA4 = perA4, kLimit = limit;
+        uint32_t* kPartials = partials;
+        int8_t* kQA = qA;
+        int8_t* kQBt = qBt;
+        float* kScales = scales;
+        uint32_t* kSync = sync;
+        uint32_t* kStatus = wstatus;
+        if (coop) {
+            void* args[] = {&kA, &kB, &kN, &kK, &kNA4, &kPerA4, &kTiles, &kPerT, &kPartials, &kQA, &kQBt,
+                            &kScales, &kSync, &kTag, &kLimit, &kStatus};
+            return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_quantize_resident), dim3(G),
+                                              dim3(kRT), args, 0, s);
+        }
+        hipLaunchKernelGGL(k_quantize_resident, dim3(G), dim3(kRT), 0, s, kA, kB, kN, kK, kNA4, kPerA4, kTiles,
+                           kPerT, kPartials, kQA, kQBt, kScales, kSync, kTag, kLimit, kStatus);
+        return hipGetLastError();
+    };
+    return launch_grid_wait(s, &ResidentDevice::grid, fits, go, status);
 }
 
 // The current device's slot, if the resident route was ever set up on it.
@@ -921,6 +1173,50 @@ int launch_fused_small(const float* A, const float* B, uint32_t M, uint32_t N, u
                        nbA, nbB, smul, lo, C, scales, wstatus);
     ANE_HIP_CHECK_LAUNCH();
     return ANE_OK;
+}
+
+bool strip_fused_eligible(uint32_t M, uint32_t N, uint32_t K, const float* A, const float* B) {
+    if (M == 0 || M > 16 || N == 0 || N % 16 || K == 0 || K % 512 || K > kSMaxK) return false;
+    if ((((uintptr_t)A) | ((uintptr_t)B)) & 15) return false;
+    // as for the resident quantizer: below ~12 MiB of B the launches
+    // without a grid-wide wait are the faster ones
+    return (uint64_t)K * N * 4 >= kResidentMinBytes && (uint64_t)K * N * 4 < kOff;
+}
+
+bool launch_fused_strip(const float* A, const float* B, uint32_t M, uint32_t N, uint32_t K, float smul, float lo,
+                        float* C, uint32_t* partials, float* scales, uint32_t* wstatus, hipStream_t s,
+                        int* status) {
+    *status = ANE_OK;
+    if (!strip_fused_eligible(M, N, K, A, B)) return false;
+    const uint64_t nA4 = (uint64_t)M * K / 4;
+    uint32_t perA4 = 0;
+    auto fits = [&](uint32_t G) {
+        if (N / 16 > G) return false;  // one strip per workgroup
+        perA4 = (uint32_t)((nA4 + G - 1) / G);
+        return perA4 <= (uint32_t)kRT;  // one float4 of A's share per thread
+    };
+    auto go = [&](uint32_t G, uint32_t* sync, uint32_t tag, uint64_t limit, bool coop) {
+        const float* kA = A;
+        const float* kB = B;
+        uint32_t kM = M, kN = N, kK = K, kPerA4 = perA4, kTag = tag;
+        float kSmul = smul, kLo = lo;
+        float* kC = C;
+        uint32_t* kPartials = partials;
+        float* kScales = scales;
+        uint32_t* kSync = sync;
+        uint64_t kLimit = limit;
+        uint32_t* kStatus = wstatus;
+        if (coop) {
+            void* args[] = {&kA, &kB, &kM, &kN, &kK, &kPerA4, &kSmul, &kLo, &kC, &kPartials, &kScales,
+                            &kSync, &kTag, &kLimit, &kStatus};
+            return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_fused_strip), dim3(G), dim3(kRT),
+                                              args, 0, s);
+        }
+        hipLaunchKernelGGL(k_fused_strip, dim3(G), dim3(kRT), 0, s, kA, kB, kM, kN, kK, kPerA4, kSmul, kLo, kC,
+                           kPartials, kScales, kSync, kTag, kLimit, kStatus);
+        return hipGetLastError();
+    };
+    return launch_grid_wait(s, &ResidentDevice::grid_strip, fits, go, status);
 }
 
 }  // namespace ane

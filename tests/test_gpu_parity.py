@@ -501,8 +501,80 @@ def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
     assert host(sc).tobytes() == np.array([sa, sb], F32).tobytes()
 
 
-def test_dense_fused_grid_wait_limit(ane, oracle):
-    """The resident quantizer's bounded grid-wide wait, forced from the host
+_STRIP = [(1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0), (5, 4096, 3072, False, 2.5),
+          (9, 3072, 4096, True, 0.75), (4, 4096, 1536, True, 1.0), (3, 2048, 4096, False, 1.0),
+          (8, 4096, 4096, True, 1.0), (12, 2048, 2048 * 3, False, 1.0)]
+
+
+@pytest.mark.parametrize("M,N,K,relu,scale", _STRIP)
+def test_dense_fused_strip_route(ane, oracle, M, N, K, relu, scale):
+    """dense_fused_i8 with at most 16 rows, K % 512 == 0 and at least 12 MiB
+    of B runs in one launch, each CU holding a 16-column strip of B (qBt
+    never written).  Bit for bit against the oracle (C and both scales):
+    rows loaded before the wait only (M <= 4), with the second batch (5-8)
+    and the third (9-16), K of 1536 (rows of 384 float4, half a thread's
+    second load), fewer strips than workgroups (N = 2048: half the
+    workgroups hold A's share and wait only), and K past 4096 (12 x 2048 x
+    6144), which the route does not take.  The workspace's qA bytes stay as
+    they were (0x5A) exactly when the strip route ran."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M * 5 + N + K)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(scale), relu, A, B)
+    finally:
+        oracle.set_threads(1)
+    _, sa = oracle.quantize_exact(A.ravel())
+    _, sb = oracle.quantize_exact(B.ravel())
+    wsb = ane.dense_fused_i8_workspace_size(M, N, K)
+    ws = torch.full((wsb,), 0x5A, dtype=torch.uint8, device="cuda")
+    C = zeros(M * N, torch.float32)
+    sc = zeros(2, torch.float32)
+    ane.dense_fused_i8(M, N, K, scale, relu, dev(A), dev(B), C, scales_out=sc, workspace=ws)
+    assert_f32_identical(host(C).reshape(M, N), ref)
+    assert host(sc).tobytes() == np.array([sa, sb], F32).tobytes()
+    qa = host(ws)[12800: 12800 + M * K]
+    assert (qa == 0x5A).all() == (K <= 4096)
+
+
+@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny", "b_nan_last"])
+def test_dense_fused_strip_special_operands(ane, oracle, case):
+    """The strip route (7 x 4096 x 4096) on the operands the quantizer
+    special-cases: a NaN or an infinity (the exact pack4 for that tensor), an
+    all-zero A, a B of denormals and signed zeros (127 / amax = +inf), and a
+    NaN in B's last row and column (the last strip's last thread)."""
+    import torch
+
+    M, N, K = 7, 4096, 4096
+    A, B = data.gemm_inputs(M, N, K, seed=13)
+    if case == "a_nan":
+        A[M - 1, K // 3] = np.nan
+    elif case == "b_inf":
+        B[K // 2, N // 3] = np.inf
+    elif case == "a_neg_inf":
+        A[0, 0] = -np.inf
+    elif case == "a_zero":
+        A[:] = 0.0
+    elif case == "b_tiny":
+        B[:] = np.where(np.arange(K * N).reshape(K, N) % 3 == 0, -0.0, F32(1e-40))
+        B[1, 2] = F32(-3e-39)
+    else:
+        B[K - 1, N - 1] = np.nan
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    finally:
+        oracle.set_threads(1)
+    C = zeros(M * N, torch.float32)
+    ane.stream_exec(ane.rec_dense_fused_i8(M, N, K, 1.0, True, dev(A), dev(B), C))
+    assert_f32_identical(host(C).reshape(M, N), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 2048, 2048), (8, 4096, 4096)])
+def test_dense_fused_grid_wait_limit(ane, oracle, M, N, K):
+    """The bounded grid-wide wait of the resident quantizer (256 x 2048 x
+    2048) and of the strip route (8 x 4096 x 4096), forced from the host
     to a one-tick limit: every workgroup still finishes, and a launch whose
     workgroups gave up is reported (C is then not valid) by stream_exec, by
     the kernel ABI's wait record (ane_hip_dense_fused_i8_status) and by the
@@ -510,7 +582,6 @@ def test_dense_fused_grid_wait_limit(ane, oracle):
     Restored to the default, the same calls are exact and report nothing."""
     import torch
 
-    M, N, K = 256, 2048, 2048
     A, B = data.gemm_inputs(M, N, K, seed=11)
     oracle.set_threads(0)
     try:
@@ -581,14 +652,15 @@ def test_dense_fused_status_unwritten_workspace(ane):
     assert lib.ane_hip_dense_fused_i8_status(0, stream) == 8
 
 
-def test_dense_fused_resident_two_streams(ane, oracle):
-    """Two resident-route dense_fused_i8 calls issued back to back on two
-    streams with nothing between them: each grid needs every CU, so the
-    library orders the second launch after the first (a stream-event wait);
-    both results are exact and no grid-wide wait gives up."""
+@pytest.mark.parametrize("M,N,K", [(256, 2048, 2048), (16, 4096, 4096)])
+def test_dense_fused_resident_two_streams(ane, oracle, M, N, K):
+    """Two dense_fused_i8 calls with a grid-wide wait (the resident
+    quantizer, 256 x 2048 x 2048; the strip route, 16 x 4096 x 4096) issued
+    back to back on two streams with nothing between them: each grid needs
+    every CU, so the library orders the second launch after the first (a
+    stream-event wait); both results are exact and no wait gives up."""
     import torch
 
-    M, N, K = 256, 2048, 2048
     ins = [data.gemm_inputs(M, N, K, seed=s) for s in (21, 22)]
     oracle.set_threads(0)
     try:
