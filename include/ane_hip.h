@@ -154,8 +154,12 @@ int ane_hip_dense_i8(uint32_t M, uint32_t N, uint32_t K, float sa, float sb,
  * Writes exactly M x N.  Optional outputs (may be null): the quantized
  * operands' scales (device float[2] = {sa, sb}).  The workspace is scratch:
  * small shapes (K <= 1024, at most 512 tiles of 16 x 16 in C) quantize
- * straight into each tile's LDS and leave the workspace's quantized-operand
- * area unwritten; ane_hip_dense_fused_i8_quantize always writes it. */
+ * straight into each tile's LDS, and so do shapes with at most 16 rows of A
+ * (K % 512 == 0, K <= 4096, N % 16 == 0, at most one 16-column strip of B
+ * per CU, at least 12 MiB of B, 16-byte aligned A and B: one launch with
+ * the grid-wide wait described below); both leave the workspace's
+ * quantized-operand area unwritten; ane_hip_dense_fused_i8_quantize always
+ * writes it. */
 size_t ane_hip_dense_fused_i8_workspace_size(int32_t M, int32_t N, int32_t K);
 int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
                            int relu, const float* A, const float* B, float* C,
@@ -164,7 +168,9 @@ int ane_hip_dense_fused_i8(int32_t M, int32_t N, int32_t K, float scale,
 
 /* The operand quantizer of dense_fused_i8 runs, for large shapes (K % 128
  * == 0, N % 64 == 0, at least 12 MiB of operands), as one launch whose
- * workgroups (one per CU) exchange their maxima through a grid-wide wait.
+ * workgroups (one per CU) exchange their maxima through a grid-wide wait;
+ * so does the whole op at up to 16 rows (the strip route above), and what
+ * follows applies to both.
  * Outside stream capture it is a cooperative launch: the runtime starts it
  * only with every workgroup resident, or refuses it and the two-pass route
  * (no wait) runs instead.  Under capture it is a plain launch.  Two such
