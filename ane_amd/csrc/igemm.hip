@@ -184,16 +184,28 @@ extern "C" int ane_hip_cblas_igemm(int variant, int semantics, uint8_t flags, ui
         if ((uint64_t)M * Ke >= (1ull << 31) || (uint64_t)N * Ke >= (1ull << 31) || (M + kT - 1) / kT > 65535u ||
             (N + kT - 1) / kT > 65535u)
             return ANE_ERR_INVALID_ARG;
-        // A rows: plain, the handler's transA addressing, or A^T (BLAS)
-        const int64_t rs = !ta ? (int64_t)lda : 1;
-        const int64_t r16 = (ta && semantics == 0) ? (int64_t)lda - 1 : 0;
-        const int64_t ksa = (ta && semantics == 1) ? (int64_t)lda : 1;
-        if ((st = gather(M, Ke, A, rs, r16, ksa, au, w.a, bu ? w.rowsum : nullptr, s))) return st;
-        // Bt rows: B^T of a K x N matrix, or B itself (transB)
-        if ((st = gather(N, Ke, B, tb ? (int64_t)ldb : 1, 0, tb ? 1 : (int64_t)ldb, bu, w.bt,
-                         au ? w.colsum : nullptr, s)))
+        // Signed operands already in the contraction's layout (A's rows, or
+        // B's rows under transB, K contiguous with 16-byte aligned rows) are
+        // read in place: no gather pass, no row sums needed (both signed).
+        const bool a_direct = !au && !bu && !ta && (lda & 15) == 0 && lda >= Ke && (((uintptr_t)A) & 15) == 0;
+        const bool b_direct = !au && !bu && tb && (ldb & 15) == 0 && ldb >= Ke && (((uintptr_t)B) & 15) == 0;
+        if (!a_direct) {
+            // A rows: plain, the handler's transA addressing, or A^T (BLAS)
+            const int64_t rs = !ta ? (int64_t)lda : 1;
+            const int64_t r16 = (ta && semantics == 0) ? (int64_t)lda - 1 : 0;
+            const int64_t ksa = (ta && semantics == 1) ? (int64_t)lda : 1;
+            if ((st = gather(M, Ke, A, rs, r16, ksa, au, w.a, bu ? w.rowsum : nullptr, s))) return st;
+        }
+        if (!b_direct) {
+            // Bt rows: B^T of a K x N matrix, or B itself (transB)
+            if ((st = gather(N, Ke, B, tb ? (int64_t)ldb : 1, 0, tb ? 1 : (int64_t)ldb, bu, w.bt,
+                             au ? w.colsum : nullptr, s)))
+                return st;
+        }
+        if ((st = ane_hip_gemm_s8_i32(M, N, Ke, a_direct ? static_cast<const int8_t*>(A) : w.a,
+                                      a_direct ? lda : Ke, b_direct ? static_cast<const int8_t*>(B) : w.bt,
+                                      b_direct ? ldb : Ke, w.acc, s)))
             return st;
-        if ((st = ane_hip_gemm_s8_i32(M, N, Ke, w.a, Ke, w.bt, Ke, w.acc, s))) return st;
     }
     const uint32_t corr = (au && bu) ? 16384u * Ke : 0u;
     const dim3 grid((N + 63) / 64, (M + 3) / 4);

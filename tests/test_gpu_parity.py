@@ -829,13 +829,39 @@ def test_cblas_igemm_opcodes_parity(ane, oracle, kind, flags, M, N, K, beta):
     assert_f32_identical(host(Cd), ref)
 
 
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,N,K,lda,ldb,beta", [(64, 96, 320, 352, 336, 0.0), (1024, 1024, 1024, 1024, 1024, 0.5),
+                                                (100, 130, 200, 208, 224, 0.0), (7, 48, 64, 64, 80, -1.0)])
+def test_cblas_igemm_in_place_operands(ane, oracle, flags, M, N, K, lda, ldb, beta):
+    """cblas_igemm (0x61, signed) with 16-byte multiples for lda and ldb: the
+    contraction reads A's rows (no transA) and B's rows (transB) in place
+    instead of gathering them, and only the first 64 * floor(K / 64) bytes of
+    each row (K = 200: the last 8 bytes of each row and the padding past K
+    are nonzero and ignored).  With transA or without transB the operand is
+    gathered as before.  Bit for bit against the handler's arithmetic."""
+    kind = "igemm"
+    lda_ = lda if not flags & 1 else M + 16
+    ldb_ = ldb if flags & 2 else N + 16
+    ldc = N + 1
+    A, B, C = _igemm_case(kind, flags, M, N, K, lda_, ldb_, ldc, seed=M + N + K + 7 * flags)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.cblas_igemm(IGEMM_VARIANT[kind], flags, M, N, K, lda_, ldb_, ldc, 1.25, beta, A, B, C)
+    finally:
+        oracle.set_threads(1)
+    Cd = dev(C)
+    ane.stream_exec(ane.rec_cblas_igemm(kind, flags, M, N, K, lda_, ldb_, ldc, 1.25, beta, dev(A), dev(B), Cd))
+    assert_f32_identical(host(Cd), ref)
+
+
 @pytest.mark.parametrize("kind", ["igemm", "ugemm", "usgemm"])
 @pytest.mark.parametrize("flags", [0, 1, 2, 3])
 @pytest.mark.parametrize("M,N,K,beta", [(33, 40, 256, 0.5), (1024, 1024, 1024, 0.0), (260, 520, 192, -2.0)])
 def test_cblas_igemm_blas_semantics(ane, oracle, kind, flags, M, N, K, beta):
     """The kernel-level BLAS form: op(A) = A^T with transA (A is K x M), and
-    C = alpha*acc + beta*C with two roundings; 1024^3 takes the 256-tile
-    contraction."""
+    C = alpha*acc + beta*C with two roundings; for igemm, lda and ldb are
+    16-byte multiples here, so A (without transA) and B (with transB) are
+    read in place."""
     lda = (K + 16) if not flags & 1 else (M + 16)
     ldb = (N + 16) if not flags & 2 else (K + 16)
     ldc = N
