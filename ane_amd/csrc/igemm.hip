@@ -27,6 +27,9 @@
 //   16384 * Ke            (both)
 // which is exact modulo 2^32, like the handler's own wrapping sums.  The row
 // sums come from the same pre-pass (integer atomics: order-free and exact).
+// Signed operands that are already K-contiguous rows (A without transA, B
+// with transB) with 16-byte aligned rows skip the pre-pass: the contraction
+// reads them in place (1024^3 transB: 15.8 -> 10.8 us, two launches fewer).
 #include "gemm_i8.hpp"
 
 namespace ane {
