@@ -683,6 +683,55 @@ def test_dense_fused_resident_two_streams(ane, oracle, M, N, K):
             C.zero_()
 
 
+@pytest.mark.parametrize("M,N,K,route", [(8, 4096, 4096, "strip"), (256, 2048, 2048, "resident"),
+                                         (50, 128, 784, "few-tile"), (300, 700, 333, "two-pass")])
+def test_dense_fused_graph_replays(ane, oracle, M, N, K, route):
+    """dense_fused_i8 captured in a HIP graph, as bench.py times it, on each
+    route: the strip route and the resident quantizer (grid-wide waits: a
+    plain launch under capture, its tag fixed at capture time), the
+    few-tile route and the two-pass quantizer.  The call is made once
+    eagerly on the capture stream (so the grid-wide-wait routes may be
+    captured there), then the graph is replayed three times with eager work
+    (a fill of C) and synchronizations between the replays; every replay's
+    C is bit-identical to the oracle and no wait gave up.  The one-launch
+    routes leave the workspace's qA bytes as they were (0x5A), which shows
+    the route the graph holds."""
+    import torch
+
+    A, B = data.gemm_inputs(M, N, K, seed=M + 2 * N + K)
+    oracle.set_threads(0)
+    try:
+        ref = oracle.dense_fused_i8(M, N, K, F32(1.0), True, A, B)
+    finally:
+        oracle.set_threads(1)
+    dA, dB = dev(A), dev(B)
+    C = zeros(M * N, torch.float32)
+    wsb = ane.dense_fused_i8_workspace_size(M, N, K)
+    ws = torch.full((wsb,), 0x5A, dtype=torch.uint8, device="cuda")
+    lib = ane.lib()
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws, stream=s)
+        s.synchronize()
+        assert_f32_identical(host(C).reshape(M, N), ref)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ane.dense_fused_i8(M, N, K, 1.0, True, dA, dB, C, workspace=ws, stream=s, check_wait=False)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert lib.ane_hip_grid_wait_status(ane._stream_handle(s)) == 0
+        ane.dense_fused_i8_status(ws, stream=s)
+        assert_f32_identical(host(C).reshape(M, N), ref)
+    qa = host(ws)[12800: 12800 + M * K]
+    assert (qa == 0x5A).all() == (route in ("strip", "few-tile"))
+    del g
+
+
 def test_dense_fused_4096_cubed_sampled(ane, oracle):
     """Config 2 at full size: both per-tensor scales exact, and a sample of
     rows of C identical to the oracle's contraction of the oracle-quantized
