@@ -503,7 +503,7 @@ def test_dense_fused_quantize_phase_bytes(ane, oracle, M, N, K):
 
 _STRIP = [(1, 4096, 4096, True, 1.0), (16, 4096, 4096, False, 1.0), (5, 4096, 3072, False, 2.5),
           (9, 3072, 4096, True, 0.75), (4, 4096, 1536, True, 1.0), (3, 2048, 4096, False, 1.0),
-          (8, 4096, 4096, True, 1.0), (12, 2048, 2048 * 3, False, 1.0)]
+          (8, 4096, 4096, True, 1.0), (12, 2048, 2048 * 3, False, 1.0), (2, 8192, 2048, True, 1.0)]
 
 
 @pytest.mark.parametrize("M,N,K,relu,scale", _STRIP)
@@ -514,8 +514,9 @@ def test_dense_fused_strip_route(ane, oracle, M, N, K, relu, scale):
     rows loaded before the wait only (M <= 4), with the second batch (5-8)
     and the third (9-16), K of 1536 (rows of 384 float4, half a thread's
     second load), fewer strips than workgroups (N = 2048: half the
-    workgroups hold A's share and wait only), and K past 4096 (12 x 2048 x
-    6144), which the route does not take.  The workspace's qA bytes stay as
+    workgroups hold A's share and wait only), K past 4096 (12 x 2048 x
+    6144) and more strips than a 256-CU device has workgroups (2 x 8192 x
+    2048), which the route does not take.  The workspace's qA bytes stay as
     they were (0x5A) exactly when the strip route ran."""
     import torch
 
@@ -535,20 +536,28 @@ def test_dense_fused_strip_route(ane, oracle, M, N, K, relu, scale):
     assert_f32_identical(host(C).reshape(M, N), ref)
     assert host(sc).tobytes() == np.array([sa, sb], F32).tobytes()
     qa = host(ws)[12800: 12800 + M * K]
-    assert (qa == 0x5A).all() == (K <= 4096)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert (qa == 0x5A).all() == (K <= 4096 and N // 16 <= cus)
 
 
-@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny", "b_nan_last"])
+@pytest.mark.parametrize("case", ["a_nan", "b_inf", "a_neg_inf", "a_zero", "b_tiny", "b_nan_last",
+                                  "a_nan_row12", "a_inf_row15"])
 def test_dense_fused_strip_special_operands(ane, oracle, case):
-    """The strip route (7 x 4096 x 4096) on the operands the quantizer
-    special-cases: a NaN or an infinity (the exact pack4 for that tensor), an
-    all-zero A, a B of denormals and signed zeros (127 / amax = +inf), and a
-    NaN in B's last row and column (the last strip's last thread)."""
+    """The strip route (7 x 4096 x 4096; 16 rows for the last two cases) on
+    the operands the quantizer special-cases: a NaN or an infinity (the exact
+    pack4 for that tensor), an all-zero A, a B of denormals and signed zeros
+    (127 / amax = +inf), a NaN in B's last row and column (the last strip's
+    last thread), and a NaN or an infinity in A's rows 8-15, which are
+    loaded after the grid-wide wait."""
     import torch
 
-    M, N, K = 7, 4096, 4096
+    M, N, K = (16 if case in ("a_nan_row12", "a_inf_row15") else 7), 4096, 4096
     A, B = data.gemm_inputs(M, N, K, seed=13)
-    if case == "a_nan":
+    if case == "a_nan_row12":
+        A[12, K - 5] = np.nan
+    elif case == "a_inf_row15":
+        A[15, 600] = -np.inf
+    elif case == "a_nan":
         A[M - 1, K // 3] = np.nan
     elif case == "b_inf":
         B[K // 2, N // 3] = np.inf
